@@ -1,0 +1,134 @@
+/*
+ * swiftltx_q4.h -- C ABI of the MI355X (gfx950) MLX 4-bit dequant matmul path.
+ *
+ * Drop-in for swift-ltx's quantized-matmul operators (Sources/SwiftLLM/Ops.swift)
+ * and the weight layout its loader produces (ModelWeights.swift:7-11):
+ *
+ *   weight  uint32 [N, K/8]          nibble k of row n = bits 4*(k%8)..+3 of word k/8
+ *   scales  fp16   [N, K/group_size]
+ *   biases  fp16   [N, K/group_size]
+ *   w[n,k] = scales[n,k/g] * q[n,k] + biases[n,k/g]      (Kernels.swift:392-395)
+ *   out[m,n] = sum_k x[m,k] * w[n,k], fp32 accumulation
+ *
+ * Conventions (all entry points):
+ *   - Every pointer is a device pointer the caller allocated; the library never
+ *     allocates, frees or keeps them.  Outputs are written, never read.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the default stream) and
+ *     nothing synchronises: results are visible to later work on that stream.
+ *     This mirrors the reference's batched mode (MetalContext.swift:109-134).
+ *   - Return value: SLTX_OK (0) or a negative sltx_status.  On failure nothing
+ *     was enqueued and sltx_last_error() (thread-local) says why.  The
+ *     reference has no error returns: it crashes (Kernels.swift:19,25-26) or,
+ *     for unchecked shapes such as K % 32 != 0, reads out of bounds
+ *     (Kernels.swift:490).  Here such shapes are rejected before any launch.
+ *   - Shape rules: K > 0, K % 32 == 0, group_size in {32, 64, 128},
+ *     K % group_size == 0, M >= 0, N >= 0 (M == 0 or N == 0 is a no-op).
+ *     x and weight must be 16-byte aligned; scales, biases and 16-bit outputs
+ *     2-byte aligned; fp32 outputs and bias 4-byte aligned.
+ *   - Thread-safe: no hidden global mutable state beyond a once-per-device init.
+ */
+#ifndef SWIFTLTX_Q4_H
+#define SWIFTLTX_Q4_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum sltx_status {
+    SLTX_OK = 0,
+    SLTX_ERR_INVALID = -1,     /* bad pointer, shape, alignment or enum */
+    SLTX_ERR_UNSUPPORTED = -2, /* valid for the reference, not built here (e.g. group_size 16) */
+    SLTX_ERR_HIP = -3          /* HIP runtime error (no device, launch failure, ...) */
+} sltx_status;
+
+typedef enum sltx_dtype {
+    SLTX_F16 = 0,
+    SLTX_BF16 = 1,
+    SLTX_F32 = 2
+} sltx_dtype;
+
+typedef enum sltx_epilogue {
+    SLTX_EPI_NONE = 0,
+    SLTX_EPI_GELU_TANH = 2 /* out = gelu_tanh(acc + bias), Kernels.swift:1774-1783 */
+} sltx_epilogue;
+
+/* LinearWeight.quantized(weight:scales:biases:K:groupSize:) (ModelWeights.swift:7-11). */
+typedef struct sltx_q4_weight {
+    const uint32_t* weight; /* [N, K/8] */
+    const uint16_t* scales; /* [N, K/group_size] fp16 */
+    const uint16_t* biases; /* [N, K/group_size] fp16 */
+    int32_t K;
+    int32_t group_size;
+} sltx_q4_weight;
+
+/* ABI version of this header (bumped on any signature change). */
+int sltx_abi_version(void);
+
+/* Checks the current HIP device is usable (gfx950).  Called lazily by every
+ * compute entry point; calling it first only moves the cost.  No counterpart
+ * in the reference (MetalContext.shared, MetalContext.swift:52-65, is its
+ * analogue). */
+int sltx_init(void);
+
+/* Message for the last non-zero status returned on this thread. */
+const char* sltx_last_error(void);
+
+/* matmulQ4(_:weight:scales:biases:M:K:N:groupSize:) -> Tensor  (Ops.swift:285-305)
+ * out[M,N] fp16 = x[M,K] fp16 . dequant(W)^T.  M == 1 runs the HBM-streaming
+ * GEMV (the reference's matmul_q4, Kernels.swift:444-620); M > 1 runs the
+ * MFMA GEMM (the reference re-reads W per row here; results agree within
+ * the stated tolerance). */
+int sltx_matmul_q4(const void* x, const uint32_t* weight, const uint16_t* scales,
+                   const uint16_t* biases, void* out, int32_t M, int32_t K, int32_t N,
+                   int32_t group_size, void* stream);
+
+/* matmulQ4Fast(_:weight:scales:biases:M:K:N:groupSize:) -> Tensor  (Ops.swift:312-345)
+ * Same product, fp16 out, through the MFMA GEMM for every M (M == 1 included). */
+int sltx_matmul_q4_fast(const void* x, const uint32_t* weight, const uint16_t* scales,
+                        const uint16_t* biases, void* out, int32_t M, int32_t K, int32_t N,
+                        int32_t group_size, void* stream);
+
+/* matmulQ4FastF32(_:weight:scales:biases:M:K:N:groupSize:) -> Tensor  (Ops.swift:348-381)
+ * Same product, fp32 out (no fp16 overflow). */
+int sltx_matmul_q4_fast_f32(const void* x, const uint32_t* weight, const uint16_t* scales,
+                            const uint16_t* biases, float* out, int32_t M, int32_t K, int32_t N,
+                            int32_t group_size, void* stream);
+
+/* siluMul(_:_:) -> Tensor  (Ops.swift:44-56; kernel silu_mul, Kernels.swift:90-98)
+ * out[i] = half(silu(float(a[i])) * float(b[i])), count fp16 elements. */
+int sltx_silu_mul(const void* a, const void* b, void* out, int64_t count, void* stream);
+
+/* linear(_:_:M:K:N:fast:) -> Tensor for the .quantized case  (Ops.swift:741-752)
+ * Routing rule kept: fast && M > 1 -> sltx_matmul_q4_fast, else sltx_matmul_q4.
+ * w->K must equal K.  The reference's .float case is a CPU fp32 matmul
+ * (LlamaModel.swift:478-493) and is outside this library. */
+int sltx_linear(const void* x, const sltx_q4_weight* w, void* out, int32_t M, int32_t K,
+                int32_t N, int32_t fast, void* stream);
+
+/* Fused SwiGLU: out[M,N] fp16 = silu(x.Wg^T) * (x.Wu^T), in one pass over
+ * both weight sets with the product formed from the fp32 accumulators.
+ * Replaces linear(gate) + linear(up) + siluMul (LlamaModel.swift:275-277
+ * prefill, :327-329 decode).  The reference rounds gate and up to fp16 before
+ * silu_mul; this keeps them in fp32 (closer to the fp64 oracle).  M == 1 runs
+ * the GEMV, M > 1 the GEMM.  gate and up must have equal K and group_size. */
+int sltx_matmul_q4_silu_mul(const void* x, const sltx_q4_weight* gate, const sltx_q4_weight* up,
+                            void* out, int32_t M, int32_t K, int32_t N, void* stream);
+
+/* Extended GEMM: x_dtype in {SLTX_F16, SLTX_BF16}; out_dtype in {SLTX_F16,
+ * SLTX_BF16, SLTX_F32}; bias (fp32 [N]) optional (NULL = none); epilogue
+ * SLTX_EPI_NONE or SLTX_EPI_GELU_TANH.  out = epi(x . dequant(W)^T + bias).
+ * Covers DiTLinear.applyF32in's quantized branch (DiTModel.swift:102-125:
+ * matmulQ4FastF32 then addBiasF32F32, Ops.swift:1780-1791) and the GELU-tanh
+ * that follows it in the DiT feed-forward (DiTModel.swift:953,
+ * Kernels.swift:1774-1783), with bf16 activations accepted directly. */
+int sltx_matmul_q4_ex(const void* x, int32_t x_dtype, const sltx_q4_weight* w, const float* bias,
+                      int32_t epilogue, void* out, int32_t out_dtype, int32_t M, int32_t N,
+                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SWIFTLTX_Q4_H */

@@ -1,0 +1,270 @@
+"""NumPy restatement of swift-ltx's MLX 4-bit dequant matmul, plus a ctypes
+loader for the C restatement in q4_oracle.c.
+
+TEST INFRASTRUCTURE ONLY: this module is the checker the HIP kernels are
+compared against.  Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg import it; the shipped library never does.
+
+Reference citations are relative to the swift-ltx tree (Sources/SwiftLLM/).
+
+Layout (ModelWeights.swift:7-11, LinearWeight.quantized):
+    weight  uint32 [N, K/8]   nibble k of row n = bits 4*(k%8).. of word k/8
+    scales  fp16   [N, K/g]
+    biases  fp16   [N, K/g]
+    w[n,k] = scales[n,k/g] * q[n,k] + biases[n,k/g]     (Kernels.swift:392-395)
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(HERE, "_build")
+LIB_PATH = os.path.join(LIB_DIR, "libq4oracle.so")
+
+
+# --------------------------------------------------------------- packing ---
+
+def pack_q4(q: np.ndarray) -> np.ndarray:
+    """[N, K] codes 0..15 -> [N, K/8] uint32, low nibble first
+    (inverse of the unpack at Kernels.swift:385-390)."""
+    q = np.asarray(q, dtype=np.uint32)
+    n, k = q.shape
+    assert k % 8 == 0
+    q = q.reshape(n, k // 8, 8)
+    shifts = (np.arange(8, dtype=np.uint32) * 4)[None, None, :]
+    return np.bitwise_or.reduce(q << shifts, axis=2).astype(np.uint32)
+
+
+def unpack_q4(w: np.ndarray) -> np.ndarray:
+    """[N, K/8] uint32 -> [N, K] uint8 codes; nibble k is
+    (word >> (4*(k%8))) & 0xF (Kernels.swift:390, :428)."""
+    w = np.asarray(w, dtype=np.uint32)
+    n, pk = w.shape
+    shifts = (np.arange(8, dtype=np.uint32) * 4)[None, None, :]
+    return ((w[:, :, None] >> shifts) & 0xF).astype(np.uint8).reshape(n, pk * 8)
+
+
+def dequant_f64(w: np.ndarray, scales: np.ndarray, biases: np.ndarray, group: int) -> np.ndarray:
+    """w = s*q + b per group, in fp64 (Kernels.swift:392-395, :430-433)."""
+    q = unpack_q4(w).astype(np.float64)
+    n, k = q.shape
+    s = np.repeat(scales.astype(np.float64), group, axis=1)
+    b = np.repeat(biases.astype(np.float64), group, axis=1)
+    assert s.shape == (n, k)
+    return s * q + b
+
+
+def matmul_q4_f64(x: np.ndarray, w: np.ndarray, scales: np.ndarray, biases: np.ndarray,
+                  group: int) -> np.ndarray:
+    """fp64 closed form y = x . dequant(W)^T, x [M,K] (fp16 or fp32-held bf16
+    values) -> [M,N] fp64.  matmul_q4 (Kernels.swift:444-620) for M==1 and the
+    quantized GEMM (Ops.swift:312-381) for M>1 compute this product."""
+    return np.asarray(x, dtype=np.float64) @ dequant_f64(w, scales, biases, group).T
+
+
+def silu_mul_f64(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """silu(a)*b in fp64 (Kernels.swift:90-98 computes it in fp32)."""
+    a = np.asarray(a, dtype=np.float64)
+    with np.errstate(over="ignore"):
+        return a / (1.0 + np.exp(-a)) * np.asarray(b, dtype=np.float64)
+
+
+def gelu_tanh_f64(v: np.ndarray) -> np.ndarray:
+    """GELU tanh approximation with the inner clamp at +-10
+    (gelu_approximate_f32, Kernels.swift:1774-1783), fp64."""
+    v = np.asarray(v, dtype=np.float64)
+    inner = np.clip(0.7978845608 * (v + 0.044715 * v ** 3), -10.0, 10.0)
+    return 0.5 * v * (1.0 + np.tanh(inner))
+
+
+# ----------------------------------------------------- bf16 (numpy has none) --
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even fp32 -> bf16 bit patterns (uint16)."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    lsb = (u >> 16) & 1
+    r = ((u + 0x7FFF + lsb) >> 16).astype(np.uint16)
+    nan = np.isnan(np.asarray(x, dtype=np.float32))
+    r[nan] = 0x7FC0
+    return r
+
+
+def bf16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# -------------------------------------------------------------- inputs ---
+
+def make_inputs(M: int, N: int, K: int, group: int = 64, seed: int = 0, x_dtype: str = "f16",
+                n_weights: int = 1):
+    """Synthetic inputs with the distributions BASELINE states:
+    x ~ N(0,1) (fp16, or bf16 bits when x_dtype == 'bf16'); codes uniform 0..15;
+    scales ~ |N(0, 0.02)| fp16; biases = -8*scales (exact in fp16).
+    Draw order from one default_rng(seed): x, then per weight set (codes, scales).
+    Returns (x, [(W, scales, biases), ...])."""
+    rng = np.random.default_rng(seed)
+    xf = rng.standard_normal((M, K), dtype=np.float32)
+    if x_dtype == "bf16":
+        x = f32_to_bf16_bits(xf)
+    else:
+        x = xf.astype(np.float16)
+    sets = []
+    for _ in range(n_weights):
+        q = rng.integers(0, 16, size=(N, K), dtype=np.uint8)
+        s = np.abs(0.02 * rng.standard_normal((N, K // group), dtype=np.float32)).astype(np.float16)
+        b = (-8.0 * s.astype(np.float32)).astype(np.float16)
+        sets.append((pack_q4(q), s, b))
+    return x, sets
+
+
+def x_values(x: np.ndarray, x_dtype: str = "f16") -> np.ndarray:
+    """fp64 values of an fp16 array or a bf16 bit-pattern array."""
+    if x_dtype == "bf16":
+        return bf16_bits_to_f32(x).astype(np.float64)
+    return np.asarray(x, dtype=np.float64)
+
+
+# ------------------------------------------------------------- metrics ---
+
+def max_rel_err(y, ref) -> float:
+    """The parity gate's metric: max_i |y_i - ref_i| / max_i |ref_i|."""
+    y = np.asarray(y, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    den = float(np.max(np.abs(ref))) if ref.size else 0.0
+    if ref.size == 0:
+        return 0.0
+    return float(np.max(np.abs(y - ref))) / max(den, 1e-30)
+
+
+def elementwise_ok(y, ref, rtol: float, atol_rms: float) -> tuple[bool, float]:
+    """|y-ref| <= rtol*|ref| + atol_rms*rms(ref) for every element; returns
+    (ok, worst ratio of error to allowance)."""
+    y = np.asarray(y, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    if ref.size == 0:
+        return True, 0.0
+    rms = math.sqrt(float(np.mean(ref * ref))) or 1e-30
+    allow = rtol * np.abs(ref) + atol_rms * rms
+    ratio = np.abs(y - ref) / allow
+    worst = float(np.max(ratio))
+    return bool(worst <= 1.0 and np.all(np.isfinite(y))), worst
+
+
+# ----------------------------------------------------------- C library ---
+
+def build_c(force: bool = False) -> str:
+    """Compile q4_oracle.c into _build/libq4oracle.so with gcc."""
+    src = os.path.join(HERE, "q4_oracle.c")
+    if (not force and os.path.exists(LIB_PATH)
+            and os.path.getmtime(LIB_PATH) >= os.path.getmtime(src)):
+        return LIB_PATH
+    os.makedirs(LIB_DIR, exist_ok=True)
+    tmp = LIB_PATH + ".tmp%d" % os.getpid()
+    subprocess.run(["gcc", "-O2", "-fPIC", "-shared", "-std=c11", "-ffp-contract=off",
+                    "-o", tmp, src, "-lm", "-lpthread"], check=True)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+_lib = None
+
+
+def lib():
+    """ctypes handle of the C oracle (built on first use if missing)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build_c()
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.c_void_p
+        I64 = ctypes.c_int64
+        L.oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.oracle_f16_to_f32.restype = ctypes.c_float
+        L.oracle_f32_to_f16.argtypes = [ctypes.c_float]
+        L.oracle_f32_to_f16.restype = ctypes.c_uint16
+        L.oracle_unpack_q4.argtypes = [P, P, I64, I64]
+        L.oracle_matmul_q4_f64.argtypes = [P, ctypes.c_int, P, P, P, P, I64, I64, I64, I64]
+        L.oracle_matmul_q4_emu.argtypes = [P, P, P, P, P, I64, I64, I64, I64]
+        L.oracle_silu_mul.argtypes = [P, P, P, I64]
+        L.oracle_gelu_tanh_f32.argtypes = [P, P, I64]
+        L.oracle_cpu_matmul_q4.argtypes = [P, P, P, P, P, I64, I64, I64, I64, ctypes.c_int]
+        L.oracle_cpu_matmul_q4.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def c_f16_to_f32(h: np.ndarray) -> np.ndarray:
+    L = lib()
+    return np.array([L.oracle_f16_to_f32(int(v)) for v in np.asarray(h, np.uint16).ravel()],
+                    dtype=np.float32)
+
+
+def c_unpack_q4(w: np.ndarray, K: int) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint32)
+    q = np.empty((w.shape[0], K), dtype=np.uint8)
+    lib().oracle_unpack_q4(_p(w), _p(q), w.shape[0], K)
+    return q
+
+
+def c_matmul_q4_f64(x, w, s, b, group, x_dtype="f16") -> np.ndarray:
+    x = np.ascontiguousarray(x).view(np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.uint32)
+    s = np.ascontiguousarray(s, dtype=np.float16).view(np.uint16)
+    b = np.ascontiguousarray(b, dtype=np.float16).view(np.uint16)
+    M, K = x.shape
+    N = w.shape[0]
+    y = np.empty((M, N), dtype=np.float64)
+    lib().oracle_matmul_q4_f64(_p(x), 1 if x_dtype == "bf16" else 0, _p(w), _p(s), _p(b),
+                               _p(y), M, N, K, group)
+    return y
+
+
+def c_matmul_q4_emu(x, w, s, b, group) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float16).view(np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.uint32)
+    s = np.ascontiguousarray(s, dtype=np.float16).view(np.uint16)
+    b = np.ascontiguousarray(b, dtype=np.float16).view(np.uint16)
+    M, K = x.shape
+    N = w.shape[0]
+    y = np.empty((M, N), dtype=np.uint16)
+    lib().oracle_matmul_q4_emu(_p(x), _p(w), _p(s), _p(b), _p(y), M, N, K, group)
+    return y.view(np.float16)
+
+
+def c_silu_mul(a, b) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float16).view(np.uint16)
+    b = np.ascontiguousarray(b, dtype=np.float16).view(np.uint16)
+    out = np.empty_like(a)
+    lib().oracle_silu_mul(_p(a), _p(b), _p(out), a.size)
+    return out.view(np.float16)
+
+
+def c_gelu_tanh_f32(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().oracle_gelu_tanh_f32(_p(x), _p(out), x.size)
+    return out
+
+
+def c_cpu_matmul_q4(x, w, s, b, group, threads=1) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float16).view(np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.uint32)
+    s = np.ascontiguousarray(s, dtype=np.float16).view(np.uint16)
+    b = np.ascontiguousarray(b, dtype=np.float16).view(np.uint16)
+    M, K = x.shape
+    N = w.shape[0]
+    y = np.empty((M, N), dtype=np.uint16)
+    rc = lib().oracle_cpu_matmul_q4(_p(x), _p(w), _p(s), _p(b), _p(y), M, N, K, group, threads)
+    if rc < 0:
+        raise RuntimeError("oracle_cpu_matmul_q4 failed")
+    return y.view(np.float16)

@@ -1,0 +1,230 @@
+"""swift-ltx MI355X 4-bit dequant matmul path: Python mirror of the reference's
+Ops entry points over the C ABI in include/swiftltx_q4.h.
+
+The shipped compute path is libswiftltx_q4.so (hand-written HIP for gfx950);
+this module only marshals torch device tensors into it with ctypes.  There is
+no fallback: if the library is missing, every entry point raises.
+
+Reference interface mirrored (Sources/SwiftLLM/ of swift-ltx):
+    matmulQ4        Ops.swift:285-305      -> matmul_q4
+    matmulQ4Fast    Ops.swift:312-345      -> matmul_q4_fast
+    matmulQ4FastF32 Ops.swift:348-381      -> matmul_q4_fast_f32
+    siluMul         Ops.swift:44-56        -> silu_mul
+    linear          Ops.swift:741-752      -> linear
+    LinearWeight    ModelWeights.swift:7-11 -> Q4Weight
+The reference returns a new Tensor from its buffer pool and crashes on error;
+here each call returns a new torch tensor (or writes `out=`) and raises
+SltxError carrying the library's status code and message.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "lib", "libswiftltx_q4.so")
+
+SLTX_OK = 0
+SLTX_ERR_INVALID = -1
+SLTX_ERR_UNSUPPORTED = -2
+SLTX_ERR_HIP = -3
+
+SLTX_F16 = 0
+SLTX_BF16 = 1
+SLTX_F32 = 2
+
+SLTX_EPI_NONE = 0
+SLTX_EPI_GELU_TANH = 2
+
+# Every symbol include/swiftltx_q4.h declares.
+EXPORTED = (
+    "sltx_abi_version",
+    "sltx_init",
+    "sltx_last_error",
+    "sltx_matmul_q4",
+    "sltx_matmul_q4_fast",
+    "sltx_matmul_q4_fast_f32",
+    "sltx_silu_mul",
+    "sltx_linear",
+    "sltx_matmul_q4_silu_mul",
+    "sltx_matmul_q4_ex",
+)
+
+
+class SltxError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+class CQ4Weight(ctypes.Structure):
+    """sltx_q4_weight."""
+    _fields_ = [
+        ("weight", ctypes.c_void_p),
+        ("scales", ctypes.c_void_p),
+        ("biases", ctypes.c_void_p),
+        ("K", ctypes.c_int32),
+        ("group_size", ctypes.c_int32),
+    ]
+
+
+_lib = None
+
+
+def lib():
+    """The loaded C library.  Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} not found: build it with `python swift-ltx_amd/build.py` "
+                "(there is no CPU fallback)")
+        L = ctypes.CDLL(LIB_PATH)
+        P, I32, I64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+        L.sltx_abi_version.restype = ctypes.c_int
+        L.sltx_init.restype = ctypes.c_int
+        L.sltx_last_error.restype = ctypes.c_char_p
+        mm = [P, P, P, P, P, I32, I32, I32, I32, P]
+        for n in ("sltx_matmul_q4", "sltx_matmul_q4_fast", "sltx_matmul_q4_fast_f32"):
+            getattr(L, n).argtypes = mm
+            getattr(L, n).restype = ctypes.c_int
+        L.sltx_silu_mul.argtypes = [P, P, P, I64, P]
+        L.sltx_silu_mul.restype = ctypes.c_int
+        W = ctypes.POINTER(CQ4Weight)
+        L.sltx_linear.argtypes = [P, W, P, I32, I32, I32, I32, P]
+        L.sltx_linear.restype = ctypes.c_int
+        L.sltx_matmul_q4_silu_mul.argtypes = [P, W, W, P, I32, I32, I32, P]
+        L.sltx_matmul_q4_silu_mul.restype = ctypes.c_int
+        L.sltx_matmul_q4_ex.argtypes = [P, I32, W, P, I32, P, I32, I32, I32, P]
+        L.sltx_matmul_q4_ex.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != SLTX_OK:
+        msg = lib().sltx_last_error().decode(errors="replace")
+        raise SltxError(rc, msg)
+
+
+def last_error() -> str:
+    return lib().sltx_last_error().decode(errors="replace")
+
+
+# ------------------------------------------------------------ torch glue ---
+
+def _torch():
+    import torch
+    return torch
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    torch = _torch()
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def _dtype_code(dt) -> int:
+    torch = _torch()
+    if dt == torch.float16:
+        return SLTX_F16
+    if dt == torch.bfloat16:
+        return SLTX_BF16
+    if dt == torch.float32:
+        return SLTX_F32
+    raise ValueError(f"unsupported dtype {dt}")
+
+
+@dataclass
+class Q4Weight:
+    """LinearWeight.quantized (ModelWeights.swift:7-11): weight uint32/int32
+    [N, K/8], scales and biases fp16 [N, K/group_size]."""
+    weight: object
+    scales: object
+    biases: object
+    K: int
+    group_size: int = 64
+
+    @property
+    def N(self) -> int:
+        return int(self.weight.shape[0])
+
+    def c(self) -> CQ4Weight:
+        return CQ4Weight(self.weight.data_ptr(), self.scales.data_ptr(), self.biases.data_ptr(),
+                         int(self.K), int(self.group_size))
+
+
+def _new(shape, dtype, like):
+    return _torch().empty(shape, dtype=dtype, device=like.device)
+
+
+def matmul_q4(x, weight, scales, biases, M, K, N, group_size, out=None, stream=None):
+    """matmulQ4 (Ops.swift:285-305): [M,N] fp16 = x[M,K] fp16 . dequant(W)^T."""
+    out = _new((M, N), _torch().float16, x) if out is None else out
+    check(lib().sltx_matmul_q4(_ptr(x), _ptr(weight), _ptr(scales), _ptr(biases), _ptr(out),
+                               M, K, N, group_size, _stream(stream)))
+    return out
+
+
+def matmul_q4_fast(x, weight, scales, biases, M, K, N, group_size, out=None, stream=None):
+    """matmulQ4Fast (Ops.swift:312-345): MFMA GEMM, fp16 out."""
+    out = _new((M, N), _torch().float16, x) if out is None else out
+    check(lib().sltx_matmul_q4_fast(_ptr(x), _ptr(weight), _ptr(scales), _ptr(biases), _ptr(out),
+                                    M, K, N, group_size, _stream(stream)))
+    return out
+
+
+def matmul_q4_fast_f32(x, weight, scales, biases, M, K, N, group_size, out=None, stream=None):
+    """matmulQ4FastF32 (Ops.swift:348-381): MFMA GEMM, fp32 out."""
+    out = _new((M, N), _torch().float32, x) if out is None else out
+    check(lib().sltx_matmul_q4_fast_f32(_ptr(x), _ptr(weight), _ptr(scales), _ptr(biases),
+                                        _ptr(out), M, K, N, group_size, _stream(stream)))
+    return out
+
+
+def silu_mul(a, b, out=None, stream=None):
+    """siluMul (Ops.swift:44-56): half(silu(a) * b), fp16."""
+    out = _torch().empty_like(a) if out is None else out
+    check(lib().sltx_silu_mul(_ptr(a), _ptr(b), _ptr(out), a.numel(), _stream(stream)))
+    return out
+
+
+def linear(x, w: Q4Weight, M, K, N, fast=False, out=None, stream=None):
+    """linear (Ops.swift:741-752), quantized case: fast && M>1 -> GEMM, else matmul_q4."""
+    out = _new((M, N), _torch().float16, x) if out is None else out
+    cw = w.c()
+    check(lib().sltx_linear(_ptr(x), ctypes.byref(cw), _ptr(out), M, K, N, 1 if fast else 0,
+                            _stream(stream)))
+    return out
+
+
+def matmul_q4_silu_mul(x, gate: Q4Weight, up: Q4Weight, M, K, N, out=None, stream=None):
+    """Fused silu(x.Wg^T) * (x.Wu^T) -> fp16 [M, N]; replaces linear(gate),
+    linear(up), siluMul (LlamaModel.swift:275-277, :327-329)."""
+    out = _new((M, N), _torch().float16, x) if out is None else out
+    g, u = gate.c(), up.c()
+    check(lib().sltx_matmul_q4_silu_mul(_ptr(x), ctypes.byref(g), ctypes.byref(u), _ptr(out), M,
+                                        K, N, _stream(stream)))
+    return out
+
+
+def matmul_q4_ex(x, w: Q4Weight, M, N, out_dtype=None, bias=None, epilogue=SLTX_EPI_NONE,
+                 out=None, stream=None):
+    """epi(x . dequant(W)^T + bias) with x fp16/bf16 and out fp16/bf16/fp32
+    (DiTLinear.applyF32in q4 branch, DiTModel.swift:102-125, + GELU-tanh)."""
+    torch = _torch()
+    if out is None:
+        out = _new((M, N), out_dtype or torch.float32, x)
+    cw = w.c()
+    check(lib().sltx_matmul_q4_ex(_ptr(x), _dtype_code(x.dtype), ctypes.byref(cw), _ptr(bias),
+                                  epilogue, _ptr(out), _dtype_code(out.dtype), M, N,
+                                  _stream(stream)))
+    return out

@@ -1,0 +1,248 @@
+// q4_capi.hip -- the C ABI (include/swiftltx_q4.h): argument validation,
+// routing and launch of the gfx950 kernels.  Validation runs before any HIP
+// call, so error paths behave the same with or without a GPU.
+#include <cstdarg>
+#include <mutex>
+#include <string>
+#include <cstdio>
+#include <cstring>
+
+#include "q4_common.hpp"
+#include "q4_launch.hpp"
+#include "../../include/swiftltx_q4.h"
+
+namespace sltx {
+
+
+
+
+
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(kErrHip, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+int log2_group(int g) { return g == 32 ? 0 : g == 64 ? 1 : g == 128 ? 2 : -1; }
+
+// Shape / pointer checks common to every matmul entry point.
+int check_weight(const char* fn, const void* x, const uint32_t* w, const uint16_t* s,
+                 const uint16_t* b, const void* out, int M, int K, int N, int g) {
+    if (M < 0 || N < 0) return fail(kErrInvalid, "%s: negative M (%d) or N (%d)", fn, M, N);
+    if (K <= 0) return fail(kErrInvalid, "%s: K must be positive (got %d)", fn, K);
+    if (K % 32 != 0) return fail(kErrInvalid, "%s: K (%d) must be a multiple of 32", fn, K);
+    if (g <= 0 || g % 8 != 0) return fail(kErrInvalid, "%s: group_size %d is not a positive multiple of 8", fn, g);
+    if (K % g != 0) return fail(kErrInvalid, "%s: K (%d) is not a multiple of group_size (%d)", fn, K, g);
+    if (log2_group(g) < 0)
+        return fail(kErrUnsupported, "%s: group_size %d unsupported (32, 64 or 128)", fn, g);
+    if (M == 0 || N == 0) return kOk;
+    if (!x || !w || !s || !b || !out) return fail(kErrInvalid, "%s: null pointer argument", fn);
+    if (!aligned(x, 16)) return fail(kErrInvalid, "%s: x must be 16-byte aligned", fn);
+    if (!aligned(w, 16)) return fail(kErrInvalid, "%s: weight must be 16-byte aligned", fn);
+    if (!aligned(s, 2) || !aligned(b, 2)) return fail(kErrInvalid, "%s: scales/biases must be 2-byte aligned", fn);
+    return kOk;
+}
+
+// Once-per-device readiness check (gfx950 code object present and runnable).
+std::mutex g_init_mu;
+int g_dev_state[64];  // 0 unknown, 1 ok, -1 bad
+
+int ensure_device() {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= 64) return fail(kErrHip, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_init_mu);
+    if (g_dev_state[dev] == 1) return kOk;
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        g_dev_state[dev] = -1;
+        return fail(kErrUnsupported, "device %d is %s; this library is built for gfx950 only", dev,
+                    prop.gcnArchName);
+    }
+    g_dev_state[dev] = 1;
+    return kOk;
+}
+
+int finish(hipError_t e, const char* fn) {
+    if (e != hipSuccess) return hip_fail(e, fn);
+    return kOk;
+}
+
+int run_gemv(const char* fn, const void* x, const sltx_q4_weight& w0, const sltx_q4_weight* w1,
+             void* out, int K, int N, hipStream_t st) {
+    GemvParams p;
+    p.x = static_cast<const uint16_t*>(x);
+    p.w0 = w0.weight;
+    p.s0 = w0.scales;
+    p.b0 = w0.biases;
+    p.w1 = w1 ? w1->weight : nullptr;
+    p.s1 = w1 ? w1->scales : nullptr;
+    p.b1 = w1 ? w1->biases : nullptr;
+    p.y = static_cast<uint16_t*>(out);
+    p.N = N;
+    p.K = K;
+    p.groups = K / w0.group_size;
+    p.gshift = log2_group(w0.group_size);
+    return finish(launch_gemv(p, w1 != nullptr, st), fn);
+}
+
+int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w0,
+             const sltx_q4_weight* w1, const float* bias, int epilogue, void* out, int y_dtype,
+             int M, int K, int N, hipStream_t st) {
+    GemmParams p;
+    p.a = x;
+    p.w0 = w0.weight;
+    p.s0 = w0.scales;
+    p.b0 = w0.biases;
+    p.w1 = w1 ? w1->weight : nullptr;
+    p.s1 = w1 ? w1->scales : nullptr;
+    p.b1 = w1 ? w1->biases : nullptr;
+    p.bias = bias;
+    p.y = out;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.groups = K / w0.group_size;
+    p.gshift = log2_group(w0.group_size);
+    p.tiles_m = p.tiles_n = 0;
+    p.y_dtype = y_dtype;
+    p.epilogue = w1 ? kEpiSiluMul : epilogue;
+    return finish(launch_gemm(p, x_dtype == kBF16, st), fn);
+}
+
+int matmul_common(const char* fn, const void* x, const uint32_t* weight, const uint16_t* scales,
+                  const uint16_t* biases, void* out, int M, int K, int N, int g, int y_dtype,
+                  bool force_gemm, void* stream) {
+    int rc = check_weight(fn, x, weight, scales, biases, out, M, K, N, g);
+    if (rc != kOk) return rc;
+    if (!aligned(out, y_dtype == kF32 ? 4 : 2)) return fail(kErrInvalid, "%s: misaligned out", fn);
+    if (M == 0 || N == 0) return kOk;
+    if ((rc = ensure_device()) != kOk) return rc;
+    const sltx_q4_weight w = {weight, scales, biases, K, g};
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (M == 1 && !force_gemm && y_dtype == kF16) return run_gemv(fn, x, w, nullptr, out, K, N, st);
+    return run_gemm(fn, x, kF16, w, nullptr, nullptr, kEpiNone, out, y_dtype, M, K, N, st);
+}
+
+}  // namespace
+}  // namespace sltx
+
+using namespace sltx;
+
+extern "C" {
+
+int sltx_abi_version(void) { return 1; }
+
+int sltx_init(void) { return ensure_device(); }
+
+const char* sltx_last_error(void) { return g_last_error.c_str(); }
+
+int sltx_matmul_q4(const void* x, const uint32_t* weight, const uint16_t* scales,
+                   const uint16_t* biases, void* out, int32_t M, int32_t K, int32_t N,
+                   int32_t group_size, void* stream) {
+    return matmul_common("sltx_matmul_q4", x, weight, scales, biases, out, M, K, N, group_size,
+                         kF16, false, stream);
+}
+
+int sltx_matmul_q4_fast(const void* x, const uint32_t* weight, const uint16_t* scales,
+                        const uint16_t* biases, void* out, int32_t M, int32_t K, int32_t N,
+                        int32_t group_size, void* stream) {
+    return matmul_common("sltx_matmul_q4_fast", x, weight, scales, biases, out, M, K, N,
+                         group_size, kF16, true, stream);
+}
+
+int sltx_matmul_q4_fast_f32(const void* x, const uint32_t* weight, const uint16_t* scales,
+                            const uint16_t* biases, float* out, int32_t M, int32_t K, int32_t N,
+                            int32_t group_size, void* stream) {
+    return matmul_common("sltx_matmul_q4_fast_f32", x, weight, scales, biases, out, M, K, N,
+                         group_size, kF32, true, stream);
+}
+
+int sltx_silu_mul(const void* a, const void* b, void* out, int64_t count, void* stream) {
+    const char* fn = "sltx_silu_mul";
+    if (count < 0) return fail(kErrInvalid, "%s: negative count", fn);
+    if (count == 0) return kOk;
+    if (!a || !b || !out) return fail(kErrInvalid, "%s: null pointer argument", fn);
+    if (!aligned(a, 2) || !aligned(b, 2) || !aligned(out, 2))
+        return fail(kErrInvalid, "%s: pointers must be 2-byte aligned", fn);
+    int rc = ensure_device();
+    if (rc != kOk) return rc;
+    return finish(launch_silu_mul(static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b),
+                                  static_cast<uint16_t*>(out), (long)count,
+                                  static_cast<hipStream_t>(stream)),
+                  fn);
+}
+
+int sltx_linear(const void* x, const sltx_q4_weight* w, void* out, int32_t M, int32_t K,
+                int32_t N, int32_t fast, void* stream) {
+    const char* fn = "sltx_linear";
+    if (!w) return fail(kErrInvalid, "%s: null weight descriptor", fn);
+    if (w->K != K) return fail(kErrInvalid, "%s: weight K (%d) != K (%d)", fn, w->K, K);
+    if (fast && M > 1)
+        return matmul_common(fn, x, w->weight, w->scales, w->biases, out, M, K, N, w->group_size,
+                             kF16, true, stream);
+    return matmul_common(fn, x, w->weight, w->scales, w->biases, out, M, K, N, w->group_size, kF16,
+                         false, stream);
+}
+
+int sltx_matmul_q4_silu_mul(const void* x, const sltx_q4_weight* gate, const sltx_q4_weight* up,
+                            void* out, int32_t M, int32_t K, int32_t N, void* stream) {
+    const char* fn = "sltx_matmul_q4_silu_mul";
+    if (!gate || !up) return fail(kErrInvalid, "%s: null weight descriptor", fn);
+    if (gate->K != K || up->K != K) return fail(kErrInvalid, "%s: weight K mismatch", fn);
+    if (gate->group_size != up->group_size)
+        return fail(kErrInvalid, "%s: gate and up group_size differ", fn);
+    int rc = check_weight(fn, x, gate->weight, gate->scales, gate->biases, out, M, K, N,
+                          gate->group_size);
+    if (rc != kOk) return rc;
+    rc = check_weight(fn, x, up->weight, up->scales, up->biases, out, M, K, N, up->group_size);
+    if (rc != kOk) return rc;
+    if (!aligned(out, 2)) return fail(kErrInvalid, "%s: misaligned out", fn);
+    if (M == 0 || N == 0) return kOk;
+    if ((rc = ensure_device()) != kOk) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (M == 1) return run_gemv(fn, x, *gate, up, out, K, N, st);
+    return run_gemm(fn, x, kF16, *gate, up, nullptr, kEpiNone, out, kF16, M, K, N, st);
+}
+
+int sltx_matmul_q4_ex(const void* x, int32_t x_dtype, const sltx_q4_weight* w, const float* bias,
+                      int32_t epilogue, void* out, int32_t out_dtype, int32_t M, int32_t N,
+                      void* stream) {
+    const char* fn = "sltx_matmul_q4_ex";
+    if (!w) return fail(kErrInvalid, "%s: null weight descriptor", fn);
+    if (x_dtype != kF16 && x_dtype != kBF16)
+        return fail(kErrInvalid, "%s: x_dtype %d must be SLTX_F16 or SLTX_BF16", fn, x_dtype);
+    if (out_dtype != kF16 && out_dtype != kBF16 && out_dtype != kF32)
+        return fail(kErrInvalid, "%s: out_dtype %d invalid", fn, out_dtype);
+    if (epilogue != kEpiNone && epilogue != kEpiGeluTanh)
+        return fail(kErrInvalid, "%s: epilogue %d invalid", fn, epilogue);
+    int rc = check_weight(fn, x, w->weight, w->scales, w->biases, out, M, w->K, N, w->group_size);
+    if (rc != kOk) return rc;
+    if (!aligned(out, out_dtype == kF32 ? 4 : 2)) return fail(kErrInvalid, "%s: misaligned out", fn);
+    if (bias && !aligned(bias, 4)) return fail(kErrInvalid, "%s: misaligned bias", fn);
+    if (M == 0 || N == 0) return kOk;
+    if ((rc = ensure_device()) != kOk) return rc;
+    return run_gemm(fn, x, x_dtype, *w, nullptr, bias, epilogue, out, out_dtype, M, w->K, N,
+                    static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,322 @@
+// q4_gemv.hip -- 4-bit dequant GEMV (decode, M == 1) for gfx950.
+//
+// Computes y[n] = sum_k x[k] * (s[n,k/g] * q[n,k] + b[n,k/g]) with fp32
+// accumulation and an fp16 store: the semantics of swift-ltx's matmul_q4
+// (Kernels.swift:444-620) at M == 1, dispatched by matmulQ4 (Ops.swift:285-305).
+// The SWIGLU variant computes silu(x.Wg^T) * (x.Wu^T) in one pass, replacing
+// linear(gate) + linear(up) + siluMul (LlamaModel.swift:327-329, Kernels.swift:90-98).
+//
+// Work decomposition (HBM-bound; every weight byte is read exactly once):
+//   * A row of K nibbles is K/32 "chunks" of 32 nibbles = one 16-byte load.
+//   * L lanes share a row: lane kl reads chunks kl, kl+L, ... (CPL of them), so a
+//     wave-wide load covers 64/L rows with contiguous 16*L-byte segments.
+//   * Each lane always sees the same chunk positions, so the x values it needs
+//     are prepared once per block (in LDS) and held in registers for all of
+//     its rows.  Each wave owns T row-iterations of 64/L rows.
+//
+// Dequant + dot (per 32-bit word of 8 nibbles q0..q7 for x0..x7):
+//   p0 = (w      & 0x000F000F) | 0x6400_6400  -> fp16 pair (1024+q0,    1024+q4)
+//   p1 = (w      & 0x00F000F0) | 0x6400_6400  -> fp16 pair (1024+16q1,  1024+16q5)
+//   p2 = (w>>8   & 0x000F000F) | 0x6400_6400  -> fp16 pair (1024+q2,    1024+q6)
+//   p3 = (w>>8   & 0x00F000F0) | 0x6400_6400  -> fp16 pair (1024+16q3,  1024+16q7)
+// dotted (v_dot2_f32_f16, fp32 accumulate) with the x pairs (x0,x4),
+// (x1/16,x5/16), (x2,x6), (x3/16,x7/16).  This gives sum(q*x) + 1024*sum(xs),
+// where xs are the x values as scaled.  The second term ("corr") depends on x
+// only and is subtracted by starting the accumulator at -corr.  Per chunk:
+//   acc += s_g * (sum q*x)  +  b_g * (sum x)
+// which is the reference's own bias factoring (Kernels.swift:594-600).
+#include "q4_common.hpp"
+#include "q4_launch.hpp"
+
+namespace sltx {
+
+
+// Prepared x for one chunk of 32 values: 16 fp16 pairs in dot order, plus
+// (-corr, sum).  Stored planar in LDS: xs[j][chunk] holds pairs 4j..4j+3.
+template <int NCH>
+struct GemvLds {
+    u32x4 xs[4][NCH];
+    float2 xc[NCH];
+};
+
+// Build the dot-order pairs for 8 consecutive x values (one weight word).
+__device__ __forceinline__ void pair_word(const f16x8& xv, uint32_t out[4], float& corr,
+                                          float& sum) {
+    const f16 sixteenth = (f16)0.0625f;
+    f16 a0 = xv[0], a1 = xv[1] * sixteenth, a2 = xv[2], a3 = xv[3] * sixteenth;
+    f16 a4 = xv[4], a5 = xv[5] * sixteenth, a6 = xv[6], a7 = xv[7] * sixteenth;
+    f16x2 p0 = {a0, a4}, p1 = {a1, a5}, p2 = {a2, a6}, p3 = {a3, a7};
+    out[0] = as_u32(p0);
+    out[1] = as_u32(p1);
+    out[2] = as_u32(p2);
+    out[3] = as_u32(p3);
+    corr += 1024.0f * ((float)a0 + (float)a1 + (float)a2 + (float)a3 + (float)a4 + (float)a5 +
+                       (float)a6 + (float)a7);
+    sum += (float)xv[0] + (float)xv[1] + (float)xv[2] + (float)xv[3] + (float)xv[4] +
+           (float)xv[5] + (float)xv[6] + (float)xv[7];
+}
+
+// sum_k q[k]*x[k] over one 32-nibble chunk, starting from -corr.
+__device__ __forceinline__ float chunk_dot(const u32x4 w, const u32x4 xq[4], float negcorr) {
+    float d0 = negcorr, d1 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t wj = w[j];
+        const uint32_t w8 = wj >> 8;
+        const uint32_t p0 = and_or(wj, 0x000F000Fu, kMagic1024x2);
+        const uint32_t p1 = and_or(wj, 0x00F000F0u, kMagic1024x2);
+        const uint32_t p2 = and_or(w8, 0x000F000Fu, kMagic1024x2);
+        const uint32_t p3 = and_or(w8, 0x00F000F0u, kMagic1024x2);
+        d0 = dot2(as_f16x2(p0), as_f16x2(xq[j][0]), d0);
+        d1 = dot2(as_f16x2(p1), as_f16x2(xq[j][1]), d1);
+        d0 = dot2(as_f16x2(p2), as_f16x2(xq[j][2]), d0);
+        d1 = dot2(as_f16x2(p3), as_f16x2(xq[j][3]), d1);
+    }
+    return d0 + d1;
+}
+
+template <int L>
+__device__ __forceinline__ float row_reduce(float v) {
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// One row-iteration's operands for one lane: CPL weight chunks per weight
+// set and their group scale/bias bit patterns (kept as 32-bit registers so
+// the loads are not merged with a wait in between).
+template <int CPL, int NW>
+struct GemvStage {
+    u32x4 w[NW][CPL];
+    uint32_t s[NW][CPL];
+    uint32_t b[NW][CPL];
+};
+
+// Row index is clamped into [0, N) so every load is unconditional (a
+// predicated load would be compiled into a branch with a wait inside it);
+// clamped rows are computed and discarded.
+template <int L, int CPL, int NW>
+__device__ __forceinline__ void gemv_load(GemvStage<CPL, NW>& st, const GemvParams& p, int r,
+                                          int kl) {
+    constexpr int NCH = L * CPL;
+    const int rr = r < p.N ? r : p.N - 1;
+#pragma unroll
+    for (int m = 0; m < NW; ++m) {
+        const u32x4* W = reinterpret_cast<const u32x4*>(m == 0 ? p.w0 : p.w1);
+        const uint16_t* S = m == 0 ? p.s0 : p.s1;
+        const uint16_t* B = m == 0 ? p.b0 : p.b1;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = kl + i * L;
+            st.w[m][i] = __builtin_nontemporal_load(&W[(size_t)rr * NCH + c]);
+            const size_t gi = (size_t)rr * p.groups + (c >> p.gshift);
+            st.s[m][i] = S[gi];
+            st.b[m][i] = B[gi];
+        }
+    }
+}
+
+template <int L, int CPL, int NW>
+__device__ __forceinline__ void gemv_compute_store(const GemvStage<CPL, NW>& st,
+                                                   const u32x4 (&xq)[CPL][4],
+                                                   const float2 (&xc)[CPL], const GemvParams& p,
+                                                   int r, int kl) {
+    float acc[NW];
+#pragma unroll
+    for (int m = 0; m < NW; ++m) {
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const float d = chunk_dot(st.w[m][i], xq[i], xc[i].x);
+            a = fmaf(h2f((uint16_t)st.s[m][i]), d, a);
+            a = fmaf(h2f((uint16_t)st.b[m][i]), xc[i].y, a);
+        }
+        acc[m] = row_reduce<L>(a);
+    }
+    if (kl == 0 && r < p.N) {
+        const float out = NW == 2 ? silu_mul_f32(acc[0], acc[NW - 1]) : acc[0];
+        p.y[r] = f2h(out);
+    }
+}
+
+// Each wave owns T consecutive row-iterations (T * 64/L rows), processed with
+// a two-stage register pipeline: the loads of iteration t+1 are in flight
+// while iteration t is computed.
+template <int L, int CPL, bool SWIGLU>
+__global__ __launch_bounds__(256) void q4_gemv_kernel(GemvParams p, int T) {
+    constexpr int RPI = 64 / L;        // rows per wave-wide instruction
+    constexpr int NCH = L * CPL;       // chunks per row (K / 32)
+    constexpr int NW = SWIGLU ? 2 : 1; // weight sets
+    __shared__ GemvLds<NCH> lds;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int kl = lane % L;
+    const int sub = lane / L;
+    const int row0 = (blockIdx.x * 4 + wave) * (RPI * T) + sub;
+
+    // x loads first: vmcnt retires in issue order, so x issued after the
+    // weights would make the x preparation wait for the HBM latency too.
+    constexpr int XPT = (NCH + 255) / 256;  // x chunks prepared per thread
+    f16x8 xr[XPT][4];
+#pragma unroll
+    for (int u = 0; u < XPT; ++u) {
+        const int c = threadIdx.x + 256 * u;
+        const int cc = c < NCH ? c : NCH - 1;
+        const f16x8* xp = reinterpret_cast<const f16x8*>(p.x + (size_t)cc * 32);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xr[u][j] = xp[j];
+    }
+
+    GemvStage<CPL, NW> sa, sb;
+    gemv_load<L, CPL, NW>(sa, p, row0, kl);
+
+    // Prepare x once per block while the first weight loads are in flight.
+#pragma unroll
+    for (int u = 0; u < XPT; ++u) {
+        const int c = threadIdx.x + 256 * u;
+        if (c < NCH) {
+            float corr = 0.0f, sum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t pr[4];
+                pair_word(xr[u][j], pr, corr, sum);
+                u32x4 v = {pr[0], pr[1], pr[2], pr[3]};
+                lds.xs[j][c] = v;
+            }
+            lds.xc[c] = make_float2(-corr, sum);
+        }
+    }
+    __syncthreads();
+
+    u32x4 xq[CPL][4];
+    float2 xc[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+        const int c = kl + i * L;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xq[i][j] = lds.xs[j][c];
+        xc[i] = lds.xc[c];
+    }
+
+    for (int t = 0; t < T; t += 2) {
+        if (t + 1 < T) gemv_load<L, CPL, NW>(sb, p, row0 + (t + 1) * RPI, kl);
+        gemv_compute_store<L, CPL, NW>(sa, xq, xc, p, row0 + t * RPI, kl);
+        if (t + 2 < T) gemv_load<L, CPL, NW>(sa, p, row0 + (t + 2) * RPI, kl);
+        if (t + 1 < T) gemv_compute_store<L, CPL, NW>(sb, xq, xc, p, row0 + (t + 1) * RPI, kl);
+    }
+}
+
+// Generic fallback for K that no (L, CPL) specialisation covers (K % 32 == 0):
+// one wave per row, x read from LDS per chunk.
+template <bool SWIGLU>
+__global__ __launch_bounds__(256) void q4_gemv_generic_kernel(GemvParams p) {
+    extern __shared__ uint8_t smem[];
+    const int nch = p.K / 32;
+    u32x4* xs = reinterpret_cast<u32x4*>(smem);              // [4][nch]
+    float2* xcv = reinterpret_cast<float2*>(xs + 4 * nch);    // [nch]
+    for (int c = threadIdx.x; c < nch; c += blockDim.x) {
+        const f16x8* xp = reinterpret_cast<const f16x8*>(p.x + (size_t)c * 32);
+        float corr = 0.0f, sum = 0.0f;
+        for (int j = 0; j < 4; ++j) {
+            uint32_t pr[4];
+            pair_word(xp[j], pr, corr, sum);
+            u32x4 v = {pr[0], pr[1], pr[2], pr[3]};
+            xs[j * nch + c] = v;
+        }
+        xcv[c] = make_float2(-corr, sum);
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= p.N) return;
+    constexpr int NW = SWIGLU ? 2 : 1;
+    float acc[NW];
+    for (int m = 0; m < NW; ++m) {
+        const u32x4* W = reinterpret_cast<const u32x4*>(m == 0 ? p.w0 : p.w1);
+        const uint16_t* S = m == 0 ? p.s0 : p.s1;
+        const uint16_t* B = m == 0 ? p.b0 : p.b1;
+        float a = 0.0f;
+        for (int c = lane; c < nch; c += 64) {
+            u32x4 xq[4];
+            for (int j = 0; j < 4; ++j) xq[j] = xs[j * nch + c];
+            const float2 xc = xcv[c];
+            const float d = chunk_dot(W[(size_t)r * nch + c], xq, xc.x);
+            const size_t gi = (size_t)r * p.groups + (c >> p.gshift);
+            a = fmaf(h2f(S[gi]), d, a);
+            a = fmaf(h2f(B[gi]), xc.y, a);
+        }
+        acc[m] = row_reduce<64>(a);
+    }
+    if (lane == 0) {
+        float out = SWIGLU ? silu_mul_f32(acc[0], acc[NW - 1]) : acc[0];
+        p.y[r] = f2h(out);
+    }
+}
+
+// ----------------------------------------------------------------- dispatch --
+
+template <int L, int CPL, bool SWIGLU>
+static hipError_t launch_lc(const GemvParams& p, hipStream_t st) {
+    constexpr int RPI = 64 / L;
+    // Row-iterations per wave: enough waves to cover the chip several times
+    // over (>= ~2048 waves) while amortising the per-block x preparation
+    // over up to 8 iterations on tall matrices (e.g. the vocabulary head).
+    const long iters = (p.N + RPI - 1) / RPI;
+    long T = iters / 2048;
+    if (T < 1) T = 1;
+    if (T > 8) T = 8;
+    const long waves = (iters + T - 1) / T;
+    const long grid = (waves + 3) / 4;
+    hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU>), dim3((unsigned)grid), dim3(256), 0, st, p,
+                       (int)T);
+    return hipGetLastError();
+}
+
+template <int L, bool SWIGLU>
+static hipError_t launch_l(const GemvParams& p, int cpl, hipStream_t st) {
+    switch (cpl) {
+        case 1: return launch_lc<L, 1, SWIGLU>(p, st);
+        case 2: return launch_lc<L, 2, SWIGLU>(p, st);
+        case 3: return launch_lc<L, 3, SWIGLU>(p, st);
+        case 4: return launch_lc<L, 4, SWIGLU>(p, st);
+        case 5: return launch_lc<L, 5, SWIGLU>(p, st);
+        case 6: return launch_lc<L, 6, SWIGLU>(p, st);
+        case 7: return launch_lc<L, 7, SWIGLU>(p, st);
+        case 8: return launch_lc<L, 8, SWIGLU>(p, st);
+    }
+    return hipErrorInvalidValue;
+}
+
+// Pick the widest L (lanes per row) that divides the chunk count with at most
+// 8 chunks per lane.  Returns 0 when no specialisation applies.
+int gemv_pick_lanes(int K, int* cpl_out) {
+    const int nch = K / 32;
+    const int lanes[3] = {64, 32, 16};
+    for (int i = 0; i < 3; ++i) {
+        const int L = lanes[i];
+        if (nch % L == 0 && nch / L >= 1 && nch / L <= 8) {
+            *cpl_out = nch / L;
+            return L;
+        }
+    }
+    return 0;
+}
+
+hipError_t launch_gemv(const GemvParams& p, bool swiglu, hipStream_t st) {
+    int cpl = 0;
+    const int L = gemv_pick_lanes(p.K, &cpl);
+    if (L == 64) return swiglu ? launch_l<64, true>(p, cpl, st) : launch_l<64, false>(p, cpl, st);
+    if (L == 32) return swiglu ? launch_l<32, true>(p, cpl, st) : launch_l<32, false>(p, cpl, st);
+    if (L == 16) return swiglu ? launch_l<16, true>(p, cpl, st) : launch_l<16, false>(p, cpl, st);
+    const size_t shm = (size_t)(p.K / 32) * (4 * sizeof(u32x4) + sizeof(float2));
+    if (shm > 64 * 1024) return hipErrorInvalidValue;
+    const int grid = (p.N + 3) / 4;
+    if (swiglu)
+        hipLaunchKernelGGL(q4_gemv_generic_kernel<true>, dim3(grid), dim3(256), shm, st, p);
+    else
+        hipLaunchKernelGGL(q4_gemv_generic_kernel<false>, dim3(grid), dim3(256), shm, st, p);
+    return hipGetLastError();
+}
+
+}  // namespace sltx

@@ -1,0 +1,51 @@
+// q4_launch.hpp -- kernel parameter blocks and host launchers shared between
+// the kernel translation units and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sltx {
+
+// GEMV (M == 1) operands; see q4_gemv.hip.
+struct GemvParams {
+    const uint16_t* x;      // [K] fp16
+    const uint32_t* w0;     // [N, K/8]
+    const uint16_t* s0;     // [N, K/g] fp16
+    const uint16_t* b0;     // [N, K/g] fp16
+    const uint32_t* w1;     // up weights (SwiGLU only, else null)
+    const uint16_t* s1;
+    const uint16_t* b1;
+    uint16_t* y;            // [N] fp16
+    int N;
+    int K;
+    int groups;             // K / g
+    int gshift;             // log2(g / 32): chunk of 32 nibbles c lies in group c >> gshift
+};
+
+// GEMM (M > 1) operands; see q4_gemm.hip.
+struct GemmParams {
+    const void* a;          // [M, K] fp16 or bf16
+    const uint32_t* w0;     // [N, K/8]
+    const uint16_t* s0;     // [N, K/g]
+    const uint16_t* b0;
+    const uint32_t* w1;     // up weights (SiLU-mul epilogue only)
+    const uint16_t* s1;
+    const uint16_t* b1;
+    const float* bias;      // [N] fp32 or null
+    void* y;                // [M, N] fp16 / bf16 / fp32
+    int M, N, K;
+    int groups;             // K / g
+    int gshift;             // log2(g / 32)
+    int tiles_m, tiles_n;   // filled by launch_gemm
+    int y_dtype;            // DType
+    int epilogue;           // Epilogue
+};
+
+hipError_t launch_gemv(const GemvParams& p, bool swiglu, hipStream_t st);
+hipError_t launch_gemm(GemmParams p, bool a_bf16, hipStream_t st);
+hipError_t launch_silu_mul(const uint16_t* a, const uint16_t* b, uint16_t* out, long count,
+                           hipStream_t st);
+int gemv_pick_lanes(int K, int* cpl_out);
+
+}  // namespace sltx

@@ -1,0 +1,153 @@
+"""C ABI surface, checked on the CPU (no GPU calls).
+
+* the library loads and exports every function include/*.h declares;
+* argument validation runs before any HIP call and returns the documented
+  status codes (the reference instead crashes or reads out of bounds, e.g.
+  K % 32 != 0 at Kernels.swift:490).
+Only validation paths that return before touching the device are exercised.
+"""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+ALIGNED = 0x10000  # fake, never dereferenced: validation fails before any access
+
+
+def header_functions():
+    names = set()
+    for h in glob.glob(os.path.join(REPO, "include", "*.h")):
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names |= set(re.findall(r"\b(sltx_\w+)\s*\(", text))
+    return names
+
+
+def test_header_matches_binding_list(pkg):
+    assert header_functions() == set(pkg.EXPORTED)
+
+
+def test_library_exports_every_header_symbol(pkg):
+    L = pkg.lib()
+    for name in header_functions():
+        assert hasattr(L, name), name
+    assert L.sltx_abi_version() == 1
+
+
+def _mm(pkg, fn="sltx_matmul_q4", x=ALIGNED, w=ALIGNED, s=ALIGNED, b=ALIGNED, out=ALIGNED,
+        M=1, K=3072, N=3072, g=64):
+    return getattr(pkg.lib(), fn)(x, w, s, b, out, M, K, N, g, None)
+
+
+@pytest.mark.parametrize("fn", ["sltx_matmul_q4", "sltx_matmul_q4_fast", "sltx_matmul_q4_fast_f32"])
+@pytest.mark.parametrize("kw,code,frag", [
+    (dict(K=100), -1, "multiple of 32"),
+    (dict(K=0), -1, "positive"),
+    (dict(M=-1), -1, "negative"),
+    (dict(N=-5), -1, "negative"),
+    (dict(g=12), -1, "multiple of 8"),
+    (dict(K=96, g=64), -1, "not a multiple of group_size"),
+    (dict(g=16, K=128), -2, "unsupported"),
+    (dict(g=256, K=512), -2, "unsupported"),
+    (dict(x=0), -1, "null"),
+    (dict(w=0), -1, "null"),
+    (dict(out=0), -1, "null"),
+    (dict(x=ALIGNED + 2), -1, "x must be 16-byte aligned"),
+    (dict(w=ALIGNED + 4), -1, "weight must be 16-byte aligned"),
+    (dict(s=ALIGNED + 1), -1, "scales/biases"),
+    (dict(out=ALIGNED + 1), -1, "misaligned out"),
+])
+def test_validation_errors(pkg, fn, kw, code, frag):
+    rc = _mm(pkg, fn=fn, **kw)
+    assert rc == code
+    assert frag in pkg.last_error()
+    assert fn in pkg.last_error()
+
+
+def test_empty_shapes_are_noops(pkg):
+    # M == 0 or N == 0: nothing to do, no device needed, null pointers allowed
+    assert _mm(pkg, M=0, x=0, out=0) == 0
+    assert _mm(pkg, N=0, w=0, s=0, b=0, out=0) == 0
+    assert pkg.lib().sltx_silu_mul(0, 0, 0, 0, None) == 0
+
+
+def test_silu_mul_validation(pkg):
+    L = pkg.lib()
+    assert L.sltx_silu_mul(ALIGNED, ALIGNED, ALIGNED, -1, None) == -1
+    assert L.sltx_silu_mul(0, ALIGNED, ALIGNED, 8, None) == -1
+    assert L.sltx_silu_mul(ALIGNED + 1, ALIGNED, ALIGNED, 8, None) == -1
+
+
+def _w(pkg, K=3072, g=64, w=ALIGNED):
+    return pkg.CQ4Weight(w, ALIGNED, ALIGNED, K, g)
+
+
+def test_linear_validation(pkg):
+    L = pkg.lib()
+    assert L.sltx_linear(ALIGNED, None, ALIGNED, 1, 3072, 64, 0, None) == -1
+    w = _w(pkg, K=2048)
+    assert L.sltx_linear(ALIGNED, ctypes.byref(w), ALIGNED, 1, 3072, 64, 0, None) == -1
+    assert "weight K" in pkg.last_error()
+    w = _w(pkg, K=3072, g=48)  # valid for the reference (g % 8 == 0), not built here
+    assert L.sltx_linear(ALIGNED, ctypes.byref(w), ALIGNED, 4, 3072, 64, 1, None) == -2
+
+
+def test_silu_mul_fused_validation(pkg):
+    L = pkg.lib()
+    g, u = _w(pkg), _w(pkg, g=32)
+    assert L.sltx_matmul_q4_silu_mul(ALIGNED, ctypes.byref(g), ctypes.byref(u), ALIGNED, 1, 3072,
+                                     64, None) == -1
+    assert "group_size differ" in pkg.last_error()
+    u = _w(pkg, K=1024)
+    assert L.sltx_matmul_q4_silu_mul(ALIGNED, ctypes.byref(g), ctypes.byref(u), ALIGNED, 1, 3072,
+                                     64, None) == -1
+    u = _w(pkg, w=ALIGNED + 8)
+    assert L.sltx_matmul_q4_silu_mul(ALIGNED, ctypes.byref(g), ctypes.byref(u), ALIGNED, 2, 3072,
+                                     64, None) == -1
+
+
+@pytest.mark.parametrize("args,frag", [
+    (dict(x_dtype=2), "x_dtype"),
+    (dict(out_dtype=7), "out_dtype"),
+    (dict(epilogue=1), "epilogue"),
+    (dict(bias=ALIGNED + 2), "misaligned bias"),
+    (dict(out=ALIGNED + 2, out_dtype=2), "misaligned out"),
+])
+def test_ex_validation(pkg, args, frag):
+    a = dict(x=ALIGNED, x_dtype=0, bias=None, epilogue=0, out=ALIGNED, out_dtype=2, M=8, N=64)
+    a.update(args)
+    w = _w(pkg)
+    rc = pkg.lib().sltx_matmul_q4_ex(a["x"], a["x_dtype"], ctypes.byref(w), a["bias"],
+                                     a["epilogue"], a["out"], a["out_dtype"], a["M"], a["N"], None)
+    assert rc == -1
+    assert frag in pkg.last_error()
+
+
+def test_python_wrapper_raises(pkg):
+    torch = pytest.importorskip("torch")
+    x = torch.zeros(1, 100, dtype=torch.float16)
+    w = torch.zeros(8, 12, dtype=torch.int32)
+    s = torch.zeros(8, 1, dtype=torch.float16)
+    with pytest.raises(pkg.SltxError) as ei:
+        pkg.matmul_q4(x, w, s, s, 1, 100, 8, 64, out=torch.zeros(1, 8, dtype=torch.float16),
+                      stream=0)
+    assert ei.value.code == pkg.SLTX_ERR_INVALID
+
+
+def test_last_error_is_thread_local(pkg):
+    import threading
+    assert _mm(pkg, K=100) == -1
+    seen = {}
+
+    def other():
+        seen["msg"] = pkg.last_error()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == ""
+    assert "multiple of 32" in pkg.last_error()

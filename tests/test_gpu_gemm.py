@@ -1,0 +1,235 @@
+"""GPU parity of the 4-bit MFMA GEMM (M > 1) through the C ABI.
+
+Reference semantics: the quantized GEMM behind matmulQ4Fast / matmulQ4FastF32
+(Ops.swift:312-381), the SwiGLU prefill path (LlamaModel.swift:275-277) and the
+DiT linear + GELU-tanh (DiTModel.swift:102-125, :953).  The reference's GEMM
+itself lives in an external package that is not available, so parity is
+against the fp64 oracle (plus a rounded-weight reference that pins the
+dequantisation rounding); tolerances are stated in tests/helpers.py.
+"""
+import numpy as np
+import pytest
+
+from helpers import (TOL_GEMM_BF16, TOL_GEMM_F16, TOL_ROUNDED_W, TOL_GEMV, assert_parity,
+                     gpu_inputs, host, load_golden, q4w, rounded_weights_bf16,
+                     rounded_weights_f16, to_dev)
+from oracle import q4_oracle as o
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("name", ["gemm_m3_n96_k256_g64", "gemm_m37_n160_k384_g64"])
+def test_golden_gemm(pkg, dev, name):
+    import torch
+    t, meta = load_golden(name)
+    M, N, K, g = (int(meta[k]) for k in ("M", "N", "K", "group_size"))
+    args = [to_dev(t[k], dev) for k in ("x", "proj.weight", "proj.scales", "proj.biases")]
+    y16 = pkg.matmul_q4_fast(*args, M, K, N, g)
+    y32 = pkg.matmul_q4_fast_f32(*args, M, K, N, g)
+    ymq = pkg.matmul_q4(*args, M, K, N, g)  # matmulQ4 with M > 1 routes to the GEMM
+    torch.cuda.synchronize()
+    assert_parity(y16.cpu().numpy(), t["y_f64"], TOL_GEMM_F16, name)
+    assert_parity(y32.cpu().numpy(), t["y_f64"], TOL_GEMM_F16, name + " f32")
+    assert torch.equal(ymq, y16)
+    assert torch.equal(y32.half(), y16)
+
+
+def test_golden_swiglu_gemm(pkg, dev):
+    import torch
+    t, meta = load_golden("swiglu_m5_n80_k256_g64")
+    M, N, K, g = (int(meta[k]) for k in ("M", "N", "K", "group_size"))
+    gate = q4w(pkg, t["gate_proj.weight"], t["gate_proj.scales"], t["gate_proj.biases"], K, g, dev)
+    up = q4w(pkg, t["up_proj.weight"], t["up_proj.scales"], t["up_proj.biases"], K, g, dev)
+    y = pkg.matmul_q4_silu_mul(to_dev(t["x"], dev), gate, up, M, K, N)
+    torch.cuda.synchronize()
+    assert_parity(y.cpu().numpy(), t["y_f64"], TOL_GEMM_F16, "swiglu gemm")
+
+
+def test_golden_dit_bf16_gelu(pkg, dev):
+    import torch
+    t, meta = load_golden("dit_m9_n64_k128_g64_bf16_gelu")
+    M, N, K, g = (int(meta[k]) for k in ("M", "N", "K", "group_size"))
+    x = to_dev(t["x"], dev).view(torch.bfloat16)
+    w = q4w(pkg, t["proj.weight"], t["proj.scales"], t["proj.biases"], K, g, dev)
+    bias = to_dev(t["bias"], dev)
+    y = pkg.matmul_q4_ex(x, w, M, N, out_dtype=torch.float32, bias=bias,
+                         epilogue=pkg.SLTX_EPI_GELU_TANH)
+    torch.cuda.synchronize()
+    pre = t["y_pre_f64"]
+    rms = float(np.sqrt(np.mean(pre * pre)))
+    err = np.abs(y.cpu().numpy() - t["y_f64"])
+    assert np.max(err) <= 1.2e-2 * rms, np.max(err) / rms
+    assert o.max_rel_err(y.cpu().numpy(), t["y_f64"]) <= 1e-2
+
+
+# (M, N, K, g): partial M/N tiles, K tails (K % 64 == 32), every group size.
+SHAPES = [
+    (2, 64, 256, 64), (3, 100, 3072, 64), (64, 128, 512, 32), (127, 256, 1024, 128),
+    (128, 128, 128, 64), (129, 130, 256, 64), (300, 1000, 768, 64), (17, 96, 96, 32),
+    (40, 72, 160, 32), (256, 512, 2048, 64),
+]
+
+
+@pytest.mark.parametrize("M,N,K,g", SHAPES)
+def test_gemm_shapes(pkg, dev, M, N, K, g):
+    import torch
+    x, [(w, s, b)] = o.make_inputs(M, N, K, g, seed=M * 31 + N + K)
+    y = pkg.matmul_q4_fast_f32(to_dev(x, dev), to_dev(w, dev), to_dev(s, dev), to_dev(b, dev), M,
+                               K, N, g)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    assert_parity(y, o.matmul_q4_f64(x, w, s, b, g), TOL_GEMM_F16, f"M={M} N={N} K={K}")
+    # weights rounded to fp16 exactly as the kernel does: fp32 accumulation only
+    ref_r = x.astype(np.float64) @ rounded_weights_f16(w, s, b, g).T
+    ok, worst = o.elementwise_ok(y, ref_r, **TOL_ROUNDED_W)
+    assert ok, worst
+
+
+@pytest.mark.parametrize("K,g", [(256, 64), (96, 32), (512, 128)])
+def test_gemm_dequant_bit_exact_identity(pkg, dev, K, g):
+    """A = I_K: row k of the output is column k of the dequantized weights, so
+    the kernel's fp16 (or bf16) dequantisation is checked bit for bit."""
+    import torch
+    N = 192
+    x, [(w, s, b)] = o.make_inputs(1, N, K, g, seed=K)
+    eye16 = np.eye(K, dtype=np.float16)
+    y = pkg.matmul_q4_fast_f32(to_dev(eye16, dev), to_dev(w, dev), to_dev(s, dev), to_dev(b, dev),
+                               K, K, N, g)
+    torch.cuda.synchronize()
+    want = rounded_weights_f16(w, s, b, g).T.astype(np.float32)
+    assert np.array_equal(y.cpu().numpy(), want)
+    eyeb = to_dev(o.f32_to_bf16_bits(np.eye(K, dtype=np.float32)), dev).view(torch.bfloat16)
+    yb = pkg.matmul_q4_ex(eyeb, q4w(pkg, w, s, b, K, g, dev), K, N, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert np.array_equal(yb.cpu().numpy(), rounded_weights_bf16(w, s, b, g).T.astype(np.float32))
+    # and the unpacked codes themselves: s = 1, b = 0
+    ones, zeros = np.ones_like(s), np.zeros_like(b)
+    yq = pkg.matmul_q4_fast_f32(to_dev(eye16, dev), to_dev(w, dev), to_dev(ones, dev),
+                                to_dev(zeros, dev), K, K, N, g)
+    torch.cuda.synchronize()
+    assert np.array_equal(yq.cpu().numpy().T.astype(np.int64), o.unpack_q4(w).astype(np.int64))
+
+
+def test_gemm_rows_match_gemv(pkg, dev):
+    """Row independence: each GEMM row equals the GEMV of that row of x."""
+    import torch
+    M, N, K, g = 9, 512, 3072, 64
+    x, [(w, s, b)] = o.make_inputs(M, N, K, g, seed=77)
+    tw, ts, tb = to_dev(w, dev), to_dev(s, dev), to_dev(b, dev)
+    tx = to_dev(x, dev)
+    yg = pkg.matmul_q4_fast_f32(tx, tw, ts, tb, M, K, N, g).cpu().numpy()
+    for m in range(M):
+        yv = pkg.matmul_q4(tx[m:m + 1].contiguous(), tw, ts, tb, 1, K, N, g)
+        torch.cuda.synchronize()
+        ok, worst = o.elementwise_ok(yv.cpu().numpy()[0], yg[m], **TOL_GEMM_F16)
+        assert ok, (m, worst)
+
+
+@pytest.mark.parametrize("M,N,K", [(2, 64, 192), (37, 200, 256), (130, 96, 3072)])
+def test_swiglu_gemm_shapes(pkg, dev, M, N, K):
+    import torch
+    g = 64
+    x, [(wg, sg, bg), (wu, su, bu)] = o.make_inputs(M, N, K, g, seed=M + N + K, n_weights=2)
+    ref = o.silu_mul_f64(o.matmul_q4_f64(x, wg, sg, bg, g), o.matmul_q4_f64(x, wu, su, bu, g))
+    y = pkg.matmul_q4_silu_mul(to_dev(x, dev), q4w(pkg, wg, sg, bg, K, g, dev),
+                               q4w(pkg, wu, su, bu, K, g, dev), M, K, N)
+    torch.cuda.synchronize()
+    assert_parity(y.cpu().numpy(), ref, TOL_GEMM_F16, f"swiglu M={M}")
+
+
+@pytest.mark.parametrize("out", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("xdt", ["f16", "bf16"])
+@pytest.mark.parametrize("epi", [0, 2])
+def test_gemm_ex_dtypes_bias_gelu(pkg, dev, out, xdt, epi):
+    import torch
+    M, N, K, g = 70, 136, 512, 64
+    x, [(w, s, b)] = o.make_inputs(M, N, K, g, seed=5, x_dtype=xdt)
+    bias = (np.random.default_rng(6).standard_normal(N) * 0.5).astype(np.float32)
+    pre = o.matmul_q4_f64(o.x_values(x, xdt), w, s, b, g) + bias
+    ref = o.gelu_tanh_f64(pre) if epi == 2 else pre
+    tx = to_dev(x, dev)
+    if xdt == "bf16":
+        tx = tx.view(torch.bfloat16)
+    odt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[out]
+    y = pkg.matmul_q4_ex(tx, q4w(pkg, w, s, b, K, g, dev), M, N, out_dtype=odt,
+                         bias=to_dev(bias, dev), epilogue=epi)
+    torch.cuda.synchronize()
+    y = y.float().cpu().numpy()
+    rms = float(np.sqrt(np.mean(pre * pre)))
+    tol_w = 1.2e-2 if xdt == "bf16" else 3e-3
+    tol_o = {"f16": 1e-3, "bf16": 4e-3, "f32": 1e-5}[out]
+    allow = tol_o * np.abs(ref) + tol_w * rms
+    assert np.all(np.abs(y - ref) <= allow), float(np.max(np.abs(y - ref) / allow))
+    assert o.max_rel_err(y, ref) <= 1e-2
+
+
+# ---- BASELINE configs at full size (sampled rows against the oracle) ----
+
+def _sample_check(y, x, w, s, b, g, rows_m, tol, what, x_dtype="f16"):
+    xs = host(x)[rows_m]
+    ref = o.matmul_q4_f64(o.x_values(xs, x_dtype), host(w), host(s), host(b), g)
+    return assert_parity(y.float().cpu().numpy()[rows_m], ref, tol, what)
+
+
+def test_prefill_gate_up_swiglu_m750(pkg, dev):
+    """X [750, 3072] x gate/up [8192 x 3072], fused SiLU x up."""
+    import torch
+    M, N, K, g = 750, 8192, 3072, 64
+    x, [(wg, sg, bg), (wu, su, bu)] = gpu_inputs(M, N, K, g, seed=3, dev=dev, n_weights=2)
+    y = pkg.matmul_q4_silu_mul(x, pkg.Q4Weight(wg, sg, bg, K, g), pkg.Q4Weight(wu, su, bu, K, g),
+                               M, K, N)
+    torch.cuda.synchronize()
+    rows = np.array([0, 1, 127, 128, 333, 640, 748, 749])
+    xs = host(x)[rows].astype(np.float64)
+    ref = o.silu_mul_f64(o.matmul_q4_f64(xs, host(wg), host(sg), host(bg), g),
+                         o.matmul_q4_f64(xs, host(wu), host(su), host(bu), g))
+    assert_parity(y.cpu().numpy()[rows], ref, TOL_GEMM_F16, "prefill gate/up")
+
+
+def test_prefill_down_m750(pkg, dev):
+    """X [750, 8192] x down [3072 x 8192], fp16 out."""
+    import torch
+    M, N, K, g = 750, 3072, 8192, 64
+    x, [(w, s, b)] = gpu_inputs(M, N, K, g, seed=4, dev=dev)
+    y = pkg.matmul_q4_fast(x, w, s, b, M, K, N, g)
+    y2 = pkg.matmul_q4_fast(x, w, s, b, M, K, N, g)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    _sample_check(y, x, w, s, b, g, np.array([0, 5, 128, 511, 749]), TOL_GEMM_F16, "prefill down")
+
+
+def test_lm_head_m750(pkg, dev):
+    """BASELINE config 4b: X [750, 3072] x lm_head [128256 x 3072]."""
+    import torch
+    M, N, K, g = 750, 128256, 3072, 64
+    x, [(w, s, b)] = gpu_inputs(M, N, K, g, seed=5, dev=dev)
+    y = pkg.matmul_q4_fast(x, w, s, b, M, K, N, g)
+    torch.cuda.synchronize()
+    rows_m = np.array([0, 300, 749])
+    cols = np.sort(np.random.default_rng(8).choice(N, size=4096, replace=False))
+    ref = o.matmul_q4_f64(host(x)[rows_m].astype(np.float64), host(w)[cols], host(s)[cols],
+                          host(b)[cols], g)
+    assert_parity(y.cpu().numpy()[rows_m][:, cols], ref, TOL_GEMM_F16, "lm_head 750")
+
+
+def test_dit_ffn_m6144_bf16(pkg, dev):
+    """bf16 X [6144, 2048] x up [8192 x 2048] -> GELU-tanh ->
+    down [2048 x 8192], fp32 out (DiTModel.swift:930-956 dataflow)."""
+    import torch
+    M, K1, N1, g = 6144, 2048, 8192, 64
+    x, [(wu, su, bu)] = gpu_inputs(M, N1, K1, g, seed=6, dev=dev, x_dtype="bf16")
+    _, [(wd, sd, bd)] = gpu_inputs(1, K1, N1, g, seed=7, dev=dev)
+    h = pkg.matmul_q4_ex(x, pkg.Q4Weight(wu, su, bu, K1, g), M, N1, out_dtype=torch.bfloat16,
+                         epilogue=pkg.SLTX_EPI_GELU_TANH)
+    y = pkg.matmul_q4_ex(h, pkg.Q4Weight(wd, sd, bd, N1, g), M, K1, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    rows = np.array([0, 1, 4095, 6143])
+    xr = o.x_values(host(x)[rows], "bf16")
+    pre = o.matmul_q4_f64(xr, host(wu), host(su), host(bu), g)
+    href = o.gelu_tanh_f64(pre)
+    hk = o.x_values(host(h)[rows], "bf16")
+    rms = float(np.sqrt(np.mean(pre * pre)))
+    assert np.max(np.abs(hk - href)) <= 1.6e-2 * rms
+    # second GEMM checked against the oracle on the kernel's own bf16 h
+    ref = o.matmul_q4_f64(hk, host(wd), host(sd), host(bd), g)
+    assert_parity(y.cpu().numpy()[rows], ref, TOL_GEMM_BF16, "dit down")

@@ -1,0 +1,249 @@
+"""Pins the CPU oracle (oracle/q4_oracle.{c,py}) independently of itself.
+
+The reference holds no golden vectors for the 4-bit matmul (its tests never
+call it), so each oracle function is checked against what the mathematics or
+a library routine fixes, chosen so that a dropped term, a wrong sign, a
+wrong index or a transposed operand fails at least one check:
+  * fp16 conversions: bit-exact against numpy's float16 casts.
+  * nibble order: known-answer words, and MLX's pack convention round trip.
+  * matmul: brute-force pure-Python loops, exact integer products (s=1, b=0),
+    b=-8s with all-8 codes giving exactly 0, linearity in x, group
+    permutation invariance, and a scale/bias transposition trap (N != K/g).
+  * silu_mul / gelu: closed forms through math.exp / math.tanh.
+"""
+import math
+
+import numpy as np
+import pytest
+
+
+# ------------------------------------------------------------------ fp16 ---
+
+def test_f16_to_f32_all_patterns(oracle):
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = oracle.c_f16_to_f32(bits)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_rne_matches_numpy(oracle):
+    rng = np.random.default_rng(0)
+    # random bit patterns over the whole float range plus targeted edge cases
+    pats = rng.integers(0, 2**32, size=200_000, dtype=np.uint64).astype(np.uint32)
+    vals = pats.view(np.float32)
+    edge = np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 65536.0, -65520.0, 1e-8, 2.0**-24,
+                     2.0**-25, 2.0**-25 * 1.0000001, 3 * 2.0**-25, 2.0**-14, 2.0**-14 * 0.99999,
+                     1.0 + 2.0**-11, 1.0 + 3 * 2.0**-11, 2048.0 + 1.0, 2048.0 + 3.0,
+                     np.inf, -np.inf], dtype=np.float32)
+    # exact ties in the normal and subnormal ranges
+    ties = (np.arange(1, 2000, dtype=np.float32) + 0.5) * np.float32(2.0**-24)
+    vals = np.concatenate([vals, edge, ties, rng.standard_normal(50_000).astype(np.float32) * 100])
+    L = oracle.lib()
+    got = np.array([L.oracle_f32_to_f16(float(v)) for v in vals], dtype=np.uint16)
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = vals.astype(np.float16).view(np.uint16)
+    nan = np.isnan(vals)
+    assert np.array_equal(got[~nan], ref[~nan])
+    assert np.all(np.isnan(got[nan].view(np.float16)))
+
+
+# ---------------------------------------------------------------- nibbles ---
+
+def test_unpack_known_words(oracle):
+    w = np.array([[0x76543210, 0xFEDCBA98, 0x0000000F, 0xF0000000]], dtype=np.uint32)
+    want = np.array([list(range(8)) + list(range(8, 16)) + [15] + [0] * 7 + [0] * 7 + [15]],
+                    dtype=np.uint8)
+    assert np.array_equal(oracle.unpack_q4(w), want)
+    assert np.array_equal(oracle.c_unpack_q4(w, 32), want)
+
+
+def test_pack_unpack_roundtrip(oracle):
+    rng = np.random.default_rng(1)
+    q = rng.integers(0, 16, size=(37, 256), dtype=np.uint8)
+    w = oracle.pack_q4(q)
+    assert w.dtype == np.uint32 and w.shape == (37, 32)
+    assert np.array_equal(oracle.unpack_q4(w), q)
+    assert np.array_equal(oracle.c_unpack_q4(w, 256), q)
+    # low nibble first: code k sits at bits 4*(k%8) of word k/8
+    k = 13
+    assert ((w[:, k // 8] >> (4 * (k % 8))) & 0xF).astype(np.uint8).tolist() == q[:, k].tolist()
+
+
+# ----------------------------------------------------------------- matmul ---
+
+def _brute(x, w, s, b, g):
+    """Pure-Python loops straight from the formula, tiny shapes only."""
+    M, K = x.shape
+    N = w.shape[0]
+    y = [[0.0] * N for _ in range(M)]
+    for m in range(M):
+        for n in range(N):
+            acc = 0.0
+            for k in range(K):
+                q = (int(w[n, k // 8]) >> (4 * (k % 8))) & 0xF
+                wk = float(s[n, k // g]) * q + float(b[n, k // g])
+                acc += float(x[m, k]) * wk
+            y[m][n] = acc
+    return np.array(y)
+
+
+@pytest.mark.parametrize("M,N,K,g", [(2, 3, 64, 32), (1, 5, 128, 64), (3, 4, 256, 128)])
+def test_matmul_brute_force(oracle, M, N, K, g):
+    x, [(w, s, b)] = oracle.make_inputs(M, N, K, g, seed=K + N)
+    # non-uniform biases so a dropped or misplaced bias term shows
+    rng = np.random.default_rng(7)
+    b = (rng.standard_normal(b.shape) * 0.1).astype(np.float16)
+    ref = _brute(x, w, s, b, g)
+    assert np.allclose(oracle.matmul_q4_f64(x, w, s, b, g), ref, rtol=1e-12, atol=1e-12)
+    assert np.allclose(oracle.c_matmul_q4_f64(x, w, s, b, g), ref, rtol=1e-12, atol=1e-12)
+
+
+def test_exact_integer_matmul(oracle):
+    rng = np.random.default_rng(2)
+    M, N, K, g = 4, 24, 192, 64
+    q = rng.integers(0, 16, size=(N, K), dtype=np.uint8)
+    xi = rng.integers(-8, 9, size=(M, K))
+    w = oracle.pack_q4(q)
+    s = np.ones((N, K // g), np.float16)
+    b = np.zeros((N, K // g), np.float16)
+    want = xi @ q.astype(np.int64).T
+    x = xi.astype(np.float16)
+    assert np.array_equal(oracle.matmul_q4_f64(x, w, s, b, g), want.astype(np.float64))
+    assert np.array_equal(oracle.c_matmul_q4_f64(x, w, s, b, g), want.astype(np.float64))
+    # emulator and CPU baseline are exact here too (integers < 2048 in fp16)
+    assert np.array_equal(oracle.c_matmul_q4_emu(x, w, s, b, g).astype(np.int64), want)
+    assert np.array_equal(oracle.c_cpu_matmul_q4(x, w, s, b, g, 2).astype(np.int64), want)
+
+
+def test_all_eight_codes_with_minus8s_bias_is_zero(oracle):
+    M, N, K, g = 3, 16, 128, 64
+    x, [(w, s, b)] = oracle.make_inputs(M, N, K, g, seed=3)
+    w8 = oracle.pack_q4(np.full((N, K), 8, np.uint8))
+    assert np.all(oracle.matmul_q4_f64(x, w8, s, b, g) == 0.0)
+    assert np.all(oracle.c_matmul_q4_f64(x, w8, s, b, g) == 0.0)
+    # matmul_q4 keeps q*s*x and b*sum(x) in separate fp32 accumulators
+    # (Kernels.swift:547-600), so its cancellation is only to fp32 rounding.
+    emu = oracle.c_matmul_q4_emu(x, w8, s, b, g).astype(np.float32)
+    assert np.all(np.abs(emu) < 1e-5) and np.any(emu != 0.0)
+
+
+def test_linearity_in_x(oracle):
+    M, N, K, g = 2, 32, 256, 64
+    x1, [(w, s, b)] = oracle.make_inputs(M, N, K, g, seed=4)
+    x2, _ = oracle.make_inputs(M, N, K, g, seed=5)
+    a = 0.37
+    lhs = oracle.matmul_q4_f64(a * x1.astype(np.float64) + x2.astype(np.float64), w, s, b, g)
+    rhs = a * oracle.matmul_q4_f64(x1, w, s, b, g) + oracle.matmul_q4_f64(x2, w, s, b, g)
+    assert np.allclose(lhs, rhs, rtol=1e-10, atol=1e-10)
+
+
+def test_group_permutation_invariance(oracle):
+    M, N, K, g = 2, 16, 256, 64
+    x, [(w, s, b)] = oracle.make_inputs(M, N, K, g, seed=6)
+    rng = np.random.default_rng(9)
+    b = (rng.standard_normal(b.shape) * 0.05).astype(np.float16)
+    perm = np.array([2, 0, 3, 1])
+    q = oracle.unpack_q4(w)
+    kperm = np.concatenate([np.arange(p * g, (p + 1) * g) for p in perm])
+    y0 = oracle.c_matmul_q4_f64(x, w, s, b, g)
+    y1 = oracle.c_matmul_q4_f64(np.ascontiguousarray(x[:, kperm]), oracle.pack_q4(q[:, kperm]),
+                                np.ascontiguousarray(s[:, perm]), np.ascontiguousarray(b[:, perm]),
+                                g)
+    assert np.allclose(y0, y1, rtol=1e-12, atol=1e-12)
+
+
+def test_scale_bias_index_trap(oracle):
+    """N == K/g with row-distinct scales: reading s[g, n] instead of s[n, g]
+    (or dropping the bias) changes the result."""
+    M, N, K, g = 1, 4, 256, 64
+    x, [(w, s, b)] = oracle.make_inputs(M, N, K, g, seed=10)
+    s = (np.arange(16, dtype=np.float32).reshape(4, 4) * 0.01 + 0.01).astype(np.float16)
+    b = (-np.arange(16, dtype=np.float32).reshape(4, 4) * 0.02).astype(np.float16)
+    y = oracle.c_matmul_q4_f64(x, w, s, b, g)
+    assert np.allclose(y, _brute(x, w, s, b, g), rtol=1e-12, atol=1e-12)
+    assert not np.allclose(y, oracle.matmul_q4_f64(x, w, np.ascontiguousarray(s.T),
+                                                   np.ascontiguousarray(b.T), g))
+    assert not np.allclose(y, oracle.matmul_q4_f64(x, w, s, np.zeros_like(b), g))
+
+
+def test_emulator_within_two_ulp(oracle):
+    M, N, K, g = 1, 256, 3072, 64
+    x, [(w, s, b)] = oracle.make_inputs(M, N, K, g, seed=11)
+    ref = oracle.matmul_q4_f64(x, w, s, b, g)
+    emu = oracle.c_matmul_q4_emu(x, w, s, b, g).astype(np.float64)
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    assert np.all(np.abs(emu - ref) <= 2 * ulp + 1e-6)
+
+
+def test_cpu_baseline_matches_f64(oracle):
+    M, N, K, g = 3, 100, 512, 64
+    x, [(w, s, b)] = oracle.make_inputs(M, N, K, g, seed=12)
+    ref = oracle.matmul_q4_f64(x, w, s, b, g)
+    for th in (1, 3):
+        y = oracle.c_cpu_matmul_q4(x, w, s, b, g, th)
+        ok, worst = oracle.elementwise_ok(y, ref, rtol=6e-4, atol_rms=1e-4)
+        assert ok, worst
+
+
+def test_baseline_distribution(oracle):
+    """BASELINE's synthetic inputs: |y| has std ~5 at K=3072, bias == -8*scale exactly."""
+    x, [(w, s, b)] = oracle.make_inputs(64, 256, 3072, 64, seed=0)
+    assert np.array_equal(b.astype(np.float32), -8.0 * s.astype(np.float32))
+    std = oracle.matmul_q4_f64(x, w, s, b, 64).std()
+    assert 4.0 < std < 6.5
+
+
+# ------------------------------------------------------------ activations ---
+
+def test_silu_mul_closed_form(oracle):
+    rng = np.random.default_rng(13)
+    a = (rng.standard_normal(4096) * 4).astype(np.float16)
+    bb = rng.standard_normal(4096).astype(np.float16)
+    got = oracle.c_silu_mul(a, bb).astype(np.float64)
+    ref = np.array([float(u) / (1.0 + math.exp(-float(u))) * float(v) for u, v in zip(a, bb)])
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    assert np.all(np.abs(got - ref) <= ulp)
+    assert np.allclose(oracle.silu_mul_f64(a, bb), ref, rtol=1e-12, atol=0)
+
+
+def test_silu_mul_special_values(oracle):
+    a = np.array([0.0, 20.0, -30.0, 1.0], np.float16)
+    b = np.array([3.0, 2.0, 1.0, 0.0], np.float16)
+    out = oracle.c_silu_mul(a, b)
+    assert out[0] == 0.0
+    assert out[1] == np.float16(40.0)
+    assert out[2] == 0.0 and np.signbit(out[2])
+    assert out[3] == 0.0
+
+
+def test_gelu_tanh_closed_form_and_clamp(oracle):
+    v = np.concatenate([np.linspace(-12, 12, 2001), [0.0, 50.0, -50.0]]).astype(np.float32)
+    got = oracle.c_gelu_tanh_f32(v).astype(np.float64)
+
+    def ref1(t):
+        inner = 0.7978845608 * (t + 0.044715 * t ** 3)
+        inner = min(max(inner, -10.0), 10.0)
+        return 0.5 * t * (1.0 + math.tanh(inner))
+
+    ref = np.array([ref1(float(t)) for t in v])
+    assert np.allclose(got, ref, rtol=2e-6, atol=2e-6)
+    assert np.allclose(oracle.gelu_tanh_f64(v), ref, rtol=1e-12, atol=1e-12)
+    # clamp: for large |v| the inner term saturates at +-10, not at +-inf
+    big = oracle.gelu_tanh_f64(np.array([-50.0]))[0]
+    assert big == pytest.approx(0.5 * -50.0 * (1.0 + math.tanh(-10.0)), rel=1e-12)
+
+
+def test_bf16_rounding(oracle):
+    vals = np.array([1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -2.5, 3.0e38], np.float32)
+    bits = oracle.f32_to_bf16_bits(vals)
+    back = oracle.bf16_bits_to_f32(bits)
+    assert back[0] == 1.0
+    assert back[1] == 1.0          # tie to even
+    assert back[2] == 1.0 + 2 ** -6  # tie to even (up)
+    assert back[3] == -2.5
+    L = oracle.lib()
+    L.oracle_f32_to_bf16.argtypes = [__import__("ctypes").c_float]
+    L.oracle_f32_to_bf16.restype = __import__("ctypes").c_uint16
+    assert [L.oracle_f32_to_bf16(float(v)) for v in vals] == bits.tolist()
