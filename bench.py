@@ -1,0 +1,392 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X 4-bit dequant matmul path (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Workload: one Llama-3.2-3B decode layer's projections at
+M = 1 with MLX 4-bit group-64 weights -- q/o [3072x3072], k/v [1024x3072],
+gate+up [8192x3072] fused with SiLU x up, down [3072x8192].  A step is one
+layer: 6 launches (q, k, v, o, gate/up+SiLU, down), down consuming the
+gate/up output.  Steps rotate over --copies distinct layers (default 40,
+2.27 GB of weights) so the 256 MB MALL cannot hold the working set, and the
+timed region replays a HIP graph of one rotation (graph capture removes the
+host launch cost, as a decode loop would).
+
+value = algorithmic bytes of all K steps / wall time of the K steps
+        (GB/s; bytes = N*K/2 + 4*N*K/64 + 2*K + 2*N per weight set).
+roofline = the dominant kernel (fused gate/up GEMV, 28.33 MB per launch):
+        bytes / its average duration, timed with HIP events inside the timed
+        region, against the 8 TB/s HBM peak.
+extra.gemm = the M > 1 MFMA GEMM legs in TFLOP/s
+        against the 2.5 PFLOP/s dense fp16/bf16 peak.
+cpu_baseline = the C restatement in oracle/ (the "port" CPU baseline, same
+        dequant-matmul, fp32 accumulate) timed on this host's cores on a bounded
+        sample of decode layers.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+METRIC = "4-bit GEMV HBM GB/s + GEMM TFLOP/s (% roofline) at Llama-3.2-3B shapes, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense fp16 / bf16
+G = 64
+
+
+def gemv_bytes(N, K, nsets=1, M=1, g=G):
+    return nsets * (N * K // 2 + 4 * N * (K // g)) + 2 * M * K + 2 * M * N
+
+
+# (name, N, K, weight sets)
+DECODE = [("q_proj", 3072, 3072, 1), ("k_proj", 1024, 3072, 1), ("v_proj", 1024, 3072, 1),
+          ("o_proj", 3072, 3072, 1), ("gate_up_proj", 8192, 3072, 2), ("down_proj", 3072, 8192, 1)]
+LAYER_BYTES = sum(gemv_bytes(N, K, n) for _, N, K, n in DECODE)  # 56,709,120
+DOMINANT = "gate_up_proj"
+DOMINANT_BYTES = gemv_bytes(8192, 3072, 2)  # 28,334,080
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=80)
+    ap.add_argument("--copies", type=int, default=40)
+    ap.add_argument("--no-gemm", action="store_true", help="skip the M>1 GEMM legs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--diag", action="store_true", help="print timing-method diagnostics")
+    return ap.parse_args()
+
+
+def rand_q4(torch, N, K, gen, dev):
+    w = torch.randint(-2**31, 2**31 - 1, (N, K // 8), generator=gen, device=dev,
+                      dtype=torch.int64).to(torch.int32)
+    s = (torch.randn(N, K // G, generator=gen, device=dev) * 0.02).abs().to(torch.float16)
+    b = (s.float() * -8.0).to(torch.float16)
+    return w, s, b
+
+
+class Layer:
+    def __init__(self, pkg, torch, gen, dev):
+        self.w = {}
+        for name, N, K, n in DECODE:
+            sets = [pkg.Q4Weight(*rand_q4(torch, N, K, gen, dev), K, G) for _ in range(n)]
+            self.w[name] = sets
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(no sharding or collectives); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    pkg.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+
+    layers = [Layer(pkg, torch, gen, dev) for _ in range(args.copies)]
+    x = torch.randn(1, 3072, generator=gen, device=dev).half()
+    attn = torch.randn(1, 3072, generator=gen, device=dev).half()
+    x2 = torch.randn(1, 3072, generator=gen, device=dev).half()
+    outs = {name: torch.empty(1, N, device=dev, dtype=torch.float16) for name, N, _, _ in DECODE}
+
+    def step(L, ev=None):
+        w = L.w
+        pkg.matmul_q4(x, *_wsb(w["q_proj"][0]), 1, 3072, 3072, G, out=outs["q_proj"])
+        pkg.matmul_q4(x, *_wsb(w["k_proj"][0]), 1, 3072, 1024, G, out=outs["k_proj"])
+        pkg.matmul_q4(x, *_wsb(w["v_proj"][0]), 1, 3072, 1024, G, out=outs["v_proj"])
+        pkg.matmul_q4(attn, *_wsb(w["o_proj"][0]), 1, 3072, 3072, G, out=outs["o_proj"])
+        if ev is not None:
+            ev[0].record()
+        pkg.matmul_q4_silu_mul(x2, w["gate_up_proj"][0], w["gate_up_proj"][1], 1, 3072, 8192,
+                               out=outs["gate_up_proj"])
+        if ev is not None:
+            ev[1].record()
+        pkg.matmul_q4(outs["gate_up_proj"], *_wsb(w["down_proj"][0]), 1, 8192, 3072, G,
+                      out=outs["down_proj"])
+
+    # eager warm-up (initialises the library's per-device state before capture)
+    for L in layers:
+        step(L)
+    torch.cuda.synchronize()
+
+    # one rotation over all copies, captured as a HIP graph, with timing events
+    # around every dominant launch (event-record nodes inside the graph)
+    nrot = args.copies
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(nrot)]
+    timing = "events in graph"
+    graph = torch.cuda.CUDAGraph()
+    try:
+        with torch.cuda.graph(graph):
+            for i, L in enumerate(layers):
+                step(L, evs[i])
+    except Exception as e:  # event nodes not capturable: graph without them
+        timing = f"graph-only dominant launches ({type(e).__name__})"
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for L in layers:
+                step(L)
+        evs = None
+    torch.cuda.synchronize()
+
+    reps_w = max(1, args.warmup // nrot)
+    reps = max(1, (args.steps + nrot - 1) // nrot)
+    steps = reps * nrot
+    for _ in range(reps_w):
+        graph.replay()
+    torch.cuda.synchronize()
+
+    dom_ms = []
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        graph.replay()
+        if evs is not None:
+            # elapsed times are read after the next replay is queued so the
+            # host never stalls the GPU; the last rotation is read after sync
+            pass
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    wall = t1 - t0
+    if evs is not None:
+        try:
+            dom_ms = [a.elapsed_time(b) for a, b in evs]
+        except Exception as e:
+            timing = f"graph-only dominant launches ({type(e).__name__} reading events)"
+            evs = None
+
+    if evs is None or not dom_ms:
+        # the dominant kernel alone: a graph of one rotation of gate/up launches,
+        # bracketed by events on the capturing stream's successor
+        g2 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g2):
+            for L in layers:
+                w = L.w["gate_up_proj"]
+                pkg.matmul_q4_silu_mul(x2, w[0], w[1], 1, 3072, 8192, out=outs["gate_up_proj"])
+        g2.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        r2 = max(1, reps // 4)
+        e0.record()
+        for _ in range(r2):
+            g2.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        dom_ms = [e0.elapsed_time(e1) / (r2 * nrot)]
+
+    dom_us = 1e3 * sum(dom_ms) / len(dom_ms)
+    achieved = DOMINANT_BYTES / (dom_us * 1e-6) / 1e9
+    value = steps * LAYER_BYTES / wall / 1e9
+
+    diag = {}
+    if args.diag:
+        diag = timing_diagnostics(pkg, torch, layers, x2, outs, reps)
+
+    gemm = {} if args.no_gemm else gemm_legs(pkg, torch, gen, dev)
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": reps_w * nrot,
+        "ms_per_step": round(1e3 * wall / steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4xf16->f32",
+        "data": "synthetic (BASELINE distributions: x~N(0,1) fp16, codes uniform 0..15, "
+                "scales |N(0,0.02)| fp16, biases -8*scale)",
+        "config": {"workload": "Llama-3.2-3B decode layer projections, M=1, MLX 4-bit g64 "
+                               "(q,k,v,o,gate+up fused SiLU*up, down); "
+                               f"{args.copies} distinct layer copies rotated",
+                   "bytes_per_step": LAYER_BYTES, "launches_per_step": 6,
+                   "graph": "one rotation captured as a HIP graph"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profiles(),
+                     "kernel": "q4_gemv_kernel<32,3,true> (gate/up fused SiLU*up)",
+                     "avg_us": round(dom_us, 3), "bytes_per_launch": DOMINANT_BYTES,
+                     "timing": timing},
+        "cpu_baseline": cpu,
+        "extra": {"gemm": gemm, **({"timing_diag": diag} if diag else {})},
+    }
+    print(json.dumps(line))
+
+
+def _wsb(q):
+    return q.weight, q.scales, q.biases
+
+
+def timing_diagnostics(pkg, torch, layers, x2, outs, reps):
+    """Dominant-kernel duration by three methods (for cross-checking rocprof)."""
+    out = {}
+    # (a) eager, per-launch events
+    es = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in layers]
+    for (a, b), L in zip(es, layers):
+        w = L.w["gate_up_proj"]
+        a.record()
+        pkg.matmul_q4_silu_mul(x2, w[0], w[1], 1, 3072, 8192, out=outs["gate_up_proj"])
+        b.record()
+    torch.cuda.synchronize()
+    out["eager_event_us"] = round(1e3 * sum(a.elapsed_time(b) for a, b in es) / len(es), 3)
+    # (b) graph of dominant launches only
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2):
+        for L in layers:
+            w = L.w["gate_up_proj"]
+            pkg.matmul_q4_silu_mul(x2, w[0], w[1], 1, 3072, 8192, out=outs["gate_up_proj"])
+    g2.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        g2.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    out["graph_only_us"] = round(1e3 * e0.elapsed_time(e1) / (10 * len(layers)), 3)
+    return out
+
+
+def gemm_legs(pkg, torch, gen, dev):
+    """BASELINE configs 3-5 (M > 1, MFMA GEMM) and 4a (lm_head GEMV), each timed
+    over a graph of R launches bracketed by events."""
+    res = {}
+
+    def timed(fn, flops=None, nbytes=None, reps=20):
+        fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(3):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = 1e3 * e0.elapsed_time(e1) / (3 * reps)
+        r = {"us": round(us, 2)}
+        if flops:
+            tf = flops / (us * 1e-6) / 1e12
+            r.update({"tflops": round(tf, 1), "frac_mfma": round(tf / MFMA_PEAK_TFLOPS, 4)})
+        if nbytes:
+            gbs = nbytes / (us * 1e-6) / 1e9
+            r.update({"gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
+        return r
+
+    M = 750
+    xa = torch.randn(M, 3072, generator=gen, device=dev).half()
+    gu = [pkg.Q4Weight(*rand_q4(torch, 8192, 3072, gen, dev), 3072, G) for _ in range(2)]
+    h = torch.empty(M, 8192, device=dev, dtype=torch.float16)
+    res["prefill_gate_up_silu_m750"] = timed(
+        lambda: pkg.matmul_q4_silu_mul(xa, gu[0], gu[1], M, 3072, 8192, out=h),
+        flops=2 * 2 * M * 8192 * 3072)
+    dw = pkg.Q4Weight(*rand_q4(torch, 3072, 8192, gen, dev), 8192, G)
+    y = torch.empty(M, 3072, device=dev, dtype=torch.float16)
+    res["prefill_down_m750"] = timed(
+        lambda: pkg.matmul_q4_fast(h, dw.weight, dw.scales, dw.biases, M, 8192, 3072, G, out=y),
+        flops=2 * M * 3072 * 8192)
+    del gu, dw
+    lm = pkg.Q4Weight(*rand_q4(torch, 128256, 3072, gen, dev), 3072, G)
+    x1 = xa[:1].contiguous()
+    y1 = torch.empty(1, 128256, device=dev, dtype=torch.float16)
+    # lm_head (222 MB) fits the 256 MB MALL when repeated, so this GEMV leg is
+    # an upper bound; the decode rotation above is the HBM-honest number
+    res["lm_head_gemv_m1"] = timed(
+        lambda: pkg.matmul_q4(x1, lm.weight, lm.scales, lm.biases, 1, 3072, 128256, G, out=y1),
+        nbytes=gemv_bytes(128256, 3072), reps=10)
+    yl = torch.empty(M, 128256, device=dev, dtype=torch.float16)
+    res["lm_head_gemm_m750"] = timed(
+        lambda: pkg.matmul_q4_fast(xa, lm.weight, lm.scales, lm.biases, M, 3072, 128256, G,
+                                   out=yl),
+        flops=2 * M * 128256 * 3072, reps=5)
+    del lm, yl
+    Md = 6144
+    xd = torch.randn(Md, 2048, generator=gen, device=dev).bfloat16()
+    up = pkg.Q4Weight(*rand_q4(torch, 8192, 2048, gen, dev), 2048, G)
+    down = pkg.Q4Weight(*rand_q4(torch, 2048, 8192, gen, dev), 8192, G)
+    hd = torch.empty(Md, 8192, device=dev, dtype=torch.bfloat16)
+    yd = torch.empty(Md, 2048, device=dev, dtype=torch.float32)
+    res["dit_ffn_up_gelu_m6144_bf16"] = timed(
+        lambda: pkg.matmul_q4_ex(xd, up, Md, 8192, out=hd, epilogue=pkg.SLTX_EPI_GELU_TANH),
+        flops=2 * Md * 8192 * 2048, reps=5)
+    res["dit_ffn_down_m6144_bf16"] = timed(
+        lambda: pkg.matmul_q4_ex(hd, down, Md, 2048, out=yd), flops=2 * Md * 2048 * 8192,
+        reps=5)
+    return res
+
+
+def cpu_baseline(seconds):
+    """The oracle's C dequant-matmul (port of the same semantics, fp32
+    accumulate, pthreads over rows) on a bounded sample: whole decode layers
+    (7 projections: gate and up unfused, plus silu_mul) repeated for about
+    `seconds`."""
+    import numpy as np
+    from oracle import q4_oracle as o
+    o.lib()
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    threads = max(1, min(cores, 16))
+    projs = [("q_proj", 3072, 3072), ("k_proj", 1024, 3072), ("v_proj", 1024, 3072),
+             ("o_proj", 3072, 3072), ("gate_proj", 8192, 3072), ("up_proj", 8192, 3072),
+             ("down_proj", 3072, 8192)]
+    data = {}
+    for i, (name, N, K) in enumerate(projs):
+        x, [(w, s, b)] = o.make_inputs(1, N, K, G, seed=100 + i)
+        data[name] = (x, w, s, b)
+    layers = 0
+    t0 = time.perf_counter()
+    while True:
+        ys = {n: o.c_cpu_matmul_q4(*data[n], G, threads) for n, _, _ in projs}
+        o.c_silu_mul(ys["gate_proj"], ys["up_proj"])
+        layers += 1
+        if time.perf_counter() - t0 >= seconds and layers >= 2:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(layers * LAYER_BYTES / dt / 1e9, 4), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{layers} decode layers (same 7 projections + silu_mul, {LAYER_BYTES} "
+                      f"algorithmic bytes each) in {dt:.1f} s, {threads} threads",
+            "host_cpus": cores}
+
+
+def traffic_from_profiles():
+    """HBM bytes per dominant launch from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), if present."""
+    path = os.path.join(REPO, "profiles", "gemv_gate_up_decode_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            try:
+                return int(float(line.split(":", 1)[1].strip()))
+            except ValueError:
+                return None
+    return None
+
+
+if __name__ == "__main__":
+    main()

@@ -229,7 +229,9 @@ def test_dit_ffn_m6144_bf16(pkg, dev):
     href = o.gelu_tanh_f64(pre)
     hk = o.x_values(host(h)[rows], "bf16")
     rms = float(np.sqrt(np.mean(pre * pre)))
-    assert np.max(np.abs(hk - href)) <= 1.6e-2 * rms
+    # bf16 weights (2^-9 per product) and the bf16 store of h (half ulp 2^-9)
+    allow = 4e-3 * np.abs(href) + 1.2e-2 * rms
+    assert np.all(np.abs(hk - href) <= allow), float(np.max(np.abs(hk - href) / allow))
     # second GEMM checked against the oracle on the kernel's own bf16 h
     ref = o.matmul_q4_f64(hk, host(wd), host(sd), host(bd), g)
     assert_parity(y.cpu().numpy()[rows], ref, TOL_GEMM_BF16, "dit down")

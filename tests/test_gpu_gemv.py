@@ -139,7 +139,11 @@ def test_gemv_full_size(pkg, dev, name, N, K):
                        N, g)
     y_again = pkg.matmul_q4(x, w, s, b, 1, K, N, g)
     torch.cuda.synchronize()
-    assert torch.equal(y2, y * 2)
+    # fp16 subnormal outputs sit on an absolute grid, where rounding does not
+    # commute with scaling; everywhere else the match is exact
+    normal = y.abs() >= 2.0 ** -13
+    assert torch.equal(y2[normal], (y * 2)[normal])
+    assert torch.all((y2.float() - 2 * y.float()).abs() <= 2.0 ** -23)
     assert torch.equal(yp, y[:, perm])
     assert torch.equal(y_again, y)  # deterministic
     rows = np.random.default_rng(N).choice(N, size=min(N, 768), replace=False)
