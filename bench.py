@@ -6,8 +6,8 @@
 Workload: one Llama-3.2-3B decode layer's projections at
 M = 1 with MLX 4-bit group-64 weights -- q/o [3072x3072], k/v [1024x3072],
 gate+up [8192x3072] fused with SiLU x up, down [3072x8192].  A step is one
-layer: 6 launches (q, k, v, o, gate/up+SiLU, down), down consuming the
-gate/up output.  Steps rotate over --copies distinct layers (default 40,
+layer: 4 launches (q/k/v rows concatenated at load time into one [5120x3072]
+weight, o, gate/up+SiLU, down), down consuming the gate/up output.  Steps rotate over --copies distinct layers (default 40,
 2.27 GB of weights) so the 256 MB MALL cannot hold the working set, and the
 timed region replays a HIP graph of one rotation (graph capture removes the
 host launch cost, as a decode loop would).
@@ -44,10 +44,12 @@ def gemv_bytes(N, K, nsets=1, M=1, g=G):
     return nsets * (N * K // 2 + 4 * N * (K // g)) + 2 * M * K + 2 * M * N
 
 
-# (name, N, K, weight sets)
-DECODE = [("q_proj", 3072, 3072, 1), ("k_proj", 1024, 3072, 1), ("v_proj", 1024, 3072, 1),
-          ("o_proj", 3072, 3072, 1), ("gate_up_proj", 8192, 3072, 2), ("down_proj", 3072, 8192, 1)]
-LAYER_BYTES = sum(gemv_bytes(N, K, n) for _, N, K, n in DECODE)  # 56,709,120
+# (name, N, K, weight sets).  q [3072], k [1024] and v [1024] rows are
+# concatenated at load time into one [5120, 3072] weight (one launch, same
+# matmulQ4 entry point); gate and up stay separate weights fused in one launch.
+DECODE = [("qkv_proj", 5120, 3072, 1), ("o_proj", 3072, 3072, 1),
+          ("gate_up_proj", 8192, 3072, 2), ("down_proj", 3072, 8192, 1)]
+LAYER_BYTES = sum(gemv_bytes(N, K, n) for _, N, K, n in DECODE)  # 56,696,832
 DOMINANT = "gate_up_proj"
 DOMINANT_BYTES = gemv_bytes(8192, 3072, 2)  # 28,334,080
 
@@ -104,18 +106,12 @@ def main():
     x2 = torch.randn(1, 3072, generator=gen, device=dev).half()
     outs = {name: torch.empty(1, N, device=dev, dtype=torch.float16) for name, N, _, _ in DECODE}
 
-    def step(L, ev=None):
+    def step(L):
         w = L.w
-        pkg.matmul_q4(x, *_wsb(w["q_proj"][0]), 1, 3072, 3072, G, out=outs["q_proj"])
-        pkg.matmul_q4(x, *_wsb(w["k_proj"][0]), 1, 3072, 1024, G, out=outs["k_proj"])
-        pkg.matmul_q4(x, *_wsb(w["v_proj"][0]), 1, 3072, 1024, G, out=outs["v_proj"])
+        pkg.matmul_q4(x, *_wsb(w["qkv_proj"][0]), 1, 3072, 5120, G, out=outs["qkv_proj"])
         pkg.matmul_q4(attn, *_wsb(w["o_proj"][0]), 1, 3072, 3072, G, out=outs["o_proj"])
-        if ev is not None:
-            ev[0].record()
         pkg.matmul_q4_silu_mul(x2, w["gate_up_proj"][0], w["gate_up_proj"][1], 1, 3072, 8192,
                                out=outs["gate_up_proj"])
-        if ev is not None:
-            ev[1].record()
         pkg.matmul_q4(outs["gate_up_proj"], *_wsb(w["down_proj"][0]), 1, 8192, 3072, G,
                       out=outs["down_proj"])
 
@@ -124,24 +120,12 @@ def main():
         step(L)
     torch.cuda.synchronize()
 
-    # one rotation over all copies, captured as a HIP graph, with timing events
-    # around every dominant launch (event-record nodes inside the graph)
+    # one rotation over all copies, captured as a HIP graph
     nrot = args.copies
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(nrot)]
-    timing = "events in graph"
     graph = torch.cuda.CUDAGraph()
-    try:
-        with torch.cuda.graph(graph):
-            for i, L in enumerate(layers):
-                step(L, evs[i])
-    except Exception as e:  # event nodes not capturable: graph without them
-        timing = f"graph-only dominant launches ({type(e).__name__})"
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            for L in layers:
-                step(L)
-        evs = None
+    with torch.cuda.graph(graph):
+        for L in layers:
+            step(L)
     torch.cuda.synchronize()
 
     reps_w = max(1, args.warmup // nrot)
@@ -151,42 +135,35 @@ def main():
         graph.replay()
     torch.cuda.synchronize()
 
-    dom_ms = []
+    # timed region: K steps as graph replays, bracketed by synchronize
     t0 = time.perf_counter()
     for _ in range(reps):
         graph.replay()
-        if evs is not None:
-            # elapsed times are read after the next replay is queued so the
-            # host never stalls the GPU; the last rotation is read after sync
-            pass
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     wall = t1 - t0
-    if evs is not None:
-        try:
-            dom_ms = [a.elapsed_time(b) for a, b in evs]
-        except Exception as e:
-            timing = f"graph-only dominant launches ({type(e).__name__} reading events)"
-            evs = None
 
-    if evs is None or not dom_ms:
-        # the dominant kernel alone: a graph of one rotation of gate/up launches,
-        # bracketed by events on the capturing stream's successor
-        g2 = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g2):
-            for L in layers:
-                w = L.w["gate_up_proj"]
-                pkg.matmul_q4_silu_mul(x2, w[0], w[1], 1, 3072, 8192, out=outs["gate_up_proj"])
+    # dominant kernel: HIP cannot report elapsed time between event nodes
+    # captured inside a graph, so the gate/up launches of the same rotation
+    # are captured alone and their replays bracketed by events on the stream
+    # they run on; duration = elapsed / launches (inter-launch gaps included)
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2):
+        for L in layers:
+            w = L.w["gate_up_proj"]
+            pkg.matmul_q4_silu_mul(x2, w[0], w[1], 1, 3072, 8192, out=outs["gate_up_proj"])
+    g2.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    r2 = max(1, reps // 2)
+    e0.record()
+    for _ in range(r2):
         g2.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        r2 = max(1, reps // 4)
-        e0.record()
-        for _ in range(r2):
-            g2.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        dom_ms = [e0.elapsed_time(e1) / (r2 * nrot)]
+    e1.record()
+    torch.cuda.synchronize()
+    dom_ms = [e0.elapsed_time(e1) / (r2 * nrot)]
+    timing = (f"HIP events around {r2} replays of a graph of the {nrot} rotated gate/up "
+              "launches")
 
     dom_us = 1e3 * sum(dom_ms) / len(dom_ms)
     achieved = DOMINANT_BYTES / (dom_us * 1e-6) / 1e9
@@ -214,9 +191,9 @@ def main():
         "data": "synthetic (BASELINE distributions: x~N(0,1) fp16, codes uniform 0..15, "
                 "scales |N(0,0.02)| fp16, biases -8*scale)",
         "config": {"workload": "Llama-3.2-3B decode layer projections, M=1, MLX 4-bit g64 "
-                               "(q,k,v,o,gate+up fused SiLU*up, down); "
-                               f"{args.copies} distinct layer copies rotated",
-                   "bytes_per_step": LAYER_BYTES, "launches_per_step": 6,
+                               "(q,k,v rows concatenated at load, o, gate+up fused SiLU*up, "
+                               f"down); {args.copies} distinct layer copies rotated",
+                   "bytes_per_step": LAYER_BYTES, "launches_per_step": len(DECODE),
                    "graph": "one rotation captured as a HIP graph"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),

@@ -9,7 +9,7 @@
 
 #include "q4_common.hpp"
 #include "q4_launch.hpp"
-#include "../../include/swiftltx_q4.h"
+#include "swiftltx_q4.h"
 
 namespace sltx {
 

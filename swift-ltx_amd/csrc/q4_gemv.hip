@@ -75,10 +75,34 @@ __device__ __forceinline__ float chunk_dot(const u32x4 w, const u32x4 xq[4], flo
     return d0 + d1;
 }
 
+// v + (v from another lane of the same 16-lane row), by DPP.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+    const int m = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false);
+    return v + __builtin_bit_cast(float, m);
+}
+
+// Sum over each aligned group of L lanes (L = 16, 32 or 64), result in every
+// lane of the group.  Within a 16-lane row: DPP quad_perm [1,0,3,2] and
+// [2,3,0,1], then row_half_mirror and row_mirror (each pairs lanes whose
+// partial sums are disjoint).  Across rows: v_permlane16_swap (row pairs)
+// and v_permlane32_swap (wave halves), each returning the two halves to add.
 template <int L>
 __device__ __forceinline__ float row_reduce(float v) {
-#pragma unroll
-    for (int off = L / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if (L >= 2) v = dpp_add<0xB1>(v);
+    if (L >= 4) v = dpp_add<0x4E>(v);
+    if (L >= 8) v = dpp_add<0x141>(v);
+    if (L >= 16) v = dpp_add<0x140>(v);
+    if (L >= 32) {
+        const unsigned u = __builtin_bit_cast(unsigned, v);
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        v = __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+    }
+    if (L >= 64) {
+        const unsigned u = __builtin_bit_cast(unsigned, v);
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        v = __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+    }
     return v;
 }
 
