@@ -121,10 +121,15 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 template <int WM, bool BF16, bool SILU, bool KTAIL>
 __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
     constexpr int BM = 64 * WM;
-    constexpr int A_STAGE = BM * BK / 8;    // 16-byte slots per A stage
-    constexpr int W_STAGE = BN * BK / 8;
-    __shared__ u32x4 lds_a[3 * A_STAGE];    // 3 stages, swizzled [row][col16]
-    __shared__ u32x4 lds_w[2 * W_STAGE];    // 2 stages
+    constexpr int NSA = WM == 2 ? 3 : 2;       // A stages (LDS budget)
+    constexpr int A_STAGE = BM * BK / 8;       // 16-byte slots per A stage
+    constexpr int W16_STAGE = BN * BK / 8;     // dequantized W, one k-tile
+    constexpr int WP_STAGE = BN * 4;           // packed W, two k-tiles (64 B per row)
+    constexpr int GPMAX = 4;                   // scale/bias groups per row per super-stage
+    __shared__ u32x4 lds_a[NSA * A_STAGE];     // swizzled [row][col16]
+    __shared__ u32x4 lds_w16[2 * W16_STAGE];   // swizzled [row][col16]
+    __shared__ u32x4 lds_wp[2 * WP_STAGE];     // swizzled [row][piece]
+    __shared__ uint16_t lds_sb[2][2][BN * GPMAX];   // [stage][scale|bias][row * GP + g]
 
     // ---- tile selection (XCD-aware) ----
     const int ntiles = p.tiles_m * p.tiles_n;
@@ -143,14 +148,33 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
+    const int nk = (p.K + BK - 1) / BK;
+    const int GP = 4 >> p.gshift;   // scale/bias groups per 128 k (g = 32, 64, 128)
+
+    // Virtual W row -> matrix row (and which matrix, for SILU).  Rows past N
+    // are clamped to row 0: computed, never stored.
+    auto wrow = [&](int v, const uint32_t*& W, const uint16_t*& S, const uint16_t*& B) {
+        int n;
+        if (SILU) {
+            const int tn = (v >> 5) & 1;
+            n = n0 + (v >> 6) * 32 + (v & 31);
+            W = tn ? p.w1 : p.w0;
+            S = tn ? p.s1 : p.s0;
+            B = tn ? p.b1 : p.b0;
+        } else {
+            n = n0 + v;
+            W = p.w0;
+            S = p.s0;
+            B = p.b0;
+        }
+        return n < p.N ? n : 0;
+    };
 
     // ---- A: direct global -> LDS (global_load_lds_dwordx4) ----
     // Each wave fills WM 1-KB pieces of a stage: piece i covers slots
-    // (wave + 8 i) * 64 .. +63, lane l landing in slot +l (the hardware puts
-    // lane l's 16 bytes at the wave's base + 16 l).  Slot s is physical
-    // column s % 8 of row s / 8, i.e. logical column (s % 8) ^ xor(row), so
-    // the swizzle is applied on the global side.  Rows past M are clamped to
-    // M-1 (computed, never stored).
+    // (wave + 8 i) * 64 .. +63, lane l landing in slot +l.  Slot s is physical
+    // column s % 8 of row s / 8, i.e. logical column (s % 8) ^ xor(row): the
+    // swizzle is applied on the global side.  Rows past M are clamped to M-1.
     const uint16_t* A = reinterpret_cast<const uint16_t*>(p.a);
     const uint16_t* a_src[WM];
     int a_col8[WM];
@@ -164,87 +188,117 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
         a_src[i] = A + (size_t)(m < p.M ? m : p.M - 1) * p.K + c16 * 8;
     }
 
-    // ---- W: global -> registers -> dequantize -> LDS ----
-    // Virtual row vr = tid % 256, half = tid / 256 (32 nibbles; the half is
-    // wave-uniform).  Rows past N are clamped to row 0 (never stored).
-    const int vr = tid & 255, whalf = tid >> 8;
-    int wn_row;
-    const uint32_t* Wsel;
-    const uint16_t *Ssel, *Bsel;
-    if (SILU) {
-        const int wv = vr >> 6, tn = (vr >> 5) & 1;
-        wn_row = n0 + wv * 32 + (vr & 31);
-        Wsel = tn ? p.w1 : p.w0;
-        Ssel = tn ? p.s1 : p.s0;
-        Bsel = tn ? p.b1 : p.b0;
-    } else {
-        wn_row = n0 + vr;
-        Wsel = p.w0;
-        Ssel = p.s0;
-        Bsel = p.b0;
+    // ---- packed W: direct global -> LDS, two k-tiles (64 B per row) ----
+    // Four lanes cover a row's 64 bytes, so each wave-wide copy reads 16 rows
+    // of 64 contiguous bytes.  Slot s is row s / 4, physical piece s % 4 =
+    // logical piece ^ ((row >> 2) & 3) (conflict-free reads below).
+    const uint32_t* wp_src[2];
+    int wp_piece[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int slot = (wave + 8 * i) * 64 + lane;
+        const int row = slot >> 2;
+        const int piece = (slot & 3) ^ ((row >> 2) & 3);
+        const uint32_t* W;
+        const uint16_t *S, *B;
+        const int n = wrow(row, W, S, B);
+        wp_piece[i] = piece;
+        wp_src[i] = W + (size_t)n * (p.K / 8) + piece * 4;
     }
-    const int wr = wn_row < p.N ? wn_row : 0;
-    const uint32_t* w_ptr = Wsel + (size_t)wr * (p.K / 8) + whalf * 4;
-    const uint16_t* s_ptr = Ssel + (size_t)wr * p.groups;
-    const uint16_t* b_ptr = Bsel + (size_t)wr * p.groups;
 
-    const int nk = (p.K + BK - 1) / BK;
+    // ---- scales / biases: GP groups per row per super-stage ----
+    // Threads 0-255 load scales, 256-511 biases; consecutive threads read
+    // consecutive groups of a row.  Values land in registers and are written
+    // to LDS one k-tile later.
+    const int sb_arr = tid >> 8;
+    const uint16_t* sb_src[GPMAX];
+    int sb_dst[GPMAX];
+#pragma unroll
+    for (int u = 0; u < GPMAX; ++u) {
+        const int v = (tid & 255) + 256 * u;
+        const int row = v / GP, g = v % GP;
+        const uint32_t* W;
+        const uint16_t *S, *B;
+        const int n = wrow(row < BN ? row : 0, W, S, B);
+        sb_src[u] = (sb_arr ? B : S) + (size_t)n * p.groups + g;
+        sb_dst[u] = v;
+    }
 
-    // Tile kt+2's loads are issued while tile kt is multiplied: A straight
-    // into LDS stage (kt+2) % 3, W into one of two register sets.  A K tail
-    // (K % 64 == 32: the last tile's upper 32 columns) clamps the A source in
-    // bounds and zeroes those LDS slots once the copy has landed, and gives
-    // the upper W half scale = bias = 0 (s*q + b = 0 whatever the codes).
-    struct WRegs {
-        u32x4 w;
-        uint32_t s, b;
-        bool zero;
-    };
+    // ---- dequant assignment: virtual row vr, half whalf (wave-uniform) ----
+    const int vr = tid & 255, whalf = tid >> 8;
+
+    const int nss = (nk + 1) / 2;   // super-stages
 
     auto load_a = [&](int kt) {   // WM vector-memory ops
         const int k0 = kt * BK;
-        u32x4* stage = lds_a + (kt % 3) * A_STAGE;
+        u32x4* stage = lds_a + (kt % NSA) * A_STAGE;
 #pragma unroll
         for (int i = 0; i < WM; ++i) {
             int off = k0;
             if (KTAIL && k0 + a_col8[i] >= p.K) off = p.K - 8 - a_col8[i];
-            __builtin_amdgcn_global_load_lds(
-                (const void*)(a_src[i] + off),
-                (lds_ptr_t)(stage + (wave + 8 * i) * 64), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)(a_src[i] + off),
+                                             (lds_ptr_t)(stage + (wave + 8 * i) * 64), 16, 0, 0);
         }
     };
     auto zero_a_tail = [&](int kt) {   // after the copy for tile kt landed
         const int k0 = kt * BK;
         if (!KTAIL || k0 + BK <= p.K) return;
-        u32x4* stage = lds_a + (kt % 3) * A_STAGE;
+        u32x4* stage = lds_a + (kt % NSA) * A_STAGE;
         const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
         for (int i = 0; i < WM; ++i)
             if (k0 + a_col8[i] >= p.K) stage[(wave + 8 * i) * 64 + lane] = z;
     };
-    auto load_w = [&](WRegs& r, int kt) {   // 3 vector-memory ops
-        const int k0 = kt * BK;
-        r.zero = KTAIL && k0 + whalf * 32 >= p.K;
-        const int wz = r.zero ? 1 : 0;
-        r.w = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(w_ptr + (k0 >> 3) - 4 * wz));
-        const int gi = (2 * kt + whalf - wz) >> p.gshift;
-        r.s = s_ptr[gi];
-        r.b = b_ptr[gi];
+    auto load_wp = [&](int ss) {   // 2 vector-memory ops
+        u32x4* stage = lds_wp + (ss & 1) * WP_STAGE;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            int off = ss * 16;   // u32 words: 64 bytes per super-stage
+            if (KTAIL && (ss * 128 + wp_piece[i] * 32) >= p.K) off = (p.K / 8) - 4 - wp_piece[i] * 4;
+            __builtin_amdgcn_global_load_lds((const void*)(wp_src[i] + off),
+                                             (lds_ptr_t)(stage + (wave + 8 * i) * 64), 16, 0, 0);
+        }
     };
-    // Dequantize word j of this thread's W chunk into W stage `stage`.
-    auto store_w = [&](const WRegs& r, int stage, int j) {
-        const uint16_t sb = (KTAIL && r.zero) ? (uint16_t)0 : (uint16_t)r.s;
-        const uint16_t bb = (KTAIL && r.zero) ? (uint16_t)0 : (uint16_t)r.b;
+    uint32_t sbr[GPMAX];
+    auto load_sb = [&](int ss) {   // GPMAX vector-memory ops (the first GP are used)
+#pragma unroll
+        for (int u = 0; u < GPMAX; ++u) {
+            int g = ss * GP;
+            if (KTAIL && g + (sb_dst[u] % GP) >= p.groups) g = p.groups - 1 - (sb_dst[u] % GP);
+            sbr[u] = sb_src[u][g];   // unused slots read an in-bounds element
+        }
+    };
+    auto store_sb = [&](int ss) {
+#pragma unroll
+        for (int u = 0; u < GPMAX; ++u)
+            if (u < GP) lds_sb[ss & 1][sb_arr][sb_dst[u]] = (uint16_t)sbr[u];
+    };
+    // Dequantize word j of this thread's 32 nibbles of tile t (packed stage ->
+    // W16 stage t & 1).
+    u32x4 wpk;
+    uint16_t dq_s, dq_b;
+    auto fetch_dq = [&](int t) {
+        const int tl = t & 1, ss = t >> 1;
+        const int piece = tl * 2 + whalf;
+        wpk = lds_wp[(ss & 1) * WP_STAGE + vr * 4 + (piece ^ ((vr >> 2) & 3))];
+        const int gl = (tl * 2 + whalf) >> p.gshift;
+        dq_s = lds_sb[ss & 1][0][vr * GP + gl];
+        dq_b = lds_sb[ss & 1][1][vr * GP + gl];
+        if (KTAIL && t * BK + whalf * 32 >= p.K) {
+            dq_s = 0;
+            dq_b = 0;
+        }
+    };
+    auto store_w = [&](int t, int j) {
         u32x4 o;
         if constexpr (BF16) {
-            o = dequant_word_bf16(r.w[j], h2f(sb), h2f(bb));
+            o = dequant_word_bf16(wpk[j], h2f(dq_s), h2f(dq_b));
         } else {
-            const f16 sh = __builtin_bit_cast(f16, sb), bh = __builtin_bit_cast(f16, bb);
+            const f16 sh = __builtin_bit_cast(f16, dq_s), bh = __builtin_bit_cast(f16, dq_b);
             const f16x2 s2 = {sh, sh}, b2 = {bh, bh};
-            o = dequant_word_f16(r.w[j], s2, b2);
+            o = dequant_word_f16(wpk[j], s2, b2);
         }
-        lds_w[stage * W_STAGE + swz(vr, whalf * 4 + j)] = o;
+        lds_w16[(t & 1) * W16_STAGE + swz(vr, whalf * 4 + j)] = o;
     };
 
     f32x16 acc[WM][2];
@@ -259,79 +313,105 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
     const int arow0 = wm * (WM * 32) + lrow;
     const int brow0 = wn * 64 + lrow;
 
-    // One k-tile: MFMAs on A stage kt % 3 and W stage kt % 2.  With LOAD, tile
-    // kt+2 is loaded (A into LDS, W into `fre`); with STORE, tile kt+1's W
-    // (in `nxt`) is dequantized into the other W stage between the k-steps.
-    // LOAD and STORE are compile-time so each step is one branch-free block.
-    auto step = [&](auto load_c, auto store_c, int kt, const WRegs& nxt, WRegs& fre) {
-        constexpr bool LOAD = decltype(load_c)::value;
-        constexpr bool STORE = decltype(store_c)::value;
-        if constexpr (LOAD) {
-            load_w(fre, kt + 2);
-            load_a(kt + 2);
+    // Prologue: super-stages 0 and 1 (k-tiles 0-3) and the first A tiles in
+    // flight; scales/biases of both super-stages to LDS; tile 0 dequantized.
+    load_sb(0);
+    load_wp(0);
+    if (nss > 1) load_wp(1);
+#pragma unroll
+    for (int t = 0; t < NSA - 1; ++t)
+        if (t < nk) load_a(t);
+    store_sb(0);   // waits for this thread's scale/bias loads
+    if (nss > 1) {
+        load_sb(1);
+        store_sb(1);
+    }
+    SLTX_WAIT_VMCNT(0);
+    zero_a_tail(0);
+    if (NSA > 2 && nk > 1) zero_a_tail(1);
+    __syncthreads();
+    fetch_dq(0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) store_w(0, j);
+    __syncthreads();
+
+    // k-tile kt: MFMAs on A stage kt % NSA and W16 stage kt & 1; tile kt+1 is
+    // dequantized into the other W16 stage between the k-steps.  Loads issued
+    // during kt: A tile kt+NSA-1; for odd kt = 2j+1 also packed W and the
+    // scale/bias registers of super-stage j+2 (written to LDS during kt+1).
+    // ODD is compile-time (the loop is unrolled by two) so that each step is
+    // one branch-free block with a constant wait count.
+    auto step = [&](auto odd_c, int kt) {
+        constexpr bool ODD = decltype(odd_c)::value;
+        const bool a_more = kt + NSA - 1 < nk;
+        const bool dq_more = kt + 1 < nk;
+        const int ss_ld = (kt + 3) >> 1;
+        const bool w_more = ODD && ss_ld < nss;
+        if (a_more) load_a(kt + NSA - 1);
+        if (w_more) {
+            load_wp(ss_ld);
+            load_sb(ss_ld);
         }
-        const u32x4* sa = lds_a + (kt % 3) * A_STAGE;
-        const u32x4* sw = lds_w + (kt & 1) * W_STAGE;
+        if (!ODD && kt >= 2 && (kt >> 1) + 1 < nss) store_sb((kt >> 1) + 1);
+        if (dq_more) fetch_dq(kt + 1);
+        const u32x4* sa = lds_a + (kt % NSA) * A_STAGE;
+        const u32x4* sw = lds_w16 + (kt & 1) * W16_STAGE;
+        // Operand fragments are double-buffered: k-step ks+1's LDS reads are
+        // issued before k-step ks's MFMAs so their latency overlaps them.
+        u32x4 af[2][WM], bf[2][2];
+        auto ldfrag = [&](int ks, int b) {
+            const int c16 = ks * 2 + lk;
+#pragma unroll
+            for (int t = 0; t < WM; ++t) af[b][t] = sa[swz(arow0 + t * 32, c16)];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) bf[b][j] = sw[swz(brow0 + j * 32, c16)];
+        };
+        ldfrag(0, 0);
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ++ks) {
-            const int c16 = ks * 2 + lk;
-            u32x4 af[WM], bf[2];
-#pragma unroll
-            for (int t = 0; t < WM; ++t) af[t] = sa[swz(arow0 + t * 32, c16)];
-#pragma unroll
-            for (int j = 0; j < 2; ++j) bf[j] = sw[swz(brow0 + j * 32, c16)];
+            const int b = ks & 1;
+            if (ks + 1 < BK / 16) ldfrag(ks + 1, b ^ 1);
 #pragma unroll
             for (int i = 0; i < WM; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = mfma32<BF16>(af[i], bf[j], acc[i][j]);
-            if constexpr (STORE) store_w(nxt, (kt + 1) & 1, ks);
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = mfma32<BF16>(af[b][i], bf[b][j], acc[i][j]);
+            if (dq_more) store_w(kt + 1, ks);
         }
-        // Tile kt+1's A copy (issued one step earlier) must have landed before
-        // the barrier; only this step's own loads may still be in flight.
-        if constexpr (LOAD)
-            SLTX_WAIT_VMCNT(WM + 3);
-        else
-            SLTX_WAIT_VMCNT(0);
-        if constexpr (STORE) zero_a_tail(kt + 1);
+        // Before the barrier, A tile kt+1 and the packed W / scales that the
+        // next step dequantizes (super-stage (kt+2)/2) must have landed.
+        // vmcnt retires in issue order; the count allows exactly the loads
+        // that were issued after the last of those:
+        //  NSA 2: A tile kt+1 was issued first in this step; after it only
+        //         this step's W + scale/bias loads (odd steps).
+        //  NSA 3: odd step: A tile kt+1 was issued in the previous (even)
+        //         step, which issued nothing else; after it, this step's A and
+        //         W + scale/bias loads.  Even step: the previous (odd) step
+        //         issued W + scale/bias after its A, and those are needed next
+        //         step, so only this step's A loads may remain.
+        constexpr int NWSB = 2 + GPMAX;
+        if constexpr (NSA == 2) {
+            if (ODD && w_more) SLTX_WAIT_VMCNT(NWSB); else SLTX_WAIT_VMCNT(0);
+        } else if constexpr (ODD) {
+            if (a_more && w_more) SLTX_WAIT_VMCNT(WM + NWSB);
+            else if (a_more) SLTX_WAIT_VMCNT(WM);
+            else if (w_more) SLTX_WAIT_VMCNT(NWSB);
+            else SLTX_WAIT_VMCNT(0);
+        } else {
+            if (a_more) SLTX_WAIT_VMCNT(WM); else SLTX_WAIT_VMCNT(0);
+        }
+        if (kt + 1 < nk) zero_a_tail(kt + 1);
         __syncthreads();
     };
     using T_ = std::true_type;
     using F_ = std::false_type;
 
-    // Prologue: tiles 0 and 1 in flight, tile 0 made ready.
-    WRegs ra, rb;
-    load_w(ra, 0);
-    load_a(0);
-    if (nk > 1) {
-        load_w(rb, 1);
-        load_a(1);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) store_w(ra, 0, j);
-    if (nk > 1)
-        SLTX_WAIT_VMCNT(WM + 3);
-    else
-        SLTX_WAIT_VMCNT(0);
-    zero_a_tail(0);
-    __syncthreads();
-    // Invariant at the top of each pass: tile kt is ready in LDS, rb holds
-    // tile kt+1's W and its A copy is in flight.
     int kt = 0;
-    for (; kt + 3 < nk; kt += 2) {
-        step(T_{}, T_{}, kt, rb, ra);
-        step(T_{}, T_{}, kt + 1, ra, rb);
+    for (; kt + 1 < nk; kt += 2) {
+        step(F_{}, kt);
+        step(T_{}, kt + 1);
     }
-    const int rem = nk - kt;   // 1, 2 or 3 tiles left
-    if (rem == 3) {
-        step(T_{}, T_{}, kt, rb, ra);
-        step(F_{}, T_{}, kt + 1, ra, rb);
-        step(F_{}, F_{}, kt + 2, rb, ra);
-    } else if (rem == 2) {
-        step(F_{}, T_{}, kt, rb, ra);
-        step(F_{}, F_{}, kt + 1, ra, rb);
-    } else {
-        step(F_{}, F_{}, kt, rb, ra);
-    }
+    if (kt < nk) step(F_{}, kt);
 
     // ---- epilogue ----
     // 32x32 accumulator layout: lane l, element v -> row 8*(v/4) + 4*(l/32) + v%4,
@@ -384,7 +464,9 @@ static int pick_wm(int M, int n_tiles) {
 
 template <int WM, bool BF16>
 static void launch_wm(const GemmParams& p, bool silu, long grid, hipStream_t st) {
-    const bool ktail = p.K % BK != 0;
+    // Packed W and scales move in 128-k super-stages: K % 128 != 0 needs the
+    // tail handling (clamped sources, zeroed dequant past K).
+    const bool ktail = p.K % (2 * BK) != 0;
     if (silu && ktail)
         hipLaunchKernelGGL((q4_gemm_kernel<WM, BF16, true, true>), dim3(grid), dim3(kThreads), 0, st, p);
     else if (silu)
