@@ -64,6 +64,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--diag", action="store_true", help="print timing-method diagnostics")
+    ap.add_argument("--traffic", action="store_true",
+                    help="only: 24 launches of the dominant kernel over 12 weight copies, then a "
+                         "256 MiB torch copy (the calibration kernel), for rocprofv3 --pmc runs")
     return ap.parse_args()
 
 
@@ -99,6 +102,10 @@ def main():
     torch.cuda.set_device(dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
+
+    if args.traffic:
+        traffic_run(pkg, torch, gen, dev)
+        return
 
     layers = [Layer(pkg, torch, gen, dev) for _ in range(args.copies)]
     x = torch.randn(1, 3072, generator=gen, device=dev).half()
@@ -205,6 +212,24 @@ def main():
         "extra": {"gemm": gemm, **({"timing_diag": diag} if diag else {})},
     }
     print(json.dumps(line))
+
+
+def traffic_run(pkg, torch, gen, dev):
+    """Workload for the FETCH_SIZE / WRITE_SIZE passes: the dominant kernel
+    (fused gate/up GEMV) 24 times over 12 distinct weight copies, then one
+    256 MiB copy_ whose counters give the bytes-per-count calibration."""
+    sets = [[pkg.Q4Weight(*rand_q4(torch, 8192, 3072, gen, dev), 3072, G) for _ in range(2)]
+            for _ in range(12)]
+    x = torch.randn(1, 3072, generator=gen, device=dev).half()
+    y = torch.empty(1, 8192, device=dev, dtype=torch.float16)
+    for _ in range(2):
+        for gate, up in sets:
+            pkg.matmul_q4_silu_mul(x, gate, up, 1, 3072, 8192, out=y)
+    src = torch.empty(256 * 2 ** 20 // 4, device=dev, dtype=torch.float32).normal_()
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print("traffic run done", flush=True)
 
 
 def _wsb(q):

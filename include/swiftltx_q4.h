@@ -12,7 +12,15 @@
  *
  * Conventions (all entry points):
  *   - Every pointer is a device pointer the caller allocated; the library never
- *     allocates, frees or keeps them.  Outputs are written, never read.
+ *     frees or keeps them.  Outputs are written, never read.
+ *   - Memory: the only device memory the library allocates is a split-K
+ *     workspace (fp32 partial sums) for GEMMs with too few output tiles to
+ *     fill the GPU (e.g. M=750 x N=3072).  There is one per (device, stream),
+ *     grown on first need (growing frees the old buffer, which waits for the
+ *     device) and kept until the process exits.  A stream being captured into
+ *     a HIP graph never allocates: if its workspace is missing or too small,
+ *     that GEMM runs unsplit (same results, lower throughput).  Capture after
+ *     one eager call on the same stream to get the split kernel into a graph.
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = the default stream) and
  *     nothing synchronises: results are visible to later work on that stream.
  *     This mirrors the reference's batched mode (MetalContext.swift:109-134).

@@ -2,7 +2,9 @@
 // routing and launch of the gfx950 kernels.  Validation runs before any HIP
 // call, so error paths behave the same with or without a GPU.
 #include <cstdarg>
+#include <map>
 #include <mutex>
+#include <utility>
 #include <string>
 #include <cstdio>
 #include <cstring>
@@ -105,6 +107,38 @@ int run_gemv(const char* fn, const void* x, const sltx_q4_weight& w0, const sltx
     return finish(launch_gemv(p, w1 != nullptr, st), fn);
 }
 
+// Split-K workspace, one per (device, stream): calls on one stream are
+// ordered, so they can share it; other streams get their own.  It grows on
+// demand (the old buffer is freed first, which waits for the device) and is
+// kept until the process ends.  A stream that is being captured into a graph
+// never allocates: if its workspace is missing or too small the GEMM runs
+// unsplit.
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> g_ws;
+
+float* splitk_workspace(hipStream_t st, size_t need) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    auto& e = g_ws[{dev, st}];
+    if (e.second >= need) return static_cast<float*>(e.first);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+        return nullptr;
+    if (e.first) {
+        if (hipFree(e.first) != hipSuccess) return nullptr;
+        e = {nullptr, 0};
+    }
+    void* ptr = nullptr;
+    const size_t bytes = need + need / 4;
+    if (hipMalloc(&ptr, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    e = {ptr, bytes};
+    return static_cast<float*>(ptr);
+}
+
 int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w0,
              const sltx_q4_weight* w1, const float* bias, int epilogue, void* out, int y_dtype,
              int M, int K, int N, hipStream_t st) {
@@ -126,6 +160,11 @@ int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w
     p.tiles_m = p.tiles_n = 0;
     p.y_dtype = y_dtype;
     p.epilogue = w1 ? kEpiSiluMul : epilogue;
+    p.ws = nullptr;
+    p.splits = 1;
+    p.split_tiles = 0;
+    const size_t need = gemm_workspace_bytes(p);
+    if (need > 0) p.ws = splitk_workspace(st, need);
     return finish(launch_gemm(p, x_dtype == kBF16, st), fn);
 }
 

@@ -118,7 +118,7 @@ __device__ __forceinline__ void store_out(const GemmParams& p, size_t o, float v
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-template <int WM, bool BF16, bool SILU, bool KTAIL>
+template <int WM, bool BF16, bool SILU, bool KTAIL, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
     constexpr int BM = 64 * WM;
     constexpr int NSA = WM == 2 ? 3 : 2;       // A stages (LDS budget)
@@ -138,9 +138,16 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
         const int per_xcd = gridDim.x >> 3;
         logical = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
     }
-    if (logical >= ntiles) return;
-    const int tile_m = logical % p.tiles_m;
-    const int tile_n = logical / p.tiles_m;
+    if (logical >= ntiles * (SPLIT ? p.splits : 1)) return;
+    const int split = SPLIT ? logical / ntiles : 0;
+    const int tile = SPLIT ? logical % ntiles : logical;
+    const int tile_m = tile % p.tiles_m;
+    const int tile_n = tile / p.tiles_m;
+    // K range of this block: k-tiles [kb, kb + nk); Kl = its extent in k.
+    const int nk_all = (p.K + BK - 1) / BK;
+    const int kb = SPLIT ? split * p.split_tiles : 0;
+    const int nk = SPLIT ? min(p.split_tiles, nk_all - kb) : nk_all;
+    const int Kl = min(p.K - kb * BK, nk * BK);
     const int m0 = tile_m * BM;
     // SILU: a tile covers 128 output columns, as 128 gate rows + 128 up rows.
     const int n0 = tile_n * (SILU ? BN / 2 : BN);
@@ -148,7 +155,6 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
-    const int nk = (p.K + BK - 1) / BK;
     const int GP = 4 >> p.gshift;   // scale/bias groups per 128 k (g = 32, 64, 128)
 
     // Virtual W row -> matrix row (and which matrix, for SILU).  Rows past N
@@ -185,7 +191,7 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
         const int c16 = (slot & 7) ^ (row & 7) ^ ((row >> 3) & 1);
         const int m = m0 + row;
         a_col8[i] = c16 * 8;
-        a_src[i] = A + (size_t)(m < p.M ? m : p.M - 1) * p.K + c16 * 8;
+        a_src[i] = A + (size_t)(m < p.M ? m : p.M - 1) * p.K + kb * BK + c16 * 8;
     }
 
     // ---- packed W: direct global -> LDS, two k-tiles (64 B per row) ----
@@ -203,7 +209,7 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
         const uint16_t *S, *B;
         const int n = wrow(row, W, S, B);
         wp_piece[i] = piece;
-        wp_src[i] = W + (size_t)n * (p.K / 8) + piece * 4;
+        wp_src[i] = W + (size_t)n * (p.K / 8) + kb * (BK / 8) + piece * 4;
     }
 
     // ---- scales / biases: GP groups per row per super-stage ----
@@ -220,7 +226,7 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
         const uint32_t* W;
         const uint16_t *S, *B;
         const int n = wrow(row < BN ? row : 0, W, S, B);
-        sb_src[u] = (sb_arr ? B : S) + (size_t)n * p.groups + g;
+        sb_src[u] = (sb_arr ? B : S) + (size_t)n * p.groups + ((2 * kb) >> p.gshift) + g;
         sb_dst[u] = v;
     }
 
@@ -235,26 +241,26 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int i = 0; i < WM; ++i) {
             int off = k0;
-            if (KTAIL && k0 + a_col8[i] >= p.K) off = p.K - 8 - a_col8[i];
+            if (KTAIL && k0 + a_col8[i] >= Kl) off = Kl - 8 - a_col8[i];
             __builtin_amdgcn_global_load_lds((const void*)(a_src[i] + off),
                                              (lds_ptr_t)(stage + (wave + 8 * i) * 64), 16, 0, 0);
         }
     };
     auto zero_a_tail = [&](int kt) {   // after the copy for tile kt landed
         const int k0 = kt * BK;
-        if (!KTAIL || k0 + BK <= p.K) return;
+        if (!KTAIL || k0 + BK <= Kl) return;
         u32x4* stage = lds_a + (kt % NSA) * A_STAGE;
         const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
         for (int i = 0; i < WM; ++i)
-            if (k0 + a_col8[i] >= p.K) stage[(wave + 8 * i) * 64 + lane] = z;
+            if (k0 + a_col8[i] >= Kl) stage[(wave + 8 * i) * 64 + lane] = z;
     };
     auto load_wp = [&](int ss) {   // 2 vector-memory ops
         u32x4* stage = lds_wp + (ss & 1) * WP_STAGE;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             int off = ss * 16;   // u32 words: 64 bytes per super-stage
-            if (KTAIL && (ss * 128 + wp_piece[i] * 32) >= p.K) off = (p.K / 8) - 4 - wp_piece[i] * 4;
+            if (KTAIL && (ss * 128 + wp_piece[i] * 32) >= Kl) off = (Kl / 8) - 4 - wp_piece[i] * 4;
             __builtin_amdgcn_global_load_lds((const void*)(wp_src[i] + off),
                                              (lds_ptr_t)(stage + (wave + 8 * i) * 64), 16, 0, 0);
         }
@@ -264,7 +270,8 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int u = 0; u < GPMAX; ++u) {
             int g = ss * GP;
-            if (KTAIL && g + (sb_dst[u] % GP) >= p.groups) g = p.groups - 1 - (sb_dst[u] % GP);
+            const int groups_l = p.groups - ((2 * kb) >> p.gshift);
+            if (KTAIL && g + (sb_dst[u] % GP) >= groups_l) g = groups_l - 1 - (sb_dst[u] % GP);
             sbr[u] = sb_src[u][g];   // unused slots read an in-bounds element
         }
     };
@@ -284,7 +291,7 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
         const int gl = (tl * 2 + whalf) >> p.gshift;
         dq_s = lds_sb[ss & 1][0][vr * GP + gl];
         dq_b = lds_sb[ss & 1][1][vr * GP + gl];
-        if (KTAIL && t * BK + whalf * 32 >= p.K) {
+        if (KTAIL && t * BK + whalf * 32 >= Kl) {
             dq_s = 0;
             dq_b = 0;
         }
@@ -423,6 +430,18 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
         for (int v = 0; v < 16; ++v) {
             const int m = m0 + wm * (WM * 32) + i * 32 + 8 * (v >> 2) + 4 * lk + (v & 3);
             if (m >= p.M) continue;
+            if constexpr (SPLIT) {
+                // raw fp32 partial sums; the reduce kernel applies the epilogue
+                const size_t nw = SILU ? 2 * (size_t)p.N : (size_t)p.N;
+                float* wsr = p.ws + ((size_t)split * p.M + m) * nw;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int n = SILU ? n0 + wn * 32 + col_l : n0 + wn * 64 + j * 32 + col_l;
+                    if (n >= p.N) continue;
+                    wsr[SILU ? j * p.N + n : n] = acc[i][j][v];
+                }
+                continue;
+            }
             if (SILU) {
                 const int n = n0 + wn * 32 + col_l;
                 if (n >= p.N) continue;
@@ -442,57 +461,129 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
     }
 }
 
-// Block-tile height: the WM (BM = 64*WM) whose tile count fills the CUs in
-// the fewest rounds with the least padding, preferring taller tiles (less
-// dequantisation per MAC) when close.
-static int pick_wm(int M, int n_tiles) {
-    int best = 2;
+// Split-K reduction: out[m, n] = epilogue(sum over splits of the partials),
+// summed in split order (deterministic).  SILU reduces gate and up
+// separately before silu(gate) * up.
+template <bool SILU>
+__global__ __launch_bounds__(256) void q4_splitk_reduce_kernel(GemmParams p) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t total = (size_t)p.M * p.N;
+    if (idx >= total) return;
+    const size_t m = idx / p.N, n = idx % p.N;
+    const size_t nw = SILU ? 2 * (size_t)p.N : (size_t)p.N;
+    const size_t stride = (size_t)p.M * nw;
+    const float* src = p.ws + m * nw + n;
+    float a = 0.0f, u = 0.0f;
+    for (int s = 0; s < p.splits; ++s) {
+        a += src[s * stride];
+        if (SILU) u += src[s * stride + p.N];
+    }
+    float out;
+    if (SILU) {
+        out = silu_mul_f32(a, u);
+    } else {
+        out = a;
+        if (p.bias) out += p.bias[n];
+        if (p.epilogue == kEpiGeluTanh) out = gelu_tanh_f32(out);
+    }
+    store_out(p, idx, out);
+}
+
+// Launch plan: block-tile height WM (BM = 64*WM) and K splits.  Scores each
+// option by useful work over the CU-rounds it occupies (tiles x splits over
+// 256 CUs), prefers taller tiles (less dequantisation per MAC) and charges
+// each split a little for the partial-sum round trip.  Splits cover an even
+// number of k-tiles (the packed-weight stages move two k-tiles at a time).
+struct GemmPlan {
+    int wm, tiles_m, tiles_n, splits, split_tiles;
+    size_t ws_bytes;
+};
+
+static GemmPlan plan_gemm(const GemmParams& p, bool allow_split) {
+    const bool silu = p.epilogue == kEpiSiluMul;
+    const int bn_out = silu ? BN / 2 : BN;
+    const int tiles_n = (p.N + bn_out - 1) / bn_out;
+    const int nk = (p.K + BK - 1) / BK;
+    GemmPlan best = {2, 0, tiles_n, 1, nk, 0};
     double best_score = -1.0;
     for (int wm = 2; wm <= 3; ++wm) {
         const int bm = 64 * wm;
-        const long tiles = (long)((M + bm - 1) / bm) * n_tiles;
-        const long rounds = (tiles + kCUs - 1) / kCUs;
-        const double util = (double)M * n_tiles / ((double)rounds * kCUs * bm);
-        const double score = util * (1.0 + 0.04 * (wm - 2));
-        if (score > best_score) {
-            best_score = score;
-            best = wm;
+        const long tiles_m = (p.M + bm - 1) / bm;
+        const long tiles = tiles_m * tiles_n;
+        const int smax = allow_split ? 8 : 1;
+        for (int s = 1; s <= smax; ++s) {
+            if (s > 1 && nk < 8 * s) break;
+            int chunk = (nk + s - 1) / s;
+            chunk = s > 1 ? (chunk + 1) / 2 * 2 : chunk;
+            const int s_eff = (nk + chunk - 1) / chunk;
+            if (s > 1 && s_eff != s) continue;
+            const long blocks = tiles * s_eff;
+            const long rounds = (blocks + kCUs - 1) / kCUs;
+            const double util = ((double)p.M * tiles_n * nk) /
+                                ((double)rounds * kCUs * bm * chunk);
+            const double score = util * (1.0 + 0.04 * (wm - 2)) * (s > 1 ? 1.0 - 0.02 * s : 1.0);
+            if (score > best_score) {
+                best_score = score;
+                const size_t nw = silu ? 2 * (size_t)p.N : (size_t)p.N;
+                best = {wm, (int)tiles_m, tiles_n, s_eff, chunk,
+                        s_eff > 1 ? (size_t)s_eff * p.M * nw * sizeof(float) : 0};
+            }
         }
     }
     return best;
 }
 
-template <int WM, bool BF16>
+size_t gemm_workspace_bytes(const GemmParams& p) { return plan_gemm(p, true).ws_bytes; }
+
+template <int WM, bool BF16, bool SPLIT>
 static void launch_wm(const GemmParams& p, bool silu, long grid, hipStream_t st) {
     // Packed W and scales move in 128-k super-stages: K % 128 != 0 needs the
     // tail handling (clamped sources, zeroed dequant past K).
     const bool ktail = p.K % (2 * BK) != 0;
     if (silu && ktail)
-        hipLaunchKernelGGL((q4_gemm_kernel<WM, BF16, true, true>), dim3(grid), dim3(kThreads), 0, st, p);
+        hipLaunchKernelGGL((q4_gemm_kernel<WM, BF16, true, true, SPLIT>), dim3(grid), dim3(kThreads), 0, st, p);
     else if (silu)
-        hipLaunchKernelGGL((q4_gemm_kernel<WM, BF16, true, false>), dim3(grid), dim3(kThreads), 0, st, p);
+        hipLaunchKernelGGL((q4_gemm_kernel<WM, BF16, true, false, SPLIT>), dim3(grid), dim3(kThreads), 0, st, p);
     else if (ktail)
-        hipLaunchKernelGGL((q4_gemm_kernel<WM, BF16, false, true>), dim3(grid), dim3(kThreads), 0, st, p);
+        hipLaunchKernelGGL((q4_gemm_kernel<WM, BF16, false, true, SPLIT>), dim3(grid), dim3(kThreads), 0, st, p);
     else
-        hipLaunchKernelGGL((q4_gemm_kernel<WM, BF16, false, false>), dim3(grid), dim3(kThreads), 0, st, p);
+        hipLaunchKernelGGL((q4_gemm_kernel<WM, BF16, false, false, SPLIT>), dim3(grid), dim3(kThreads), 0, st, p);
+}
+
+template <bool SPLIT>
+static void launch_dtype(const GemmParams& p, bool a_bf16, bool silu, long grid, int wm,
+                         hipStream_t st) {
+    if (a_bf16) {
+        if (wm == 2) launch_wm<2, true, SPLIT>(p, silu, grid, st);
+        else launch_wm<3, true, SPLIT>(p, silu, grid, st);
+    } else {
+        if (wm == 2) launch_wm<2, false, SPLIT>(p, silu, grid, st);
+        else launch_wm<3, false, SPLIT>(p, silu, grid, st);
+    }
 }
 
 hipError_t launch_gemm(GemmParams p, bool a_bf16, hipStream_t st) {
     const bool silu = p.epilogue == kEpiSiluMul;
-    const int bn_out = silu ? BN / 2 : BN;
-    p.tiles_n = (p.N + bn_out - 1) / bn_out;
-    const int wm = pick_wm(p.M, p.tiles_n);
-    p.tiles_m = (p.M + 64 * wm - 1) / (64 * wm);
+    GemmPlan plan = plan_gemm(p, p.ws != nullptr);
+    p.tiles_m = plan.tiles_m;
+    p.tiles_n = plan.tiles_n;
+    p.splits = plan.splits;
+    p.split_tiles = plan.split_tiles;
     const long ntiles = (long)p.tiles_m * p.tiles_n;
     if (ntiles <= 0) return hipSuccess;
-    const long grid = (ntiles + 7) / 8 * 8;
+    const long blocks = ntiles * p.splits;
+    const long grid = (blocks + 7) / 8 * 8;
     if (grid > 0x7fffffffL) return hipErrorInvalidValue;
-    if (a_bf16) {
-        if (wm == 2) launch_wm<2, true>(p, silu, grid, st);
-        else launch_wm<3, true>(p, silu, grid, st);
+    if (p.splits > 1) {
+        launch_dtype<true>(p, a_bf16, silu, grid, plan.wm, st);
+        const size_t total = (size_t)p.M * p.N;
+        const long rgrid = (long)((total + 255) / 256);
+        if (silu)
+            hipLaunchKernelGGL(q4_splitk_reduce_kernel<true>, dim3(rgrid), dim3(256), 0, st, p);
+        else
+            hipLaunchKernelGGL(q4_splitk_reduce_kernel<false>, dim3(rgrid), dim3(256), 0, st, p);
     } else {
-        if (wm == 2) launch_wm<2, false>(p, silu, grid, st);
-        else launch_wm<3, false>(p, silu, grid, st);
+        launch_dtype<false>(p, a_bf16, silu, grid, plan.wm, st);
     }
     return hipGetLastError();
 }

@@ -40,9 +40,16 @@ struct GemmParams {
     int tiles_m, tiles_n;   // filled by launch_gemm
     int y_dtype;            // DType
     int epilogue;           // Epilogue
+    float* ws;              // split-K partials [splits][M][N or 2N] (null: no split)
+    int splits;             // filled by launch_gemm
+    int split_tiles;        // k-tiles per split (even), filled by launch_gemm
 };
 
 hipError_t launch_gemv(const GemvParams& p, bool swiglu, hipStream_t st);
+// Bytes of split-K workspace the launch of `p` would use (0: it does not split).
+size_t gemm_workspace_bytes(const GemmParams& p);
+// Launches the GEMM; splits K only if p.ws is non-null (and then needs
+// gemm_workspace_bytes(p) bytes there).
 hipError_t launch_gemm(GemmParams p, bool a_bf16, hipStream_t st);
 hipError_t launch_silu_mul(const uint16_t* a, const uint16_t* b, uint16_t* out, long count,
                            hipStream_t st);

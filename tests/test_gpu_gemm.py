@@ -235,3 +235,77 @@ def test_dit_ffn_m6144_bf16(pkg, dev):
     # second GEMM checked against the oracle on the kernel's own bf16 h
     ref = o.matmul_q4_f64(hk, host(wd), host(sd), host(bd), g)
     assert_parity(y.cpu().numpy()[rows], ref, TOL_GEMM_BF16, "dit down")
+
+
+# ---- split-K: few output tiles, long K (the kernel splits K and reduces the
+# fp32 partials in split order, then applies the epilogue) ----
+
+@pytest.mark.parametrize("M,N,K,xdt,epi,out", [
+    (40, 300, 4096, "f16", 2, "f16"),      # 2 tiles x 8 splits, bias + GELU
+    (130, 200, 8192, "bf16", 0, "f32"),    # bf16 activations, fp32 out
+    (7, 96, 2048, "f16", 0, "f16"),
+])
+def test_gemm_split_k(pkg, dev, M, N, K, xdt, epi, out):
+    import torch
+    g = 64
+    x, [(w, s, b)] = o.make_inputs(M, N, K, g, seed=M + K, x_dtype=xdt)
+    bias = (np.random.default_rng(3).standard_normal(N) * 0.5).astype(np.float32)
+    pre = o.matmul_q4_f64(o.x_values(x, xdt), w, s, b, g) + bias
+    ref = o.gelu_tanh_f64(pre) if epi == 2 else pre
+    tx = to_dev(x, dev)
+    if xdt == "bf16":
+        tx = tx.view(torch.bfloat16)
+    odt = {"f16": torch.float16, "f32": torch.float32}[out]
+    qw = q4w(pkg, w, s, b, K, g, dev)
+    y = pkg.matmul_q4_ex(tx, qw, M, N, out_dtype=odt, bias=to_dev(bias, dev), epilogue=epi)
+    y2 = pkg.matmul_q4_ex(tx, qw, M, N, out_dtype=odt, bias=to_dev(bias, dev), epilogue=epi)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)  # the split reduction is ordered: deterministic
+    y = y.float().cpu().numpy()
+    rms = float(np.sqrt(np.mean(pre * pre)))
+    tol_w = 1.2e-2 if xdt == "bf16" else 3e-3
+    tol_o = {"f16": 1e-3, "f32": 1e-5}[out]
+    allow = tol_o * np.abs(ref) + tol_w * rms
+    assert np.all(np.abs(y - ref) <= allow), float(np.max(np.abs(y - ref) / allow))
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 256, 4096), (3, 128, 8192)])
+def test_swiglu_gemm_split_k(pkg, dev, M, N, K):
+    import torch
+    g = 64
+    x, [(wg, sg, bg), (wu, su, bu)] = o.make_inputs(M, N, K, g, seed=N + K, n_weights=2)
+    ref = o.silu_mul_f64(o.matmul_q4_f64(x, wg, sg, bg, g), o.matmul_q4_f64(x, wu, su, bu, g))
+    y = pkg.matmul_q4_silu_mul(to_dev(x, dev), q4w(pkg, wg, sg, bg, K, g, dev),
+                               q4w(pkg, wu, su, bu, K, g, dev), M, K, N)
+    torch.cuda.synchronize()
+    assert_parity(y.cpu().numpy(), ref, TOL_GEMM_F16, f"swiglu split M={M}")
+
+
+def test_split_k_under_graph_capture(pkg, dev):
+    """A split-K GEMM captured in a graph (workspace allocated by an eager call
+    first) replays to the eager result; a fresh stream captured cold runs
+    unsplit and still matches."""
+    import torch
+    M, N, K, g = 16, 256, 4096, 64
+    x, [(w, s, b)] = o.make_inputs(M, N, K, g, seed=12)
+    tx, qw = to_dev(x, dev), q4w(pkg, w, s, b, K, g, dev)
+    ref = pkg.matmul_q4_fast_f32(tx, qw.weight, qw.scales, qw.biases, M, K, N, g)
+    torch.cuda.synchronize()
+    for warm in (True, False):
+        out = torch.empty(M, N, device=dev, dtype=torch.float32)
+        st = torch.cuda.Stream()
+        if warm:
+            with torch.cuda.stream(st):
+                pkg.matmul_q4_fast_f32(tx, qw.weight, qw.scales, qw.biases, M, K, N, g, out=out,
+                                       stream=st)
+            st.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=st):
+            pkg.matmul_q4_fast_f32(tx, qw.weight, qw.scales, qw.biases, M, K, N, g, out=out)
+        for _ in range(3):
+            out.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            ok, worst = o.elementwise_ok(out.cpu().numpy(), ref.cpu().numpy().astype(np.float64),
+                                         rtol=1e-5, atol_rms=1e-5)
+            assert ok, (warm, worst)
