@@ -272,11 +272,17 @@ def gemm_legs(pkg, torch, gen, dev):
     over a graph of R launches bracketed by events."""
     res = {}
 
+    # the library keeps its split-K workspace per stream and never allocates
+    # while a stream is being captured: warm up on the stream the graph is
+    # captured on
+    cap = torch.cuda.Stream()
+
     def timed(fn, flops=None, nbytes=None, reps=20):
-        fn()
+        with torch.cuda.stream(cap):
+            fn()
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
+        with torch.cuda.graph(g, stream=cap):
             for _ in range(reps):
                 fn()
         g.replay()

@@ -16,11 +16,13 @@
  *   - Memory: the only device memory the library allocates is a split-K
  *     workspace (fp32 partial sums) for GEMMs with too few output tiles to
  *     fill the GPU (e.g. M=750 x N=3072).  There is one per (device, stream),
- *     grown on first need (growing frees the old buffer, which waits for the
- *     device) and kept until the process exits.  A stream being captured into
- *     a HIP graph never allocates: if its workspace is missing or too small,
+ *     grown on first need to at least twice its old size; a replaced buffer
+ *     is never freed (a graph captured earlier may still use it), so every
+ *     buffer lives until the process exits.  A stream being captured into a
+ *     HIP graph never allocates: if its workspace is missing or too small,
  *     that GEMM runs unsplit (same results, lower throughput).  Capture after
- *     one eager call on the same stream to get the split kernel into a graph.
+ *     one eager call on the same stream to get the split kernel into a graph
+ *     (with torch, pass that stream to torch.cuda.graph(..., stream=s)).
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = the default stream) and
  *     nothing synchronises: results are visible to later work on that stream.
  *     This mirrors the reference's batched mode (MetalContext.swift:109-134).

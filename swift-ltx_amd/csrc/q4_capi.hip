@@ -1,10 +1,12 @@
 // q4_capi.hip -- the C ABI (include/swiftltx_q4.h): argument validation,
 // routing and launch of the gfx950 kernels.  Validation runs before any HIP
 // call, so error paths behave the same with or without a GPU.
+#include <algorithm>
 #include <cstdarg>
 #include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
 #include <string>
 #include <cstdio>
 #include <cstring>
@@ -14,12 +16,6 @@
 #include "swiftltx_q4.h"
 
 namespace sltx {
-
-
-
-
-
-
 namespace {
 
 thread_local std::string g_last_error;
@@ -109,12 +105,14 @@ int run_gemv(const char* fn, const void* x, const sltx_q4_weight& w0, const sltx
 
 // Split-K workspace, one per (device, stream): calls on one stream are
 // ordered, so they can share it; other streams get their own.  It grows on
-// demand (the old buffer is freed first, which waits for the device) and is
-// kept until the process ends.  A stream that is being captured into a graph
-// never allocates: if its workspace is missing or too small the GEMM runs
-// unsplit.
+// demand to at least twice its old size.  A replaced buffer is never freed:
+// graphs captured earlier may still name it, so it is kept (with the current
+// one) until the process ends; doubling bounds the retired total by the
+// current size.  A stream that is being captured into a graph never
+// allocates: if its workspace is missing or too small the GEMM runs unsplit.
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> g_ws;
+std::vector<void*> g_ws_retired;
 
 float* splitk_workspace(hipStream_t st, size_t need) {
     int dev = 0;
@@ -125,16 +123,13 @@ float* splitk_workspace(hipStream_t st, size_t need) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
         return nullptr;
-    if (e.first) {
-        if (hipFree(e.first) != hipSuccess) return nullptr;
-        e = {nullptr, 0};
-    }
     void* ptr = nullptr;
-    const size_t bytes = need + need / 4;
+    const size_t bytes = std::max(need + need / 4, 2 * e.second);
     if (hipMalloc(&ptr, bytes) != hipSuccess) {
         (void)hipGetLastError();
         return nullptr;
     }
+    if (e.first) g_ws_retired.push_back(e.first);
     e = {ptr, bytes};
     return static_cast<float*>(ptr);
 }

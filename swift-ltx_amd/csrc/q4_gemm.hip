@@ -8,30 +8,41 @@
 // (LlamaModel.swift:275-277); the bias + GELU-tanh epilogue covers
 // DiTLinear.applyF32in + geluApproximateF32 (DiTModel.swift:102-125, :953).
 //
-// Block: 512 threads = 8 waves in a 2 (M) x 4 (N) layout; block tile
-// BM x 256 x 64 with BM = 64*WM (WM = 2 or 3), each wave computing
-// (32*WM) x 64 with v_mfma_f32_32x32x16_{f16,bf16} (WM x 2 accumulator tiles).
-//  * A tile (BM x 64, fp16 or bf16) is copied global -> LDS directly
-//    (global_load_lds_dwordx4) into a 3-stage ring, two tiles ahead.
-//  * W tile (256 rows x 64 nibbles = 32 B per row) is loaded one 16-byte
-//    chunk per thread, dequantized in registers to fp16 (or bf16) with its
-//    group's scale and bias, and written to LDS: dequantized once per block
-//    and shared by both M-waves.  fp16: nibbles are spread to bytes, paired
-//    with v_perm_b32, turned into 1024+q by mantissa insertion, reduced to q
-//    exactly, then one fp16 FMA q*s+b (a single rounding).  bf16: q*s+b in
-//    fp32, rounded once to bf16.
-//  * LDS rows are 128 bytes with an XOR swizzle of the 16-byte columns (see
-//    swz) that keeps the MFMA operand reads and the tile stores free of bank
-//    conflicts.
-//  * W goes through two staging register sets: tile k+2 is loaded while
-//    tile k is multiplied, and tile k+1 (loaded one iteration earlier) is
-//    dequantized into the other of two W stages between the k-steps of tile
-//    k's MFMAs; one barrier per k-tile.
+// Block: 512 threads = 8 waves, two per SIMD.  The block tile is BM x 256 x 64
+// (BM = 64*WM activation rows, 256 weight rows); wave w owns weight rows
+// 32w..32w+31 and all BM activation rows, i.e. BM/32 tiles of
+// v_mfma_f32_32x32x16_{f16,bf16} along M.  No weight row is dequantized
+// twice, and each dequantized B fragment feeds BM/32 MFMAs.  Two waves per
+// SIMD let one wave's dequantization and LDS reads issue while the other's
+// MFMAs occupy the matrix core (an MFMA blocks its own wave's issue for about
+// half of its 32 cycles).
+//  * The B operand never passes through LDS as fp16.  In a 32x32x16 MFMA lane
+//    l supplies 8 consecutive k of column l%32.  Inside each 64-wide k-tile, k
+//    is permuted so that k-step s of lane half h covers 8-nibble word 4h+s of
+//    the row: over a k-tile a lane reads one aligned 16-byte piece of its row,
+//    and each k-step's B fragment is exactly one packed word, dequantized in
+//    registers just before use (v_perm_b32 byte pairing, mantissa insertion,
+//    one v_pk_fma_f16 q*s+b per pair).  The A fragments follow the same
+//    permutation by reading 16-byte column 4h+s of the A tile.
+//  * Packed W (256 rows x 64 B per pair of k-tiles) and the per-group
+//    (scale, bias) pairs are staged through LDS with coalesced loads (four
+//    lanes per 64-byte row segment), so no lane gathers 16 bytes per row.
+//  * A (BM x 64 fp16/bf16 per k-tile) is copied global -> LDS directly
+//    (global_load_lds_dwordx4) into a 4-stage ring, three k-tiles ahead.
+//  * LDS rows are 128 bytes with an XOR swizzle of the 16-byte columns (swz):
+//    the A fragment reads (16 consecutive rows, one logical column) and the
+//    copies are free of bank conflicts.
+//  * SILU pairs gate and up rows of the same output columns in waves 2c and
+//    2c+1; the up tile is handed to the gate wave through LDS at the end.
+//  * One barrier per k-tile.  Everything the next tile's first k-step needs
+//    (its A fragments, its packed words and scale/bias) is already visible
+//    before that barrier, so it is read during the last k-step of the current
+//    tile and the MFMA stream does not drain at tile boundaries.
 //  * Tile order is XCD-aware: the 8 XCDs receive workgroups round-robin, so
-//    consecutive logical tiles (M fastest) are mapped to one XCD so that the
+//    consecutive logical tiles (M fastest) are mapped to one XCD and the
 //    M-blocks sharing a weight column block share that XCD's L2.
-//  * BM is chosen per launch so the tile count fills the 256 CUs in whole
-//    rounds (M = 750: BM = 192 gives 4 x 64 = 256 tiles for gate/up).
+//  * Shapes with too few output tiles to fill 256 CUs split K; partial sums
+//    go to an fp32 workspace and a second kernel adds them in split order.
 #include <type_traits>
 
 #include "q4_common.hpp"
@@ -40,15 +51,18 @@
 namespace sltx {
 
 constexpr int BN = 256, BK = 64;
-constexpr int kThreads = 512;
+constexpr int NW = 8;                  // waves per block (two per SIMD)
+constexpr int kThreads = 64 * NW;
+constexpr int NT = BN / 32 / NW;       // 32-row weight tiles (MFMA N-tiles) per wave
 constexpr int kCUs = 256;
+constexpr int NSA = 4;     // A stages in LDS
+constexpr int GPMAX = 4;   // scale/bias groups per row per 128 k (group size 32)
 
 // LDS layout of a 64-wide k-tile: 128-byte rows of eight 16-byte columns.
 // Logical column c of row r sits at physical column c ^ (r & 7) ^ ((r >> 3) & 1).
-// A ds_read_b128 is served 16 lanes at a time by 64 4-byte banks (256 B): the
-// MFMA operand reads (16 consecutive rows, one logical column) and the tile
-// stores then hit 16 distinct (row parity, column) slots, i.e. no bank
-// conflicts; any 8 consecutive rows also land in 8 distinct columns.
+// A ds_read_b128 is served 16 lanes at a time by 64 4-byte banks (256 B): 16
+// consecutive rows reading one logical column hit 16 distinct (row parity,
+// column) slots, i.e. no bank conflicts.
 __device__ __forceinline__ int swz(int row, int col16) {
     return row * 8 + (col16 ^ (row & 7) ^ ((row >> 3) & 1));
 }
@@ -118,18 +132,61 @@ __device__ __forceinline__ void store_out(const GemmParams& p, size_t o, float v
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-template <int WM, bool BF16, bool SILU, bool KTAIL, bool SPLIT>
+// Workgroup barrier for LDS hand-offs only.  __syncthreads() adds a
+// workgroup release fence, which on gfx950 waits for every outstanding
+// vector-memory op (vmcnt(0)), including the direct-to-LDS copies issued for
+// k-tiles still three steps ahead.  Here each wave waits for its own LDS ops
+// (lgkmcnt(0)); the copies a barrier must cover are waited for explicitly
+// with SLTX_WAIT_VMCNT before it.  The memory clobber keeps the compiler from
+// moving memory accesses across the barrier.
+#define SLTX_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+
+// Scale and bias of one (row, group), packed as fp16 bits scale | bias << 16.
+struct SB {
+    uint32_t v[NT];
+};
+
+// GEN = false: K % 128 == 0 and group size 64; every load is a direct-to-LDS
+// copy with a fixed count per k-tile and exact wait counts.  GEN = true: any
+// supported shape (K % 32 == 0, group 32/64/128): scale/bias staged through
+// registers, clamped tails, zero-filled A past K, full waits.
+template <int WM, bool BF16, bool SILU, bool GEN, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
     constexpr int BM = 64 * WM;
-    constexpr int NSA = WM == 2 ? 3 : 2;       // A stages (LDS budget)
+    constexpr int TM = BM / 32;                // MFMA tiles along M per wave
     constexpr int A_STAGE = BM * BK / 8;       // 16-byte slots per A stage
-    constexpr int W16_STAGE = BN * BK / 8;     // dequantized W, one k-tile
-    constexpr int WP_STAGE = BN * 4;           // packed W, two k-tiles (64 B per row)
-    constexpr int GPMAX = 4;                   // scale/bias groups per row per super-stage
-    __shared__ u32x4 lds_a[NSA * A_STAGE];     // swizzled [row][col16]
-    __shared__ u32x4 lds_w16[2 * W16_STAGE];   // swizzled [row][col16]
-    __shared__ u32x4 lds_wp[2 * WP_STAGE];     // swizzled [row][piece]
-    __shared__ uint16_t lds_sb[2][2][BN * GPMAX];   // [stage][scale|bias][row * GP + g]
+    constexpr int NA = A_STAGE / kThreads;     // A copies per thread per k-tile
+    constexpr int WP_STAGE = BN * 4;           // packed W of two k-tiles: 64 B per row
+    constexpr int NWP = WP_STAGE / kThreads;   // packed-W copies per thread per super-stage
+    constexpr int NPAIR = BN * GPMAX / kThreads;   // GEN: (row, group) pairs per thread per super-stage
+    constexpr int NSB = BN * 2 / kThreads;         // fast path: scale/bias copies per thread per super-stage
+    // Each stage is its own array: the compiler then knows that reads of one
+    // stage do not alias a direct-to-LDS copy in flight into another, and
+    // does not wait for that copy (stage indices are compile-time below).
+    __shared__ u32x4 lds_a0[A_STAGE], lds_a1[A_STAGE], lds_a2[A_STAGE], lds_a3[A_STAGE];
+    __shared__ u32x4 lds_wp0[WP_STAGE], lds_wp1[WP_STAGE];   // [row][piece ^ ((row >> 2) & 3)]
+    // Scale/bias.  Fast path (group 64): per super-stage and row one dword of
+    // the two groups' scales and one of their biases, [row][scales, biases],
+    // copied direct to LDS.  Generic path: [row * GP + group] = scale | bias
+    // << 16, staged through registers.
+    __shared__ uint32_t lds_sb0[GEN ? BN * GPMAX : BN * 2], lds_sb1[GEN ? BN * GPMAX : BN * 2];
+    static_assert(NSA == 4, "stage arrays");
+    // A stage of k-tile t is t % 4, packed-W stage of super-stage ss is ss % 2.
+    auto a_stage = [&](auto sc) -> u32x4* {
+        constexpr int S = decltype(sc)::value & 3;
+        if constexpr (S == 0) return lds_a0;
+        else if constexpr (S == 1) return lds_a1;
+        else if constexpr (S == 2) return lds_a2;
+        else return lds_a3;
+    };
+    auto wp_stage = [&](auto sc) -> u32x4* {
+        if constexpr ((decltype(sc)::value & 1) == 0) return lds_wp0;
+        else return lds_wp1;
+    };
+    auto sb_stage = [&](auto sc) -> uint32_t* {
+        if constexpr ((decltype(sc)::value & 1) == 0) return lds_sb0;
+        else return lds_sb1;
+    };
 
     // ---- tile selection (XCD-aware) ----
     const int ntiles = p.tiles_m * p.tiles_n;
@@ -148,17 +205,20 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
     const int kb = SPLIT ? split * p.split_tiles : 0;
     const int nk = SPLIT ? min(p.split_tiles, nk_all - kb) : nk_all;
     const int Kl = min(p.K - kb * BK, nk * BK);
+    const int nss = (nk + 1) / 2;   // super-stages (pairs of k-tiles)
     const int m0 = tile_m * BM;
     // SILU: a tile covers 128 output columns, as 128 gate rows + 128 up rows.
     const int n0 = tile_n * (SILU ? BN / 2 : BN);
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave & 1, wn = wave >> 1;
+    const int lane = tid & 63, wn = tid >> 6;
+    const int lrow = lane & 31, h = lane >> 5;
     const int GP = 4 >> p.gshift;   // scale/bias groups per 128 k (g = 32, 64, 128)
 
-    // Virtual W row -> matrix row (and which matrix, for SILU).  Rows past N
-    // are clamped to row 0: computed, never stored.
+    // Virtual W row -> matrix row (and which matrix, for SILU).  Wave wn owns
+    // virtual rows 64wn..64wn+63 as two 32-row MFMA tiles; with SILU tile 0 is
+    // gate and tile 1 up for the same 32 output columns.  Rows past N are
+    // clamped to row 0: computed, never stored.
     auto wrow = [&](int v, const uint32_t*& W, const uint16_t*& S, const uint16_t*& B) {
         int n;
         if (SILU) {
@@ -177,16 +237,16 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
     };
 
     // ---- A: direct global -> LDS (global_load_lds_dwordx4) ----
-    // Each wave fills WM 1-KB pieces of a stage: piece i covers slots
-    // (wave + 8 i) * 64 .. +63, lane l landing in slot +l.  Slot s is physical
-    // column s % 8 of row s / 8, i.e. logical column (s % 8) ^ xor(row): the
-    // swizzle is applied on the global side.  Rows past M are clamped to M-1.
+    // Copy i of wave wn fills slots (wn + 4 i) * 64 .. +63, lane l landing in
+    // slot +l.  Slot s is physical column s % 8 of row s / 8, i.e. logical
+    // column (s % 8) ^ xor(row): the swizzle is applied on the global side.
+    // Rows past M are clamped to M-1.
     const uint16_t* A = reinterpret_cast<const uint16_t*>(p.a);
-    const uint16_t* a_src[WM];
-    int a_col8[WM];
+    const uint16_t* a_src[NA];
+    int a_col8[NA];
 #pragma unroll
-    for (int i = 0; i < WM; ++i) {
-        const int slot = (wave + 8 * i) * 64 + lane;
+    for (int i = 0; i < NA; ++i) {
+        const int slot = (wn + NW * i) * 64 + lane;
         const int row = slot >> 3;
         const int c16 = (slot & 7) ^ (row & 7) ^ ((row >> 3) & 1);
         const int m = m0 + row;
@@ -198,11 +258,11 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
     // Four lanes cover a row's 64 bytes, so each wave-wide copy reads 16 rows
     // of 64 contiguous bytes.  Slot s is row s / 4, physical piece s % 4 =
     // logical piece ^ ((row >> 2) & 3) (conflict-free reads below).
-    const uint32_t* wp_src[2];
-    int wp_piece[2];
+    const uint32_t* wp_src[NWP];
+    int wp_piece[NWP];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int slot = (wave + 8 * i) * 64 + lane;
+    for (int i = 0; i < NWP; ++i) {
+        const int slot = (wn + NW * i) * 64 + lane;
         const int row = slot >> 2;
         const int piece = (slot & 3) ^ ((row >> 2) & 3);
         const uint32_t* W;
@@ -212,244 +272,360 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
         wp_src[i] = W + (size_t)n * (p.K / 8) + kb * (BK / 8) + piece * 4;
     }
 
-    // ---- scales / biases: GP groups per row per super-stage ----
-    // Threads 0-255 load scales, 256-511 biases; consecutive threads read
-    // consecutive groups of a row.  Values land in registers and are written
-    // to LDS one k-tile later.
-    const int sb_arr = tid >> 8;
-    const uint16_t* sb_src[GPMAX];
-    int sb_dst[GPMAX];
+    // ---- scale / bias ----
+    const int g_base = (2 * kb) >> p.gshift;
+    // Fast path: copy i of wave wn fills dwords (wn + 4 i) * 64 + lane of the
+    // stage, i.e. row slot / 2, scales (even slot) or biases (odd slot); the
+    // source is the dword holding groups 2 ss and 2 ss + 1 of that row (4-byte
+    // aligned: groups and g_base are even when K % 128 == 0 and splits cover
+    // whole super-stages).
+    const uint32_t* sbd_src[NSB];
 #pragma unroll
-    for (int u = 0; u < GPMAX; ++u) {
-        const int v = (tid & 255) + 256 * u;
+    for (int i = 0; i < NSB; ++i) {
+        const int slot = (wn + NW * i) * 64 + lane;
+        const uint32_t* W;
+        const uint16_t *S, *B;
+        const int n = wrow(slot >> 1, W, S, B);
+        sbd_src[i] = reinterpret_cast<const uint32_t*>((slot & 1 ? B : S) + (size_t)n * p.groups + g_base);
+    }
+    // Generic path: pair v = tid + 256 u is (row v / GP, group v % GP).
+    // Consecutive threads read consecutive groups of a row.  Values land in
+    // registers and are written to LDS one k-tile later; pairs past the tile
+    // (v >= 256 GP) read row 0 and land in unused LDS slots.
+    const uint16_t* s_src[NPAIR];
+    const uint16_t* b_src[NPAIR];
+    int sb_g[NPAIR];
+#pragma unroll
+    for (int u = 0; u < NPAIR; ++u) {
+        const int v = tid + kThreads * u;
         const int row = v / GP, g = v % GP;
         const uint32_t* W;
         const uint16_t *S, *B;
         const int n = wrow(row < BN ? row : 0, W, S, B);
-        sb_src[u] = (sb_arr ? B : S) + (size_t)n * p.groups + ((2 * kb) >> p.gshift) + g;
-        sb_dst[u] = v;
+        s_src[u] = S + (size_t)n * p.groups + g_base + g;
+        b_src[u] = B + (size_t)n * p.groups + g_base + g;
+        sb_g[u] = g;
     }
 
-    // ---- dequant assignment: virtual row vr, half whalf (wave-uniform) ----
-    const int vr = tid & 255, whalf = tid >> 8;
-
-    const int nss = (nk + 1) / 2;   // super-stages
-
-    auto load_a = [&](int kt) {   // WM vector-memory ops
-        const int k0 = kt * BK;
-        u32x4* stage = lds_a + (kt % NSA) * A_STAGE;
+    // load_a / zero_a_tail / fetch_w take the tile index t with its value mod
+    // 4 as a compile-time constant TP; load_wp / store_sb take the super-stage
+    // with its parity.
+    auto load_a = [&](auto tp, int t) {   // NA vector-memory ops (tiles past the end re-read the last)
+        const int k0 = min(t, nk - 1) * BK;
+        u32x4* stage = a_stage(tp);
 #pragma unroll
-        for (int i = 0; i < WM; ++i) {
+        for (int i = 0; i < NA; ++i) {
             int off = k0;
-            if (KTAIL && k0 + a_col8[i] >= Kl) off = Kl - 8 - a_col8[i];
+            if (GEN && k0 + a_col8[i] >= Kl) off = Kl - 8 - a_col8[i];
             __builtin_amdgcn_global_load_lds((const void*)(a_src[i] + off),
-                                             (lds_ptr_t)(stage + (wave + 8 * i) * 64), 16, 0, 0);
+                                             (lds_ptr_t)(stage + (wn + NW * i) * 64), 16, 0, 0);
         }
     };
-    auto zero_a_tail = [&](int kt) {   // after the copy for tile kt landed
-        const int k0 = kt * BK;
-        if (!KTAIL || k0 + BK <= Kl) return;
-        u32x4* stage = lds_a + (kt % NSA) * A_STAGE;
+    auto zero_a_tail = [&](auto tp, int t) {   // GEN: after the copy of tile t landed
+        const int k0 = t * BK;
+        if (t >= nk || k0 + BK <= Kl) return;
+        u32x4* stage = a_stage(tp);
         const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int i = 0; i < WM; ++i)
-            if (k0 + a_col8[i] >= Kl) stage[(wave + 8 * i) * 64 + lane] = z;
+        for (int i = 0; i < NA; ++i)
+            if (k0 + a_col8[i] >= Kl) stage[(wn + NW * i) * 64 + lane] = z;
     };
-    auto load_wp = [&](int ss) {   // 2 vector-memory ops
-        u32x4* stage = lds_wp + (ss & 1) * WP_STAGE;
+    auto load_wp = [&](auto sp, int ss) {   // NWP vector-memory ops
+        const int sc = min(ss, nss - 1);
+        u32x4* stage = wp_stage(sp);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            int off = ss * 16;   // u32 words: 64 bytes per super-stage
-            if (KTAIL && (ss * 128 + wp_piece[i] * 32) >= Kl) off = (Kl / 8) - 4 - wp_piece[i] * 4;
+        for (int i = 0; i < NWP; ++i) {
+            int off = sc * 16;   // u32 words: 64 bytes per super-stage
+            if (GEN && sc * 128 + wp_piece[i] * 32 >= Kl) off = (Kl / 8) - 4 - wp_piece[i] * 4;
             __builtin_amdgcn_global_load_lds((const void*)(wp_src[i] + off),
-                                             (lds_ptr_t)(stage + (wave + 8 * i) * 64), 16, 0, 0);
+                                             (lds_ptr_t)(stage + (wn + NW * i) * 64), 16, 0, 0);
         }
     };
-    uint32_t sbr[GPMAX];
-    auto load_sb = [&](int ss) {   // GPMAX vector-memory ops (the first GP are used)
+    auto load_sb_dma = [&](auto sp, int ss) {   // fast path: NSB vector-memory ops
+        const int sc = min(ss, nss - 1);
+        uint32_t* stage = sb_stage(sp);
 #pragma unroll
-        for (int u = 0; u < GPMAX; ++u) {
-            int g = ss * GP;
-            const int groups_l = p.groups - ((2 * kb) >> p.gshift);
-            if (KTAIL && g + (sb_dst[u] % GP) >= groups_l) g = groups_l - 1 - (sb_dst[u] % GP);
-            sbr[u] = sb_src[u][g];   // unused slots read an in-bounds element
-        }
+        for (int i = 0; i < NSB; ++i)
+            __builtin_amdgcn_global_load_lds((const void*)(sbd_src[i] + sc),
+                                             (lds_ptr_t)(stage + (wn + NW * i) * 64), 4, 0, 0);
     };
-    auto store_sb = [&](int ss) {
+    uint32_t s_reg[NPAIR], b_reg[NPAIR];
+    auto load_sb = [&](int ss) {   // generic path: 2 NPAIR vector-memory ops
+        const int sc = min(ss, nss - 1);
+        const int groups_l = p.groups - g_base;
 #pragma unroll
-        for (int u = 0; u < GPMAX; ++u)
-            if (u < GP) lds_sb[ss & 1][sb_arr][sb_dst[u]] = (uint16_t)sbr[u];
-    };
-    // Dequantize word j of this thread's 32 nibbles of tile t (packed stage ->
-    // W16 stage t & 1).
-    u32x4 wpk;
-    uint16_t dq_s, dq_b;
-    auto fetch_dq = [&](int t) {
-        const int tl = t & 1, ss = t >> 1;
-        const int piece = tl * 2 + whalf;
-        wpk = lds_wp[(ss & 1) * WP_STAGE + vr * 4 + (piece ^ ((vr >> 2) & 3))];
-        const int gl = (tl * 2 + whalf) >> p.gshift;
-        dq_s = lds_sb[ss & 1][0][vr * GP + gl];
-        dq_b = lds_sb[ss & 1][1][vr * GP + gl];
-        if (KTAIL && t * BK + whalf * 32 >= Kl) {
-            dq_s = 0;
-            dq_b = 0;
+        for (int u = 0; u < NPAIR; ++u) {
+            int g = sc * GP;
+            if (GEN && g + sb_g[u] >= groups_l) g = groups_l - 1 - sb_g[u];
+            s_reg[u] = s_src[u][g];
+            b_reg[u] = b_src[u][g];
         }
     };
-    auto store_w = [&](int t, int j) {
-        u32x4 o;
-        if constexpr (BF16) {
-            o = dequant_word_bf16(wpk[j], h2f(dq_s), h2f(dq_b));
-        } else {
-            const f16 sh = __builtin_bit_cast(f16, dq_s), bh = __builtin_bit_cast(f16, dq_b);
-            const f16x2 s2 = {sh, sh}, b2 = {bh, bh};
-            o = dequant_word_f16(wpk[j], s2, b2);
-        }
-        lds_w16[(t & 1) * W16_STAGE + swz(vr, whalf * 4 + j)] = o;
+    auto store_sb = [&](auto sp) {
+        uint32_t* stage = sb_stage(sp);
+#pragma unroll
+        for (int u = 0; u < NPAIR; ++u)
+            stage[tid + kThreads * u] = (s_reg[u] & 0xFFFFu) | (b_reg[u] << 16);
     };
 
-    f32x16 acc[WM][2];
+    // Packed words (16 bytes: this lane's four k-steps) and scale|bias of
+    // tile t for both of the wave's 32-row MFMA tiles.
+    auto fetch_w = [&](auto tp, int t, u32x4 (&wk)[NT], SB& sb) {
+        constexpr int TP = decltype(tp)::value & 3;
+        constexpr int TL = TP & 1, SP = (TP >> 1) & 1;   // tile within / parity of super-stage
+        const u32x4* ws = wp_stage(std::integral_constant<int, SP>{});
+        const int piece = TL * 2 + h;
 #pragma unroll
-    for (int i = 0; i < WM; ++i)
+        for (int j = 0; j < NT; ++j) {
+            const int vr = wn * 32 * NT + j * 32 + lrow;
+            wk[j] = ws[vr * 4 + (piece ^ ((vr >> 2) & 3))];
+            uint32_t v;
+            if constexpr (GEN) {
+                v = sb_stage(std::integral_constant<int, SP>{})[vr * GP + (piece >> p.gshift)];
+            } else {
+                // group TL of the super-stage: half TL of the scale and bias dwords
+                const uint2 d = reinterpret_cast<const uint2*>(sb_stage(std::integral_constant<int, SP>{}))[vr];
+                v = __builtin_amdgcn_perm(d.y, d.x, TL ? 0x07060302u : 0x05040100u);
+            }
+            if (GEN && t * BK + h * 32 >= Kl) v = 0;   // k past K: w = 0
+            sb.v[j] = v;
+        }
+    };
+    // B fragment of k-step ks for MFMA tile j.
+    auto dequant = [&](const u32x4 (&wk)[NT], const SB& sb, int ks, u32x4 (&dst)[NT]) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < NT; ++j) {
+            const uint32_t v = sb.v[j];
+            if constexpr (BF16) {
+                dst[j] = dequant_word_bf16(wk[j][ks], h2f((uint16_t)(v & 0xFFFFu)),
+                                           h2f((uint16_t)(v >> 16)));
+            } else {
+                const f16x2 s2 = as_f16x2(__builtin_amdgcn_perm(v, v, 0x01000100u));
+                const f16x2 b2 = as_f16x2(__builtin_amdgcn_perm(v, v, 0x03020302u));
+                dst[j] = dequant_word_f16(wk[j][ks], s2, b2);
+            }
+        }
+    };
+    auto read_a = [&](const u32x4* sa, int ks, u32x4 (&dst)[TM]) {
+        const int c16 = 4 * h + ks;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) dst[i] = sa[swz(i * 32 + lrow, c16)];
+    };
+
+    f32x16 acc[TM][NT];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    const int lrow = lane & 31, lk = lane >> 5;
-    const int arow0 = wm * (WM * 32) + lrow;
-    const int brow0 = wn * 64 + lrow;
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
 
-    // Prologue: super-stages 0 and 1 (k-tiles 0-3) and the first A tiles in
-    // flight; scales/biases of both super-stages to LDS; tile 0 dequantized.
-    load_sb(0);
-    load_wp(0);
-    if (nss > 1) load_wp(1);
-#pragma unroll
-    for (int t = 0; t < NSA - 1; ++t)
-        if (t < nk) load_a(t);
-    store_sb(0);   // waits for this thread's scale/bias loads
-    if (nss > 1) {
+    // Prologue: A tiles 0..2 and packed W / scale-bias of super-stages 0 and
+    // 1 in flight.  k-tile 0 needs A tiles 0 and 1 and super-stage 0 before
+    // it starts; A tile 2 and super-stage 1 (issued last) may still land
+    // during it (the wait at the end of k-tile 0 covers them).  Generic path:
+    // scale/bias of super-stage 0 to LDS, super-stage 1's stay in registers
+    // and are written at the end of k-tile 0.
+    if constexpr (GEN) {
+        load_a(I0{}, 0);
+        load_a(I1{}, 1);
+        load_a(I2{}, 2);
+        load_wp(I0{}, 0);
+        load_wp(I1{}, 1);
+        load_sb(0);
+        SLTX_WAIT_VMCNT(0);
+        store_sb(I0{});
         load_sb(1);
-        store_sb(1);
+        SLTX_WAIT_VMCNT(0);
+        zero_a_tail(I0{}, 0);
+        zero_a_tail(I1{}, 1);
+        zero_a_tail(I2{}, 2);
+    } else {
+        load_a(I0{}, 0);
+        load_a(I1{}, 1);
+        load_wp(I0{}, 0);
+        load_sb_dma(I0{}, 0);
+        load_a(I2{}, 2);
+        load_wp(I1{}, 1);
+        load_sb_dma(I1{}, 1);
+        SLTX_WAIT_VMCNT(NA + NWP + NSB);
     }
-    SLTX_WAIT_VMCNT(0);
-    zero_a_tail(0);
-    if (NSA > 2 && nk > 1) zero_a_tail(1);
-    __syncthreads();
-    fetch_dq(0);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) store_w(0, j);
-    __syncthreads();
+    SLTX_LDS_BARRIER();
 
-    // k-tile kt: MFMAs on A stage kt % NSA and W16 stage kt & 1; tile kt+1 is
-    // dequantized into the other W16 stage between the k-steps.  Loads issued
-    // during kt: A tile kt+NSA-1; for odd kt = 2j+1 also packed W and the
-    // scale/bias registers of super-stage j+2 (written to LDS during kt+1).
-    // ODD is compile-time (the loop is unrolled by two) so that each step is
-    // one branch-free block with a constant wait count.
-    auto step = [&](auto odd_c, int kt) {
-        constexpr bool ODD = decltype(odd_c)::value;
-        const bool a_more = kt + NSA - 1 < nk;
-        const bool dq_more = kt + 1 < nk;
-        const int ss_ld = (kt + 3) >> 1;
-        const bool w_more = ODD && ss_ld < nss;
-        if (a_more) load_a(kt + NSA - 1);
-        if (w_more) {
-            load_wp(ss_ld);
-            load_sb(ss_ld);
+    u32x4 wk_c[NT], wk_n[NT];
+    SB sb_c, sb_n;
+    u32x4 af[2][TM], bq[2][NT];
+    fetch_w(I0{}, 0, wk_c, sb_c);
+    read_a(a_stage(I0{}), 0, af[0]);
+    dequant(wk_c, sb_c, 0, bq[0]);
+
+    // k-tile kt (TP = kt % 4, compile-time): MFMAs on A stage TP with B
+    // dequantized from tile kt's packed words.  Issued during kt: A tile kt+3;
+    // for odd kt = 2j+1 the packed W and scale/bias registers of super-stage
+    // j+2 (the latter written to LDS at the end of k-tile kt+1).  The operands
+    // of tile kt+1's first k-step are formed during the last k-step.  Each
+    // tile is one branch-free block with a constant wait count.
+    auto step = [&](auto tp, int kt) {
+        constexpr int TP = decltype(tp)::value;
+        constexpr bool ODD = TP & 1;
+        using N1 = std::integral_constant<int, (TP + 1) & 3>;
+        using N3 = std::integral_constant<int, (TP + 3) & 3>;
+        load_a(N3{}, kt + NSA - 1);
+        if constexpr (ODD) {
+            // super-stage (kt+3)/2: parity ((TP+3) >> 1) & 1
+            load_wp(std::integral_constant<int, ((TP + 3) >> 1) & 1>{}, (kt + 3) >> 1);
+            if constexpr (GEN) load_sb((kt + 3) >> 1);
+            else load_sb_dma(std::integral_constant<int, ((TP + 3) >> 1) & 1>{}, (kt + 3) >> 1);
         }
-        if (!ODD && kt >= 2 && (kt >> 1) + 1 < nss) store_sb((kt >> 1) + 1);
-        if (dq_more) fetch_dq(kt + 1);
-        const u32x4* sa = lds_a + (kt % NSA) * A_STAGE;
-        const u32x4* sw = lds_w16 + (kt & 1) * W16_STAGE;
-        // Operand fragments are double-buffered: k-step ks+1's LDS reads are
-        // issued before k-step ks's MFMAs so their latency overlaps them.
-        u32x4 af[2][WM], bf[2][2];
-        auto ldfrag = [&](int ks, int b) {
-            const int c16 = ks * 2 + lk;
-#pragma unroll
-            for (int t = 0; t < WM; ++t) af[b][t] = sa[swz(arow0 + t * 32, c16)];
-#pragma unroll
-            for (int j = 0; j < 2; ++j) bf[b][j] = sw[swz(brow0 + j * 32, c16)];
-        };
-        ldfrag(0, 0);
+        const u32x4* sa = a_stage(tp);
+        const u32x4* sa_n = a_stage(N1{});
+        __builtin_amdgcn_sched_barrier(0);
+        // Each k-step: this step's MFMAs (operands read / dequantized during
+        // the previous step) with the next step's A fragment reads and B
+        // dequantization interleaved.  The first MFMA goes before any new LDS
+        // read: the compiler's wait for its operands then covers only reads
+        // issued a full k-step earlier (it cannot count LDS reads separately
+        // while direct-to-LDS copies are in flight, so every LDS wait it
+        // emits waits for all of them).  The scheduling-group barriers fix
+        // that order: 1 MFMA, then one read per MFMA, then MFMAs with three
+        // VALU ops each.  Step 0 also reads tile kt+1's packed words and
+        // scale/bias (used from step 3 on).
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ++ks) {
             const int b = ks & 1;
-            if (ks + 1 < BK / 16) ldfrag(ks + 1, b ^ 1);
 #pragma unroll
-            for (int i = 0; i < WM; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = mfma32<BF16>(af[b][i], bf[b][j], acc[i][j]);
-            if (dq_more) store_w(kt + 1, ks);
+                for (int j = 0; j < NT; ++j) acc[i][j] = mfma32<BF16>(af[b][i], bq[b][j], acc[i][j]);
+            if (ks + 1 < BK / 16) {
+                read_a(sa, ks + 1, af[b ^ 1]);
+                dequant(wk_c, sb_c, ks + 1, bq[b ^ 1]);
+            } else {
+                read_a(sa_n, 0, af[b ^ 1]);
+                dequant(wk_n, sb_n, 0, bq[b ^ 1]);
+            }
+            if (ks == 0) fetch_w(N1{}, kt + 1, wk_n, sb_n);
+            constexpr int NR0 = TM + 2 * NT;   // LDS reads in step 0
+            const int nr = ks == 0 ? NR0 : TM;
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);       // VALU
+#pragma unroll
+            for (int q = 1; q < NT * TM; ++q) {
+                if (q <= NR0 && q <= nr) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // VALU
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        // Before the barrier, A tile kt+1 and the packed W / scales that the
-        // next step dequantizes (super-stage (kt+2)/2) must have landed.
-        // vmcnt retires in issue order; the count allows exactly the loads
-        // that were issued after the last of those:
-        //  NSA 2: A tile kt+1 was issued first in this step; after it only
-        //         this step's W + scale/bias loads (odd steps).
-        //  NSA 3: odd step: A tile kt+1 was issued in the previous (even)
-        //         step, which issued nothing else; after it, this step's A and
-        //         W + scale/bias loads.  Even step: the previous (odd) step
-        //         issued W + scale/bias after its A, and those are needed next
-        //         step, so only this step's A loads may remain.
-        constexpr int NWSB = 2 + GPMAX;
-        if constexpr (NSA == 2) {
-            if (ODD && w_more) SLTX_WAIT_VMCNT(NWSB); else SLTX_WAIT_VMCNT(0);
+        // even kt: scale/bias of super-stage (kt+2)/2 (parity ((TP+2) >> 1) & 1)
+        if constexpr (GEN && !ODD) store_sb(std::integral_constant<int, ((TP + 2) >> 1) & 1>{});
+        // Before the barrier, A tile kt+2 and the packed W / scale-bias of
+        // tile kt+2 must have landed (they are read during k-tile kt+1).
+        // vmcnt retires in issue order.  Even kt issued only A tile kt+3;
+        // odd kt issued A tile kt+3 and super-stage (kt+3)/2 after A tile
+        // kt+2 (issued at kt-1, which issued nothing else).
+        if constexpr (GEN) {
+            SLTX_WAIT_VMCNT(0);
+            zero_a_tail(std::integral_constant<int, (TP + 2) & 3>{}, kt + 2);
         } else if constexpr (ODD) {
-            if (a_more && w_more) SLTX_WAIT_VMCNT(WM + NWSB);
-            else if (a_more) SLTX_WAIT_VMCNT(WM);
-            else if (w_more) SLTX_WAIT_VMCNT(NWSB);
-            else SLTX_WAIT_VMCNT(0);
+            SLTX_WAIT_VMCNT(NA + NWP + NSB);
         } else {
-            if (a_more) SLTX_WAIT_VMCNT(WM); else SLTX_WAIT_VMCNT(0);
+            SLTX_WAIT_VMCNT(NA);
         }
-        if (kt + 1 < nk) zero_a_tail(kt + 1);
-        __syncthreads();
+        SLTX_LDS_BARRIER();
+#pragma unroll
+        for (int j = 0; j < NT; ++j) wk_c[j] = wk_n[j];
+        sb_c = sb_n;
     };
-    using T_ = std::true_type;
-    using F_ = std::false_type;
 
     int kt = 0;
-    for (; kt + 1 < nk; kt += 2) {
-        step(F_{}, kt);
-        step(T_{}, kt + 1);
+    for (; kt + 3 < nk; kt += 4) {
+        step(I0{}, kt);
+        step(I1{}, kt + 1);
+        step(I2{}, kt + 2);
+        step(I3{}, kt + 3);
     }
-    if (kt < nk) step(F_{}, kt);
+    if (kt < nk) step(I0{}, kt);
+    if (kt + 1 < nk) step(I1{}, kt + 1);
+    if (kt + 2 < nk) step(I2{}, kt + 2);
 
     // ---- epilogue ----
     // 32x32 accumulator layout: lane l, element v -> row 8*(v/4) + 4*(l/32) + v%4,
-    // column l%32.
-    const int col_l = lane & 31;
+    // column l%32.  MFMA tile j of wave wn holds virtual weight rows vb..vb+31,
+    // vb = wn*32*NT + j*32: with SILU, matrix (vb >> 5) & 1 (gate 0, up 1) and
+    // output columns n0 + (vb >> 6)*32 + l%32.
+    auto out_col = [&](int j) {
+        const int vb = wn * 32 * NT + j * 32;
+        return SILU ? n0 + (vb >> 6) * 32 + lrow : n0 + vb + lrow;
+    };
+    if constexpr (SPLIT) {
+        // raw fp32 partial sums; the reduce kernel applies the epilogue
+        const size_t nw = SILU ? 2 * (size_t)p.N : (size_t)p.N;
 #pragma unroll
-    for (int i = 0; i < WM; ++i) {
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int m = m0 + wm * (WM * 32) + i * 32 + 8 * (v >> 2) + 4 * lk + (v & 3);
-            if (m >= p.M) continue;
-            if constexpr (SPLIT) {
-                // raw fp32 partial sums; the reduce kernel applies the epilogue
-                const size_t nw = SILU ? 2 * (size_t)p.N : (size_t)p.N;
+            for (int v = 0; v < 16; ++v) {
+                const int m = m0 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                if (m >= p.M) continue;
                 float* wsr = p.ws + ((size_t)split * p.M + m) * nw;
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int n = SILU ? n0 + wn * 32 + col_l : n0 + wn * 64 + j * 32 + col_l;
-                    if (n >= p.N) continue;
-                    wsr[SILU ? j * p.N + n : n] = acc[i][j][v];
+                for (int j = 0; j < NT; ++j) {
+                    const int n = out_col(j);
+                    const int tn = ((wn * 32 * NT + j * 32) >> 5) & 1;
+                    if (n < p.N) wsr[SILU ? tn * p.N + n : n] = acc[i][j][v];
                 }
-                continue;
             }
-            if (SILU) {
-                const int n = n0 + wn * 32 + col_l;
+        return;
+    }
+    if constexpr (SILU && NT == 1) {
+        // Gate and up of the same columns sit in waves 2c and 2c+1: the up
+        // wave hands its tile over through LDS (the A stages, once no copy
+        // into them is in flight).
+        SLTX_WAIT_VMCNT(0);
+        SLTX_LDS_BARRIER();
+        const int c = wn >> 1;
+        float* xb = reinterpret_cast<float*>(c == 0 ? lds_a0 : c == 1 ? lds_a1 : c == 2 ? lds_a2 : lds_a3);
+        static_assert(BM * 32 * 4 <= A_STAGE * 16, "exchange fits one A stage");
+        if (wn & 1) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    xb[(i * 32 + 8 * (v >> 2) + 4 * h + (v & 3)) * 32 + lrow] = acc[i][0][v];
+        }
+        SLTX_LDS_BARRIER();
+        if (wn & 1) return;
+        const int n = out_col(0);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int r = i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                const int m = m0 + r;
+                if (m >= p.M || n >= p.N) continue;
+                store_out(p, (size_t)m * p.N + n, silu_mul_f32(acc[i][0][v], xb[r * 32 + lrow]));
+            }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int m = m0 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+            if (m >= p.M) continue;
+            if constexpr (SILU) {   // NT == 2: tile 0 gate, tile 1 up
+                const int n = out_col(0);
                 if (n >= p.N) continue;
-                store_out(p, (size_t)m * p.N + n, silu_mul_f32(acc[i][0][v], acc[i][1][v]));
+                store_out(p, (size_t)m * p.N + n, silu_mul_f32(acc[i][0][v], acc[i][NT - 1][v]));
             } else {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int n = n0 + wn * 64 + j * 32 + col_l;
+                for (int j = 0; j < NT; ++j) {
+                    const int n = out_col(j);
                     if (n >= p.N) continue;
                     float out = acc[i][j][v];
                     if (p.bias) out += p.bias[n];
@@ -491,9 +667,10 @@ __global__ __launch_bounds__(256) void q4_splitk_reduce_kernel(GemmParams p) {
 
 // Launch plan: block-tile height WM (BM = 64*WM) and K splits.  Scores each
 // option by useful work over the CU-rounds it occupies (tiles x splits over
-// 256 CUs), prefers taller tiles (less dequantisation per MAC) and charges
-// each split a little for the partial-sum round trip.  Splits cover an even
-// number of k-tiles (the packed-weight stages move two k-tiles at a time).
+// 256 CUs), prefers taller tiles (each dequantized B fragment feeds BM/32
+// MFMAs) and charges each split a little for the partial-sum round trip.
+// Splits cover an even number of k-tiles (packed weights move two k-tiles at
+// a time).
 struct GemmPlan {
     int wm, tiles_m, tiles_n, splits, split_tiles;
     size_t ws_bytes;
@@ -521,7 +698,7 @@ static GemmPlan plan_gemm(const GemmParams& p, bool allow_split) {
             const long rounds = (blocks + kCUs - 1) / kCUs;
             const double util = ((double)p.M * tiles_n * nk) /
                                 ((double)rounds * kCUs * bm * chunk);
-            const double score = util * (1.0 + 0.04 * (wm - 2)) * (s > 1 ? 1.0 - 0.02 * s : 1.0);
+            const double score = util * (1.0 + 0.08 * (wm - 2)) * (s > 1 ? 1.0 - 0.02 * s : 1.0);
             if (score > best_score) {
                 best_score = score;
                 const size_t nw = silu ? 2 * (size_t)p.N : (size_t)p.N;
@@ -537,14 +714,14 @@ size_t gemm_workspace_bytes(const GemmParams& p) { return plan_gemm(p, true).ws_
 
 template <int WM, bool BF16, bool SPLIT>
 static void launch_wm(const GemmParams& p, bool silu, long grid, hipStream_t st) {
-    // Packed W and scales move in 128-k super-stages: K % 128 != 0 needs the
-    // tail handling (clamped sources, zeroed dequant past K).
-    const bool ktail = p.K % (2 * BK) != 0;
-    if (silu && ktail)
+    // The fixed-count kernel needs whole 128-k super-stages and group size 64
+    // (scales and biases move as dword pairs of groups).
+    const bool gen = p.K % (2 * BK) != 0 || p.gshift != 1;
+    if (silu && gen)
         hipLaunchKernelGGL((q4_gemm_kernel<WM, BF16, true, true, SPLIT>), dim3(grid), dim3(kThreads), 0, st, p);
     else if (silu)
         hipLaunchKernelGGL((q4_gemm_kernel<WM, BF16, true, false, SPLIT>), dim3(grid), dim3(kThreads), 0, st, p);
-    else if (ktail)
+    else if (gen)
         hipLaunchKernelGGL((q4_gemm_kernel<WM, BF16, false, true, SPLIT>), dim3(grid), dim3(kThreads), 0, st, p);
     else
         hipLaunchKernelGGL((q4_gemm_kernel<WM, BF16, false, false, SPLIT>), dim3(grid), dim3(kThreads), 0, st, p);
