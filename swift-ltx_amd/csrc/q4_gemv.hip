@@ -166,7 +166,9 @@ __device__ __forceinline__ void gemv_compute_store(const GemvStage<CPL, NW>& st,
 // Each wave owns T consecutive row-iterations (T * 64/L rows), processed with
 // a two-stage register pipeline: the loads of iteration t+1 are in flight
 // while iteration t is computed.
-template <int L, int CPL, bool SWIGLU>
+// MULTI: T >= 2 row-iterations per wave (compile-time, so the one-iteration
+// kernel carries no loop).
+template <int L, int CPL, bool SWIGLU, bool MULTI>
 __global__ __launch_bounds__(256) void q4_gemv_kernel(GemvParams p, int T) {
     constexpr int RPI = 64 / L;        // rows per wave-wide instruction
     constexpr int NCH = L * CPL;       // chunks per row (K / 32)
@@ -191,11 +193,17 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(GemvParams p, int T) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) xr[u][j] = xp[j];
     }
+    __builtin_amdgcn_sched_barrier(0);   // keep every x load ahead of the weight loads
 
+    // The first stage's weight loads are issued before the x preparation and
+    // stay in flight across the barrier below; the second stage follows after
+    // it (measured: issuing both at once is slower for the 28 MB gate/up
+    // launch, and keeps twice the registers live during the x preparation).
     GemvStage<CPL, NW> sa, sb;
     gemv_load<L, CPL, NW>(sa, p, row0, kl);
+    __builtin_amdgcn_sched_barrier(0);
 
-    // Prepare x once per block while the first weight loads are in flight.
+    // Prepare x once per block while the weight loads are in flight.
 #pragma unroll
     for (int u = 0; u < XPT; ++u) {
         const int c = threadIdx.x + 256 * u;
@@ -211,7 +219,9 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(GemvParams p, int T) {
             lds.xc[c] = make_float2(-corr, sum);
         }
     }
-    __syncthreads();
+    // LDS-only barrier: __syncthreads() would also wait for every
+    // outstanding weight load (its release fence waits on vmcnt(0)).
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
     u32x4 xq[CPL][4];
     float2 xc[CPL];
@@ -223,11 +233,15 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(GemvParams p, int T) {
         xc[i] = lds.xc[c];
     }
 
-    for (int t = 0; t < T; t += 2) {
-        if (t + 1 < T) gemv_load<L, CPL, NW>(sb, p, row0 + (t + 1) * RPI, kl);
-        gemv_compute_store<L, CPL, NW>(sa, xq, xc, p, row0 + t * RPI, kl);
-        if (t + 2 < T) gemv_load<L, CPL, NW>(sa, p, row0 + (t + 2) * RPI, kl);
-        if (t + 1 < T) gemv_compute_store<L, CPL, NW>(sb, xq, xc, p, row0 + (t + 1) * RPI, kl);
+    if constexpr (MULTI) {
+        for (int t = 0; t < T; t += 2) {
+            if (t + 1 < T) gemv_load<L, CPL, NW>(sb, p, row0 + (t + 1) * RPI, kl);
+            gemv_compute_store<L, CPL, NW>(sa, xq, xc, p, row0 + t * RPI, kl);
+            if (t + 2 < T) gemv_load<L, CPL, NW>(sa, p, row0 + (t + 2) * RPI, kl);
+            if (t + 1 < T) gemv_compute_store<L, CPL, NW>(sb, xq, xc, p, row0 + (t + 1) * RPI, kl);
+        }
+    } else {
+        gemv_compute_store<L, CPL, NW>(sa, xq, xc, p, row0, kl);
     }
 }
 
@@ -292,8 +306,12 @@ static hipError_t launch_lc(const GemvParams& p, hipStream_t st) {
     if (T > 8) T = 8;
     const long waves = (iters + T - 1) / T;
     const long grid = (waves + 3) / 4;
-    hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU>), dim3((unsigned)grid), dim3(256), 0, st, p,
-                       (int)T);
+    if (T > 1)
+        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, true>), dim3((unsigned)grid), dim3(256), 0,
+                           st, p, (int)T);
+    else
+        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, false>), dim3((unsigned)grid), dim3(256), 0,
+                           st, p, 1);
     return hipGetLastError();
 }
 
