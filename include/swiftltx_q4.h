@@ -137,6 +137,52 @@ int sltx_matmul_q4_ex(const void* x, int32_t x_dtype, const sltx_q4_weight* w, c
                       int32_t epilogue, void* out, int32_t out_dtype, int32_t M, int32_t N,
                       void* stream);
 
+/* ---- Decode-layer fusion: the operators on either side of the projections ----
+ * Norm weights are fp32 (ModelWeights.swift:123,147-148 loads them as float).
+ * rms_norm(v)[k] = half(r[k] * rsqrt(mean(v^2) + eps) * weight[k]), r = the
+ * fp16 input; the sum of squares runs in fp32 (rms_norm, Kernels.swift:40-86). */
+
+/* rmsNorm(_:weight:eps:dim:) -> Tensor  (Ops.swift:8-27), rows x dim fp16.
+ * For M > 1 (prefill); at M = 1 use the fused form below. */
+int sltx_rms_norm(const void* x, const float* weight, float eps, void* out, int32_t rows,
+                  int32_t dim, void* stream);
+
+/* residualRmsNorm(_:_:weight:eps:dim:) -> (residual, normed)  (Ops.swift:256-279;
+ * kernel residual_rms_norm, Kernels.swift:238-290): residual_out = half(a + b);
+ * norm_out = rms_norm of it, with the sum of squares over the unrounded a + b.
+ * residual_out and norm_out must not overlap. */
+int sltx_residual_rms_norm(const void* a, const void* b, const float* weight, float eps,
+                           void* residual_out, void* norm_out, int32_t rows, int32_t dim,
+                           void* stream);
+
+/* rmsNorm + linear at M = 1 (LlamaModel.swift:288-292: input_layernorm, then
+ * the q/k/v projections, here one weight with q|k|v rows concatenated):
+ * out[1,N] fp16 = rms_norm(x) . dequant(W)^T, with K = w->K.  The normalized
+ * vector is formed inside the GEMV and not written.  x and norm_weight 16-byte
+ * aligned. */
+int sltx_rmsnorm_matmul_q4(const void* x, const float* norm_weight, float eps,
+                           const sltx_q4_weight* w, void* out, int32_t N, void* stream);
+
+/* residualRmsNorm + linear(gate) + linear(up) + siluMul at M = 1
+ * (LlamaModel.swift:326-329): residual_out[K] = half(a + b) (the residual
+ * stream, needed by the final add); out[1,N] = silu(n . Wg^T) * (n . Wu^T)
+ * with n = rms_norm(residual), fp32 gate/up products (as
+ * sltx_matmul_q4_silu_mul).  a, b, norm_weight, residual_out 16-byte aligned;
+ * residual_out must not overlap a or b. */
+int sltx_residual_rmsnorm_matmul_q4_silu_mul(const void* a, const void* b,
+                                             const float* norm_weight, float eps,
+                                             void* residual_out, const sltx_q4_weight* gate,
+                                             const sltx_q4_weight* up, void* out, int32_t N,
+                                             void* stream);
+
+/* linear + elemAdd  (LlamaModel.swift:330-331, Ops.swift:72-84; add kernel,
+ * Kernels.swift:121-128): out[M,N] fp16 = half(residual + half(x . dequant(W)^T)),
+ * the projection rounded to fp16 before the add as in the reference.  M == 1
+ * runs the GEMV, M > 1 the GEMM.  out may be residual itself (in place) but
+ * must not otherwise overlap it, nor x. */
+int sltx_matmul_q4_residual(const void* x, const sltx_q4_weight* w, const void* residual,
+                            void* out, int32_t M, int32_t N, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

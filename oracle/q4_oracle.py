@@ -82,6 +82,42 @@ def gelu_tanh_f64(v: np.ndarray) -> np.ndarray:
     return 0.5 * v * (1.0 + np.tanh(inner))
 
 
+# ------------------------------------------------- norms and residual add ---
+
+def rms_norm_ref(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
+    """rms_norm (Kernels.swift:40-86) over the last axis: fp16 x, fp32 weight.
+    sum of squares of float(x) (here in fp64; the kernel's fp32 sum differs
+    below fp32 rounding), rms = rsqrt(mean + eps) rounded to fp32, then
+    out = half(float(x) * rms * weight) evaluated in fp32 left to right."""
+    xf = np.asarray(x, dtype=np.float16).astype(np.float32)
+    ss = np.sum(xf.astype(np.float64) ** 2, axis=-1, keepdims=True)
+    rms = (1.0 / np.sqrt(ss / xf.shape[-1] + eps)).astype(np.float32)
+    return ((xf * rms) * np.asarray(weight, dtype=np.float32)).astype(np.float16)
+
+
+def residual_rms_norm_ref(a: np.ndarray, b: np.ndarray, weight: np.ndarray,
+                          eps: float) -> tuple[np.ndarray, np.ndarray]:
+    """residual_rms_norm (Kernels.swift:238-290): v = float(a) + float(b);
+    residual = half(v); the sum of squares uses the unrounded v; the norm is
+    applied to the rounded residual.  Returns (residual, normed), fp16."""
+    v = (np.asarray(a, dtype=np.float16).astype(np.float32)
+         + np.asarray(b, dtype=np.float16).astype(np.float32))
+    residual = v.astype(np.float16)
+    ss = np.sum(v.astype(np.float64) ** 2, axis=-1, keepdims=True)
+    rms = (1.0 / np.sqrt(ss / v.shape[-1] + eps)).astype(np.float32)
+    normed = ((residual.astype(np.float32) * rms) * np.asarray(weight, dtype=np.float32))
+    return residual, normed.astype(np.float16)
+
+
+def residual_add_ref(residual: np.ndarray, y: np.ndarray) -> np.ndarray:
+    """linear then elemAdd (LlamaModel.swift:330-331; add kernel,
+    Kernels.swift:121-128): the projection is fp16 first, the sum is rounded
+    to fp16 again."""
+    yh = np.asarray(y, dtype=np.float64).astype(np.float16)
+    return (np.asarray(residual, dtype=np.float16).astype(np.float32)
+            + yh.astype(np.float32)).astype(np.float16)
+
+
 # ----------------------------------------------------- bf16 (numpy has none) --
 
 def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:

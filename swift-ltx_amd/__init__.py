@@ -49,6 +49,11 @@ EXPORTED = (
     "sltx_linear",
     "sltx_matmul_q4_silu_mul",
     "sltx_matmul_q4_ex",
+    "sltx_rms_norm",
+    "sltx_residual_rms_norm",
+    "sltx_rmsnorm_matmul_q4",
+    "sltx_residual_rmsnorm_matmul_q4_silu_mul",
+    "sltx_matmul_q4_residual",
 )
 
 
@@ -98,6 +103,15 @@ def lib():
         L.sltx_matmul_q4_silu_mul.restype = ctypes.c_int
         L.sltx_matmul_q4_ex.argtypes = [P, I32, W, P, I32, P, I32, I32, I32, P]
         L.sltx_matmul_q4_ex.restype = ctypes.c_int
+        F = ctypes.c_float
+        L.sltx_rms_norm.argtypes = [P, P, F, P, I32, I32, P]
+        L.sltx_residual_rms_norm.argtypes = [P, P, P, F, P, P, I32, I32, P]
+        L.sltx_rmsnorm_matmul_q4.argtypes = [P, P, F, W, P, I32, P]
+        L.sltx_residual_rmsnorm_matmul_q4_silu_mul.argtypes = [P, P, P, F, P, W, W, P, I32, P]
+        L.sltx_matmul_q4_residual.argtypes = [P, W, P, P, I32, I32, P]
+        for n in ("sltx_rms_norm", "sltx_residual_rms_norm", "sltx_rmsnorm_matmul_q4",
+                  "sltx_residual_rmsnorm_matmul_q4_silu_mul", "sltx_matmul_q4_residual"):
+            getattr(L, n).restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -227,4 +241,56 @@ def matmul_q4_ex(x, w: Q4Weight, M, N, out_dtype=None, bias=None, epilogue=SLTX_
     check(lib().sltx_matmul_q4_ex(_ptr(x), _dtype_code(x.dtype), ctypes.byref(cw), _ptr(bias),
                                   epilogue, _ptr(out), _dtype_code(out.dtype), M, N,
                                   _stream(stream)))
+    return out
+
+
+def rms_norm(x, weight, eps, rows, dim, out=None, stream=None):
+    """rmsNorm (Ops.swift:8-27): fp16 [rows, dim], fp32 weight [dim]."""
+    out = _new((rows, dim), _torch().float16, x) if out is None else out
+    check(lib().sltx_rms_norm(_ptr(x), _ptr(weight), eps, _ptr(out), rows, dim, _stream(stream)))
+    return out
+
+
+def residual_rms_norm(a, b, weight, eps, rows, dim, residual_out=None, norm_out=None,
+                      stream=None):
+    """residualRmsNorm (Ops.swift:256-279) -> (residual, normed), fp16 [rows, dim]."""
+    torch = _torch()
+    residual_out = _new((rows, dim), torch.float16, a) if residual_out is None else residual_out
+    norm_out = _new((rows, dim), torch.float16, a) if norm_out is None else norm_out
+    check(lib().sltx_residual_rms_norm(_ptr(a), _ptr(b), _ptr(weight), eps, _ptr(residual_out),
+                                       _ptr(norm_out), rows, dim, _stream(stream)))
+    return residual_out, norm_out
+
+
+def rmsnorm_matmul_q4(x, norm_weight, eps, w: Q4Weight, N, out=None, stream=None):
+    """rms_norm(x) . dequant(W)^T at M = 1 (input_layernorm + q|k|v,
+    LlamaModel.swift:288-292) -> fp16 [1, N]."""
+    out = _new((1, N), _torch().float16, x) if out is None else out
+    cw = w.c()
+    check(lib().sltx_rmsnorm_matmul_q4(_ptr(x), _ptr(norm_weight), eps, ctypes.byref(cw),
+                                       _ptr(out), N, _stream(stream)))
+    return out
+
+
+def residual_rmsnorm_matmul_q4_silu_mul(a, b, norm_weight, eps, gate: Q4Weight, up: Q4Weight, N,
+                                        residual_out=None, out=None, stream=None):
+    """residualRmsNorm + gate/up + siluMul at M = 1 (LlamaModel.swift:326-329)
+    -> (residual [1, K], activated [1, N])."""
+    torch = _torch()
+    residual_out = _new((1, gate.K), torch.float16, a) if residual_out is None else residual_out
+    out = _new((1, N), torch.float16, a) if out is None else out
+    g, u = gate.c(), up.c()
+    check(lib().sltx_residual_rmsnorm_matmul_q4_silu_mul(
+        _ptr(a), _ptr(b), _ptr(norm_weight), eps, _ptr(residual_out), ctypes.byref(g),
+        ctypes.byref(u), _ptr(out), N, _stream(stream)))
+    return residual_out, out
+
+
+def matmul_q4_residual(x, w: Q4Weight, residual, M, N, out=None, stream=None):
+    """half(residual + half(x . dequant(W)^T)): linear + elemAdd
+    (LlamaModel.swift:330-331) -> fp16 [M, N]."""
+    out = _new((M, N), _torch().float16, x) if out is None else out
+    cw = w.c()
+    check(lib().sltx_matmul_q4_residual(_ptr(x), ctypes.byref(cw), _ptr(residual), _ptr(out), M,
+                                        N, _stream(stream)))
     return out

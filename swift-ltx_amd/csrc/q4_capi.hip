@@ -39,6 +39,11 @@ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 
 int log2_group(int g) { return g == 32 ? 0 : g == 64 ? 1 : g == 128 ? 2 : -1; }
 
+bool overlap(const void* a, size_t na, const void* b, size_t nb) {
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return x < y + nb && y < x + na;
+}
+
 // Shape / pointer checks common to every matmul entry point.
 int check_weight(const char* fn, const void* x, const uint32_t* w, const uint16_t* s,
                  const uint16_t* b, const void* out, int M, int K, int N, int g) {
@@ -85,8 +90,18 @@ int finish(hipError_t e, const char* fn) {
     return kOk;
 }
 
+// Optional GEMV prologue / epilogue operands (see GemvParams).
+struct GemvFuse {
+    int pro = kProNone;
+    const void* xb = nullptr;
+    const float* norm_w = nullptr;
+    float eps = 0.0f;
+    void* res_out = nullptr;
+    const void* residual = nullptr;
+};
+
 int run_gemv(const char* fn, const void* x, const sltx_q4_weight& w0, const sltx_q4_weight* w1,
-             void* out, int K, int N, hipStream_t st) {
+             void* out, int K, int N, hipStream_t st, const GemvFuse& fz = GemvFuse()) {
     GemvParams p;
     p.x = static_cast<const uint16_t*>(x);
     p.w0 = w0.weight;
@@ -100,6 +115,12 @@ int run_gemv(const char* fn, const void* x, const sltx_q4_weight& w0, const sltx
     p.K = K;
     p.groups = K / w0.group_size;
     p.gshift = log2_group(w0.group_size);
+    p.pro = fz.pro;
+    p.xb = static_cast<const uint16_t*>(fz.xb);
+    p.norm_w = fz.norm_w;
+    p.eps = fz.eps;
+    p.res_out = static_cast<uint16_t*>(fz.res_out);
+    p.residual = static_cast<const uint16_t*>(fz.residual);
     return finish(launch_gemv(p, w1 != nullptr, st), fn);
 }
 
@@ -136,7 +157,7 @@ float* splitk_workspace(hipStream_t st, size_t need) {
 
 int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w0,
              const sltx_q4_weight* w1, const float* bias, int epilogue, void* out, int y_dtype,
-             int M, int K, int N, hipStream_t st) {
+             int M, int K, int N, hipStream_t st, const void* residual = nullptr) {
     GemmParams p;
     p.a = x;
     p.w0 = w0.weight;
@@ -155,6 +176,7 @@ int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w
     p.tiles_m = p.tiles_n = 0;
     p.y_dtype = y_dtype;
     p.epilogue = w1 ? kEpiSiluMul : epilogue;
+    p.residual = static_cast<const uint16_t*>(residual);
     p.ws = nullptr;
     p.splits = 1;
     p.split_tiles = 0;
@@ -277,6 +299,121 @@ int sltx_matmul_q4_ex(const void* x, int32_t x_dtype, const sltx_q4_weight* w, c
     if ((rc = ensure_device()) != kOk) return rc;
     return run_gemm(fn, x, x_dtype, *w, nullptr, bias, epilogue, out, out_dtype, M, w->K, N,
                     static_cast<hipStream_t>(stream));
+}
+
+int sltx_rms_norm(const void* x, const float* weight, float eps, void* out, int32_t rows,
+                  int32_t dim, void* stream) {
+    const char* fn = "sltx_rms_norm";
+    if (rows < 0 || dim < 0) return fail(kErrInvalid, "%s: negative rows (%d) or dim (%d)", fn, rows, dim);
+    if (rows == 0 || dim == 0) return kOk;
+    if (!x || !weight || !out) return fail(kErrInvalid, "%s: null pointer argument", fn);
+    if (!aligned(x, 2) || !aligned(out, 2) || !aligned(weight, 4))
+        return fail(kErrInvalid, "%s: misaligned pointer", fn);
+    int rc = ensure_device();
+    if (rc != kOk) return rc;
+    return finish(launch_rms_norm(static_cast<const uint16_t*>(x), nullptr, weight, eps, nullptr,
+                                  static_cast<uint16_t*>(out), rows, dim,
+                                  static_cast<hipStream_t>(stream)),
+                  fn);
+}
+
+int sltx_residual_rms_norm(const void* a, const void* b, const float* weight, float eps,
+                           void* residual_out, void* norm_out, int32_t rows, int32_t dim,
+                           void* stream) {
+    const char* fn = "sltx_residual_rms_norm";
+    if (rows < 0 || dim < 0) return fail(kErrInvalid, "%s: negative rows (%d) or dim (%d)", fn, rows, dim);
+    if (rows == 0 || dim == 0) return kOk;
+    if (!a || !b || !weight || !residual_out || !norm_out)
+        return fail(kErrInvalid, "%s: null pointer argument", fn);
+    if (!aligned(a, 2) || !aligned(b, 2) || !aligned(residual_out, 2) || !aligned(norm_out, 2) ||
+        !aligned(weight, 4))
+        return fail(kErrInvalid, "%s: misaligned pointer", fn);
+    const size_t nb = (size_t)rows * dim * 2;
+    if (overlap(residual_out, nb, norm_out, nb))
+        return fail(kErrInvalid, "%s: residual_out and norm_out overlap", fn);
+    int rc = ensure_device();
+    if (rc != kOk) return rc;
+    return finish(launch_rms_norm(static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b),
+                                  weight, eps, static_cast<uint16_t*>(residual_out),
+                                  static_cast<uint16_t*>(norm_out), rows, dim,
+                                  static_cast<hipStream_t>(stream)),
+                  fn);
+}
+
+int sltx_rmsnorm_matmul_q4(const void* x, const float* norm_weight, float eps,
+                           const sltx_q4_weight* w, void* out, int32_t N, void* stream) {
+    const char* fn = "sltx_rmsnorm_matmul_q4";
+    if (!w) return fail(kErrInvalid, "%s: null weight descriptor", fn);
+    int rc = check_weight(fn, x, w->weight, w->scales, w->biases, out, 1, w->K, N, w->group_size);
+    if (rc != kOk) return rc;
+    if (N == 0) return kOk;
+    if (!norm_weight) return fail(kErrInvalid, "%s: null norm_weight", fn);
+    if (!aligned(norm_weight, 16)) return fail(kErrInvalid, "%s: norm_weight must be 16-byte aligned", fn);
+    if (!aligned(out, 2)) return fail(kErrInvalid, "%s: misaligned out", fn);
+    if ((rc = ensure_device()) != kOk) return rc;
+    GemvFuse fz;
+    fz.pro = kProRms;
+    fz.norm_w = norm_weight;
+    fz.eps = eps;
+    return run_gemv(fn, x, *w, nullptr, out, w->K, N, static_cast<hipStream_t>(stream), fz);
+}
+
+int sltx_residual_rmsnorm_matmul_q4_silu_mul(const void* a, const void* b,
+                                             const float* norm_weight, float eps,
+                                             void* residual_out, const sltx_q4_weight* gate,
+                                             const sltx_q4_weight* up, void* out, int32_t N,
+                                             void* stream) {
+    const char* fn = "sltx_residual_rmsnorm_matmul_q4_silu_mul";
+    if (!gate || !up) return fail(kErrInvalid, "%s: null weight descriptor", fn);
+    if (gate->K != up->K) return fail(kErrInvalid, "%s: gate and up K differ", fn);
+    if (gate->group_size != up->group_size)
+        return fail(kErrInvalid, "%s: gate and up group_size differ", fn);
+    const int K = gate->K;
+    int rc = check_weight(fn, a, gate->weight, gate->scales, gate->biases, out, 1, K, N,
+                          gate->group_size);
+    if (rc != kOk) return rc;
+    rc = check_weight(fn, a, up->weight, up->scales, up->biases, out, 1, K, N, up->group_size);
+    if (rc != kOk) return rc;
+    if (N == 0) return kOk;
+    if (!b || !norm_weight || !residual_out) return fail(kErrInvalid, "%s: null pointer argument", fn);
+    if (!aligned(b, 16) || !aligned(norm_weight, 16) || !aligned(residual_out, 16))
+        return fail(kErrInvalid, "%s: b, norm_weight and residual_out must be 16-byte aligned", fn);
+    if (!aligned(out, 2)) return fail(kErrInvalid, "%s: misaligned out", fn);
+    const size_t kb = (size_t)K * 2;
+    if (overlap(residual_out, kb, a, kb) || overlap(residual_out, kb, b, kb))
+        return fail(kErrInvalid, "%s: residual_out overlaps an input", fn);
+    if ((rc = ensure_device()) != kOk) return rc;
+    GemvFuse fz;
+    fz.pro = kProResidualRms;
+    fz.xb = b;
+    fz.norm_w = norm_weight;
+    fz.eps = eps;
+    fz.res_out = residual_out;
+    return run_gemv(fn, a, *gate, up, out, K, N, static_cast<hipStream_t>(stream), fz);
+}
+
+int sltx_matmul_q4_residual(const void* x, const sltx_q4_weight* w, const void* residual,
+                            void* out, int32_t M, int32_t N, void* stream) {
+    const char* fn = "sltx_matmul_q4_residual";
+    if (!w) return fail(kErrInvalid, "%s: null weight descriptor", fn);
+    int rc = check_weight(fn, x, w->weight, w->scales, w->biases, out, M, w->K, N, w->group_size);
+    if (rc != kOk) return rc;
+    if (M == 0 || N == 0) return kOk;
+    if (!residual) return fail(kErrInvalid, "%s: null residual", fn);
+    if (!aligned(residual, 2) || !aligned(out, 2)) return fail(kErrInvalid, "%s: misaligned pointer", fn);
+    const size_t ob = (size_t)M * N * 2;
+    if (residual != out && overlap(residual, ob, out, ob))
+        return fail(kErrInvalid, "%s: residual and out overlap without being equal", fn);
+    if (overlap(x, (size_t)M * w->K * 2, out, ob)) return fail(kErrInvalid, "%s: out overlaps x", fn);
+    if ((rc = ensure_device()) != kOk) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (M == 1) {
+        GemvFuse fz;
+        fz.residual = residual;
+        return run_gemv(fn, x, *w, nullptr, out, w->K, N, st, fz);
+    }
+    return run_gemm(fn, x, kF16, *w, nullptr, nullptr, kEpiResidual, out, kF16, M, w->K, N, st,
+                    residual);
 }
 
 }  // extern "C"

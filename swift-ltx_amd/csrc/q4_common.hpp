@@ -84,6 +84,14 @@ enum Epilogue : int {
     kEpiNone = 0,
     kEpiSiluMul = 1,   // y = silu(x.Wg^T) * (x.Wu^T)  (two weight sets)
     kEpiGeluTanh = 2,  // y = gelu_tanh(x.W^T + bias)
+    kEpiResidual = 3,  // y = half(residual + half(x.W^T))  (linear + elemAdd, fp16 out)
 };
+
+// linear(...) then elemAdd(residual, .) (LlamaModel.swift:330-331): the
+// projection is rounded to fp16 first, then added in fp32 and rounded again
+// (the reference's add kernel, Kernels.swift:121-128).
+__device__ __forceinline__ uint16_t residual_add_f16(uint16_t residual, float acc) {
+    return f2h(h2f(residual) + h2f(f2h(acc)));
+}
 
 }  // namespace sltx

@@ -125,6 +125,17 @@ __device__ __forceinline__ void store_out(const GemmParams& p, size_t o, float v
         reinterpret_cast<uint16_t*>(p.y)[o] = f2h(v);
 }
 
+// Non-SiLU epilogues: + bias, GELU-tanh, or the residual add (fp16 out).
+__device__ __forceinline__ void epi_store(const GemmParams& p, size_t o, int n, float v) {
+    if (p.bias) v += p.bias[n];
+    if (p.epilogue == kEpiGeluTanh) v = gelu_tanh_f32(v);
+    if (p.epilogue == kEpiResidual) {
+        reinterpret_cast<uint16_t*>(p.y)[o] = residual_add_f16(p.residual[o], v);
+        return;
+    }
+    store_out(p, o, v);
+}
+
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
 // vmcnt bits [3:0] and [15:14], expcnt [6:4] = 7, lgkmcnt [11:8] = 15).
 #define SLTX_WAIT_VMCNT(n) \
@@ -627,10 +638,7 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
                 for (int j = 0; j < NT; ++j) {
                     const int n = out_col(j);
                     if (n >= p.N) continue;
-                    float out = acc[i][j][v];
-                    if (p.bias) out += p.bias[n];
-                    if (p.epilogue == kEpiGeluTanh) out = gelu_tanh_f32(out);
-                    store_out(p, (size_t)m * p.N + n, out);
+                    epi_store(p, (size_t)m * p.N + n, n, acc[i][j][v]);
                 }
             }
         }
@@ -654,15 +662,10 @@ __global__ __launch_bounds__(256) void q4_splitk_reduce_kernel(GemmParams p) {
         a += src[s * stride];
         if (SILU) u += src[s * stride + p.N];
     }
-    float out;
-    if (SILU) {
-        out = silu_mul_f32(a, u);
-    } else {
-        out = a;
-        if (p.bias) out += p.bias[n];
-        if (p.epilogue == kEpiGeluTanh) out = gelu_tanh_f32(out);
-    }
-    store_out(p, idx, out);
+    if (SILU)
+        store_out(p, idx, silu_mul_f32(a, u));
+    else
+        epi_store(p, idx, (int)n, a);
 }
 
 // Launch plan: block-tile height WM (BM = 64*WM) and K splits.  Scores each

@@ -37,6 +37,7 @@ template <int NCH>
 struct GemvLds {
     u32x4 xs[4][NCH];
     float2 xc[NCH];
+    float red[4];   // per-wave partial sums of squares (RMS-norm prologue)
 };
 
 // Build the dot-order pairs for 8 consecutive x values (one weight word).
@@ -159,7 +160,7 @@ __device__ __forceinline__ void gemv_compute_store(const GemvStage<CPL, NW>& st,
     }
     if (kl == 0 && r < p.N) {
         const float out = NW == 2 ? silu_mul_f32(acc[0], acc[NW - 1]) : acc[0];
-        p.y[r] = f2h(out);
+        p.y[r] = p.residual ? residual_add_f16(p.residual[r], out) : f2h(out);
     }
 }
 
@@ -167,8 +168,10 @@ __device__ __forceinline__ void gemv_compute_store(const GemvStage<CPL, NW>& st,
 // a two-stage register pipeline: the loads of iteration t+1 are in flight
 // while iteration t is computed.
 // MULTI: T >= 2 row-iterations per wave (compile-time, so the one-iteration
-// kernel carries no loop).
-template <int L, int CPL, bool SWIGLU, bool MULTI>
+// kernel carries no loop).  PRO (GemvPro): the input is x, rms_norm(x) or
+// rms_norm(x + xb); each block recomputes the norm of its own copy of the
+// input vector (K values) while its first weight loads are in flight.
+template <int L, int CPL, bool SWIGLU, bool MULTI, int PRO>
 __global__ __launch_bounds__(256) void q4_gemv_kernel(GemvParams p, int T) {
     constexpr int RPI = 64 / L;        // rows per wave-wide instruction
     constexpr int NCH = L * CPL;       // chunks per row (K / 32)
@@ -184,7 +187,10 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(GemvParams p, int T) {
     // x loads first: vmcnt retires in issue order, so x issued after the
     // weights would make the x preparation wait for the HBM latency too.
     constexpr int XPT = (NCH + 255) / 256;  // x chunks prepared per thread
+    constexpr bool NORM = PRO != kProNone, RES = PRO == kProResidualRms;
     f16x8 xr[XPT][4];
+    f16x8 xb[RES ? XPT : 1][4];
+    f32x4 nw[NORM ? XPT : 1][8];
 #pragma unroll
     for (int u = 0; u < XPT; ++u) {
         const int c = threadIdx.x + 256 * u;
@@ -192,6 +198,16 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(GemvParams p, int T) {
         const f16x8* xp = reinterpret_cast<const f16x8*>(p.x + (size_t)cc * 32);
 #pragma unroll
         for (int j = 0; j < 4; ++j) xr[u][j] = xp[j];
+        if constexpr (RES) {
+            const f16x8* bp = reinterpret_cast<const f16x8*>(p.xb + (size_t)cc * 32);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xb[u][j] = bp[j];
+        }
+        if constexpr (NORM) {
+            const f32x4* wp = reinterpret_cast<const f32x4*>(p.norm_w + (size_t)cc * 32);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) nw[u][q] = wp[q];
+        }
     }
     __builtin_amdgcn_sched_barrier(0);   // keep every x load ahead of the weight loads
 
@@ -202,6 +218,48 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(GemvParams p, int T) {
     GemvStage<CPL, NW> sa, sb;
     gemv_load<L, CPL, NW>(sa, p, row0, kl);
     __builtin_amdgcn_sched_barrier(0);
+
+    if constexpr (NORM) {
+        // rms_norm (Kernels.swift:40-86) / residual_rms_norm (Kernels.swift:238-290):
+        // v = x (or a + b, whose fp16 rounding is the residual stream); the
+        // sum of squares uses the unrounded v; out = half(r * rms * w) with r
+        // the (rounded) input and rms = rsqrt(mean(v^2) + eps).
+        float ss = 0.0f;
+#pragma unroll
+        for (int u = 0; u < XPT; ++u) {
+            const int c = threadIdx.x + 256 * u;
+            if (c >= NCH) continue;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    float v = (float)xr[u][j][e];
+                    if constexpr (RES) {
+                        v += (float)xb[u][j][e];
+                        xr[u][j][e] = (f16)v;
+                    }
+                    ss += v * v;
+                }
+            if constexpr (RES) {
+                if (blockIdx.x == 0) {
+                    f16x8* rp = reinterpret_cast<f16x8*>(p.res_out + (size_t)c * 32);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) rp[j] = xr[u][j];
+                }
+            }
+        }
+        ss = row_reduce<64>(ss);
+        if ((threadIdx.x & 63) == 0) lds.red[threadIdx.x >> 6] = ss;
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const float rms = rsqrtf((lds.red[0] + lds.red[1] + lds.red[2] + lds.red[3]) / (float)p.K + p.eps);
+#pragma unroll
+        for (int u = 0; u < XPT; ++u)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    xr[u][j][e] = (f16)((float)xr[u][j][e] * rms * nw[u][(j * 8 + e) >> 2][e & 3]);
+    }
 
     // Prepare x once per block while the weight loads are in flight.
 #pragma unroll
@@ -253,12 +311,42 @@ __global__ __launch_bounds__(256) void q4_gemv_generic_kernel(GemvParams p) {
     const int nch = p.K / 32;
     u32x4* xs = reinterpret_cast<u32x4*>(smem);              // [4][nch]
     float2* xcv = reinterpret_cast<float2*>(xs + 4 * nch);    // [nch]
+    float* red = reinterpret_cast<float*>(xcv + nch);         // [4]
+    // Input element i: x, or the (rounded) residual x + xb; rms_norm applied
+    // when the prologue asks for it (same formulas as the specialized kernel).
+    auto in_val = [&](int i) {
+        float v = h2f(p.x[i]);
+        if (p.pro == kProResidualRms) v = h2f(f2h(v + h2f(p.xb[i])));
+        return v;
+    };
+    float rms = 0.0f;
+    if (p.pro != kProNone) {
+        float ss = 0.0f;
+        for (int i = threadIdx.x; i < p.K; i += blockDim.x) {
+            float v = h2f(p.x[i]);
+            if (p.pro == kProResidualRms) {
+                v += h2f(p.xb[i]);
+                if (blockIdx.x == 0) p.res_out[i] = f2h(v);
+            }
+            ss += v * v;
+        }
+        ss = row_reduce<64>(ss);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        rms = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)p.K + p.eps);
+    }
     for (int c = threadIdx.x; c < nch; c += blockDim.x) {
         const f16x8* xp = reinterpret_cast<const f16x8*>(p.x + (size_t)c * 32);
         float corr = 0.0f, sum = 0.0f;
         for (int j = 0; j < 4; ++j) {
             uint32_t pr[4];
-            pair_word(xp[j], pr, corr, sum);
+            f16x8 xv = xp[j];
+            if (p.pro != kProNone)
+                for (int e = 0; e < 8; ++e) {
+                    const int i = c * 32 + j * 8 + e;
+                    xv[e] = (f16)(in_val(i) * rms * p.norm_w[i]);
+                }
+            pair_word(xv, pr, corr, sum);
             u32x4 v = {pr[0], pr[1], pr[2], pr[3]};
             xs[j * nch + c] = v;
         }
@@ -288,7 +376,7 @@ __global__ __launch_bounds__(256) void q4_gemv_generic_kernel(GemvParams p) {
     }
     if (lane == 0) {
         float out = SWIGLU ? silu_mul_f32(acc[0], acc[NW - 1]) : acc[0];
-        p.y[r] = f2h(out);
+        p.y[r] = p.residual ? residual_add_f16(p.residual[r], out) : f2h(out);
     }
 }
 
@@ -306,12 +394,22 @@ static hipError_t launch_lc(const GemvParams& p, hipStream_t st) {
     if (T > 8) T = 8;
     const long waves = (iters + T - 1) / T;
     const long grid = (waves + 3) / 4;
-    if (T > 1)
-        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, true>), dim3((unsigned)grid), dim3(256), 0,
-                           st, p, (int)T);
+    // Prologues instantiated: rms_norm for the plain GEMV (q|k|v after
+    // input_layernorm), residual + rms_norm for the fused gate/up.
+    constexpr int PRO_N = SWIGLU ? kProResidualRms : kProRms;
+    const bool norm = p.pro != kProNone;
+    if (T > 1 && norm)
+        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, true, PRO_N>), dim3((unsigned)grid), dim3(256),
+                           0, st, p, (int)T);
+    else if (T > 1)
+        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, true, kProNone>), dim3((unsigned)grid),
+                           dim3(256), 0, st, p, (int)T);
+    else if (norm)
+        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, false, PRO_N>), dim3((unsigned)grid), dim3(256),
+                           0, st, p, 1);
     else
-        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, false>), dim3((unsigned)grid), dim3(256), 0,
-                           st, p, 1);
+        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, false, kProNone>), dim3((unsigned)grid),
+                           dim3(256), 0, st, p, 1);
     return hipGetLastError();
 }
 
@@ -346,12 +444,13 @@ int gemv_pick_lanes(int K, int* cpl_out) {
 }
 
 hipError_t launch_gemv(const GemvParams& p, bool swiglu, hipStream_t st) {
+    if (p.pro != kProNone && p.pro != (swiglu ? kProResidualRms : kProRms)) return hipErrorInvalidValue;
     int cpl = 0;
     const int L = gemv_pick_lanes(p.K, &cpl);
     if (L == 64) return swiglu ? launch_l<64, true>(p, cpl, st) : launch_l<64, false>(p, cpl, st);
     if (L == 32) return swiglu ? launch_l<32, true>(p, cpl, st) : launch_l<32, false>(p, cpl, st);
     if (L == 16) return swiglu ? launch_l<16, true>(p, cpl, st) : launch_l<16, false>(p, cpl, st);
-    const size_t shm = (size_t)(p.K / 32) * (4 * sizeof(u32x4) + sizeof(float2));
+    const size_t shm = (size_t)(p.K / 32) * (4 * sizeof(u32x4) + sizeof(float2)) + 4 * sizeof(float);
     if (shm > 64 * 1024) return hipErrorInvalidValue;
     const int grid = (p.N + 3) / 4;
     if (swiglu)

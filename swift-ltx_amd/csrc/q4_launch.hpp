@@ -21,7 +21,18 @@ struct GemvParams {
     int K;
     int groups;             // K / g
     int gshift;             // log2(g / 32): chunk of 32 nibbles c lies in group c >> gshift
+    // Prologue (GemvPro): the GEMV's input is x itself, rms_norm(x), or
+    // rms_norm(x + xb) with the rounded sum written to res_out (by block 0).
+    int pro;
+    const uint16_t* xb;     // second addend (GemvPro::kResidualRms)
+    const float* norm_w;    // [K] fp32 norm weight
+    float eps;
+    uint16_t* res_out;      // [K] fp16 residual stream out (kResidualRms)
+    // Epilogue: y = half(residual + half(x . W^T)) when non-null.
+    const uint16_t* residual;
 };
+
+enum GemvPro : int { kProNone = 0, kProRms = 1, kProResidualRms = 2 };
 
 // GEMM (M > 1) operands; see q4_gemm.hip.
 struct GemmParams {
@@ -40,6 +51,7 @@ struct GemmParams {
     int tiles_m, tiles_n;   // filled by launch_gemm
     int y_dtype;            // DType
     int epilogue;           // Epilogue
+    const uint16_t* residual;   // [M, N] fp16, epilogue kEpiResidual
     float* ws;              // split-K partials [splits][M][N or 2N] (null: no split)
     int splits;             // filled by launch_gemm
     int split_tiles;        // k-tiles per split (even), filled by launch_gemm
@@ -53,6 +65,9 @@ size_t gemm_workspace_bytes(const GemmParams& p);
 hipError_t launch_gemm(GemmParams p, bool a_bf16, hipStream_t st);
 hipError_t launch_silu_mul(const uint16_t* a, const uint16_t* b, uint16_t* out, long count,
                            hipStream_t st);
+// Row-wise RMS norm, optionally of a + b (then the rounded sum goes to res_out).
+hipError_t launch_rms_norm(const uint16_t* a, const uint16_t* b, const float* w, float eps,
+                           uint16_t* res_out, uint16_t* out, int rows, int dim, hipStream_t st);
 int gemv_pick_lanes(int K, int* cpl_out);
 
 }  // namespace sltx

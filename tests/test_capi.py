@@ -151,3 +151,70 @@ def test_last_error_is_thread_local(pkg):
     t.join()
     assert seen["msg"] == ""
     assert "multiple of 32" in pkg.last_error()
+
+
+# ---- decode-layer fusion entry points: validation paths only ----
+
+def _wq(pkg, K=3072, g=64, weight=ALIGNED):
+    return pkg.CQ4Weight(weight, ALIGNED, ALIGNED, K, g)
+
+
+def test_rms_norm_validation(pkg):
+    L = pkg.lib()
+    assert L.sltx_rms_norm(ALIGNED, ALIGNED, 1e-5, ALIGNED, 0, 3072, None) == 0
+    assert L.sltx_rms_norm(ALIGNED, ALIGNED, 1e-5, ALIGNED, -1, 3072, None) == -1
+    assert L.sltx_rms_norm(0, ALIGNED, 1e-5, ALIGNED, 1, 3072, None) == -1
+    assert "null" in pkg.last_error()
+    assert L.sltx_rms_norm(ALIGNED, ALIGNED + 2, 1e-5, ALIGNED, 1, 3072, None) == -1
+    assert "misaligned" in pkg.last_error()
+    # residual_out and norm_out overlapping
+    assert L.sltx_residual_rms_norm(ALIGNED, ALIGNED, ALIGNED, 1e-5, ALIGNED, ALIGNED + 64, 1,
+                                    3072, None) == -1
+    assert "overlap" in pkg.last_error()
+
+
+def test_rmsnorm_matmul_validation(pkg):
+    L = pkg.lib()
+    w = _wq(pkg)
+    assert L.sltx_rmsnorm_matmul_q4(ALIGNED, 0, 1e-5, ctypes.byref(w), ALIGNED, 5120, None) == -1
+    assert "norm_weight" in pkg.last_error()
+    assert L.sltx_rmsnorm_matmul_q4(ALIGNED, ALIGNED + 4, 1e-5, ctypes.byref(w), ALIGNED, 5120,
+                                    None) == -1
+    assert "16-byte" in pkg.last_error()
+    bad = _wq(pkg, K=100)
+    assert L.sltx_rmsnorm_matmul_q4(ALIGNED, ALIGNED, 1e-5, ctypes.byref(bad), ALIGNED, 5120,
+                                    None) == -1
+    assert "multiple of 32" in pkg.last_error()
+    assert L.sltx_rmsnorm_matmul_q4(ALIGNED, ALIGNED, 1e-5, ctypes.byref(w), ALIGNED, 0, None) == 0
+
+
+def test_residual_rmsnorm_silu_validation(pkg):
+    L = pkg.lib()
+    g, u = _wq(pkg), _wq(pkg)
+    fn = L.sltx_residual_rmsnorm_matmul_q4_silu_mul
+    # residual_out overlapping a
+    assert fn(ALIGNED, 0x20000, ALIGNED, 1e-5, ALIGNED + 16, ctypes.byref(g), ctypes.byref(u),
+              0x30000, 8192, None) == -1
+    assert "overlaps" in pkg.last_error()
+    u2 = _wq(pkg, K=2048)
+    assert fn(ALIGNED, 0x20000, ALIGNED, 1e-5, 0x40000, ctypes.byref(g), ctypes.byref(u2),
+              0x30000, 8192, None) == -1
+    assert "K differ" in pkg.last_error()
+    assert fn(ALIGNED, 0x20000, ALIGNED, 1e-5, 0x40000 + 8, ctypes.byref(g), ctypes.byref(u),
+              0x30000, 8192, None) == -1
+    assert "16-byte" in pkg.last_error()
+
+
+def test_matmul_residual_validation(pkg):
+    L = pkg.lib()
+    w = _wq(pkg, K=8192)
+    fn = L.sltx_matmul_q4_residual
+    assert fn(ALIGNED, ctypes.byref(w), 0, 0x40000, 1, 3072, None) == -1
+    assert "null residual" in pkg.last_error()
+    # out overlapping residual without being equal
+    assert fn(ALIGNED, ctypes.byref(w), 0x40000, 0x40000 + 2, 1, 3072, None) == -1
+    assert "overlap" in pkg.last_error()
+    # out overlapping x
+    assert fn(ALIGNED, ctypes.byref(w), 0x40000, ALIGNED + 32, 1, 3072, None) == -1
+    assert "overlaps x" in pkg.last_error()
+    assert fn(ALIGNED, ctypes.byref(w), 0x40000, 0x40000, 0, 3072, None) == 0

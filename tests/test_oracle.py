@@ -247,3 +247,74 @@ def test_bf16_rounding(oracle):
     L.oracle_f32_to_bf16.argtypes = [__import__("ctypes").c_float]
     L.oracle_f32_to_bf16.restype = __import__("ctypes").c_uint16
     assert [L.oracle_f32_to_bf16(float(v)) for v in vals] == bits.tolist()
+
+
+# ------------------------------------------------ norms and residual add ---
+# rms_norm / residual_rms_norm (Kernels.swift:40-86, :238-290) are pinned by
+# what the definition fixes: a constant vector maps to sign(c) * w, the output
+# of a unit-weight norm has RMS 1 and points along x, power-of-two scaling of x
+# leaves it bit-identical (eps = 0), b = 0 reduces the residual form to the
+# plain one, and the residual equals numpy's own fp16 addition.
+
+def test_rms_norm_constant_vector():
+    from oracle import q4_oracle as o
+    w = np.array([0.5, 1.25, -2.0, 3.0] * 16, dtype=np.float32)
+    for c in (0.75, -3.0, 0.001):
+        x = np.full((1, 64), c, dtype=np.float16)
+        out = o.rms_norm_ref(x, w, 0.0)
+        assert np.array_equal(out[0], (np.sign(c) * w).astype(np.float16))
+
+
+def test_rms_norm_unit_rms_and_direction():
+    from oracle import q4_oracle as o
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((5, 3072)).astype(np.float16) * np.float16(7)
+    out = o.rms_norm_ref(x, np.ones(3072, np.float32), 1e-6).astype(np.float64)
+    rms = np.sqrt(np.mean(out ** 2, axis=1))
+    assert np.all(np.abs(rms - 1.0) < 1e-3)
+    xf = x.astype(np.float64)
+    cos = np.sum(out * xf, axis=1) / (np.linalg.norm(out, axis=1) * np.linalg.norm(xf, axis=1))
+    assert np.all(cos > 1 - 1e-6)
+
+
+def test_rms_norm_power_of_two_scaling_exact():
+    from oracle import q4_oracle as o
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((3, 256)).astype(np.float16)
+    w = rng.standard_normal(256).astype(np.float32)
+    base = o.rms_norm_ref(x, w, 0.0)
+    for k in (-3, 2, 5):
+        xs = (x.astype(np.float32) * 2.0 ** k).astype(np.float16)
+        assert np.array_equal(xs.astype(np.float32), x.astype(np.float32) * 2.0 ** k)
+        assert np.array_equal(o.rms_norm_ref(xs, w, 0.0), base)
+
+
+def test_rms_norm_eps_dominates_zero_vector():
+    from oracle import q4_oracle as o
+    out = o.rms_norm_ref(np.zeros((1, 32), np.float16), np.ones(32, np.float32), 1e-5)
+    assert np.array_equal(out, np.zeros((1, 32), np.float16))
+
+
+def test_residual_rms_norm_reductions():
+    from oracle import q4_oracle as o
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal((2, 512)).astype(np.float16)
+    b = rng.standard_normal((2, 512)).astype(np.float16)
+    w = rng.standard_normal(512).astype(np.float32)
+    res, nrm = o.residual_rms_norm_ref(a, b, w, 1e-5)
+    assert np.array_equal(res, a + b)                       # numpy's fp16 add
+    r2, n2 = o.residual_rms_norm_ref(b, a, w, 1e-5)
+    assert np.array_equal(res, r2) and np.array_equal(nrm, n2)
+    r0, n0 = o.residual_rms_norm_ref(a, np.zeros_like(a), w, 1e-5)
+    assert np.array_equal(r0, a)
+    assert np.array_equal(n0, o.rms_norm_ref(a, w, 1e-5))
+
+
+def test_residual_add_ref():
+    from oracle import q4_oracle as o
+    rng = np.random.default_rng(6)
+    r = rng.standard_normal(64).astype(np.float16)
+    y = rng.standard_normal(64) * 3
+    assert np.array_equal(o.residual_add_ref(np.zeros(64, np.float16), y), y.astype(np.float16))
+    assert np.array_equal(o.residual_add_ref(r, np.zeros(64)), r)
+    assert np.array_equal(o.residual_add_ref(r, y), r + y.astype(np.float16))
