@@ -180,6 +180,8 @@ def main():
     if args.diag:
         diag = timing_diagnostics(pkg, torch, layers, x2, outs, reps)
 
+    fused = fused_layer_leg(pkg, torch, gen, dev, layers, reps)
+
     gemm = {} if args.no_gemm else gemm_legs(pkg, torch, gen, dev)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 
@@ -209,9 +211,57 @@ def main():
                      "avg_us": round(dom_us, 3), "bytes_per_launch": DOMINANT_BYTES,
                      "timing": timing},
         "cpu_baseline": cpu,
-        "extra": {"gemm": gemm, **({"timing_diag": diag} if diag else {})},
+        "extra": {"decode_layer_fused_norms": fused, "gemm": gemm,
+                  **({"timing_diag": diag} if diag else {})},
     }
     print(json.dumps(line))
+
+
+def fused_layer_leg(pkg, torch, gen, dev, layers, reps):
+    """The same decode layer with the operators around the projections fused
+    in (LlamaModel.swift:288-331): rms_norm -> q|k|v, o, residual add +
+    rms_norm -> gate/up + SiLU x up, down + residual add.  Still 4 launches;
+    the norm weights (fp32) and the residual vectors add a few KB per layer."""
+    K, F = 3072, 8192
+    n1 = (1.0 + 0.1 * torch.randn(K, generator=gen, device=dev)).float()
+    n2 = (1.0 + 0.1 * torch.randn(K, generator=gen, device=dev)).float()
+    x = torch.randn(1, K, generator=gen, device=dev).half()
+    attn = torch.randn(1, K, generator=gen, device=dev).half()
+    qkv = torch.empty(1, 5120, device=dev, dtype=torch.float16)
+    o = torch.empty(1, K, device=dev, dtype=torch.float16)
+    res = torch.empty(1, K, device=dev, dtype=torch.float16)
+    act = torch.empty(1, F, device=dev, dtype=torch.float16)
+    out = torch.empty(1, K, device=dev, dtype=torch.float16)
+
+    def step(L):
+        w = L.w
+        pkg.rmsnorm_matmul_q4(x, n1, 1e-5, w["qkv_proj"][0], 5120, out=qkv)
+        pkg.linear(attn, w["o_proj"][0], 1, K, K, out=o)
+        pkg.residual_rmsnorm_matmul_q4_silu_mul(x, o, n2, 1e-5, w["gate_up_proj"][0],
+                                                w["gate_up_proj"][1], F, residual_out=res,
+                                                out=act)
+        pkg.matmul_q4_residual(act, w["down_proj"][0], res, 1, K, out=out)
+
+    for L in layers:
+        step(L)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for L in layers:
+            step(L)
+    g.replay()
+    torch.cuda.synchronize()
+    r = max(1, reps)
+    t0 = time.perf_counter()
+    for _ in range(r):
+        g.replay()
+    torch.cuda.synchronize()
+    us = 1e6 * (time.perf_counter() - t0) / (r * len(layers))
+    nbytes = LAYER_BYTES + 2 * K * 4 + 5 * 2 * K
+    return {"us_per_layer": round(us, 3), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "bytes_per_layer": nbytes, "launches_per_layer": 4,
+            "note": "rms_norm, residual add + rms_norm and the final residual add run inside "
+                    "the projections' kernels"}
 
 
 def traffic_run(pkg, torch, gen, dev):

@@ -137,6 +137,26 @@ int sltx_matmul_q4_ex(const void* x, int32_t x_dtype, const sltx_q4_weight* w, c
                       int32_t epilogue, void* out, int32_t out_dtype, int32_t M, int32_t N,
                       void* stream);
 
+/* GeGLU: out[M,N] fp16 = gelu_tanh(x.Wg^T) * (x.Wu^T), GELU-tanh with the
+ * inner clamp at +-10 (Kernels.swift:1785-1795), in one pass over both weight
+ * sets.  Replaces matmulQ4Fast(wi_0) + matmulQ4Fast(wi_1) +
+ * geluApproximateF16 + elemMulF16 in the T5 encoder FFN (T5Encoder.swift:191-199).
+ * The reference rounds the two products (and the GELU) to fp16 and multiplies
+ * in half precision; here both products stay fp32 and the result is rounded
+ * once.  M == 1 runs the GEMV, M > 1 the GEMM. */
+int sltx_matmul_q4_geglu(const void* x, const sltx_q4_weight* gate, const sltx_q4_weight* up,
+                         void* out, int32_t M, int32_t K, int32_t N, void* stream);
+
+/* embeddingQ4Batch(weight:scales:biases:tokenIds:K:groupSize:) -> Tensor [n, K]
+ * (Ops.swift:163-187; kernel embedding_q4_batch, Kernels.swift:368-396), and
+ * embeddingQ4 for one token (n = 1; Ops.swift:189-208, Kernels.swift:409-434):
+ * out[t, k] fp16 = half(float(q[id_t, k]) * s + b), fp32 math.  table is the
+ * quantized embedding (Llama ties it to the lm_head, ModelWeights.swift:126-130)
+ * with vocab rows; token_ids is device int32 [n].  Ids outside [0, vocab)
+ * give zero rows (the reference reads out of bounds).  out 16-byte aligned. */
+int sltx_embedding_q4(const sltx_q4_weight* table, int32_t vocab, const int32_t* token_ids,
+                      int32_t n, void* out, void* stream);
+
 /* ---- Decode-layer fusion: the operators on either side of the projections ----
  * Norm weights are fp32 (ModelWeights.swift:123,147-148 loads them as float).
  * rms_norm(v)[k] = half(r[k] * rsqrt(mean(v^2) + eps) * weight[k]), r = the

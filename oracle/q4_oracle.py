@@ -118,6 +118,25 @@ def residual_add_ref(residual: np.ndarray, y: np.ndarray) -> np.ndarray:
             + yh.astype(np.float32)).astype(np.float16)
 
 
+def embedding_q4_ref(w: np.ndarray, scales: np.ndarray, biases: np.ndarray, ids, group: int
+                     ) -> np.ndarray:
+    """embedding_q4_batch (Kernels.swift:368-396): rows ids of the 4-bit table,
+    out = half(float(q) * s + b) with the product and sum in fp32 (q*s is exact
+    in fp32, so a fused multiply-add rounds the same).  Ids outside
+    [0, vocab) give zero rows (where the reference reads out of bounds)."""
+    ids = np.asarray(ids, dtype=np.int64)
+    vocab, K = w.shape[0], w.shape[1] * 8
+    out = np.zeros((len(ids), K), dtype=np.float16)
+    ok = (ids >= 0) & (ids < vocab)
+    if ok.any():
+        r = ids[ok]
+        q = unpack_q4(w[r]).astype(np.float32)
+        s = np.repeat(np.asarray(scales[r], np.float16).astype(np.float32), group, axis=1)
+        b = np.repeat(np.asarray(biases[r], np.float16).astype(np.float32), group, axis=1)
+        out[ok] = (q * s + b).astype(np.float16)
+    return out
+
+
 # ----------------------------------------------------- bf16 (numpy has none) --
 
 def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:

@@ -49,6 +49,8 @@ EXPORTED = (
     "sltx_linear",
     "sltx_matmul_q4_silu_mul",
     "sltx_matmul_q4_ex",
+    "sltx_matmul_q4_geglu",
+    "sltx_embedding_q4",
     "sltx_rms_norm",
     "sltx_residual_rms_norm",
     "sltx_rmsnorm_matmul_q4",
@@ -104,6 +106,10 @@ def lib():
         L.sltx_matmul_q4_ex.argtypes = [P, I32, W, P, I32, P, I32, I32, I32, P]
         L.sltx_matmul_q4_ex.restype = ctypes.c_int
         F = ctypes.c_float
+        L.sltx_matmul_q4_geglu.argtypes = [P, W, W, P, I32, I32, I32, P]
+        L.sltx_matmul_q4_geglu.restype = ctypes.c_int
+        L.sltx_embedding_q4.argtypes = [W, I32, P, I32, P, P]
+        L.sltx_embedding_q4.restype = ctypes.c_int
         L.sltx_rms_norm.argtypes = [P, P, F, P, I32, I32, P]
         L.sltx_residual_rms_norm.argtypes = [P, P, P, F, P, P, I32, I32, P]
         L.sltx_rmsnorm_matmul_q4.argtypes = [P, P, F, W, P, I32, P]
@@ -293,4 +299,25 @@ def matmul_q4_residual(x, w: Q4Weight, residual, M, N, out=None, stream=None):
     cw = w.c()
     check(lib().sltx_matmul_q4_residual(_ptr(x), ctypes.byref(cw), _ptr(residual), _ptr(out), M,
                                         N, _stream(stream)))
+    return out
+
+
+def matmul_q4_geglu(x, gate: Q4Weight, up: Q4Weight, M, K, N, out=None, stream=None):
+    """gelu_tanh(x.Wg^T) * (x.Wu^T) -> fp16 [M, N]: the T5 encoder FFN's
+    gate/up (T5Encoder.swift:191-199)."""
+    out = _new((M, N), _torch().float16, x) if out is None else out
+    g, u = gate.c(), up.c()
+    check(lib().sltx_matmul_q4_geglu(_ptr(x), ctypes.byref(g), ctypes.byref(u), _ptr(out), M, K,
+                                     N, _stream(stream)))
+    return out
+
+
+def embedding_q4(table: Q4Weight, vocab, token_ids, out=None, stream=None):
+    """embeddingQ4Batch (Ops.swift:163-187): dequantized rows [n, K] fp16 of a
+    4-bit table for int32 device token ids."""
+    n = int(token_ids.numel())
+    out = _new((n, table.K), _torch().float16, token_ids) if out is None else out
+    cw = table.c()
+    check(lib().sltx_embedding_q4(ctypes.byref(cw), vocab, _ptr(token_ids), n, _ptr(out),
+                                  _stream(stream)))
     return out

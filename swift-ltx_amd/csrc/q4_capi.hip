@@ -98,6 +98,7 @@ struct GemvFuse {
     float eps = 0.0f;
     void* res_out = nullptr;
     const void* residual = nullptr;
+    bool gelu = false;
 };
 
 int run_gemv(const char* fn, const void* x, const sltx_q4_weight& w0, const sltx_q4_weight* w1,
@@ -121,6 +122,7 @@ int run_gemv(const char* fn, const void* x, const sltx_q4_weight& w0, const sltx
     p.eps = fz.eps;
     p.res_out = static_cast<uint16_t*>(fz.res_out);
     p.residual = static_cast<const uint16_t*>(fz.residual);
+    p.gelu = fz.gelu ? 1 : 0;
     return finish(launch_gemv(p, w1 != nullptr, st), fn);
 }
 
@@ -175,7 +177,7 @@ int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w
     p.gshift = log2_group(w0.group_size);
     p.tiles_m = p.tiles_n = 0;
     p.y_dtype = y_dtype;
-    p.epilogue = w1 ? kEpiSiluMul : epilogue;
+    p.epilogue = w1 ? (epilogue == kEpiGeluMul ? kEpiGeluMul : kEpiSiluMul) : epilogue;
     p.residual = static_cast<const uint16_t*>(residual);
     p.ws = nullptr;
     p.splits = 1;
@@ -299,6 +301,61 @@ int sltx_matmul_q4_ex(const void* x, int32_t x_dtype, const sltx_q4_weight* w, c
     if ((rc = ensure_device()) != kOk) return rc;
     return run_gemm(fn, x, x_dtype, *w, nullptr, bias, epilogue, out, out_dtype, M, w->K, N,
                     static_cast<hipStream_t>(stream));
+}
+
+int sltx_matmul_q4_geglu(const void* x, const sltx_q4_weight* gate, const sltx_q4_weight* up,
+                         void* out, int32_t M, int32_t K, int32_t N, void* stream) {
+    const char* fn = "sltx_matmul_q4_geglu";
+    if (!gate || !up) return fail(kErrInvalid, "%s: null weight descriptor", fn);
+    if (gate->K != K || up->K != K) return fail(kErrInvalid, "%s: weight K mismatch", fn);
+    if (gate->group_size != up->group_size)
+        return fail(kErrInvalid, "%s: gate and up group_size differ", fn);
+    int rc = check_weight(fn, x, gate->weight, gate->scales, gate->biases, out, M, K, N,
+                          gate->group_size);
+    if (rc != kOk) return rc;
+    rc = check_weight(fn, x, up->weight, up->scales, up->biases, out, M, K, N, up->group_size);
+    if (rc != kOk) return rc;
+    if (!aligned(out, 2)) return fail(kErrInvalid, "%s: misaligned out", fn);
+    if (M == 0 || N == 0) return kOk;
+    if ((rc = ensure_device()) != kOk) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (M == 1) {
+        GemvFuse fz;
+        fz.gelu = true;
+        return run_gemv(fn, x, *gate, up, out, K, N, st, fz);
+    }
+    return run_gemm(fn, x, kF16, *gate, up, nullptr, kEpiGeluMul, out, kF16, M, K, N, st);
+}
+
+int sltx_embedding_q4(const sltx_q4_weight* table, int32_t vocab, const int32_t* token_ids,
+                      int32_t n, void* out, void* stream) {
+    const char* fn = "sltx_embedding_q4";
+    if (!table) return fail(kErrInvalid, "%s: null weight descriptor", fn);
+    if (vocab < 0 || n < 0) return fail(kErrInvalid, "%s: negative vocab (%d) or n (%d)", fn, vocab, n);
+    const int K = table->K, g = table->group_size;
+    if (K <= 0 || K % 32 != 0) return fail(kErrInvalid, "%s: K (%d) must be a positive multiple of 32", fn, K);
+    if (g <= 0 || g % 8 != 0 || K % g != 0)
+        return fail(kErrInvalid, "%s: group_size %d invalid for K %d", fn, g, K);
+    if (log2_group(g) < 0) return fail(kErrUnsupported, "%s: group_size %d unsupported (32, 64 or 128)", fn, g);
+    if (n == 0) return kOk;
+    if (!table->weight || !table->scales || !table->biases || !token_ids || !out)
+        return fail(kErrInvalid, "%s: null pointer argument", fn);
+    if (!aligned(table->weight, 4) || !aligned(table->scales, 2) || !aligned(table->biases, 2) ||
+        !aligned(token_ids, 4) || !aligned(out, 16))
+        return fail(kErrInvalid, "%s: misaligned pointer (out must be 16-byte aligned)", fn);
+    int rc = ensure_device();
+    if (rc != kOk) return rc;
+    EmbedParams p;
+    p.w = table->weight;
+    p.s = table->scales;
+    p.b = table->biases;
+    p.ids = token_ids;
+    p.out = static_cast<uint16_t*>(out);
+    p.vocab = vocab;
+    p.K = K;
+    p.groups = K / g;
+    p.glog2 = log2_group(g) + 5;
+    return finish(launch_embedding_q4(p, n, static_cast<hipStream_t>(stream)), fn);
 }
 
 int sltx_rms_norm(const void* x, const float* weight, float eps, void* out, int32_t rows,

@@ -85,7 +85,14 @@ enum Epilogue : int {
     kEpiSiluMul = 1,   // y = silu(x.Wg^T) * (x.Wu^T)  (two weight sets)
     kEpiGeluTanh = 2,  // y = gelu_tanh(x.W^T + bias)
     kEpiResidual = 3,  // y = half(residual + half(x.W^T))  (linear + elemAdd, fp16 out)
+    kEpiGeluMul = 4,   // y = gelu_tanh(x.Wg^T) * (x.Wu^T)  (two weight sets; T5 GeGLU)
 };
+
+// Gated activations of the two-weight-set epilogues: SiLU (Llama MLP) or
+// GELU-tanh (T5 GeGLU, T5Encoder.swift:191-199), on fp32 products.
+__device__ __forceinline__ float glu_f32(bool gelu, float gate, float up) {
+    return gelu ? gelu_tanh_f32(gate) * up : silu_mul_f32(gate, up);
+}
 
 // linear(...) then elemAdd(residual, .) (LlamaModel.swift:330-331): the
 // projection is rounded to fp16 first, then added in fp32 and rounded again

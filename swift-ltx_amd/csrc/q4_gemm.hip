@@ -619,7 +619,7 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
                 const int r = i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
                 const int m = m0 + r;
                 if (m >= p.M || n >= p.N) continue;
-                store_out(p, (size_t)m * p.N + n, silu_mul_f32(acc[i][0][v], xb[r * 32 + lrow]));
+                store_out(p, (size_t)m * p.N + n, glu_f32(p.epilogue == kEpiGeluMul, acc[i][0][v], xb[r * 32 + lrow]));
             }
         return;
     }
@@ -632,7 +632,7 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
             if constexpr (SILU) {   // NT == 2: tile 0 gate, tile 1 up
                 const int n = out_col(0);
                 if (n >= p.N) continue;
-                store_out(p, (size_t)m * p.N + n, silu_mul_f32(acc[i][0][v], acc[i][NT - 1][v]));
+                store_out(p, (size_t)m * p.N + n, glu_f32(p.epilogue == kEpiGeluMul, acc[i][0][v], acc[i][NT - 1][v]));
             } else {
 #pragma unroll
                 for (int j = 0; j < NT; ++j) {
@@ -663,7 +663,7 @@ __global__ __launch_bounds__(256) void q4_splitk_reduce_kernel(GemmParams p) {
         if (SILU) u += src[s * stride + p.N];
     }
     if (SILU)
-        store_out(p, idx, silu_mul_f32(a, u));
+        store_out(p, idx, glu_f32(p.epilogue == kEpiGeluMul, a, u));
     else
         epi_store(p, idx, (int)n, a);
 }
@@ -680,7 +680,7 @@ struct GemmPlan {
 };
 
 static GemmPlan plan_gemm(const GemmParams& p, bool allow_split) {
-    const bool silu = p.epilogue == kEpiSiluMul;
+    const bool silu = p.epilogue == kEpiSiluMul || p.epilogue == kEpiGeluMul;
     const int bn_out = silu ? BN / 2 : BN;
     const int tiles_n = (p.N + bn_out - 1) / bn_out;
     const int nk = (p.K + BK - 1) / BK;
@@ -743,7 +743,7 @@ static void launch_dtype(const GemmParams& p, bool a_bf16, bool silu, long grid,
 }
 
 hipError_t launch_gemm(GemmParams p, bool a_bf16, hipStream_t st) {
-    const bool silu = p.epilogue == kEpiSiluMul;
+    const bool silu = p.epilogue == kEpiSiluMul || p.epilogue == kEpiGeluMul;
     GemmPlan plan = plan_gemm(p, p.ws != nullptr);
     p.tiles_m = plan.tiles_m;
     p.tiles_n = plan.tiles_n;

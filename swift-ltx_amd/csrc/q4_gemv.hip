@@ -115,6 +115,7 @@ struct GemvStage {
     u32x4 w[NW][CPL];
     uint32_t s[NW][CPL];
     uint32_t b[NW][CPL];
+    uint32_t res;   // residual of the row (residual epilogue only)
 };
 
 // Row index is clamped into [0, N) so every load is unconditional (a
@@ -139,6 +140,8 @@ __device__ __forceinline__ void gemv_load(GemvStage<CPL, NW>& st, const GemvPara
             st.b[m][i] = B[gi];
         }
     }
+    // fetched with the weights so the epilogue does not wait a memory latency
+    if (p.residual) st.res = p.residual[rr];
 }
 
 template <int L, int CPL, int NW>
@@ -159,8 +162,8 @@ __device__ __forceinline__ void gemv_compute_store(const GemvStage<CPL, NW>& st,
         acc[m] = row_reduce<L>(a);
     }
     if (kl == 0 && r < p.N) {
-        const float out = NW == 2 ? silu_mul_f32(acc[0], acc[NW - 1]) : acc[0];
-        p.y[r] = p.residual ? residual_add_f16(p.residual[r], out) : f2h(out);
+        const float out = NW == 2 ? glu_f32(p.gelu, acc[0], acc[NW - 1]) : acc[0];
+        p.y[r] = p.residual ? residual_add_f16((uint16_t)st.res, out) : f2h(out);
     }
 }
 
@@ -193,6 +196,10 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(GemvParams p, int T) {
     f32x4 nw[NORM ? XPT : 1][8];
 #pragma unroll
     for (int u = 0; u < XPT; ++u) {
+        // Waves whose chunks all lie past NCH load nothing (wave-uniform
+        // branch): at K = 3072 only 96 of 256 threads own a chunk, and
+        // redundant loads would only delay the weight loads queued behind them.
+        if (__builtin_amdgcn_readfirstlane((int)(threadIdx.x & ~63u)) + 256 * u >= NCH) continue;
         const int c = threadIdx.x + 256 * u;
         const int cc = c < NCH ? c : NCH - 1;
         const f16x8* xp = reinterpret_cast<const f16x8*>(p.x + (size_t)cc * 32);
@@ -375,7 +382,7 @@ __global__ __launch_bounds__(256) void q4_gemv_generic_kernel(GemvParams p) {
         acc[m] = row_reduce<64>(a);
     }
     if (lane == 0) {
-        float out = SWIGLU ? silu_mul_f32(acc[0], acc[NW - 1]) : acc[0];
+        float out = SWIGLU ? glu_f32(p.gelu, acc[0], acc[NW - 1]) : acc[0];
         p.y[r] = p.residual ? residual_add_f16(p.residual[r], out) : f2h(out);
     }
 }

@@ -30,6 +30,7 @@ struct GemvParams {
     uint16_t* res_out;      // [K] fp16 residual stream out (kResidualRms)
     // Epilogue: y = half(residual + half(x . W^T)) when non-null.
     const uint16_t* residual;
+    int gelu;               // two weight sets: gelu_tanh(g) * u instead of silu(g) * u
 };
 
 enum GemvPro : int { kProNone = 0, kProRms = 1, kProResidualRms = 2 };
@@ -57,7 +58,19 @@ struct GemmParams {
     int split_tiles;        // k-tiles per split (even), filled by launch_gemm
 };
 
+// 4-bit embedding gather (q4_embed.hip).
+struct EmbedParams {
+    const uint32_t* w;      // [vocab, K/8]
+    const uint16_t* s;      // [vocab, K/g]
+    const uint16_t* b;
+    const int32_t* ids;     // [n] token ids (device)
+    uint16_t* out;          // [n, K] fp16
+    int vocab, K, groups;
+    int glog2;              // log2(g)
+};
+
 hipError_t launch_gemv(const GemvParams& p, bool swiglu, hipStream_t st);
+hipError_t launch_embedding_q4(const EmbedParams& p, int n, hipStream_t st);
 // Bytes of split-K workspace the launch of `p` would use (0: it does not split).
 size_t gemm_workspace_bytes(const GemmParams& p);
 // Launches the GEMM; splits K only if p.ws is non-null (and then needs

@@ -196,3 +196,66 @@ def test_decode_layer_fused_matches_unfused(pkg, dev):
     assert_parity(qkv.cpu().numpy(), qkv2.cpu().numpy().astype(np.float64), TOL_GEMV, "qkv")
     assert_parity(act.cpu().numpy(), act2.cpu().numpy().astype(np.float64), TOL_GEMV, "gate/up")
     assert_parity(out.cpu().numpy(), out2.cpu().numpy().astype(np.float64), TOL_GEMV, "layer out")
+
+
+# (M, N, K, g): GEMV; GEMM; GEMM with split-K (few output tiles); generic path
+GEGLU_SHAPES = [(1, 2048, 512, 64), (33, 1024, 512, 64), (750, 512, 8192, 64), (7, 100, 96, 32)]
+
+
+@pytest.mark.parametrize("M,N,K,g", GEGLU_SHAPES)
+def test_geglu(pkg, dev, M, N, K, g):
+    """T5 encoder FFN gate/up (T5Encoder.swift:191-199) against the fp64
+    closed form with GELU-tanh (inner clamp +-10)."""
+    import torch
+    x, [(wg, sg, bg), (wu, su, bu)] = o.make_inputs(M, N, K, g, seed=M + N + K, n_weights=2)
+    gv = o.matmul_q4_f64(x, wg, sg, bg, g)
+    uv = o.matmul_q4_f64(x, wu, su, bu, g)
+    ref = o.gelu_tanh_f64(gv) * uv
+    y = pkg.matmul_q4_geglu(to_dev(x, dev), q4w(pkg, wg, sg, bg, K, g, dev),
+                            q4w(pkg, wu, su, bu, K, g, dev), M, K, N)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy().astype(np.float64)
+    assert o.max_rel_err(y, ref) <= GATE
+    # each product carries the matmul bound, propagated through gelu(g) * u
+    tol = TOL_GEMV if M == 1 else TOL_GEMM_F16
+    eg = tol["rtol"] * np.abs(gv) + tol["atol_rms"] * np.sqrt(np.mean(gv ** 2))
+    eu = tol["rtol"] * np.abs(uv) + tol["atol_rms"] * np.sqrt(np.mean(uv ** 2))
+    allow = (_gelu_slope(gv) * np.abs(uv) * eg + np.abs(o.gelu_tanh_f64(gv)) * eu
+             + np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64))
+    d = np.abs(y - ref)
+    assert np.all(d <= allow), f"geglu M={M}: worst {np.max(d / allow):.2f}x the allowance"
+
+
+def _gelu_slope(v):
+    """|d gelu_tanh / dv| at v, plus a margin for the curvature over the
+    (small) error interval."""
+    c = 0.7978845608
+    t = np.tanh(np.clip(c * (v + 0.044715 * v ** 3), -10, 10))
+    d = 0.5 * (1 + t) + 0.5 * v * (1 - t * t) * c * (1 + 3 * 0.044715 * v * v)
+    return np.abs(d) + 0.2
+
+
+@pytest.mark.parametrize("vocab,K,g", [(1000, 3072, 64), (300, 96, 32), (50, 4096, 128)])
+def test_embedding_q4(pkg, dev, vocab, K, g):
+    """Bit-exact against the oracle (fp32 q*s + b, one fp16 rounding); ids out
+    of range give zero rows."""
+    import torch
+    _, [(w, s, b)] = o.make_inputs(1, vocab, K, g, seed=vocab + K)
+    rng = np.random.default_rng(vocab)
+    ids = np.concatenate([rng.integers(0, vocab, 37), [0, vocab - 1, -1, vocab, 5]]).astype(np.int32)
+    out = pkg.embedding_q4(q4w(pkg, w, s, b, K, g, dev), vocab, to_dev(ids, dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), o.embedding_q4_ref(w, s, b, ids, g))
+
+
+def test_embedding_q4_full_vocab(pkg, dev):
+    """Llama-3.2-3B tied embedding size (128256 x 3072): sampled ids."""
+    import torch
+    vocab, K, g = 128256, 3072, 64
+    _, [(w, s, b)] = gpu_inputs(1, vocab, K, g, seed=31, dev=dev)
+    ids = np.random.default_rng(2).integers(0, vocab, 64).astype(np.int32)
+    out = pkg.embedding_q4(pkg.Q4Weight(w, s, b, K, g), vocab, to_dev(ids, dev))
+    torch.cuda.synchronize()
+    idt = torch.from_numpy(ids.astype(np.int64)).to(dev)
+    ref = o.embedding_q4_ref(host(w[idt]), host(s[idt]), host(b[idt]), np.arange(len(ids)), g)
+    assert np.array_equal(out.cpu().numpy(), ref)

@@ -318,3 +318,26 @@ def test_residual_add_ref():
     assert np.array_equal(o.residual_add_ref(np.zeros(64, np.float16), y), y.astype(np.float16))
     assert np.array_equal(o.residual_add_ref(r, np.zeros(64)), r)
     assert np.array_equal(o.residual_add_ref(r, y), r + y.astype(np.float16))
+
+
+def test_embedding_q4_ref_exact_and_closed_form(oracle):
+    """Rows match the fp64 closed form exactly when every value is
+    representable (power-of-two scales, integer biases) and to 1 fp16 ulp
+    otherwise; bad ids give zero rows; row order follows the ids."""
+    from oracle import q4_oracle as o
+    rng = np.random.default_rng(9)
+    V, K, g = 40, 256, 64
+    q = rng.integers(0, 16, (V, K))
+    w = o.pack_q4(q)
+    s = (2.0 ** -rng.integers(0, 6, (V, K // g))).astype(np.float16)
+    b = rng.integers(-8, 8, (V, K // g)).astype(np.float16)
+    ids = [3, 0, 39, 3, -1, 40]
+    out = o.embedding_q4_ref(w, s, b, ids, g)
+    ref = o.dequant_f64(w, s, b, g)
+    assert np.array_equal(out[:4].astype(np.float64), ref[[3, 0, 39, 3]])
+    assert not out[4:].any()
+    s2 = (np.abs(rng.standard_normal((V, K // g))) * 0.02).astype(np.float16)
+    b2 = (-8 * s2.astype(np.float32)).astype(np.float16)
+    out2 = o.embedding_q4_ref(w, s2, b2, [5, 17], g).astype(np.float64)
+    ref2 = o.dequant_f64(w, s2, b2, g)[[5, 17]]
+    assert np.all(np.abs(out2 - ref2) <= np.spacing(np.abs(ref2).astype(np.float16)))
