@@ -203,6 +203,64 @@ int sltx_residual_rmsnorm_matmul_q4_silu_mul(const void* a, const void* b,
 int sltx_matmul_q4_residual(const void* x, const sltx_q4_weight* w, const void* residual,
                             void* out, int32_t M, int32_t N, void* stream);
 
+/* ---- safetensors weights (SafeTensorsFile, SafeTensors.swift:41-118) ----
+ * Reads the files swift-ltx's loader reads (ModelWeights.swift:40-154) into
+ * caller-allocated device memory.  The header (8-byte LE length, JSON object,
+ * optional "__metadata__") is parsed once at open; entries with other dtypes
+ * are skipped as in the reference.  A tensor whose byte range does not match
+ * its shape and dtype or lies outside the file makes the file invalid (the
+ * reference would read out of bounds).  A file handle may be shared between
+ * threads (device reads are serialised per handle). */
+typedef struct sltx_st_file sltx_st_file;
+
+/* TensorDType (SafeTensors.swift:15-31) */
+typedef enum sltx_st_dtype {
+    SLTX_ST_F32 = 0,
+    SLTX_ST_F16 = 1,
+    SLTX_ST_BF16 = 2,
+    SLTX_ST_I8 = 3,
+    SLTX_ST_U8 = 4,
+    SLTX_ST_I32 = 5,
+    SLTX_ST_U32 = 6
+} sltx_st_dtype;
+
+/* TensorInfo (SafeTensors.swift:7-13): offset is relative to the data region. */
+typedef struct sltx_st_info {
+    int32_t dtype;      /* sltx_st_dtype */
+    int32_t ndim;       /* <= 8 */
+    int64_t shape[8];
+    uint64_t offset;
+    uint64_t nbytes;
+} sltx_st_info;
+
+/* SafeTensorsFile(url:) (SafeTensors.swift:41-89).  *out is closed with
+ * sltx_st_close. */
+int sltx_st_open(const char* path, sltx_st_file** out);
+void sltx_st_close(sltx_st_file* file);
+
+/* Number of tensors, and their names in sorted order (index < count). */
+int sltx_st_num_tensors(const sltx_st_file* file);
+const char* sltx_st_name(const sltx_st_file* file, int32_t index);
+
+/* tensors[name] (SafeTensors.swift:35): SLTX_ERR_INVALID if absent. */
+int sltx_st_info_of(const sltx_st_file* file, const char* name, sltx_st_info* out);
+
+/* readTensorRaw(_:into:) (SafeTensors.swift:205-214): raw bytes to host memory. */
+int sltx_st_read_host(sltx_st_file* file, const char* name, void* dst, uint64_t capacity);
+
+/* readTensorIntoBuffer (SafeTensors.swift:175-186) with a HIP device
+ * destination: raw bytes, streamed through pinned staging buffers and
+ * enqueued on stream; returns once the data is on the device.  Reading into
+ * an offset of a larger allocation concatenates tensors (e.g. q|k|v rows). */
+int sltx_st_read_device(sltx_st_file* file, const char* name, void* dst, uint64_t capacity,
+                        void* stream);
+
+/* loadFloat (ModelWeights.swift:96-108, bf16 branch of :66-75): an F32, F16
+ * or BF16 tensor widened to fp32 on the host while streaming, count = capacity
+ * in floats. */
+int sltx_st_read_device_f32(sltx_st_file* file, const char* name, float* dst, uint64_t count,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

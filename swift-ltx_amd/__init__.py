@@ -56,6 +56,14 @@ EXPORTED = (
     "sltx_rmsnorm_matmul_q4",
     "sltx_residual_rmsnorm_matmul_q4_silu_mul",
     "sltx_matmul_q4_residual",
+    "sltx_st_open",
+    "sltx_st_close",
+    "sltx_st_num_tensors",
+    "sltx_st_name",
+    "sltx_st_info_of",
+    "sltx_st_read_host",
+    "sltx_st_read_device",
+    "sltx_st_read_device_f32",
 )
 
 
@@ -77,6 +85,13 @@ class CQ4Weight(ctypes.Structure):
 
 
 _lib = None
+
+
+class CStInfo(ctypes.Structure):
+    """sltx_st_info: TensorInfo (SafeTensors.swift:7-13)."""
+    _fields_ = [("dtype", ctypes.c_int32), ("ndim", ctypes.c_int32),
+                ("shape", ctypes.c_int64 * 8), ("offset", ctypes.c_uint64),
+                ("nbytes", ctypes.c_uint64)]
 
 
 def lib():
@@ -118,6 +133,24 @@ def lib():
         for n in ("sltx_rms_norm", "sltx_residual_rms_norm", "sltx_rmsnorm_matmul_q4",
                   "sltx_residual_rmsnorm_matmul_q4_silu_mul", "sltx_matmul_q4_residual"):
             getattr(L, n).restype = ctypes.c_int
+        VP = ctypes.c_void_p
+        L.sltx_st_open.argtypes = [ctypes.c_char_p, ctypes.POINTER(VP)]
+        L.sltx_st_open.restype = ctypes.c_int
+        L.sltx_st_close.argtypes = [VP]
+        L.sltx_st_close.restype = None
+        L.sltx_st_num_tensors.argtypes = [VP]
+        L.sltx_st_num_tensors.restype = ctypes.c_int
+        L.sltx_st_name.argtypes = [VP, I32]
+        L.sltx_st_name.restype = ctypes.c_char_p
+        L.sltx_st_info_of.argtypes = [VP, ctypes.c_char_p, ctypes.POINTER(CStInfo)]
+        L.sltx_st_info_of.restype = ctypes.c_int
+        U64 = ctypes.c_uint64
+        L.sltx_st_read_host.argtypes = [VP, ctypes.c_char_p, VP, U64]
+        L.sltx_st_read_host.restype = ctypes.c_int
+        L.sltx_st_read_device.argtypes = [VP, ctypes.c_char_p, VP, U64, VP]
+        L.sltx_st_read_device.restype = ctypes.c_int
+        L.sltx_st_read_device_f32.argtypes = [VP, ctypes.c_char_p, VP, U64, VP]
+        L.sltx_st_read_device_f32.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -321,3 +354,82 @@ def embedding_q4(table: Q4Weight, vocab, token_ids, out=None, stream=None):
     check(lib().sltx_embedding_q4(ctypes.byref(cw), vocab, _ptr(token_ids), n, _ptr(out),
                                   _stream(stream)))
     return out
+
+
+# ------------------------------------------------------------ safetensors ---
+# sltx_st_dtype codes -> (safetensors name, numpy dtype)
+ST_DTYPES = {0: ("F32", "float32"), 1: ("F16", "float16"), 2: ("BF16", "uint16"),
+             3: ("I8", "int8"), 4: ("U8", "uint8"), 5: ("I32", "int32"), 6: ("U32", "uint32")}
+
+
+class TensorInfo:
+    """TensorInfo (SafeTensors.swift:7-13)."""
+
+    def __init__(self, name, c):
+        self.name = name
+        self.dtype = ST_DTYPES[c.dtype][0]
+        self.code = c.dtype
+        self.shape = tuple(int(c.shape[i]) for i in range(c.ndim))
+        self.offset = int(c.offset)
+        self.byte_count = int(c.nbytes)
+
+    def __repr__(self):
+        return f"TensorInfo({self.name!r}, {self.dtype}, {self.shape}, {self.byte_count} B)"
+
+
+class SafeTensorsFile:
+    """SafeTensorsFile (SafeTensors.swift:41-118) over the native reader:
+    header parsed at open; tensors read to host (numpy) or straight into a
+    device tensor."""
+
+    def __init__(self, path):
+        self.path = os.fspath(path)
+        h = ctypes.c_void_p()
+        check(lib().sltx_st_open(self.path.encode(), ctypes.byref(h)))
+        self._h = h
+        L = lib()
+        self.tensors = {}
+        for i in range(L.sltx_st_num_tensors(h)):
+            name = L.sltx_st_name(h, i).decode()
+            c = CStInfo()
+            check(L.sltx_st_info_of(h, name.encode(), ctypes.byref(c)))
+            self.tensors[name] = TensorInfo(name, c)
+
+    def close(self):
+        if self._h:
+            lib().sltx_st_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def read_host(self, name):
+        """readTensorRaw (SafeTensors.swift:205-214) -> numpy array (BF16 as uint16 bits)."""
+        import numpy as np
+        info = self.tensors[name]
+        out = np.empty(info.shape, dtype=ST_DTYPES[info.code][1])
+        check(lib().sltx_st_read_host(self._h, name.encode(), out.ctypes.data, out.nbytes))
+        return out
+
+    def read_device(self, name, out, byte_offset=0, stream=None):
+        """Raw bytes of `name` into device tensor `out` at byte_offset."""
+        cap = out.numel() * out.element_size() - byte_offset
+        check(lib().sltx_st_read_device(self._h, name.encode(), out.data_ptr() + byte_offset, cap,
+                                        _stream(stream)))
+        return out
+
+    def read_device_f32(self, name, out, stream=None):
+        """loadFloat (ModelWeights.swift:96-108): F32/F16/BF16 widened to fp32."""
+        check(lib().sltx_st_read_device_f32(self._h, name.encode(), out.data_ptr(), out.numel(),
+                                            _stream(stream)))
+        return out
+
+
+def load_safetensors(directory):
+    """loadSafeTensors(from:) (SafeTensors.swift:256-262): every *.safetensors
+    file in the directory, sorted by file name."""
+    names = sorted(f for f in os.listdir(directory) if f.endswith(".safetensors"))
+    return [SafeTensorsFile(os.path.join(directory, f)) for f in names]

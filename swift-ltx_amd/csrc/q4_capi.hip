@@ -16,9 +16,22 @@
 #include "swiftltx_q4.h"
 
 namespace sltx {
-namespace {
 
 thread_local std::string g_last_error;
+
+// Records the thread's last error message and returns code (shared with the
+// safetensors reader, q4_st.hip).
+int set_error(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+namespace {
 
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int fail(int code, const char* fmt, ...) {

@@ -83,4 +83,7 @@ hipError_t launch_rms_norm(const uint16_t* a, const uint16_t* b, const float* w,
                            uint16_t* res_out, uint16_t* out, int rows, int dim, hipStream_t st);
 int gemv_pick_lanes(int K, int* cpl_out);
 
+// Sets the calling thread's sltx_last_error() message; returns code.
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
 }  // namespace sltx
