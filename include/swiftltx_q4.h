@@ -13,9 +13,10 @@
  * Conventions (all entry points):
  *   - Every pointer is a device pointer the caller allocated; the library never
  *     frees or keeps them.  Outputs are written, never read.
- *   - Memory: the only device memory the library allocates is a split-K
- *     workspace (fp32 partial sums) for GEMMs with too few output tiles to
- *     fill the GPU (e.g. M=750 x N=3072).  There is one per (device, stream),
+ *   - Memory: the only device memory the library allocates is a per-stream
+ *     workspace: fp32 partial sums for GEMMs with too few output tiles to
+ *     fill the GPU (split-K, e.g. M=750 x N=3072), and the probabilities and
+ *     candidate list of sltx_sample_top_p.  There is one per (device, stream),
  *     grown on first need to at least twice its old size; a replaced buffer
  *     is never freed (a graph captured earlier may still use it), so every
  *     buffer lives until the process exits.  A stream being captured into a
@@ -202,6 +203,35 @@ int sltx_residual_rmsnorm_matmul_q4_silu_mul(const void* a, const void* b,
  * must not otherwise overlap it, nor x. */
 int sltx_matmul_q4_residual(const void* x, const sltx_q4_weight* w, const void* residual,
                             void* out, int32_t M, int32_t N, void* stream);
+
+/* ---- Token selection after the lm_head (LlamaModel.swift:153,161) ----
+ * Both read n logits (SLTX_F16 or SLTX_F32, device) and write one int32 token
+ * id to device memory, so the next step's embedding gather can consume it
+ * without a host round trip. */
+
+/* argmax(_:) -> Int  (Ops.swift:757-781): the first index of the maximum.
+ * NaNs never win; a NaN at index 0 gives 0, as the reference's strict ">"
+ * scan from element 0 does. */
+int sltx_argmax(const void* logits, int32_t dtype, int32_t n, int32_t* out_index, void* stream);
+
+/* sample(_:temperature:topP:repetitionPenalty:seenTokens:) -> Int
+ * (Ops.swift:785-806, sampleFromLogits Ops.swift:2060-2098), in fp32:
+ * each distinct id of seen[0..n_seen) in [0, n) has its logit divided by
+ * repetition_penalty when positive, else multiplied; all logits are divided
+ * by temperature; softmax; tokens ordered by probability descending (ties by
+ * ascending id: the reference's sort is unstable); the shortest prefix whose
+ * running sum reaches top_p is kept (all tokens if none does); then
+ * r = u * (that sum) and the first token of the prefix at which r minus the
+ * running probabilities is <= 0 is chosen.  u is the caller's uniform draw in
+ * [0, 1) (the reference calls Float.random).  temperature, top_p and
+ * repetition_penalty > 0; n <= 2^24.  Running sums are exact (integer masses
+ * floor(p * 2^52)) where the reference sums sequentially in fp32, and the
+ * softmax denominator is a fixed-order tree: a draw within fp32 rounding of
+ * a token boundary may pick the neighbouring token.  Uses the per-stream workspace (see above): under
+ * graph capture it must already hold sample workspace for this n. */
+int sltx_sample_top_p(const void* logits, int32_t dtype, int32_t n, float temperature,
+                      float top_p, float repetition_penalty, const int32_t* seen,
+                      int32_t n_seen, float u, int32_t* out_index, void* stream);
 
 /* ---- safetensors weights (SafeTensorsFile, SafeTensors.swift:41-118) ----
  * Reads the files swift-ltx's loader reads (ModelWeights.swift:40-154) into

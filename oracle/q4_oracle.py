@@ -137,6 +137,98 @@ def embedding_q4_ref(w: np.ndarray, scales: np.ndarray, biases: np.ndarray, ids,
     return out
 
 
+# -------------------------------------------------------- token selection --
+
+def argmax_ref(logits) -> int:
+    """argmax (Ops.swift:757-781): scan from element 0 keeping the first
+    strictly greater value, so NaNs never win and a NaN at index 0 gives 0."""
+    v = np.asarray(logits).astype(np.float32)
+    if np.isnan(v[0]):
+        return 0
+    return int(np.argmax(np.where(np.isnan(v), -np.inf, v)))
+
+
+def sample_ref(logits, temperature: float, top_p: float, penalty: float, seen, u: float,
+               detail: bool = False, gpu_sums: bool = False):
+    """sample + sampleFromLogits (Ops.swift:785-806, 2060-2098) in fp32:
+    penalty on each distinct seen id < n (divide positive, multiply the rest),
+    divide by temperature, softmax, order by probability descending, shortest
+    prefix with running sum >= top_p (else all), r = u * that sum, then
+    r -= p_i until r <= 0.  The reference's sort is unstable; ties are ordered
+    here by ascending id.
+
+    gpu_sums=False: the reference's sequential fp32 sums (numpy's
+    add.accumulate is sequential) for the softmax denominator and the running
+    sums.
+    gpu_sums=True: the sums the GPU kernel forms instead, for a tighter check
+    of it: the softmax denominator as 1024 strided sequential partial sums
+    folded by a halving tree, and exact running sums of the integer masses
+    floor(p * 2^52): cutoff = first token whose inclusive mass reaches
+    ceil(top_p * 2^52), chosen = first whose inclusive mass reaches
+    ceil(u * mass at the cutoff).
+
+    Returns the token, or (token, info) with the order, sorted probabilities,
+    cutoff and running sum there when detail is set."""
+    f32 = np.float32
+    lg = np.asarray(logits).astype(f32).copy()
+    n = lg.size
+    pen = f32(penalty)
+    for t in sorted(set(int(t) for t in (seen if seen is not None else []))):
+        if 0 <= t < n:
+            lg[t] = lg[t] / pen if lg[t] > 0 else lg[t] * pen
+    lg = lg / f32(temperature)
+    mx = f32(-3.4028234663852886e38)   # -greatestFiniteMagnitude
+    live = lg[~np.isnan(lg)]
+    if live.size:
+        mx = max(mx, f32(live.max()))
+    with np.errstate(over="ignore", under="ignore", invalid="ignore"):
+        e = np.exp(lg - mx).astype(f32)
+        if gpu_sums:
+            E = np.zeros(-(-n // 1024) * 1024, f32)
+            E[:n] = e
+            part = np.add.accumulate(E.reshape(-1, 1024), axis=0, dtype=f32)[-1].copy()
+            h = 512
+            while h:
+                part[:h] = part[:h] + part[h:2 * h]
+                h //= 2
+            s = part[0]
+        else:
+            s = np.add.accumulate(e, dtype=f32)[-1]
+        p = (e / s).astype(f32)
+    order = np.lexsort((np.arange(n), -p))
+    ps = p[order]
+    if gpu_sums:
+        mass = np.floor(ps.astype(np.float64) * 2.0 ** 52).astype(np.uint64)
+        cum = np.cumsum(mass, dtype=np.uint64)
+        t1 = np.uint64(math.ceil(min(float(f32(top_p)), 4.0) * 2.0 ** 52))
+        k1 = int(np.searchsorted(cum, t1, "left"))
+        cutoff = k1 + 1 if k1 < n else n
+        cum_prob = int(cum[cutoff - 1])
+        t2 = np.uint64(math.ceil(float(f32(u)) * float(cum_prob)))
+        tok = int(order[int(np.searchsorted(cum, t2, "left"))])
+        cum_out, r = cum_prob * 2.0 ** -52, float(t2) * 2.0 ** -52
+    else:
+        cum = np.add.accumulate(ps, dtype=f32)
+        hit = np.nonzero(cum >= f32(top_p))[0]
+        cutoff = int(hit[0]) + 1 if hit.size else n
+        cum_prob = cum[cutoff - 1]
+        r = f32(u) * cum_prob
+        walk = np.subtract.accumulate(np.concatenate([[r], ps[:cutoff]]).astype(f32),
+                                      dtype=f32)[1:]
+        le = np.nonzero(walk <= 0)[0]
+        tok = int(order[le[0]]) if le.size else int(order[0])
+        cum_out, r = float(cum_prob), float(r)
+    if detail:
+        info = {"order": order, "probs": ps, "cutoff": cutoff, "cum": cum_out, "r": r}
+        if not gpu_sums:   # the rounding the sequential fp32 sums carry here
+            c64 = np.cumsum(ps.astype(np.float64))
+            info["cum_err"] = np.abs(cum.astype(np.float64) - c64)
+            s64 = np.sum(e.astype(np.float64))
+            info["sum_rel_err"] = abs(float(s) - s64) / s64 if s64 > 0 else 0.0
+        return tok, info
+    return tok
+
+
 # ----------------------------------------------------- bf16 (numpy has none) --
 
 def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:

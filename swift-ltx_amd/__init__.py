@@ -56,6 +56,8 @@ EXPORTED = (
     "sltx_rmsnorm_matmul_q4",
     "sltx_residual_rmsnorm_matmul_q4_silu_mul",
     "sltx_matmul_q4_residual",
+    "sltx_argmax",
+    "sltx_sample_top_p",
     "sltx_st_open",
     "sltx_st_close",
     "sltx_st_num_tensors",
@@ -130,8 +132,11 @@ def lib():
         L.sltx_rmsnorm_matmul_q4.argtypes = [P, P, F, W, P, I32, P]
         L.sltx_residual_rmsnorm_matmul_q4_silu_mul.argtypes = [P, P, P, F, P, W, W, P, I32, P]
         L.sltx_matmul_q4_residual.argtypes = [P, W, P, P, I32, I32, P]
+        L.sltx_argmax.argtypes = [P, I32, I32, P, P]
+        L.sltx_sample_top_p.argtypes = [P, I32, I32, F, F, F, P, I32, F, P, P]
         for n in ("sltx_rms_norm", "sltx_residual_rms_norm", "sltx_rmsnorm_matmul_q4",
-                  "sltx_residual_rmsnorm_matmul_q4_silu_mul", "sltx_matmul_q4_residual"):
+                  "sltx_residual_rmsnorm_matmul_q4_silu_mul", "sltx_matmul_q4_residual",
+                  "sltx_argmax", "sltx_sample_top_p"):
             getattr(L, n).restype = ctypes.c_int
         VP = ctypes.c_void_p
         L.sltx_st_open.argtypes = [ctypes.c_char_p, ctypes.POINTER(VP)]
@@ -352,6 +357,42 @@ def embedding_q4(table: Q4Weight, vocab, token_ids, out=None, stream=None):
     out = _new((n, table.K), _torch().float16, token_ids) if out is None else out
     cw = table.c()
     check(lib().sltx_embedding_q4(ctypes.byref(cw), vocab, _ptr(token_ids), n, _ptr(out),
+                                  _stream(stream)))
+    return out
+
+
+def _logits_dtype(logits):
+    torch = _torch()
+    if logits.dtype == torch.float16:
+        return SLTX_F16
+    if logits.dtype == torch.float32:
+        return SLTX_F32
+    raise TypeError(f"logits must be float16 or float32, not {logits.dtype}")
+
+
+def argmax(logits, out=None, stream=None):
+    """argmax (Ops.swift:757-781) on the device: int32 [1] tensor holding the
+    first index of the maximum of a contiguous fp16/fp32 vector."""
+    out = _new((1,), _torch().int32, logits) if out is None else out
+    check(lib().sltx_argmax(_ptr(logits), _logits_dtype(logits), int(logits.numel()), _ptr(out),
+                            _stream(stream)))
+    return out
+
+
+def sample(logits, temperature=0.7, top_p=0.9, repetition_penalty=1.1, seen_tokens=None,
+           u=None, out=None, stream=None):
+    """sample(_:temperature:topP:repetitionPenalty:seenTokens:) (Ops.swift:785-806)
+    on the device -> int32 [1] tensor.  seen_tokens: int32 device tensor (or
+    None); u: uniform draw in [0, 1) (drawn here with Python's random when
+    None, as the reference draws Float.random)."""
+    import random
+    if u is None:
+        u = random.random()
+    out = _new((1,), _torch().int32, logits) if out is None else out
+    n_seen = 0 if seen_tokens is None else int(seen_tokens.numel())
+    check(lib().sltx_sample_top_p(_ptr(logits), _logits_dtype(logits), int(logits.numel()),
+                                  temperature, top_p, repetition_penalty,
+                                  _ptr(seen_tokens) if n_seen else None, n_seen, u, _ptr(out),
                                   _stream(stream)))
     return out
 

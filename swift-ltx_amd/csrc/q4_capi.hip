@@ -139,18 +139,20 @@ int run_gemv(const char* fn, const void* x, const sltx_q4_weight& w0, const sltx
     return finish(launch_gemv(p, w1 != nullptr, st), fn);
 }
 
-// Split-K workspace, one per (device, stream): calls on one stream are
-// ordered, so they can share it; other streams get their own.  It grows on
+// Per-stream workspace (split-K partial sums, sampling scratch), one per
+// (device, stream): calls on one stream are ordered, so they can share it;
+// other streams get their own.  It grows on
 // demand to at least twice its old size.  A replaced buffer is never freed:
 // graphs captured earlier may still name it, so it is kept (with the current
 // one) until the process ends; doubling bounds the retired total by the
 // current size.  A stream that is being captured into a graph never
-// allocates: if its workspace is missing or too small the GEMM runs unsplit.
+// allocates: if its workspace is missing or too small the GEMM runs unsplit
+// and sampling returns an error.
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> g_ws;
 std::vector<void*> g_ws_retired;
 
-float* splitk_workspace(hipStream_t st, size_t need) {
+float* stream_workspace(hipStream_t st, size_t need) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
     std::lock_guard<std::mutex> lk(g_ws_mu);
@@ -196,7 +198,7 @@ int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w
     p.splits = 1;
     p.split_tiles = 0;
     const size_t need = gemm_workspace_bytes(p);
-    if (need > 0) p.ws = splitk_workspace(st, need);
+    if (need > 0) p.ws = stream_workspace(st, need);
     return finish(launch_gemm(p, x_dtype == kBF16, st), fn);
 }
 
@@ -369,6 +371,58 @@ int sltx_embedding_q4(const sltx_q4_weight* table, int32_t vocab, const int32_t*
     p.groups = K / g;
     p.glog2 = log2_group(g) + 5;
     return finish(launch_embedding_q4(p, n, static_cast<hipStream_t>(stream)), fn);
+}
+
+int sltx_argmax(const void* logits, int32_t dtype, int32_t n, int32_t* out_index, void* stream) {
+    const char* fn = "sltx_argmax";
+    if (n <= 0) return fail(kErrInvalid, "%s: n must be positive (got %d)", fn, n);
+    if (dtype != kF16 && dtype != kF32)
+        return fail(kErrInvalid, "%s: dtype %d must be SLTX_F16 or SLTX_F32", fn, dtype);
+    if (!logits || !out_index) return fail(kErrInvalid, "%s: null pointer argument", fn);
+    if (!aligned(logits, dtype == kF32 ? 4 : 2) || !aligned(out_index, 4))
+        return fail(kErrInvalid, "%s: misaligned pointer", fn);
+    int rc = ensure_device();
+    if (rc != kOk) return rc;
+    return finish(launch_argmax(logits, dtype, n, out_index, static_cast<hipStream_t>(stream)), fn);
+}
+
+int sltx_sample_top_p(const void* logits, int32_t dtype, int32_t n, float temperature,
+                      float top_p, float repetition_penalty, const int32_t* seen, int32_t n_seen,
+                      float u, int32_t* out_index, void* stream) {
+    const char* fn = "sltx_sample_top_p";
+    if (n <= 0) return fail(kErrInvalid, "%s: n must be positive (got %d)", fn, n);
+    if (n > (1 << 24)) return fail(kErrInvalid, "%s: n = %d exceeds 2^24 tokens", fn, n);
+    if (dtype != kF16 && dtype != kF32)
+        return fail(kErrInvalid, "%s: dtype %d must be SLTX_F16 or SLTX_F32", fn, dtype);
+    if (!(temperature > 0.0f) || !(top_p > 0.0f) || !(repetition_penalty > 0.0f))
+        return fail(kErrInvalid, "%s: temperature, top_p and repetition_penalty must be positive", fn);
+    if (!(u >= 0.0f && u < 1.0f)) return fail(kErrInvalid, "%s: u must lie in [0, 1)", fn);
+    if (n_seen < 0) return fail(kErrInvalid, "%s: negative n_seen", fn);
+    if (!logits || !out_index || (n_seen > 0 && !seen))
+        return fail(kErrInvalid, "%s: null pointer argument", fn);
+    if (!aligned(logits, dtype == kF32 ? 4 : 2) || !aligned(out_index, 4) ||
+        (seen && !aligned(seen, 4)))
+        return fail(kErrInvalid, "%s: misaligned pointer", fn);
+    int rc = ensure_device();
+    if (rc != kOk) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    void* ws = stream_workspace(st, sample_workspace_bytes(n));
+    if (!ws)
+        return fail(kErrInvalid,
+                    "%s: no workspace for n = %d on this stream (it is being captured: sample "
+                    "once eagerly on the same stream first)", fn, n);
+    SampleParams p;
+    p.logits = logits;
+    p.dtype = dtype;
+    p.n = n;
+    p.temperature = temperature;
+    p.top_p = top_p;
+    p.penalty = repetition_penalty;
+    p.u = u;
+    p.seen = seen;
+    p.n_seen = n_seen;
+    p.out = out_index;
+    return finish(launch_sample(p, ws, st), fn);
 }
 
 int sltx_rms_norm(const void* x, const float* weight, float eps, void* out, int32_t rows,

@@ -69,8 +69,24 @@ struct EmbedParams {
     int glog2;              // log2(g)
 };
 
+// Token selection after the lm_head (q4_sample.hip).
+struct SampleParams {
+    const void* logits;     // [n] fp16 or fp32
+    int dtype;              // kF16 / kF32
+    int n;
+    float temperature, top_p, penalty, u;
+    const int32_t* seen;    // [n_seen] token ids (device)
+    int n_seen;
+    float* probs;           // workspace, filled by launch_sample
+    uint32_t* bitmap;
+    int32_t* out;           // [1] chosen token (device)
+};
+
 hipError_t launch_gemv(const GemvParams& p, bool swiglu, hipStream_t st);
 hipError_t launch_embedding_q4(const EmbedParams& p, int n, hipStream_t st);
+size_t sample_workspace_bytes(int n);
+hipError_t launch_argmax(const void* logits, int dtype, int n, int32_t* out, hipStream_t st);
+hipError_t launch_sample(SampleParams p, void* ws, hipStream_t st);
 // Bytes of split-K workspace the launch of `p` would use (0: it does not split).
 size_t gemm_workspace_bytes(const GemmParams& p);
 // Launches the GEMM; splits K only if p.ws is non-null (and then needs

@@ -218,3 +218,28 @@ def test_matmul_residual_validation(pkg):
     assert fn(ALIGNED, ctypes.byref(w), 0x40000, ALIGNED + 32, 1, 3072, None) == -1
     assert "overlaps x" in pkg.last_error()
     assert fn(ALIGNED, ctypes.byref(w), 0x40000, 0x40000, 0, 3072, None) == 0
+
+
+def test_argmax_and_sample_validation(pkg):
+    L = pkg.lib()
+    A, O = ALIGNED, 0x40000
+    assert L.sltx_argmax(A, 0, 0, O, None) == -1 and "positive" in pkg.last_error()
+    assert L.sltx_argmax(A, 1, 10, O, None) == -1 and "SLTX_F16" in pkg.last_error()   # bf16
+    assert L.sltx_argmax(None, 0, 10, O, None) == -1 and "null" in pkg.last_error()
+    assert L.sltx_argmax(A + 2, 2, 10, O, None) == -1 and "misaligned" in pkg.last_error()
+    fn = L.sltx_sample_top_p
+
+    def call(n=100, dt=0, t=0.7, p=0.9, r=1.1, seen=None, ns=0, u=0.5, logits=A, out=O):
+        return fn(logits, dt, n, t, p, r, seen, ns, u, out, None)
+    assert call(n=0) == -1 and "positive" in pkg.last_error()
+    assert call(n=(1 << 24) + 1) == -1 and "2^24" in pkg.last_error()
+    assert call(dt=1) == -1 and "SLTX_F16" in pkg.last_error()
+    for bad in (dict(t=0.0), dict(t=-1.0), dict(p=0.0), dict(r=0.0), dict(t=float("nan"))):
+        assert call(**bad) == -1 and "must be positive" in pkg.last_error(), bad
+    for u in (-0.1, 1.0, float("nan")):
+        assert call(u=u) == -1 and "[0, 1)" in pkg.last_error()
+    assert call(ns=-1) == -1 and "n_seen" in pkg.last_error()
+    assert call(ns=3, seen=None) == -1 and "null" in pkg.last_error()
+    assert call(out=None) == -1 and "null" in pkg.last_error()
+    assert call(out=O + 2) == -1 and "misaligned" in pkg.last_error()
+    assert call(seen=A + 1, ns=2) == -1 and "misaligned" in pkg.last_error()

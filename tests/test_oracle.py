@@ -341,3 +341,134 @@ def test_embedding_q4_ref_exact_and_closed_form(oracle):
     out2 = o.embedding_q4_ref(w, s2, b2, [5, 17], g).astype(np.float64)
     ref2 = o.dequant_f64(w, s2, b2, g)[[5, 17]]
     assert np.all(np.abs(out2 - ref2) <= np.spacing(np.abs(ref2).astype(np.float16)))
+
+
+# -------------------------------------------------------- token selection --
+# argmax_ref: a pure-Python transcription of the scan on small vectors, and
+# numpy's argmax (first occurrence) wherever no NaN is present.
+# sample_ref: a hand-worked nucleus, the closed forms that a vanishing top_p
+# reduces sampling to argmax of the penalised logits and u = 0 to the most
+# probable token, penalties applied once per distinct id, and an inverse-CDF
+# count over a grid of u that reproduces the fp64 softmax of logits / T.
+
+def _scan_argmax(v):
+    best, bv = 0, float(v[0])
+    for i in range(1, len(v)):
+        if float(v[i]) > bv:
+            best, bv = i, float(v[i])
+    return best
+
+
+def test_argmax_ref_scan_and_numpy():
+    from oracle import q4_oracle as o
+    rng = np.random.default_rng(20)
+    for n in (1, 2, 17, 300):
+        for dt in (np.float16, np.float32):
+            v = rng.standard_normal(n).astype(dt)
+            assert o.argmax_ref(v) == int(np.argmax(v)) == _scan_argmax(v)
+            v = rng.integers(-3, 3, n).astype(dt)            # many ties: first wins
+            assert o.argmax_ref(v) == int(np.argmax(v)) == _scan_argmax(v)
+    nan, inf = np.nan, np.inf
+    for v in ([nan, 5.0, 7.0], [1.0, nan, 7.0, 7.0], [-inf, -inf], [-inf, nan], [2.0, inf, inf, nan],
+              [nan], [0.0, -0.0]):
+        a = np.array(v, dtype=np.float32)
+        assert o.argmax_ref(a) == _scan_argmax(a), v
+    assert o.argmax_ref(np.array([nan, 5.0], np.float32)) == 0
+    assert o.argmax_ref(np.array([1.0, nan, 7.0, 7.0], np.float32)) == 2
+
+
+def test_sample_ref_hand_worked_nucleus():
+    """p = [0.1, 0.2, 0.3, 0.4]: order 3, 2, 1, 0; top_p 0.65 keeps {3, 2}
+    (running sums 0.4, 0.7) and r = u * 0.7 picks 3 below r = 0.4, else 2."""
+    from oracle import q4_oracle as o
+    lg = np.log(np.array([1.0, 2.0, 3.0, 4.0])).astype(np.float32)
+    for u, tok in ((0.0, 3), (0.5, 3), (0.6, 2), (0.9, 2), (0.999, 2)):
+        assert o.sample_ref(lg, 1.0, 0.65, 1.0, [], u) == tok, u
+    for u, tok in ((0.05, 3), (0.5, 2), (0.8, 1), (0.95, 0)):   # top_p 0.95: all four
+        assert o.sample_ref(lg, 1.0, 0.95, 1.0, [], u) == tok, u
+    t, info = o.sample_ref(lg, 1.0, 0.65, 1.0, [], 0.5, detail=True)
+    assert info["cutoff"] == 2 and list(info["order"]) == [3, 2, 1, 0]
+    assert abs(info["cum"] - 0.7) < 1e-6
+
+
+def test_sample_ref_tiny_top_p_is_penalised_argmax():
+    from oracle import q4_oracle as o
+    rng = np.random.default_rng(21)
+    for n in (5, 64, 1000):
+        lg = (rng.standard_normal(n) * 3).astype(np.float32)
+        seen = rng.integers(0, n, 7)
+        pen = lg.copy()
+        for t in set(seen.tolist()):
+            pen[t] = pen[t] / np.float32(1.3) if pen[t] > 0 else pen[t] * np.float32(1.3)
+        for u in (0.0, 0.37, 0.999):
+            for T in (0.5, 1.0, 2.0):
+                assert o.sample_ref(lg, T, 1e-9, 1.3, seen, u) == int(np.argmax(pen))
+
+
+def test_sample_ref_penalty_once_per_token_and_sign():
+    from oracle import q4_oracle as o
+    a = np.array([2.0, 1.7], np.float32)            # once: 1.818 > 1.7; twice: 1.653 < 1.7
+    assert o.sample_ref(a, 1.0, 1e-9, 1.1, [0, 0, 0], 0.5) == 0
+    b = np.array([-1.0, -1.05], np.float32)         # non-positive logits are multiplied
+    assert o.sample_ref(b, 1.0, 1e-9, 1.1, [0], 0.5) == 1
+    c = np.array([0.0, -0.01], np.float32)          # zero counts as non-positive: stays 0
+    assert o.sample_ref(c, 1.0, 1e-9, 5.0, [0], 0.5) == 0
+    assert o.sample_ref(a, 1.0, 1e-9, 1.1, [2, 99, -1], 0.5) == 0   # ids >= n are ignored
+
+
+def test_sample_ref_u_grid_reproduces_softmax():
+    """top_p above 1 keeps every token; over u = (j + 1/2) / G the walk is
+    the inverse CDF of the sorted probabilities, so token t is drawn
+    G * p_t times (within one count per token boundary), p = fp64
+    softmax(logits / T)."""
+    from oracle import q4_oracle as o
+    rng = np.random.default_rng(22)
+    lg = rng.standard_normal(12).astype(np.float32)
+    for T in (0.7, 1.0, 1.9):
+        G = 20000
+        counts = np.zeros(12, np.int64)
+        for j in range(G):
+            counts[o.sample_ref(lg, T, 1.5, 1.0, [], (j + 0.5) / G)] += 1
+        z = lg.astype(np.float64) / np.float64(np.float32(T))
+        p = np.exp(z - z.max())
+        p /= p.sum()
+        assert np.all(np.abs(counts - G * p) <= 2.0), (T, counts, G * p)
+
+
+def test_sample_ref_nucleus_support_and_renormalisation():
+    """For top_p < 1 only the shortest most-probable prefix reaching top_p is
+    drawn, in proportion to its renormalised probabilities."""
+    from oracle import q4_oracle as o
+    p = np.array([0.05, 0.3, 0.1, 0.25, 0.2, 0.1])
+    lg = np.log(p).astype(np.float32)
+    G = 10000
+    counts = np.zeros(6, np.int64)
+    for j in range(G):
+        counts[o.sample_ref(lg, 1.0, 0.7, 1.0, [], (j + 0.5) / G)] += 1
+    keep = [1, 3, 4]                                 # 0.3 + 0.25 + 0.2 = 0.75 >= 0.7
+    assert set(np.nonzero(counts)[0]) == set(keep)
+    assert np.all(np.abs(counts[keep] - G * p[keep] / 0.75) <= 2.0)
+
+
+def test_sample_ref_gpu_sums_agree_with_reference_sums():
+    """The exact-mass form differs from the reference's sequential fp32 sums
+    only by rounding: on the hand-worked nucleus and grids far from token
+    boundaries both give the same token."""
+    from oracle import q4_oracle as o
+    lg = np.log(np.array([1.0, 2.0, 3.0, 4.0])).astype(np.float32)
+    for top_p, u in ((0.65, 0.0), (0.65, 0.5), (0.65, 0.6), (0.95, 0.05), (0.95, 0.5),
+                     (0.95, 0.8), (0.95, 0.95), (1e-9, 0.7), (2.0, 0.3)):
+        assert o.sample_ref(lg, 1.0, top_p, 1.0, [], u, gpu_sums=True) == \
+            o.sample_ref(lg, 1.0, top_p, 1.0, [], u), (top_p, u)
+    rng = np.random.default_rng(23)
+    agree = 0
+    for k in range(200):
+        x = (rng.standard_normal(3000) * 2).astype(np.float32)
+        u = float(rng.random())
+        a = o.sample_ref(x, 0.8, 0.9, 1.1, [1, 2, 2], u, gpu_sums=True)
+        b, info = o.sample_ref(x, 0.8, 0.9, 1.1, [1, 2, 2], u, detail=True)
+        agree += a == b
+        pos = list(info["order"]).index(a)
+        c = np.cumsum(info["probs"].astype(np.float64))
+        assert c[pos] >= info["r"] - 1e-5 and (pos == 0 or c[pos - 1] <= info["r"] + 1e-5)
+    assert agree >= 190
