@@ -15,8 +15,9 @@
  *     frees or keeps them.  Outputs are written, never read.
  *   - Memory: the only device memory the library allocates is a per-stream
  *     workspace: fp32 partial sums for GEMMs with too few output tiles to
- *     fill the GPU (split-K, e.g. M=750 x N=3072), and the probabilities and
- *     candidate list of sltx_sample_top_p.  There is one per (device, stream),
+ *     fill the GPU (split-K, e.g. M=750 x N=3072), the block partials of
+ *     sltx_argmax, and the probabilities and candidate list of
+ *     sltx_sample_top_p.  There is one per (device, stream),
  *     grown on first need to at least twice its old size; a replaced buffer
  *     is never freed (a graph captured earlier may still use it), so every
  *     buffer lives until the process exits.  A stream being captured into a
@@ -211,7 +212,8 @@ int sltx_matmul_q4_residual(const void* x, const sltx_q4_weight* w, const void* 
 
 /* argmax(_:) -> Int  (Ops.swift:757-781): the first index of the maximum.
  * NaNs never win; a NaN at index 0 gives 0, as the reference's strict ">"
- * scan from element 0 does. */
+ * scan from element 0 does.  Uses 2 KB of the per-stream workspace (see
+ * above): under graph capture call it once eagerly on that stream first. */
 int sltx_argmax(const void* logits, int32_t dtype, int32_t n, int32_t* out_index, void* stream);
 
 /* sample(_:temperature:topP:repetitionPenalty:seenTokens:) -> Int

@@ -160,9 +160,11 @@ def sample_ref(logits, temperature: float, top_p: float, penalty: float, seen, u
     gpu_sums=False: the reference's sequential fp32 sums (numpy's
     add.accumulate is sequential) for the softmax denominator and the running
     sums.
-    gpu_sums=True: the sums the GPU kernel forms instead, for a tighter check
-    of it: the softmax denominator as 1024 strided sequential partial sums
-    folded by a halving tree, and exact running sums of the integer masses
+    gpu_sums=True: the sums the GPU kernels form instead, for a tighter check
+    of them: the softmax denominator over G = min(256, ceil(n/1024)) blocks of
+    256 threads, thread j adding tokens 4q..4q+3 for q = j, j + 256G, ... in
+    order, each block folding its threads by a halving tree, the block sums
+    added in block order; and exact running sums of the integer masses
     floor(p * 2^52): cutoff = first token whose inclusive mass reaches
     ceil(top_p * 2^52), chosen = first whose inclusive mass reaches
     ceil(u * mass at the cutoff).
@@ -184,14 +186,18 @@ def sample_ref(logits, temperature: float, top_p: float, penalty: float, seen, u
     with np.errstate(over="ignore", under="ignore", invalid="ignore"):
         e = np.exp(lg - mx).astype(f32)
         if gpu_sums:
-            E = np.zeros(-(-n // 1024) * 1024, f32)
+            G = min(256, -(-n // 1024))
+            T = 256 * G
+            R = -(-n // (4 * T))
+            E = np.zeros(R * 4 * T, f32)
             E[:n] = e
-            part = np.add.accumulate(E.reshape(-1, 1024), axis=0, dtype=f32)[-1].copy()
-            h = 512
+            seq = E.reshape(R, T, 4).transpose(0, 2, 1).reshape(R * 4, T)
+            blk = np.add.accumulate(seq, axis=0, dtype=f32)[-1].reshape(G, 256).copy()
+            h = 128
             while h:
-                part[:h] = part[:h] + part[h:2 * h]
+                blk[:, :h] = blk[:, :h] + blk[:, h:2 * h]
                 h //= 2
-            s = part[0]
+            s = np.add.accumulate(blk[:, 0], dtype=f32)[-1]
         else:
             s = np.add.accumulate(e, dtype=f32)[-1]
         p = (e / s).astype(f32)

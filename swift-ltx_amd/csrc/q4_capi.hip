@@ -383,7 +383,13 @@ int sltx_argmax(const void* logits, int32_t dtype, int32_t n, int32_t* out_index
         return fail(kErrInvalid, "%s: misaligned pointer", fn);
     int rc = ensure_device();
     if (rc != kOk) return rc;
-    return finish(launch_argmax(logits, dtype, n, out_index, static_cast<hipStream_t>(stream)), fn);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    void* ws = stream_workspace(st, argmax_workspace_bytes());
+    if (!ws)
+        return fail(kErrInvalid,
+                    "%s: no workspace on this stream (it is being captured: call it once eagerly "
+                    "on the same stream first)", fn);
+    return finish(launch_argmax(logits, dtype, n, out_index, ws, st), fn);
 }
 
 int sltx_sample_top_p(const void* logits, int32_t dtype, int32_t n, float temperature,

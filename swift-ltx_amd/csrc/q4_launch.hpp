@@ -77,15 +77,24 @@ struct SampleParams {
     float temperature, top_p, penalty, u;
     const int32_t* seen;    // [n_seen] token ids (device)
     int n_seen;
-    float* probs;           // workspace, filled by launch_sample
-    uint32_t* bitmap;
     int32_t* out;           // [1] chosen token (device)
+    // carved from the workspace by launch_sample
+    float* probs;           // [n] logits -> exp -> probabilities
+    uint32_t* bitmap;       // [n/32] seen ids
+    float* mpart;           // block maxima
+    float* spart;           // block sums
+    uint32_t* h0cnt;        // level-0 histogram (4096 bins)
+    unsigned long long* h0mass;
+    uint32_t* ccount;       // compacted candidates
+    uint2* cand;            // [n] (probability bits, id)
 };
 
 hipError_t launch_gemv(const GemvParams& p, bool swiglu, hipStream_t st);
 hipError_t launch_embedding_q4(const EmbedParams& p, int n, hipStream_t st);
 size_t sample_workspace_bytes(int n);
-hipError_t launch_argmax(const void* logits, int dtype, int n, int32_t* out, hipStream_t st);
+size_t argmax_workspace_bytes();
+hipError_t launch_argmax(const void* logits, int dtype, int n, int32_t* out, void* ws,
+                         hipStream_t st);
 hipError_t launch_sample(SampleParams p, void* ws, hipStream_t st);
 // Bytes of split-K workspace the launch of `p` would use (0: it does not split).
 size_t gemm_workspace_bytes(const GemmParams& p);

@@ -3,14 +3,13 @@
 // argmax (Ops.swift:757-781) and temperature / top-p / repetition-penalty
 // sampling (sample, Ops.swift:785-810; sampleFromLogits, Ops.swift:2060-2098),
 // which the reference runs on the CPU over all vocabulary logits per token.
-// One workgroup of 1024 threads; the logits are read from HBM once into an fp32
-// workspace (L2-resident, 0.5 MB for 128256 tokens).
 //
 // The probabilities follow the reference's fp32 steps: penalty (divide
 // positive, multiply non-positive logits of the distinct seen tokens), divide
-// by temperature, softmax (max, exp, sum, divide).  The softmax denominator is
-// a fixed-order sum (per-thread strided sums, then a halving tree) instead of
-// a sequential loop.
+// by temperature, softmax (max, exp, sum, divide).  The softmax denominator
+// is a fixed-order sum: each grid thread adds its tokens in index order, a
+// block folds its 256 threads by a halving tree, and the block sums are added
+// in block order.
 // The nucleus and the draw use exact running sums instead of the reference's
 // sequential fp32 ones: each probability p carries the integer mass
 // floor(p * 2^52), and in the order (p descending, id ascending; the
@@ -18,36 +17,41 @@
 // running mass reaches ceil(top_p * 2^52) (all tokens if none does), and the
 // chosen token is the first whose inclusive running mass reaches
 // ceil(u * mass at the cutoff) -- the reference's "r -= p until r <= 0".
-// Nothing is sorted: both positions are weighted radix selects over the key
-// (p bits, then 2^24-1-id), 8 bits a pass, with per-digit counts and masses
-// in LDS; a pass stops early once its digit holds a single token.
+//
+// Nothing is sorted in HBM.  Tokens are ranked by the 56-bit key
+// D = (bits of p) << 24 | (2^24 - 1 - id), descending, and both positions are
+// weighted radix selects over D, 12 bits a level:
+//   sample_init     (only with seen ids) mark them in a bitmap
+//   sample_scale    l = penalised logit / temperature; block maxima; clears
+//                   the level-0 histogram
+//   sample_exp      e = exp(l - max); block sums
+//   sample_prob     p = e / sum; level-0 histogram (p bits 31..20: count and
+//                   mass per bin)
+//   sample_gather   each block finds, from the histogram, the bin holding the
+//                   cutoff and the bins the draw can reach, and compacts their
+//                   tokens (no grid-wide fence or last-block hand-off: on a
+//                   chip whose XCDs have separate L2s those cost more than
+//                   re-reading the 48 KB histogram per block)
+//   sample_select   one workgroup: up to 64 candidates are sorted in one
+//                   wave's registers and scanned; more go through levels 1-4
+//                   (in LDS when they fit), a level stopping once its bin
+//                   holds a single token
 #include "q4_common.hpp"
 #include "q4_launch.hpp"
 
 namespace sltx {
 namespace {
 
-constexpr int kSampleThreads = 1024;
-constexpr int kSelPasses = 7;              // 4 over the probability bits, 3 over the id
-constexpr uint32_t kIdMask = 0xFFFFFFu;    // ids < 2^24
+constexpr int kGridThreads = 256;   // grid kernels: 4 consecutive tokens a thread per step
+constexpr int kMaxBlocks = 256;
+constexpr int kSelThreads = 1024;   // sample_select / sample_init
+constexpr int kBins = 4096;         // 12-bit digits
+constexpr int kCandLds = 8192;      // candidates sample_select holds in LDS
+constexpr uint32_t kIdMask = 0xFFFFFFu;
 
 __device__ __forceinline__ float load_logit(const void* p, int dtype, int i) {
     if (dtype == kF32) return reinterpret_cast<const float*>(p)[i];
     return h2f(reinterpret_cast<const uint16_t*>(p)[i]);
-}
-
-// block reductions (fixed order: per-thread partials, then a tree over LDS)
-template <typename T, typename Op>
-__device__ T block_reduce(T v, T* red, Op op) {
-    red[threadIdx.x] = v;
-    __syncthreads();
-    for (int s = kSampleThreads / 2; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s) red[threadIdx.x] = op(red[threadIdx.x], red[threadIdx.x + s]);
-        __syncthreads();
-    }
-    const T r = red[0];
-    __syncthreads();
-    return r;
 }
 
 // floor(p * 2^52) for a non-negative fp32 p given by its bits (0 below 2^-52;
@@ -61,248 +65,605 @@ __device__ __forceinline__ unsigned long long mass_of(uint32_t key) {
     return sh <= -24 ? 0ull : m >> -sh;
 }
 
-// digit d of the order key: probability bits 31..0, then lo = 2^24-1-id bits
-// 23..0, 8 bits a digit, most significant first
-__device__ __forceinline__ uint32_t digit_of(int d, uint32_t key, uint32_t lo) {
-    return d < 4 ? (key >> (24 - 8 * d)) & 255u : (lo >> (16 - 8 * (d - 4))) & 255u;
+__device__ __forceinline__ unsigned long long order_key(uint32_t key, uint32_t id) {
+    return ((unsigned long long)key << 24) | (kIdMask - id);
 }
 
-__device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+__device__ __forceinline__ uint32_t lanes_below(unsigned long long mask) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
-struct SelHist {
-    uint32_t cnt[kSelPasses][256];
-    unsigned long long mass[kSelPasses][256];
-    uint32_t pk[kSelPasses], pl[kSelPasses];   // prefixes each pass was counted under
-    int valid[kSelPasses];
-};
+__device__ __forceinline__ unsigned long long target_top_p(float top_p) {
+    return (unsigned long long)ceil(fmin((double)top_p, 4.0) * 0x1p52);
+}
 
-struct SelState {
-    uint32_t pk, mk, pl, ml;     // key / lo prefix and mask chosen so far
-    unsigned long long above;    // mass of the tokens before the current digit
-    unsigned long long cum;      // found: inclusive mass at the token; else the total
-    int found, done, idx;
-};
+__device__ __forceinline__ unsigned long long target_draw(float u, unsigned long long cum) {
+    return (unsigned long long)ceil((double)u * (double)cum);
+}
 
-// Weighted select: the first token, in key-descending order, whose inclusive
-// running mass reaches target.  A pass's histogram is kept and reused by a
-// later select that reaches the same prefix.  Whole block; ends synchronised.
-__device__ void weighted_select(const float* pr, int n, unsigned long long target, SelState& S,
-                                SelHist& H) {
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    if (tid == 0) {
-        S.pk = S.mk = S.pl = S.ml = 0u;
-        S.above = S.cum = 0ull;
-        S.found = S.done = 0;
-        S.idx = -1;
+// Exclusive prefix sum over the block's threads (in thread order).
+template <int NT>
+__device__ unsigned long long block_excl_scan(unsigned long long v, unsigned long long* wsum) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    unsigned long long x = v;
+    for (int o = 1; o < 64; o <<= 1) {
+        const unsigned long long y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) wsum[wid] = x;
+    __syncthreads();
+    if (wid == 0) {
+        unsigned long long w = lane < NT / 64 ? wsum[lane] : 0ull;
+        for (int o = 1; o < NT / 64; o <<= 1) {
+            const unsigned long long y = __shfl_up(w, o, 64);
+            if (lane >= o) w += y;
+        }
+        if (lane < NT / 64) wsum[lane] = w;
     }
     __syncthreads();
-    for (int d = 0; d < kSelPasses; ++d) {
-        const uint32_t pk = S.pk, mk = S.mk, pl = S.pl, ml = S.ml;
-        const bool cached = H.valid[d] && H.pk[d] == pk && H.pl[d] == pl;
-        __syncthreads();   // everyone has read S before thread 0 updates it
-        if (!cached) {
-            for (int b = tid; b < 256; b += kSampleThreads) {
-                H.cnt[d][b] = 0u;
-                H.mass[d][b] = 0ull;
-            }
-            __syncthreads();
-            // wave-uniform loop: every lane runs every iteration (the
-            // aggregation below shuffles across the whole wave)
-            for (int i0 = tid & ~63; i0 < n; i0 += kSampleThreads) {
-                const int i = i0 + lane;
-                const uint32_t key = i < n ? __float_as_uint(pr[i]) : 0u;
-                const uint32_t lo = kIdMask - (uint32_t)i;
-                const bool act = i < n && (key & mk) == pk && (lo & ml) == pl;
-                const uint32_t b = digit_of(d, key, lo);
-                const unsigned long long m = mass_of(key);
-                if (d == 0) {
-                    // the first digit (sign + exponent bits) is shared by most
-                    // of a wave: one atomic per distinct digit
-                    unsigned long long rem = __ballot(act);
-                    while (rem) {
-                        const int leader = __ffsll((long long)rem) - 1;
-                        const uint32_t bl = __builtin_amdgcn_readlane(b, leader);
-                        const bool mine = act && b == bl;
-                        const unsigned long long same = __ballot(mine);
-                        const unsigned long long ms = wave_sum_u64(mine ? m : 0ull);
-                        if (lane == leader) {
-                            atomicAdd(&H.cnt[d][bl], (uint32_t)__popcll(same));
-                            atomicAdd(&H.mass[d][bl], ms);
-                        }
-                        rem &= ~same;
-                    }
-                } else if (act) {
-                    atomicAdd(&H.cnt[d][b], 1u);
-                    if (m) atomicAdd(&H.mass[d][b], m);
-                }
-            }
-            __syncthreads();
+    const unsigned long long r = x - v + (wid > 0 ? wsum[wid - 1] : 0ull);
+    __syncthreads();
+    return r;
+}
+
+struct BinSel {
+    int found, bin;
+    uint32_t cnt;
+    unsigned long long excl, incl, total;
+};
+
+struct SelScratch {
+    unsigned long long wsum[16];
+    int best;
+};
+
+// kBins bins in descending bin order, after `above` mass, spread over the
+// block (BPT consecutive bins a thread).  load() reads the bins and scans
+// their masses; find(target) gives the highest non-empty bin whose inclusive
+// running mass reaches target (found), its exclusive / inclusive mass and
+// count, and the total.  Whole block; cnt and mass may be global or LDS.
+// Both end synchronised.
+template <int NT>
+struct BinScan {
+    static constexpr int BPT = kBins / NT;
+    uint32_t c[BPT];
+    unsigned long long m[BPT];
+    unsigned long long excl, tot;
+    int top;   // this thread's bins: top, top-1, ..., top-BPT+1
+
+    __device__ void load(const uint32_t* cnt, const unsigned long long* mass,
+                         unsigned long long above, SelScratch& sc) {
+        top = kBins - 1 - (int)threadIdx.x * BPT;
+        tot = 0ull;
+#pragma unroll
+        for (int k = 0; k < BPT; ++k) {
+            c[k] = cnt[top - k];
+            m[k] = mass[top - k];
+            tot += m[k];
         }
-        if (tid == 0) {
-            if (!cached) {
-                H.valid[d] = 1;
-                H.pk[d] = pk;
-                H.pl[d] = pl;
-            }
-            unsigned long long above = S.above;
-            int sel = -1;
-            for (int b = 255; b >= 0; --b) {
-                if (!H.cnt[d][b]) continue;
-                const unsigned long long m = H.mass[d][b];
-                if (above + m >= target) {
-                    sel = b;
-                    break;
-                }
-                above += m;
-            }
-            if (sel < 0) {          // target beyond the total mass
-                S.cum = above;
-                S.done = 1;
-            } else {
-                if (d < 4) {
-                    S.pk = pk | ((uint32_t)sel << (24 - 8 * d));
-                    S.mk = mk | (255u << (24 - 8 * d));
-                } else {
-                    S.pl = pl | ((uint32_t)sel << (16 - 8 * (d - 4)));
-                    S.ml = ml | (255u << (16 - 8 * (d - 4)));
-                }
-                S.above = above;
-                S.cum = above + H.mass[d][sel];
-                if (H.cnt[d][sel] == 1u) {
-                    S.found = 1;
-                    S.done = 1;
-                }
-            }
-        }
-        __syncthreads();
-        if (S.done) break;
+        excl = above + block_excl_scan<NT>(tot, sc.wsum);
     }
-    if (S.found) {   // the one token under the final prefix
-        const uint32_t pk = S.pk, mk = S.mk, pl = S.pl, ml = S.ml;
-        for (int i = tid; i < n; i += kSampleThreads) {
-            const uint32_t key = __float_as_uint(pr[i]);
-            const uint32_t lo = kIdMask - (uint32_t)i;
-            if ((key & mk) == pk && (lo & ml) == pl) S.idx = i;
+
+    __device__ void find(unsigned long long target, BinSel& out, SelScratch& sc) {
+        if (threadIdx.x == 0) sc.best = -1;
+        __syncthreads();
+        int best = -1;
+        unsigned long long run = excl;
+#pragma unroll
+        for (int k = 0; k < BPT; ++k) {
+            run += m[k];
+            if (best < 0 && c[k] && run >= target) best = top - k;
+        }
+        if (best >= 0) atomicMax(&sc.best, best);
+        __syncthreads();
+        const int B = sc.best;
+        if ((int)threadIdx.x == NT - 1) {
+            out.total = excl + tot;
+            out.found = B >= 0;
+        }
+        if (B >= 0 && B <= top && B > top - BPT) {
+            unsigned long long e = excl, mb = 0ull;
+            uint32_t cb = 0u;
+#pragma unroll
+            for (int k = 0; k < BPT; ++k) {
+                if (k < top - B) e += m[k];
+                if (k == top - B) {
+                    mb = m[k];
+                    cb = c[k];
+                }
+            }
+            out.bin = B;
+            out.excl = e;
+            out.incl = e + mb;
+            out.cnt = cb;
         }
         __syncthreads();
     }
+};
+
+struct LevelHist {
+    uint32_t cnt[kBins];
+    unsigned long long mass[kBins];
+    uint32_t id[kBins];
+};
+
+// Levels 1-4 of the weighted select inside level-0 bin `bin` (exclusive mass
+// `above`): the token whose inclusive running mass first reaches target.
+// Whole block; returns the id (-1 only for non-finite input) and sets cum_out
+// to its inclusive mass.
+__device__ int select_in_bin(const uint2* cand, int C, int bin, unsigned long long above,
+                             unsigned long long target, LevelHist& H, SelScratch& sc, BinSel& bs,
+                             unsigned long long& cum_out) {
+    const int tid = threadIdx.x;
+    unsigned long long P = (unsigned long long)bin << 44;
+    unsigned long long Mk = 0xFFFull << 44;
+    for (int lev = 1; lev <= 4; ++lev) {
+        const int shift = lev == 1 ? 32 : lev == 2 ? 20 : lev == 3 ? 8 : 0;
+        const unsigned long long wmask = lev == 4 ? 0xFFull : 0xFFFull;
+        for (int b = tid; b < kBins; b += kSelThreads) {
+            H.cnt[b] = 0u;
+            H.mass[b] = 0ull;
+        }
+        __syncthreads();
+        for (int c = tid; c < C; c += kSelThreads) {
+            const uint2 e = cand[c];
+            const unsigned long long D = order_key(e.x, e.y);
+            if ((D & Mk) != P) continue;
+            const int dg = (int)((D >> shift) & wmask);
+            atomicAdd(&H.cnt[dg], 1u);
+            const unsigned long long m = mass_of(e.x);
+            if (m) atomicAdd(&H.mass[dg], m);
+            H.id[dg] = e.y;   // read only when the bin holds one token
+        }
+        __syncthreads();
+        BinScan<kSelThreads> scan;
+        scan.load(H.cnt, H.mass, above, sc);
+        scan.find(target, bs, sc);
+        if (!bs.found) return -1;
+        P |= (unsigned long long)bs.bin << shift;
+        Mk |= wmask << shift;
+        above = bs.excl;
+        if (bs.cnt == 1u) {
+            cum_out = bs.incl;
+            const int id = (int)H.id[bs.bin];
+            __syncthreads();
+            return id;
+        }
+    }
+    return -1;   // not reached: the full key is unique
+}
+
+// The single token of level-0 bin `bin` among the candidates.
+__device__ int only_in_bin(const uint2* cand, int C, int bin, int* s_id) {
+    if (threadIdx.x == 0) *s_id = -1;
+    __syncthreads();
+    for (int c = threadIdx.x; c < C; c += kSelThreads) {
+        const uint2 e = cand[c];
+        if ((int)(e.x >> 20) == bin) *s_id = (int)e.y;
+    }
+    __syncthreads();
+    const int r = *s_id;
+    __syncthreads();
+    return r;
+}
+
+// argmax helpers: NaNs never win, ties go to the lower index
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+    return bi < 0 || v > bv || (v == bv && i < bi);
+}
+
+__device__ void block_best(float& bv, int& bi, float* rv, int* ri) {
+    const int t = threadIdx.x;
+    rv[t] = bv;
+    ri[t] = bi;
+    __syncthreads();
+    for (int s = kGridThreads / 2; s > 0; s >>= 1) {
+        if (t < s && ri[t + s] >= 0 && better(rv[t + s], ri[t + s], rv[t], ri[t])) {
+            rv[t] = rv[t + s];
+            ri[t] = ri[t + s];
+        }
+        __syncthreads();
+    }
+    bv = rv[0];
+    bi = ri[0];
 }
 
 }  // namespace
 
-// argmax: first index of the maximum (NaNs never win; NaN at index 0 -> 0).
-__global__ __launch_bounds__(kSampleThreads) void argmax_kernel(const void* logits, int dtype,
-                                                                int n, int32_t* out) {
-    __shared__ float rv[kSampleThreads];
-    __shared__ int ri[kSampleThreads];
+// ------------------------------------------------------------------ argmax --
+// Per-block first maxima, then the first maximum of those; a NaN at index 0
+// gives 0 (the reference's strict ">" scan from element 0).
+
+__global__ __launch_bounds__(kGridThreads) void argmax_partial_kernel(const void* logits, int dtype,
+                                                                      int n, float* pv, int* pi) {
+    __shared__ float rv[kGridThreads];
+    __shared__ int ri[kGridThreads];
     float bv = 0.0f;
     int bi = -1;
-    for (int i = threadIdx.x; i < n; i += kSampleThreads) {
-        const float v = load_logit(logits, dtype, i);
-        if (v != v) continue;
-        if (bi < 0 || v > bv) {   // strided increasing i: first maximum per thread
-            bv = v;
-            bi = i;
+    const int T = gridDim.x * kGridThreads;
+    for (int q = blockIdx.x * kGridThreads + threadIdx.x; 4 * q < n; q += T) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = 4 * q + k;
+            if (i >= n) break;
+            const float v = load_logit(logits, dtype, i);
+            if (v == v && (bi < 0 || v > bv)) {   // increasing i: first maximum
+                bv = v;
+                bi = i;
+            }
         }
     }
-    rv[threadIdx.x] = bv;
-    ri[threadIdx.x] = bi;
+    block_best(bv, bi, rv, ri);
+    if (threadIdx.x == 0) {
+        pv[blockIdx.x] = bv;
+        pi[blockIdx.x] = bi;
+    }
+}
+
+__global__ __launch_bounds__(kGridThreads) void argmax_final_kernel(const void* logits, int dtype,
+                                                                    const float* pv, const int* pi,
+                                                                    int blocks, int32_t* out) {
+    __shared__ float rv[kGridThreads];
+    __shared__ int ri[kGridThreads];
+    float bv = 0.0f;
+    int bi = -1;
+    if ((int)threadIdx.x < blocks) {
+        bv = pv[threadIdx.x];
+        bi = pi[threadIdx.x];
+    }
+    block_best(bv, bi, rv, ri);
+    if (threadIdx.x == 0) {
+        const float v0 = load_logit(logits, dtype, 0);
+        *out = (v0 != v0 || bi < 0) ? 0 : bi;
+    }
+}
+
+// ---------------------------------------------------------------- sampling --
+
+// launched only when there are seen ids
+__global__ __launch_bounds__(kSelThreads) void sample_init_kernel(SampleParams p) {
+    for (int w = threadIdx.x; w < (p.n + 31) / 32; w += kSelThreads) p.bitmap[w] = 0u;
     __syncthreads();
-    for (int s = kSampleThreads / 2; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s) {
-            const float ov = rv[threadIdx.x + s];
-            const int oi = ri[threadIdx.x + s];
-            const int mi = ri[threadIdx.x];
-            if (oi >= 0 && (mi < 0 || ov > rv[threadIdx.x] || (ov == rv[threadIdx.x] && oi < mi))) {
-                rv[threadIdx.x] = ov;
-                ri[threadIdx.x] = oi;
+    for (int j = threadIdx.x; j < p.n_seen; j += kSelThreads) {
+        const int t = p.seen[j];
+        if (t >= 0 && t < p.n) atomicOr(&p.bitmap[t >> 5], 1u << (t & 31));
+    }
+}
+
+// l = (seen ? penalised : logit) / temperature; block maxima
+__global__ __launch_bounds__(kGridThreads) void sample_scale_kernel(SampleParams p) {
+    __shared__ float red[kGridThreads];
+    const int n = p.n;
+    const int T = gridDim.x * kGridThreads;
+    for (int b = blockIdx.x * kGridThreads + threadIdx.x; b < kBins; b += T) {
+        p.h0cnt[b] = 0u;
+        p.h0mass[b] = 0ull;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) *p.ccount = 0u;
+    float mx = -3.402823466e38f;   // -greatestFiniteMagnitude
+    for (int q = blockIdx.x * kGridThreads + threadIdx.x; 4 * q < n; q += T) {
+        // bits 4q..4q+3 of the seen bitmap
+        const uint32_t seen = p.n_seen > 0 ? (p.bitmap[q >> 3] >> ((q & 7) * 4)) & 15u : 0u;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = 4 * q + k;
+            if (i >= n) break;
+            float l = load_logit(p.logits, p.dtype, i);
+            if (seen & (1u << k)) l = l > 0.0f ? l / p.penalty : l * p.penalty;
+            l = l / p.temperature;
+            p.probs[i] = l;
+            mx = fmaxf(mx, l);
+        }
+    }
+    red[threadIdx.x] = mx;
+    __syncthreads();
+    for (int s = kGridThreads / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) p.mpart[blockIdx.x] = red[0];
+}
+
+// e = exp(l - max); block sums (each thread in index order, then a halving tree)
+__global__ __launch_bounds__(kGridThreads) void sample_exp_kernel(SampleParams p) {
+    __shared__ float red[kGridThreads];
+    const int n = p.n;
+    const int T = gridDim.x * kGridThreads;
+    red[threadIdx.x] = (int)threadIdx.x < (int)gridDim.x ? p.mpart[threadIdx.x] : -3.402823466e38f;
+    __syncthreads();
+    for (int s = kGridThreads / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
+        __syncthreads();
+    }
+    const float mx = red[0];
+    __syncthreads();
+    float sm = 0.0f;
+    for (int q = blockIdx.x * kGridThreads + threadIdx.x; 4 * q < n; q += T) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = 4 * q + k;
+            if (i >= n) break;
+            const float e = expf(p.probs[i] - mx);
+            p.probs[i] = e;
+            sm += e;
+        }
+    }
+    red[threadIdx.x] = sm;
+    __syncthreads();
+    for (int s = kGridThreads / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + s];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) p.spart[blockIdx.x] = red[0];
+}
+
+// p = e / sum (block sums added in block order); level-0 histogram
+__global__ __launch_bounds__(kGridThreads) void sample_prob_kernel(SampleParams p) {
+    __shared__ uint32_t hc[kBins];
+    __shared__ unsigned long long hm[kBins];
+    __shared__ float s_sum;
+    const int n = p.n;
+    const int T = gridDim.x * kGridThreads;
+    for (int b = threadIdx.x; b < kBins; b += kGridThreads) {
+        hc[b] = 0u;
+        hm[b] = 0ull;
+    }
+    // block sums added in block order: loaded in parallel, folded by wave 0
+    if (threadIdx.x < 64) {
+        float s = 0.0f;
+        for (int c = 0; c < (int)gridDim.x; c += 64) {
+            const int b = c + (int)threadIdx.x;
+            const float v = b < (int)gridDim.x ? p.spart[b] : 0.0f;
+            const int m = (int)gridDim.x - c < 64 ? (int)gridDim.x - c : 64;
+            for (int j = 0; j < m; ++j)
+                s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+        }
+        if (threadIdx.x == 0) s_sum = s;
+    }
+    __syncthreads();
+    const float sm = s_sum;
+    for (int q = blockIdx.x * kGridThreads + threadIdx.x; 4 * q < n; q += T) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = 4 * q + k;
+            if (i >= n) break;
+            const float pv = p.probs[i] / sm;
+            p.probs[i] = pv;
+            const uint32_t key = __float_as_uint(pv);
+            atomicAdd(&hc[key >> 20], 1u);
+            const unsigned long long m = mass_of(key);
+            if (m) atomicAdd(&hm[key >> 20], m);
+        }
+    }
+    __syncthreads();
+    for (int b = threadIdx.x; b < kBins; b += kGridThreads) {
+        if (hc[b]) atomicAdd(&p.h0cnt[b], hc[b]);
+        if (hm[b]) atomicAdd(&p.h0mass[b], hm[b]);
+    }
+}
+
+// Compacts the tokens of the cutoff's level-0 bin and of every bin the draw
+// can land in: its target lies in [ceil(u * T1), ceil(u * incl(cutoff bin))]
+// since the cutoff token's inclusive mass is at least T1 and at most its
+// bin's.
+__global__ __launch_bounds__(kGridThreads) void sample_gather_kernel(SampleParams p) {
+    constexpr int kWaves = kGridThreads / 64;
+    __shared__ uint32_t offs[kWaves * 4];   // per wave and sub-step: slot offset in the block
+    __shared__ uint32_t s_base;
+    __shared__ SelScratch sc;
+    __shared__ BinSel s1, s2;
+    const int n = p.n;
+    const int T = gridDim.x * kGridThreads;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const unsigned long long t1 = target_top_p(p.top_p);
+    BinScan<kGridThreads> scan;
+    scan.load(p.h0cnt, p.h0mass, 0ull, sc);
+    scan.find(t1, s1, sc);
+    unsigned long long tlo, thi;
+    if (s1.found) {
+        tlo = target_draw(p.u, t1);
+        thi = target_draw(p.u, s1.incl);
+    } else {
+        tlo = thi = target_draw(p.u, s1.total);
+    }
+    scan.find(thi, s2, sc);
+    const int lo = s2.found ? s2.bin : 0;
+    scan.find(tlo, s2, sc);
+    const int hi = s2.found ? s2.bin : kBins - 1;
+    const int b1 = s1.found ? s1.bin : -1;
+    // block-uniform loop; one atomic a block reserves its slots
+    for (int qb = blockIdx.x * kGridThreads; 4 * qb < n; qb += T) {
+        const int q = qb + (int)threadIdx.x;
+        uint32_t key[4];
+        unsigned long long bal[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = 4 * q + k;
+            key[k] = i < n ? __float_as_uint(p.probs[i]) : 0u;
+            const int b = (int)(key[k] >> 20);
+            bal[k] = __ballot(i < n && (b == b1 || (b >= lo && b <= hi)));
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) offs[wid * 4 + k] = (uint32_t)__popcll(bal[k]);
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint32_t tot = 0u;
+            for (int j = 0; j < kWaves * 4; ++j) {
+                const uint32_t c = offs[j];
+                offs[j] = tot;
+                tot += c;
+            }
+            s_base = tot ? atomicAdd(p.ccount, tot) : 0u;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if ((bal[k] >> lane) & 1ull)
+                p.cand[s_base + offs[wid * 4 + k] + lanes_below(bal[k])] =
+                    make_uint2(key[k], (uint32_t)(4 * q + k));
+        }
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(kSelThreads) void sample_select_kernel(SampleParams p) {
+    __shared__ uint2 lc[kCandLds];
+    __shared__ LevelHist H;
+    __shared__ SelScratch sc;
+    __shared__ BinSel s0, bs;
+    __shared__ BinSel s1;
+    __shared__ int s_id;
+    const int C = (int)*p.ccount;
+    const unsigned long long t1 = target_top_p(p.top_p);
+    BinScan<kSelThreads> scan0;   // the level-0 histogram
+    scan0.load(p.h0cnt, p.h0mass, 0ull, sc);
+    scan0.find(t1, s1, sc);       // the cutoff's bin
+
+    if (C <= 64) {
+        // Few candidates (the usual nucleus of a peaked distribution): one
+        // wave sorts them by key and scans their masses.  First the mass of
+        // all bins above each bin, into H.mass.
+        {
+            unsigned long long run = scan0.excl;
+#pragma unroll
+            for (int k = 0; k < BinScan<kSelThreads>::BPT; ++k) {
+                H.mass[scan0.top - k] = run;
+                run += scan0.m[k];
             }
         }
         __syncthreads();
+        if (threadIdx.x >= 64) return;
+        const int lane = threadIdx.x;
+        const uint2 e = lane < C ? p.cand[lane] : make_uint2(0u, 0u);
+        unsigned long long sk = lane < C ? (1ull << 63) | order_key(e.x, e.y) : 0ull;
+        // bitonic sort, descending, across the wave
+        for (int k = 2; k <= 64; k <<= 1) {
+            for (int j = k >> 1; j > 0; j >>= 1) {
+                const unsigned long long o = __shfl_xor(sk, j, 64);
+                const bool take_max = ((lane & j) == 0) == ((lane & k) == 0);
+                sk = take_max ? (sk > o ? sk : o) : (sk < o ? sk : o);
+            }
+        }
+        const bool valid = (sk >> 63) != 0ull;
+        const uint32_t key = (uint32_t)(sk >> 24);
+        const int id = (int)(kIdMask - (uint32_t)(sk & kIdMask));
+        const int bin = valid ? (int)(key >> 20) : -1;
+        const unsigned long long m = valid ? mass_of(key) : 0ull;
+        // inclusive running mass inside each bin (bins are contiguous runs)
+        unsigned long long S = m;
+        for (int o = 1; o < 64; o <<= 1) {
+            const unsigned long long y = __shfl_up(S, o, 64);
+            if (lane >= o) S += y;
+        }
+        const int prev_bin = __shfl_up(bin, 1, 64);
+        const bool head = valid && (lane == 0 || prev_bin != bin);
+        const unsigned long long heads = __ballot(head) & ((2ull << lane) - 1ull);
+        const int start = heads ? 63 - __clzll((long long)heads) : 0;
+        const unsigned long long before = __shfl(S, start > 0 ? start - 1 : 0, 64);
+        const unsigned long long cum =
+            (valid ? H.mass[bin] : 0ull) + S - (start > 0 ? before : 0ull);
+        unsigned long long cut = s1.total;
+        if (s1.found) {
+            const unsigned long long hit = __ballot(valid && bin == s1.bin && cum >= t1);
+            cut = hit ? __shfl(cum, __ffsll((long long)hit) - 1, 64) : s1.incl;
+        }
+        const unsigned long long t2 = target_draw(p.u, cut);
+        const unsigned long long hit2 = __ballot(valid && cum >= t2);
+        const int chosen = __shfl(id, hit2 ? __ffsll((long long)hit2) - 1 : 0, 64);
+        if (lane == 0) *p.out = hit2 ? chosen : 0;
+        return;
     }
-    if (threadIdx.x == 0) {
-        const float v0 = load_logit(logits, dtype, 0);
-        *out = (v0 != v0 || ri[0] < 0) ? 0 : ri[0];
+
+    const uint2* cand = p.cand;
+    if (C <= kCandLds) {
+        for (int c = threadIdx.x; c < C; c += kSelThreads) lc[c] = p.cand[c];
+        cand = lc;
     }
+    __syncthreads();
+    // the cutoff: its inclusive mass
+    unsigned long long cum = s1.total;
+    if (s1.found) {
+        if (s1.cnt == 1u)
+            cum = s1.incl;
+        else
+            (void)select_in_bin(cand, C, s1.bin, s1.excl, t1, H, sc, bs, cum);
+    }
+    // the draw
+    const unsigned long long t2 = target_draw(p.u, cum);
+    scan0.find(t2, s0, sc);
+    int id = -1;
+    if (s0.found) {
+        if (s0.cnt == 1u) {
+            id = only_in_bin(cand, C, s0.bin, &s_id);
+        } else {
+            unsigned long long c2 = 0ull;
+            id = select_in_bin(cand, C, s0.bin, s0.excl, t2, H, sc, bs, c2);
+        }
+    }
+    if (threadIdx.x == 0) *p.out = id < 0 ? 0 : id;
 }
 
-__global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleParams p) {
-    __shared__ float redf[kSampleThreads];
-    __shared__ SelHist hist;
-    __shared__ SelState sel;
-    const int n = p.n;
-    float* pr = p.probs;
+// ------------------------------------------------------------------- host --
 
-    // 1. fp32 copy of the logits; clear the seen-token bitmap and the
-    //    histogram cache
-    for (int i = threadIdx.x; i < n; i += kSampleThreads) pr[i] = load_logit(p.logits, p.dtype, i);
-    for (int w = threadIdx.x; w < (n + 31) / 32; w += kSampleThreads) p.bitmap[w] = 0u;
-    if (threadIdx.x < kSelPasses) hist.valid[threadIdx.x] = 0;
-    __syncthreads();
-    // 2. repetition penalty, once per distinct token (the reference's Set)
-    for (int j = threadIdx.x; j < p.n_seen; j += kSampleThreads) {
-        const int t = p.seen[j];
-        if (t < 0 || t >= n) continue;
-        const uint32_t bit = 1u << (t & 31);
-        if (atomicOr(&p.bitmap[t >> 5], bit) & bit) continue;
-        const float l = pr[t];
-        pr[t] = l > 0.0f ? l / p.penalty : l * p.penalty;
-    }
-    __syncthreads();
-    // 3. temperature, max
-    float mx = -3.402823466e38f;   // -greatestFiniteMagnitude
-    for (int i = threadIdx.x; i < n; i += kSampleThreads) {
-        const float l = pr[i] / p.temperature;
-        pr[i] = l;
-        mx = fmaxf(mx, l);
-    }
-    mx = block_reduce(mx, redf, [](float a, float b) { return fmaxf(a, b); });
-    // 4. exp and sum, 5. normalise
-    float sm = 0.0f;
-    for (int i = threadIdx.x; i < n; i += kSampleThreads) {
-        const float e = expf(pr[i] - mx);
-        pr[i] = e;
-        sm += e;
-    }
-    sm = block_reduce(sm, redf, [](float a, float b) { return a + b; });
-    for (int i = threadIdx.x; i < n; i += kSampleThreads) pr[i] = pr[i] / sm;
-    __syncthreads();
+namespace {
 
-    // 6. the nucleus: first token whose running mass reaches top_p
-    const double tp = fmin((double)p.top_p, 4.0);
-    weighted_select(pr, n, (unsigned long long)ceil(tp * 0x1p52), sel, hist);
-    const unsigned long long cum = sel.cum;   // at the cutoff, or the total
-    __syncthreads();
-    // 7. the draw: first token whose running mass reaches u * cum
-    weighted_select(pr, n, (unsigned long long)ceil((double)p.u * (double)cum), sel, hist);
-    if (!sel.found) {   // only for non-finite probabilities: the first token
-        __syncthreads();
-        weighted_select(pr, n, 0ull, sel, hist);
-    }
-    if (threadIdx.x == 0) *p.out = sel.idx < 0 ? 0 : sel.idx;
+int grid_blocks(int n) {
+    const int b = (n + 4 * kGridThreads - 1) / (4 * kGridThreads);
+    return b < kMaxBlocks ? b : kMaxBlocks;
 }
+
+size_t up256(size_t b) { return (b + 255) / 256 * 256; }
+
+}  // namespace
+
+size_t argmax_workspace_bytes() { return 2 * kMaxBlocks * 4; }
 
 size_t sample_workspace_bytes(int n) {
-    const size_t probs = ((size_t)n * 4 + 255) / 256 * 256;
-    const size_t bitmap = (((size_t)n + 31) / 32 * 4 + 255) / 256 * 256;
-    return probs + bitmap;
+    return up256((size_t)n * 4) + up256(((size_t)n + 31) / 32 * 4) + 2 * up256(kMaxBlocks * 4) +
+           up256(kBins * 4) + up256(kBins * 8) + 256 + up256((size_t)n * 8);
 }
 
-hipError_t launch_argmax(const void* logits, int dtype, int n, int32_t* out, hipStream_t st) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kSampleThreads), 0, st, logits, dtype, n, out);
+hipError_t launch_argmax(const void* logits, int dtype, int n, int32_t* out, void* ws,
+                         hipStream_t st) {
+    const int G = grid_blocks(n);
+    float* pv = static_cast<float*>(ws);
+    int* pi = reinterpret_cast<int*>(pv + kMaxBlocks);
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(G), dim3(kGridThreads), 0, st, logits, dtype, n,
+                       pv, pi);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kGridThreads), 0, st, logits, dtype, pv,
+                       pi, G, out);
     return hipGetLastError();
 }
 
 hipError_t launch_sample(SampleParams p, void* ws, hipStream_t st) {
     char* w = static_cast<char*>(ws);
-    const size_t probs = ((size_t)p.n * 4 + 255) / 256 * 256;
+    const size_t n = (size_t)p.n;
     p.probs = reinterpret_cast<float*>(w);
-    p.bitmap = reinterpret_cast<uint32_t*>(w + probs);
-    hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(kSampleThreads), 0, st, p);
+    w += up256(n * 4);
+    p.bitmap = reinterpret_cast<uint32_t*>(w);
+    w += up256((n + 31) / 32 * 4);
+    p.mpart = reinterpret_cast<float*>(w);
+    w += up256(kMaxBlocks * 4);
+    p.spart = reinterpret_cast<float*>(w);
+    w += up256(kMaxBlocks * 4);
+    p.h0cnt = reinterpret_cast<uint32_t*>(w);
+    w += up256(kBins * 4);
+    p.h0mass = reinterpret_cast<unsigned long long*>(w);
+    w += up256(kBins * 8);
+    p.ccount = reinterpret_cast<uint32_t*>(w);
+    w += 256;
+    p.cand = reinterpret_cast<uint2*>(w);
+    const int G = grid_blocks(p.n);
+    if (p.n_seen > 0)
+        hipLaunchKernelGGL(sample_init_kernel, dim3(1), dim3(kSelThreads), 0, st, p);
+    hipLaunchKernelGGL(sample_scale_kernel, dim3(G), dim3(kGridThreads), 0, st, p);
+    hipLaunchKernelGGL(sample_exp_kernel, dim3(G), dim3(kGridThreads), 0, st, p);
+    hipLaunchKernelGGL(sample_prob_kernel, dim3(G), dim3(kGridThreads), 0, st, p);
+    hipLaunchKernelGGL(sample_gather_kernel, dim3(G), dim3(kGridThreads), 0, st, p);
+    hipLaunchKernelGGL(sample_select_kernel, dim3(1), dim3(kSelThreads), 0, st, p);
     return hipGetLastError();
 }
 

