@@ -181,6 +181,7 @@ def main():
         diag = timing_diagnostics(pkg, torch, layers, x2, outs, reps)
 
     fused = fused_layer_leg(pkg, torch, gen, dev, layers, reps)
+    select = token_select_leg(pkg, torch, gen, dev)
 
     gemm = {} if args.no_gemm else gemm_legs(pkg, torch, gen, dev)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
@@ -211,7 +212,7 @@ def main():
                      "avg_us": round(dom_us, 3), "bytes_per_launch": DOMINANT_BYTES,
                      "timing": timing},
         "cpu_baseline": cpu,
-        "extra": {"decode_layer_fused_norms": fused, "gemm": gemm,
+        "extra": {"decode_layer_fused_norms": fused, "token_select": select, "gemm": gemm,
                   **({"timing_diag": diag} if diag else {})},
     }
     print(json.dumps(line))
@@ -262,6 +263,40 @@ def fused_layer_leg(pkg, torch, gen, dev, layers, reps):
             "bytes_per_layer": nbytes, "launches_per_layer": 4,
             "note": "rms_norm, residual add + rms_norm and the final residual add run inside "
                     "the projections' kernels"}
+
+
+def token_select_leg(pkg, torch, gen, dev, vocab=128256, reps=200):
+    """Token selection after the lm_head (LlamaModel.swift:153,161): argmax
+    and temperature 0.7 / top-p 0.9 / repetition penalty 1.1 sampling over
+    Llama 3.2's 128256 fp16 logits (N(0, 3^2): a nucleus of a few tokens, as
+    for a trained model) with 64 seen ids.  Each is captured as a HIP graph on
+    its own stream (after one eager call there, which sizes the workspace) and
+    replayed; us per call includes the graph's launch gaps."""
+    logits = (3.0 * torch.randn(vocab, generator=gen, device=dev)).half()
+    seen = torch.randint(0, vocab, (64,), generator=gen, device=dev, dtype=torch.int32)
+    out = torch.empty(1, device=dev, dtype=torch.int32)
+    res = {}
+    for name, fn in (("argmax", lambda s: pkg.argmax(logits, out=out, stream=s)),
+                     ("sample_top_p", lambda s: pkg.sample(logits, 0.7, 0.9, 1.1, seen, 0.5,
+                                                           out=out, stream=s))):
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            fn(s)
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(10):
+                fn(s)
+        g.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps // 10):
+            g.replay()
+        torch.cuda.synchronize()
+        res[name + "_us"] = round(1e6 * (time.perf_counter() - t0) / (reps // 10 * 10), 2)
+    res["vocab"] = vocab
+    res["launches"] = {"argmax": 2, "sample_top_p": 6}
+    return res
 
 
 def traffic_run(pkg, torch, gen, dev):
