@@ -55,17 +55,19 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
     return __builtin_bit_cast(uint16_t, (__bf16)f);  // round to nearest even
 }
 
-// Epilogue activations, fp32.
+// Epilogue activations, fp32, with the hardware exp2 (__expf) and reciprocal
+// (about 1e-6 relative; the outputs are rounded to 16 bits).
 // silu_mul (Kernels.swift:90-98): v / (1 + exp(-v)) * u
 __device__ __forceinline__ float silu_mul_f32(float v, float u) {
-    return (v / (1.0f + __expf(-v))) * u;
+    return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)) * u;
 }
 
-// gelu_approximate_f32 (Kernels.swift:1774-1783): inner clamped to +-10.
+// gelu_approximate_f32 (Kernels.swift:1774-1783), inner clamped to +-10:
+// 0.5 v (1 + tanh(inner)) written as v / (1 + exp(-2 inner)).
 __device__ __forceinline__ float gelu_tanh_f32(float v) {
     float inner = 0.7978845608f * (v + 0.044715f * v * v * v);
     inner = fminf(fmaxf(inner, -10.0f), 10.0f);
-    return 0.5f * v * (1.0f + tanhf(inner));
+    return v * __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * inner));
 }
 
 // Status codes shared with the C ABI (include/swiftltx_q4.h).

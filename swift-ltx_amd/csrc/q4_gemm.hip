@@ -136,6 +136,88 @@ __device__ __forceinline__ void epi_store(const GemmParams& p, size_t o, int n, 
     store_out(p, o, v);
 }
 
+// Whether rows of y (and of the residual) can take 16-byte vector stores.
+__device__ __forceinline__ bool out_vec_ok(const GemmParams& p) {
+    return (p.N & 7) == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0 &&
+           (p.epilogue != kEpiResidual || (reinterpret_cast<uintptr_t>(p.residual) & 15) == 0);
+}
+
+// Eight consecutive outputs row[n0 .. n0+7] (columns past N dropped): one
+// 16-byte store (two for fp32) when `vec` (N % 8 == 0, 16-byte aligned y),
+// else one store per element.
+__device__ __forceinline__ void store_out8(const GemmParams& p, size_t row, int n0,
+                                           const float* v, bool vec) {
+    if (vec && n0 + 8 <= p.N) {
+        if (p.y_dtype == kF32) {
+            f32x4* d = reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.y) + row + n0);
+            d[0] = f32x4{v[0], v[1], v[2], v[3]};
+            d[1] = f32x4{v[4], v[5], v[6], v[7]};
+        } else {
+            u32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t lo = p.y_dtype == kBF16 ? f2bf(v[2 * e]) : f2h(v[2 * e]);
+                const uint32_t hi = p.y_dtype == kBF16 ? f2bf(v[2 * e + 1]) : f2h(v[2 * e + 1]);
+                o[e] = lo | (hi << 16);
+            }
+            *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(p.y) + row + n0) = o;
+        }
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        if (n0 + e < p.N) store_out(p, row + n0 + e, v[e]);
+}
+
+// Non-SiLU epilogue (bias, GELU-tanh, residual add) on eight consecutive
+// outputs, then stored as store_out8 does.
+__device__ __forceinline__ void epi_store8(const GemmParams& p, size_t row, int n0, float* v,
+                                           bool vec) {
+    if (p.bias) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] += p.bias[n0 + e < p.N ? n0 + e : 0];
+    }
+    if (p.epilogue == kEpiGeluTanh) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = gelu_tanh_f32(v[e]);
+    }
+    if (p.epilogue == kEpiResidual) {
+        if (vec && n0 + 8 <= p.N) {
+            const u32x4 r = *reinterpret_cast<const u32x4*>(p.residual + row + n0);
+            u32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t lo = residual_add_f16((uint16_t)(r[e] & 0xFFFFu), v[2 * e]);
+                const uint32_t hi = residual_add_f16((uint16_t)(r[e] >> 16), v[2 * e + 1]);
+                o[e] = lo | (hi << 16);
+            }
+            *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(p.y) + row + n0) = o;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (n0 + e < p.N)
+                    reinterpret_cast<uint16_t*>(p.y)[row + n0 + e] =
+                        residual_add_f16(p.residual[row + n0 + e], v[e]);
+        }
+        return;
+    }
+    store_out8(p, row, n0, v, vec);
+}
+
+// Eight raw fp32 partial sums into a workspace row (16-byte aligned rows when
+// N % 4 == 0).
+__device__ __forceinline__ void store_f32x8(float* wsr, int n0, int N, const float* v) {
+    if ((N & 3) == 0 && n0 + 8 <= N) {
+        f32x4* d = reinterpret_cast<f32x4*>(wsr + n0);
+        d[0] = f32x4{v[0], v[1], v[2], v[3]};
+        d[1] = f32x4{v[4], v[5], v[6], v[7]};
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        if (n0 + e < N) wsr[n0 + e] = v[e];
+}
+
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
 // vmcnt bits [3:0] and [15:14], expcnt [6:4] = 7, lgkmcnt [11:8] = 15).
 #define SLTX_WAIT_VMCNT(n) \
@@ -566,114 +648,128 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
     if (kt + 2 < nk) step(I2{}, kt + 2);
 
     // ---- epilogue ----
-    // 32x32 accumulator layout: lane l, element v -> row 8*(v/4) + 4*(l/32) + v%4,
-    // column l%32.  MFMA tile j of wave wn holds virtual weight rows vb..vb+31,
-    // vb = wn*32*NT + j*32: with SILU, matrix (vb >> 5) & 1 (gate 0, up 1) and
-    // output columns n0 + (vb >> 6)*32 + l%32.
-    auto out_col = [&](int j) {
-        const int vb = wn * 32 * NT + j * 32;
-        return SILU ? n0 + (vb >> 6) * 32 + lrow : n0 + vb + lrow;
-    };
-    if constexpr (SPLIT) {
-        // raw fp32 partial sums; the reduce kernel applies the epilogue
-        const size_t nw = SILU ? 2 * (size_t)p.N : (size_t)p.N;
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int m = m0 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                if (m >= p.M) continue;
-                float* wsr = p.ws + ((size_t)split * p.M + m) * nw;
-#pragma unroll
-                for (int j = 0; j < NT; ++j) {
-                    const int n = out_col(j);
-                    const int tn = ((wn * 32 * NT + j * 32) >> 5) & 1;
-                    if (n < p.N) wsr[SILU ? tn * p.N + n : n] = acc[i][j][v];
-                }
-            }
-        return;
-    }
-    if constexpr (SILU && NT == 1) {
-        // Gate and up of the same columns sit in waves 2c and 2c+1: the up
-        // wave hands its tile over through LDS (the A stages, once no copy
-        // into them is in flight).
-        SLTX_WAIT_VMCNT(0);
-        SLTX_LDS_BARRIER();
-        const int c = wn >> 1;
-        float* xb = reinterpret_cast<float*>(c == 0 ? lds_a0 : c == 1 ? lds_a1 : c == 2 ? lds_a2 : lds_a3);
-        static_assert(BM * 32 * 4 <= A_STAGE * 16, "exchange fits one A stage");
-        if (wn & 1) {
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int v = 0; v < 16; ++v)
-                    xb[(i * 32 + 8 * (v >> 2) + 4 * h + (v & 3)) * 32 + lrow] = acc[i][0][v];
-        }
-        SLTX_LDS_BARRIER();
-        if (wn & 1) return;
-        const int n = out_col(0);
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int r = i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                const int m = m0 + r;
-                if (m >= p.M || n >= p.N) continue;
-                store_out(p, (size_t)m * p.N + n, glu_f32(p.epilogue == kEpiGeluMul, acc[i][0][v], xb[r * 32 + lrow]));
-            }
-        return;
-    }
+    // Each 32-row accumulator tile is staged through LDS (the A stages, idle
+    // once the last copy into them has landed) as two fp32 [32][128] buffers:
+    // with SILU gate (0) and up (1) of the block's 128 output columns,
+    // otherwise output columns 0-127 (0) and 128-255 (1).  All 512 threads
+    // then apply the epilogue to 8 consecutive columns each (thread t: row
+    // t / 16, columns 8 (t % 16)) and store them as 16-byte vectors.
+    static_assert(NT == 1, "one 32-row MFMA tile of W rows per wave");
+    static_assert(32 * 128 * 4 <= A_STAGE * 16, "a 32 x 128 fp32 tile fits one A stage");
+    SLTX_WAIT_VMCNT(0);
+    SLTX_LDS_BARRIER();
+    float* const eb0 = reinterpret_cast<float*>(lds_a0);
+    float* const eb1 = reinterpret_cast<float*>(lds_a1);
+    float* const wdst = (SILU ? (wn & 1) : (wn >> 2)) ? eb1 : eb0;
+    const int wcol = (SILU ? (wn >> 1) : (wn & 3)) * 32 + lrow;
+    const int er = tid >> 4, ec = (tid & 15) * 8;
+    const bool vec = out_vec_ok(p);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int m = m0 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-            if (m >= p.M) continue;
-            if constexpr (SILU) {   // NT == 2: tile 0 gate, tile 1 up
-                const int n = out_col(0);
-                if (n >= p.N) continue;
-                store_out(p, (size_t)m * p.N + n, glu_f32(p.epilogue == kEpiGeluMul, acc[i][0][v], acc[i][NT - 1][v]));
-            } else {
+        for (int v = 0; v < 16; ++v) wdst[(8 * (v >> 2) + 4 * h + (v & 3)) * 128 + wcol] = acc[i][0][v];
+        SLTX_LDS_BARRIER();
+        const int m = m0 + i * 32 + er;
+        if (m < p.M) {
+            float x0[8], x1[8];
+            const f32x4* r0 = reinterpret_cast<const f32x4*>(eb0 + er * 128 + ec);
+            const f32x4* r1 = reinterpret_cast<const f32x4*>(eb1 + er * 128 + ec);
+            const f32x4 a0 = r0[0], a1 = r0[1], b0 = r1[0], b1 = r1[1];
 #pragma unroll
-                for (int j = 0; j < NT; ++j) {
-                    const int n = out_col(j);
-                    if (n >= p.N) continue;
-                    epi_store(p, (size_t)m * p.N + n, n, acc[i][j][v]);
-                }
+            for (int e = 0; e < 4; ++e) {
+                x0[e] = a0[e];
+                x0[4 + e] = a1[e];
+                x1[e] = b0[e];
+                x1[4 + e] = b1[e];
+            }
+            if constexpr (SPLIT) {
+                // raw fp32 partial sums; the reduce kernel applies the epilogue
+                const size_t nw = SILU ? 2 * (size_t)p.N : (size_t)p.N;
+                float* wsr = p.ws + ((size_t)split * p.M + m) * nw;
+                store_f32x8(wsr, n0 + ec, p.N, x0);
+                if constexpr (SILU)
+                    store_f32x8(wsr + p.N, n0 + ec, p.N, x1);   // up partials follow gate's
+                else
+                    store_f32x8(wsr, n0 + 128 + ec, p.N, x1);
+            } else if constexpr (SILU) {
+                const bool gelu = p.epilogue == kEpiGeluMul;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x0[e] = glu_f32(gelu, x0[e], x1[e]);
+                store_out8(p, (size_t)m * p.N, n0 + ec, x0, vec);
+            } else {
+                epi_store8(p, (size_t)m * p.N, n0 + ec, x0, vec);
+                epi_store8(p, (size_t)m * p.N, n0 + 128 + ec, x1, vec);
             }
         }
+        SLTX_LDS_BARRIER();
     }
 }
+
 
 // Split-K reduction: out[m, n] = epilogue(sum over splits of the partials),
 // summed in split order (deterministic).  SILU reduces gate and up
 // separately before silu(gate) * up.
 template <bool SILU>
 __global__ __launch_bounds__(256) void q4_splitk_reduce_kernel(GemmParams p) {
+    // each thread: 8 consecutive outputs of one row
+    const int nb8 = (p.N + 7) / 8;
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const size_t total = (size_t)p.M * p.N;
-    if (idx >= total) return;
-    const size_t m = idx / p.N, n = idx % p.N;
+    if (idx >= (size_t)p.M * nb8) return;
+    const size_t m = idx / nb8;
+    const int n0 = (int)(idx % nb8) * 8;
     const size_t nw = SILU ? 2 * (size_t)p.N : (size_t)p.N;
     const size_t stride = (size_t)p.M * nw;
-    const float* src = p.ws + m * nw + n;
-    float a = 0.0f, u = 0.0f;
-    for (int s = 0; s < p.splits; ++s) {
-        a += src[s * stride];
-        if (SILU) u += src[s * stride + p.N];
+    const float* src = p.ws + m * nw;
+    const bool vin = (p.N & 7) == 0;   // 16-byte aligned workspace rows and no tail
+    float a[8], u[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a[e] = u[e] = 0.0f;
+    for (int s = 0; s < p.splits; ++s, src += stride) {
+        if (vin) {
+            const f32x4* q = reinterpret_cast<const f32x4*>(src + n0);
+            const f32x4 q0 = q[0], q1 = q[1];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                a[e] += q0[e];
+                a[4 + e] += q1[e];
+            }
+            if (SILU) {
+                const f32x4* r = reinterpret_cast<const f32x4*>(src + p.N + n0);
+                const f32x4 r0 = r[0], r1 = r[1];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    u[e] += r0[e];
+                    u[4 + e] += r1[e];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                if (n0 + e < p.N) {
+                    a[e] += src[n0 + e];
+                    if (SILU) u[e] += src[p.N + n0 + e];
+                }
+            }
+        }
     }
-    if (SILU)
-        store_out(p, idx, glu_f32(p.epilogue == kEpiGeluMul, a, u));
-    else
-        epi_store(p, idx, (int)n, a);
+    const bool vec = out_vec_ok(p);
+    if (SILU) {
+        const bool gelu = p.epilogue == kEpiGeluMul;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] = glu_f32(gelu, a[e], u[e]);
+        store_out8(p, m * p.N, n0, a, vec);
+    } else {
+        epi_store8(p, m * p.N, n0, a, vec);
+    }
 }
 
-// Launch plan: block-tile height WM (BM = 64*WM) and K splits.  Scores each
-// option by useful work over the CU-rounds it occupies (tiles x splits over
-// 256 CUs), prefers taller tiles (each dequantized B fragment feeds BM/32
-// MFMAs) and charges each split a little for the partial-sum round trip.
-// Splits cover an even number of k-tiles (packed weights move two k-tiles at
-// a time).
+// Launch plan: block-tile height WM (BM = 64*WM) and K splits, chosen by
+// estimated time on 256 CUs: rounds of blocks x k-tiles per block x the
+// measured time of one k-tile (1.37 us at BM = 192, 0.85 us at BM = 128, a
+// 256-row W tile), plus about 10 us per launch (prologue, epilogue), plus,
+// when split, writing the fp32 partials (~6 TB/s) and the reduce pass
+// reading them back (~4 TB/s, its own launch).  Splits cover an even number
+// of k-tiles (packed weights move two k-tiles at a time).
 struct GemmPlan {
     int wm, tiles_m, tiles_n, splits, split_tiles;
     size_t ws_bytes;
@@ -684,12 +780,14 @@ static GemmPlan plan_gemm(const GemmParams& p, bool allow_split) {
     const int bn_out = silu ? BN / 2 : BN;
     const int tiles_n = (p.N + bn_out - 1) / bn_out;
     const int nk = (p.K + BK - 1) / BK;
+    const size_t nw = silu ? 2 * (size_t)p.N : (size_t)p.N;
     GemmPlan best = {2, 0, tiles_n, 1, nk, 0};
-    double best_score = -1.0;
+    double best_us = 1e30;
     for (int wm = 2; wm <= 3; ++wm) {
         const int bm = 64 * wm;
         const long tiles_m = (p.M + bm - 1) / bm;
         const long tiles = tiles_m * tiles_n;
+        const double kt_us = wm == 3 ? 1.37 : 0.85;
         const int smax = allow_split ? 8 : 1;
         for (int s = 1; s <= smax; ++s) {
             if (s > 1 && nk < 8 * s) break;
@@ -699,12 +797,13 @@ static GemmPlan plan_gemm(const GemmParams& p, bool allow_split) {
             if (s > 1 && s_eff != s) continue;
             const long blocks = tiles * s_eff;
             const long rounds = (blocks + kCUs - 1) / kCUs;
-            const double util = ((double)p.M * tiles_n * nk) /
-                                ((double)rounds * kCUs * bm * chunk);
-            const double score = util * (1.0 + 0.08 * (wm - 2)) * (s > 1 ? 1.0 - 0.02 * s : 1.0);
-            if (score > best_score) {
-                best_score = score;
-                const size_t nw = silu ? 2 * (size_t)p.N : (size_t)p.N;
+            double us = (double)rounds * chunk * kt_us + 10.0;
+            if (s_eff > 1) {
+                const double part = (double)s_eff * p.M * nw * 4.0;
+                us += part / 6.0e6 + 3.0 + (part + (double)p.M * p.N * 2.0) / 4.0e6;
+            }
+            if (us < best_us) {
+                best_us = us;
                 best = {wm, (int)tiles_m, tiles_n, s_eff, chunk,
                         s_eff > 1 ? (size_t)s_eff * p.M * nw * sizeof(float) : 0};
             }
@@ -756,7 +855,7 @@ hipError_t launch_gemm(GemmParams p, bool a_bf16, hipStream_t st) {
     if (grid > 0x7fffffffL) return hipErrorInvalidValue;
     if (p.splits > 1) {
         launch_dtype<true>(p, a_bf16, silu, grid, plan.wm, st);
-        const size_t total = (size_t)p.M * p.N;
+        const size_t total = (size_t)p.M * ((p.N + 7) / 8);
         const long rgrid = (long)((total + 255) / 256);
         if (silu)
             hipLaunchKernelGGL(q4_splitk_reduce_kernel<true>, dim3(rgrid), dim3(256), 0, st, p);
