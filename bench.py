@@ -208,7 +208,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profiles(),
-                     "kernel": "q4_gemv_kernel<32,3,true,true> (gate/up fused SiLU*up)",
+                     "kernel": "q4_gemv_kernel<32,3,true,false,0> (gate/up fused SiLU*up)",
                      "avg_us": round(dom_us, 3), "bytes_per_launch": DOMINANT_BYTES,
                      "timing": timing},
         "cpu_baseline": cpu,

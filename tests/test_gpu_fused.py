@@ -193,9 +193,24 @@ def test_decode_layer_fused_matches_unfused(pkg, dev):
     out2 = (res2.float() + down2.float()).half()
     torch.cuda.synchronize()
     assert torch.equal(res, res2)
-    assert_parity(qkv.cpu().numpy(), qkv2.cpu().numpy().astype(np.float64), TOL_GEMV, "qkv")
-    assert_parity(act.cpu().numpy(), act2.cpu().numpy().astype(np.float64), TOL_GEMV, "gate/up")
-    assert_parity(out.cpu().numpy(), out2.cpu().numpy().astype(np.float64), TOL_GEMV, "layer out")
+    _assert_two_paths(qkv, qkv2, TOL_GEMV, "qkv")
+    _assert_two_paths(act, act2, TOL_GEMV, "gate/up")
+    _assert_two_paths(out, out2, TOL_GEMV, "layer out")
+
+
+def _assert_two_paths(a, b, tol, what):
+    """Two fp16 GPU results of the same exact value v: each is within the
+    GEMV bound of v before its own fp16 rounding (half an ulp), so they may
+    differ by twice the bound plus one fp16 ulp (kernels with different
+    instruction schedules round their fp32 sums differently)."""
+    a = a.cpu().numpy().astype(np.float64)
+    b16 = b.cpu().numpy()
+    b = b16.astype(np.float64)
+    allow = (2 * (tol["rtol"] * np.abs(b) + tol["atol_rms"] * np.sqrt(np.mean(b ** 2)))
+             + np.spacing(np.abs(b16)).astype(np.float64))
+    d = np.abs(a - b)
+    assert np.all(d <= allow), f"{what}: worst {np.max(d / allow):.2f}x the allowance"
+    assert o.max_rel_err(a, b) <= GATE, what
 
 
 # (M, N, K, g): GEMV; GEMM; GEMM with split-K (few output tiles); generic path
