@@ -125,17 +125,6 @@ __device__ __forceinline__ void store_out(const GemmParams& p, size_t o, float v
         reinterpret_cast<uint16_t*>(p.y)[o] = f2h(v);
 }
 
-// Non-SiLU epilogues: + bias, GELU-tanh, or the residual add (fp16 out).
-__device__ __forceinline__ void epi_store(const GemmParams& p, size_t o, int n, float v) {
-    if (p.bias) v += p.bias[n];
-    if (p.epilogue == kEpiGeluTanh) v = gelu_tanh_f32(v);
-    if (p.epilogue == kEpiResidual) {
-        reinterpret_cast<uint16_t*>(p.y)[o] = residual_add_f16(p.residual[o], v);
-        return;
-    }
-    store_out(p, o, v);
-}
-
 // Whether rows of y (and of the residual) can take 16-byte vector stores.
 __device__ __forceinline__ bool out_vec_ok(const GemmParams& p) {
     return (p.N & 7) == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0 &&

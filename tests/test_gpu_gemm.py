@@ -309,3 +309,40 @@ def test_split_k_under_graph_capture(pkg, dev):
             ok, worst = o.elementwise_ok(out.cpu().numpy(), ref.cpu().numpy().astype(np.float64),
                                          rtol=1e-5, atol_rms=1e-5)
             assert ok, (warm, worst)
+
+
+@pytest.mark.parametrize("kind", ["plain", "silu", "residual", "f32_bias_gelu"])
+@pytest.mark.parametrize("M,N,K", [(33, 256, 512), (750, 3072, 8192)])
+def test_unaligned_outputs_match_aligned(pkg, dev, kind, M, N, K):
+    """Outputs (and the residual input) 2 bytes (fp16) or 4 bytes (fp32) off a
+    16-byte boundary take the per-element store path of the staged epilogue
+    (and of the split-K reduction at M=750, K=8192); the values must be
+    bit-identical to the aligned run's."""
+    import torch
+    x, [(w, s, b), (w2, s2, b2)] = gpu_inputs(M, N, K, 64, seed=M + K, dev=dev, n_weights=2)
+    W = pkg.Q4Weight(w, s, b, K, 64)
+    W2 = pkg.Q4Weight(w2, s2, b2, K, 64)
+    f32 = kind == "f32_bias_gelu"
+    dt = torch.float32 if f32 else torch.float16
+    res_a = (torch.randn(M, N, device=dev) * 4).half()
+    res_buf = torch.empty(M * N + 1, device=dev, dtype=torch.float16)
+    res_u = res_buf[1:].view(M, N)
+    res_u.copy_(res_a)
+    bias = torch.randn(N, device=dev)
+
+    def run(out, res):
+        if kind == "plain":
+            return pkg.linear(x, W, M, K, N, fast=True, out=out)
+        if kind == "silu":
+            return pkg.matmul_q4_silu_mul(x, W, W2, M, K, N, out=out)
+        if kind == "residual":
+            return pkg.matmul_q4_residual(x, W, res, M, N, out=out)
+        return pkg.matmul_q4_ex(x, W, M, N, out_dtype=torch.float32, bias=bias,
+                                epilogue=pkg.SLTX_EPI_GELU_TANH, out=out)
+
+    aligned = run(torch.empty(M, N, device=dev, dtype=dt), res_a)
+    buf = torch.empty(M * N + 1, device=dev, dtype=dt)
+    unaligned = run(buf[1:].view(M, N), res_u)
+    torch.cuda.synchronize()
+    assert unaligned.data_ptr() % 16 != 0
+    assert torch.equal(aligned, unaligned), kind
