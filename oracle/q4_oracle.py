@@ -161,10 +161,13 @@ def sample_ref(logits, temperature: float, top_p: float, penalty: float, seen, u
     add.accumulate is sequential) for the softmax denominator and the running
     sums.
     gpu_sums=True: the sums the GPU kernels form instead, for a tighter check
-    of them: the softmax denominator over G = min(256, ceil(n/1024)) blocks of
-    256 threads, thread j adding tokens 4q..4q+3 for q = j, j + 256G, ... in
-    order, each block folding its threads by a halving tree, the block sums
-    added in block order; and exact running sums of the integer masses
+    of them: an online softmax over G = min(256, ceil(n/1024)) blocks of 256
+    threads, thread j holding tokens 4q..4q+3 for q = j, j + 256G, ...: block
+    b's max m_b, its s_b = sum of exp(l - m_b) (each thread in token order,
+    then a halving tree over the block), and the denominator: the terms
+    s_b * exp(m_b - max), padded to 256 and summed as four 64-term halving
+    trees combined as (w0 + w1) + (w2 + w3); p = exp(l - max) / that;
+    and exact running sums of the integer masses
     floor(p * 2^52): cutoff = first token whose inclusive mass reaches
     ceil(top_p * 2^52), chosen = first whose inclusive mass reaches
     ceil(u * mass at the cutoff).
@@ -189,15 +192,27 @@ def sample_ref(logits, temperature: float, top_p: float, penalty: float, seen, u
             G = min(256, -(-n // 1024))
             T = 256 * G
             R = -(-n // (4 * T))
-            E = np.zeros(R * 4 * T, f32)
-            E[:n] = e
-            seq = E.reshape(R, T, 4).transpose(0, 2, 1).reshape(R * 4, T)
+            L3 = np.full(R * 4 * T, -np.inf, f32)
+            L3[:n] = lg
+            L3 = L3.reshape(R, T, 4)
+            mb = L3.reshape(R, G, 256, 4).max(axis=(0, 2, 3)).astype(f32)   # block maxima
+            E = np.exp(L3 - np.repeat(mb, 256)[None, :, None]).astype(f32)
+            seq = E.transpose(0, 2, 1).reshape(R * 4, T)
             blk = np.add.accumulate(seq, axis=0, dtype=f32)[-1].reshape(G, 256).copy()
             h = 128
             while h:
                 blk[:, :h] = blk[:, :h] + blk[:, h:2 * h]
                 h //= 2
-            s = np.add.accumulate(blk[:, 0], dtype=f32)[-1]
+            M = f32(mb.max())
+            terms = np.zeros(256, f32)
+            terms[:G] = (blk[:, 0] * np.exp(mb - M).astype(f32)).astype(f32)
+            w = terms.reshape(4, 64).copy()
+            h = 32
+            while h:
+                w[:, :h] = w[:, :h] + w[:, h:2 * h]
+                h //= 2
+            s = f32(f32(w[0, 0] + w[1, 0]) + f32(w[2, 0] + w[3, 0]))
+            e = np.exp(lg - M).astype(f32)
         else:
             s = np.add.accumulate(e, dtype=f32)[-1]
         p = (e / s).astype(f32)

@@ -79,10 +79,9 @@ struct SampleParams {
     int n_seen;
     int32_t* out;           // [1] chosen token (device)
     // carved from the workspace by launch_sample
-    float* probs;           // [n] logits -> exp -> probabilities
-    uint32_t* bitmap;       // [n/32] seen ids
+    float* probs;           // [n] scaled logits, then probabilities
     float* mpart;           // block maxima
-    float* spart;           // block sums
+    float* spart;           // block exp-sums (relative to the block maxima)
     uint32_t* h0cnt;        // level-0 histogram (4096 bins)
     unsigned long long* h0mass;
     uint32_t* ccount;       // compacted candidates

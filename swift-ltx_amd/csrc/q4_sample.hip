@@ -7,9 +7,12 @@
 // The probabilities follow the reference's fp32 steps: penalty (divide
 // positive, multiply non-positive logits of the distinct seen tokens), divide
 // by temperature, softmax (max, exp, sum, divide).  The softmax denominator
-// is a fixed-order sum: each grid thread adds its tokens in index order, a
-// block folds its 256 threads by a halving tree, and the block sums are added
-// in block order.
+// is a fixed-order sum: each block b forms m_b = the max of its logits and
+// s_b = sum of exp(l - m_b) (each thread over its tokens in index order, then
+// a halving tree over the block's 256 threads); sum = the terms
+// s_b * exp(m_b - max) over four 64-term halving trees, combined as
+// (w0 + w1) + (w2 + w3) -- an online softmax, so one pass over the logits
+// yields both.
 // The nucleus and the draw use exact running sums instead of the reference's
 // sequential fp32 ones: each probability p carries the integer mass
 // floor(p * 2^52), and in the order (p descending, id ascending; the
@@ -21,12 +24,11 @@
 // Nothing is sorted in HBM.  Tokens are ranked by the 56-bit key
 // D = (bits of p) << 24 | (2^24 - 1 - id), descending, and both positions are
 // weighted radix selects over D, 12 bits a level:
-//   sample_init     (only with seen ids) mark them in a bitmap
-//   sample_scale    l = penalised logit / temperature; block maxima; clears
+//   sample_scale    l = penalised logit / temperature (the block's seen ids
+//                   marked in an LDS bitmap); block max and exp-sum; clears
 //                   the level-0 histogram
-//   sample_exp      e = exp(l - max); block sums
-//   sample_prob     p = e / sum; level-0 histogram (p bits 31..20: count and
-//                   mass per bin)
+//   sample_prob     p = exp(l - max) / sum; level-0 histogram (p bits
+//                   31..20: count and mass per bin)
 //   sample_gather   each block finds, from the histogram, the bin holding the
 //                   cutoff and the bins the draw can reach, and compacts their
 //                   tokens (no grid-wide fence or last-block hand-off: on a
@@ -44,10 +46,13 @@ namespace {
 
 constexpr int kGridThreads = 256;   // grid kernels: 4 consecutive tokens a thread per step
 constexpr int kMaxBlocks = 256;
-constexpr int kSelThreads = 1024;   // sample_select / sample_init
+constexpr int kSelThreads = 1024;   // sample_select
 constexpr int kBins = 4096;         // 12-bit digits
 constexpr int kCandLds = 8192;      // candidates sample_select holds in LDS
 constexpr uint32_t kIdMask = 0xFFFFFFu;
+// seen-id bitmap of one scale block: up to 64 quads a thread (n <= 2^24
+// with 256 blocks of 256 threads), 4 bits a quad
+constexpr int kSeenWords = 64 * 4 * kGridThreads / 32;
 
 __device__ __forceinline__ float load_logit(const void* p, int dtype, int i) {
     if (dtype == kF32) return reinterpret_cast<const float*>(p)[i];
@@ -321,114 +326,131 @@ __global__ __launch_bounds__(kGridThreads) void argmax_final_kernel(const void* 
 
 // ---------------------------------------------------------------- sampling --
 
-// launched only when there are seen ids
-__global__ __launch_bounds__(kSelThreads) void sample_init_kernel(SampleParams p) {
-    for (int w = threadIdx.x; w < (p.n + 31) / 32; w += kSelThreads) p.bitmap[w] = 0u;
-    __syncthreads();
-    for (int j = threadIdx.x; j < p.n_seen; j += kSelThreads) {
-        const int t = p.seen[j];
-        if (t >= 0 && t < p.n) atomicOr(&p.bitmap[t >> 5], 1u << (t & 31));
-    }
-}
-
-// l = (seen ? penalised : logit) / temperature; block maxima
+// l = (seen ? penalised : logit) / temperature; per block the max m_b of l
+// and s_b = sum of exp(l - m_b).  Thread t of block b handles quads
+// q = 256 b + t + k T (tokens 4q..4q+3), k = 0, 1, ...; the block's seen ids
+// are marked in an LDS bitmap indexed by (k, t, token within the quad).
 __global__ __launch_bounds__(kGridThreads) void sample_scale_kernel(SampleParams p) {
     __shared__ float red[kGridThreads];
+    __shared__ uint32_t seen_bm[kSeenWords];
     const int n = p.n;
     const int T = gridDim.x * kGridThreads;
+    const int nq = (n + 3) / 4;
     for (int b = blockIdx.x * kGridThreads + threadIdx.x; b < kBins; b += T) {
         p.h0cnt[b] = 0u;
         p.h0mass[b] = 0ull;
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) *p.ccount = 0u;
+    if (p.n_seen > 0) {
+        for (int w = threadIdx.x; w < kSeenWords; w += kGridThreads) seen_bm[w] = 0u;
+        __syncthreads();
+        for (int j = threadIdx.x; j < p.n_seen; j += kGridThreads) {
+            const int t = p.seen[j];
+            if (t < 0 || t >= n) continue;
+            const int q = t >> 2, r = q % T;
+            if (r / kGridThreads != (int)blockIdx.x) continue;
+            const int bit = (q / T) * (4 * kGridThreads) + (r % kGridThreads) * 4 + (t & 3);
+            atomicOr(&seen_bm[bit >> 5], 1u << (bit & 31));
+        }
+        __syncthreads();
+    }
     float mx = -3.402823466e38f;   // -greatestFiniteMagnitude
-    for (int q = blockIdx.x * kGridThreads + threadIdx.x; 4 * q < n; q += T) {
-        // bits 4q..4q+3 of the seen bitmap
-        const uint32_t seen = p.n_seen > 0 ? (p.bitmap[q >> 3] >> ((q & 7) * 4)) & 15u : 0u;
+    float l0[4] = {0.0f, 0.0f, 0.0f, 0.0f};   // the first quad, kept for the exp-sum pass
+    int k = 0;
+    for (int q = blockIdx.x * kGridThreads + threadIdx.x; q < nq; q += T, ++k) {
+        const int bit0 = k * (4 * kGridThreads) + threadIdx.x * 4;
+        const uint32_t seen = p.n_seen > 0 ? (seen_bm[bit0 >> 5] >> (bit0 & 31)) & 15u : 0u;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int i = 4 * q + k;
+        for (int e = 0; e < 4; ++e) {
+            const int i = 4 * q + e;
             if (i >= n) break;
             float l = load_logit(p.logits, p.dtype, i);
-            if (seen & (1u << k)) l = l > 0.0f ? l / p.penalty : l * p.penalty;
+            if (seen & (1u << e)) l = l > 0.0f ? l / p.penalty : l * p.penalty;
             l = l / p.temperature;
             p.probs[i] = l;
+            if (k == 0) l0[e] = l;
             mx = fmaxf(mx, l);
         }
     }
     red[threadIdx.x] = mx;
     __syncthreads();
-    for (int s = kGridThreads / 2; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
+    for (int s2 = kGridThreads / 2; s2 > 0; s2 >>= 1) {
+        if ((int)threadIdx.x < s2) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s2]);
         __syncthreads();
     }
-    if (threadIdx.x == 0) p.mpart[blockIdx.x] = red[0];
-}
-
-// e = exp(l - max); block sums (each thread in index order, then a halving tree)
-__global__ __launch_bounds__(kGridThreads) void sample_exp_kernel(SampleParams p) {
-    __shared__ float red[kGridThreads];
-    const int n = p.n;
-    const int T = gridDim.x * kGridThreads;
-    red[threadIdx.x] = (int)threadIdx.x < (int)gridDim.x ? p.mpart[threadIdx.x] : -3.402823466e38f;
-    __syncthreads();
-    for (int s = kGridThreads / 2; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
-        __syncthreads();
-    }
-    const float mx = red[0];
+    const float mb = red[0];
     __syncthreads();
     float sm = 0.0f;
-    for (int q = blockIdx.x * kGridThreads + threadIdx.x; 4 * q < n; q += T) {
+    for (int q = blockIdx.x * kGridThreads + threadIdx.x, kk = 0; q < nq; q += T, ++kk) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int i = 4 * q + k;
+        for (int e = 0; e < 4; ++e) {
+            const int i = 4 * q + e;
             if (i >= n) break;
-            const float e = expf(p.probs[i] - mx);
-            p.probs[i] = e;
-            sm += e;
+            sm += expf((kk == 0 ? l0[e] : p.probs[i]) - mb);
         }
     }
     red[threadIdx.x] = sm;
     __syncthreads();
-    for (int s = kGridThreads / 2; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + s];
+    for (int s2 = kGridThreads / 2; s2 > 0; s2 >>= 1) {
+        if ((int)threadIdx.x < s2) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + s2];
         __syncthreads();
     }
-    if (threadIdx.x == 0) p.spart[blockIdx.x] = red[0];
+    if (threadIdx.x == 0) {
+        p.mpart[blockIdx.x] = mb;
+        p.spart[blockIdx.x] = red[0];
+    }
 }
 
-// p = e / sum (block sums added in block order); level-0 histogram
+// p = exp(l - max) / sum, sum = the block exp-sums rescaled to the global
+// max and added in a fixed order; level-0 histogram
 __global__ __launch_bounds__(kGridThreads) void sample_prob_kernel(SampleParams p) {
     __shared__ uint32_t hc[kBins];
     __shared__ unsigned long long hm[kBins];
-    __shared__ float s_sum;
+    __shared__ float s_sum, s_max, wred[kGridThreads / 64];
     const int n = p.n;
     const int T = gridDim.x * kGridThreads;
     for (int b = threadIdx.x; b < kBins; b += kGridThreads) {
         hc[b] = 0u;
         hm[b] = 0ull;
     }
-    // block sums added in block order: loaded in parallel, folded by wave 0
-    if (threadIdx.x < 64) {
-        float s = 0.0f;
-        for (int c = 0; c < (int)gridDim.x; c += 64) {
-            const int b = c + (int)threadIdx.x;
-            const float v = b < (int)gridDim.x ? p.spart[b] : 0.0f;
-            const int m = (int)gridDim.x - c < 64 ? (int)gridDim.x - c : 64;
-            for (int j = 0; j < m; ++j)
-                s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
-        }
-        if (threadIdx.x == 0) s_sum = s;
+    // this thread's first quad, requested before the fold below
+    float l0[4];
+    {
+        const int q = blockIdx.x * kGridThreads + (int)threadIdx.x;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) l0[k] = 4 * q + k < n ? p.probs[4 * q + k] : 0.0f;
+    }
+    // The global max and the denominator: thread t holds block t's pair; the
+    // max is exact in any order; the sum of the rescaled terms runs as a
+    // halving tree within each wave (lanes 32 apart first), then
+    // (w0 + w1) + (w2 + w3).
+    const int G = (int)gridDim.x;
+    const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
+    const float mt = t < G ? p.mpart[t] : -3.402823466e38f;
+    const float st = t < G ? p.spart[t] : 0.0f;
+    float wm = mt;
+    for (int o = 32; o > 0; o >>= 1) wm = fmaxf(wm, __shfl_xor(wm, o, 64));
+    if (lane == 0) wred[wid] = wm;
+    __syncthreads();
+    const float gmax = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+    float term = t < G ? st * expf(mt - gmax) : 0.0f;
+    for (int o = 32; o > 0; o >>= 1) term += __shfl_down(term, o, 64);
+    __syncthreads();   // every wave has read wred
+    if (lane == 0) wred[wid] = term;
+    __syncthreads();
+    if (t == 0) {
+        s_sum = (wred[0] + wred[1]) + (wred[2] + wred[3]);
+        s_max = gmax;
     }
     __syncthreads();
-    const float sm = s_sum;
+    const float sm = s_sum, mx = s_max;
     for (int q = blockIdx.x * kGridThreads + threadIdx.x; 4 * q < n; q += T) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int i = 4 * q + k;
             if (i >= n) break;
-            const float pv = p.probs[i] / sm;
+            const float pv = expf((q == (int)(blockIdx.x * kGridThreads + threadIdx.x) ? l0[k]
+                                                                             : p.probs[i]) - mx) / sm;
             p.probs[i] = pv;
             const uint32_t key = __float_as_uint(pv);
             atomicAdd(&hc[key >> 20], 1u);
@@ -456,6 +478,14 @@ __global__ __launch_bounds__(kGridThreads) void sample_gather_kernel(SampleParam
     const int n = p.n;
     const int T = gridDim.x * kGridThreads;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    // this thread's first quad, requested before the histogram scan so the
+    // two memory latencies overlap
+    uint32_t key0[4];
+    {
+        const int q = blockIdx.x * kGridThreads + (int)threadIdx.x;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) key0[k] = 4 * q + k < n ? __float_as_uint(p.probs[4 * q + k]) : 0u;
+    }
     const unsigned long long t1 = target_top_p(p.top_p);
     BinScan<kGridThreads> scan;
     scan.load(p.h0cnt, p.h0mass, 0ull, sc);
@@ -480,7 +510,8 @@ __global__ __launch_bounds__(kGridThreads) void sample_gather_kernel(SampleParam
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int i = 4 * q + k;
-            key[k] = i < n ? __float_as_uint(p.probs[i]) : 0u;
+            key[k] = qb == (int)(blockIdx.x * kGridThreads) ? key0[k]
+                     : i < n ? __float_as_uint(p.probs[i]) : 0u;
             const int b = (int)(key[k] >> 20);
             bal[k] = __ballot(i < n && (b == b1 || (b >= lo && b <= hi)));
         }
@@ -622,7 +653,7 @@ size_t up256(size_t b) { return (b + 255) / 256 * 256; }
 size_t argmax_workspace_bytes() { return 2 * kMaxBlocks * 4; }
 
 size_t sample_workspace_bytes(int n) {
-    return up256((size_t)n * 4) + up256(((size_t)n + 31) / 32 * 4) + 2 * up256(kMaxBlocks * 4) +
+    return up256((size_t)n * 4) + 2 * up256(kMaxBlocks * 4) +
            up256(kBins * 4) + up256(kBins * 8) + 256 + up256((size_t)n * 8);
 }
 
@@ -643,8 +674,6 @@ hipError_t launch_sample(SampleParams p, void* ws, hipStream_t st) {
     const size_t n = (size_t)p.n;
     p.probs = reinterpret_cast<float*>(w);
     w += up256(n * 4);
-    p.bitmap = reinterpret_cast<uint32_t*>(w);
-    w += up256((n + 31) / 32 * 4);
     p.mpart = reinterpret_cast<float*>(w);
     w += up256(kMaxBlocks * 4);
     p.spart = reinterpret_cast<float*>(w);
@@ -657,10 +686,7 @@ hipError_t launch_sample(SampleParams p, void* ws, hipStream_t st) {
     w += 256;
     p.cand = reinterpret_cast<uint2*>(w);
     const int G = grid_blocks(p.n);
-    if (p.n_seen > 0)
-        hipLaunchKernelGGL(sample_init_kernel, dim3(1), dim3(kSelThreads), 0, st, p);
     hipLaunchKernelGGL(sample_scale_kernel, dim3(G), dim3(kGridThreads), 0, st, p);
-    hipLaunchKernelGGL(sample_exp_kernel, dim3(G), dim3(kGridThreads), 0, st, p);
     hipLaunchKernelGGL(sample_prob_kernel, dim3(G), dim3(kGridThreads), 0, st, p);
     hipLaunchKernelGGL(sample_gather_kernel, dim3(G), dim3(kGridThreads), 0, st, p);
     hipLaunchKernelGGL(sample_select_kernel, dim3(1), dim3(kSelThreads), 0, st, p);
