@@ -67,6 +67,9 @@ def parse():
     ap.add_argument("--traffic", action="store_true",
                     help="only: 24 launches of the dominant kernel over 12 weight copies, then a "
                          "256 MiB torch copy (the calibration kernel), for rocprofv3 --pmc runs")
+    ap.add_argument("--gemm-pmc", action="store_true",
+                    help="only: 10 launches each of the M=750 prefill gate/up (SiLU) and down "
+                         "GEMMs, for rocprofv3 --pmc MFMA-utilisation runs")
     return ap.parse_args()
 
 
@@ -105,6 +108,9 @@ def main():
 
     if args.traffic:
         traffic_run(pkg, torch, gen, dev)
+        return
+    if args.gemm_pmc:
+        gemm_pmc_run(pkg, torch, gen, dev)
         return
 
     layers = [Layer(pkg, torch, gen, dev) for _ in range(args.copies)]
@@ -315,6 +321,26 @@ def traffic_run(pkg, torch, gen, dev):
     dst.copy_(src)
     torch.cuda.synchronize()
     print("traffic run done", flush=True)
+
+
+def gemm_pmc_run(pkg, torch, gen, dev):
+    """Workload for the MFMA-utilisation passes: the M=750 prefill GEMMs
+    (gate/up with SiLU x up, and down, split-K) 10 times each, after one
+    warm-up launch each."""
+    M, K, F = 750, 3072, 8192
+    x = torch.randn(M, K, generator=gen, device=dev).half()
+    a = torch.randn(M, F, generator=gen, device=dev).half()
+    gate = pkg.Q4Weight(*rand_q4(torch, F, K, gen, dev), K, G)
+    up = pkg.Q4Weight(*rand_q4(torch, F, K, gen, dev), K, G)
+    down = pkg.Q4Weight(*rand_q4(torch, K, F, gen, dev), F, G)
+    y = torch.empty(M, F, device=dev, dtype=torch.float16)
+    z = torch.empty(M, K, device=dev, dtype=torch.float16)
+    for _ in range(11):
+        pkg.matmul_q4_silu_mul(x, gate, up, M, K, F, out=y)
+    for _ in range(11):
+        pkg.linear(a, down, M, F, K, fast=True, out=z)
+    torch.cuda.synchronize()
+    print("gemm pmc run done", flush=True)
 
 
 def _wsb(q):
