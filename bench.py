@@ -186,6 +186,7 @@ def main():
     if args.diag:
         diag = timing_diagnostics(pkg, torch, layers, x2, outs, reps)
 
+    copy_gbs = stream_copy_ceiling(torch, dev)
     fused = fused_layer_leg(pkg, torch, gen, dev, layers, reps)
     select = token_select_leg(pkg, torch, gen, dev)
 
@@ -216,7 +217,11 @@ def main():
                      "traffic": traffic_from_profiles(),
                      "kernel": "q4_gemv_kernel<32,3,true,false,0> (gate/up fused SiLU*up)",
                      "avg_us": round(dom_us, 3), "bytes_per_launch": DOMINANT_BYTES,
-                     "timing": timing},
+                     "timing": timing,
+                     "measured_ceiling": {"gbs": copy_gbs,
+                                          "what": "1 GiB device copy (torch copy_) in a graph, "
+                                                  "bytes read + written per second",
+                                          "frac": round(achieved / copy_gbs, 4)}},
         "cpu_baseline": cpu,
         "extra": {"decode_layer_fused_norms": fused, "token_select": select, "gemm": gemm,
                   **({"timing_diag": diag} if diag else {})},
@@ -485,11 +490,48 @@ def cpu_baseline(seconds):
         if time.perf_counter() - t0 >= seconds and layers >= 2:
             break
     dt = time.perf_counter() - t0
+    # single-thread scalar run of the same layer, about a quarter of the time
+    layers1 = 0
+    t1 = time.perf_counter()
+    while True:
+        ys = {n: o.c_cpu_matmul_q4(*data[n], G, 1) for n, _, _ in projs}
+        o.c_silu_mul(ys["gate_proj"], ys["up_proj"])
+        layers1 += 1
+        if time.perf_counter() - t1 >= seconds / 4 and layers1 >= 1:
+            break
+    dt1 = time.perf_counter() - t1
     return {"value": round(layers * LAYER_BYTES / dt / 1e9, 4), "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": f"{layers} decode layers (same 7 projections + silu_mul, {LAYER_BYTES} "
                       f"algorithmic bytes each) in {dt:.1f} s, {threads} threads",
-            "host_cpus": cores}
+            "host_cpus": cores,
+            "single_thread": {"value": round(layers1 * LAYER_BYTES / dt1 / 1e9, 4),
+                              "unit": "GB/s",
+                              "sample": f"{layers1} decode layers in {dt1:.1f} s, 1 thread"}}
+
+
+def stream_copy_ceiling(torch, dev, gib=1, reps=10):
+    """Measured HBM ceiling: a device-to-device copy of `gib` GiB (torch
+    copy_), captured in a graph and replayed; bytes read + written per second."""
+    n = gib * 2 ** 30 // 2
+    src = torch.empty(n, device=dev, dtype=torch.float16).normal_()
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        dst.copy_(src)
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g.replay()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / reps
+    gbs = 2 * n * 2 / dt / 1e9
+    del src, dst
+    torch.cuda.empty_cache()
+    return round(gbs, 1)
 
 
 def traffic_from_profiles():
