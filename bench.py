@@ -188,6 +188,7 @@ def main():
 
     copy_gbs = stream_copy_ceiling(torch, dev)
     fused = fused_layer_leg(pkg, torch, gen, dev, layers, reps)
+    decode = decode_token_leg(pkg, torch, gen, dev, layers)
     select = token_select_leg(pkg, torch, gen, dev)
 
     gemm = {} if args.no_gemm else gemm_legs(pkg, torch, gen, dev)
@@ -223,7 +224,8 @@ def main():
                                                   "bytes read + written per second",
                                           "frac": round(achieved / copy_gbs, 4)}},
         "cpu_baseline": cpu,
-        "extra": {"decode_layer_fused_norms": fused, "token_select": select, "gemm": gemm,
+        "extra": {"decode_layer_fused_norms": fused, "decode_token_greedy": decode,
+                  "token_select": select, "gemm": gemm,
                   **({"timing_diag": diag} if diag else {})},
     }
     print(json.dumps(line))
@@ -274,6 +276,49 @@ def fused_layer_leg(pkg, torch, gen, dev, layers, reps):
             "bytes_per_layer": nbytes, "launches_per_layer": 4,
             "note": "rms_norm, residual add + rms_norm and the final residual add run inside "
                     "the projections' kernels"}
+
+
+def decode_token_leg(pkg, torch, gen, dev, layers, reps=20):
+    """A greedy Llama-3.2-3B decode step's matmul path (swiftltx_amd.decode):
+    4-bit embedding gather, 28 layers (RMSNorm + q|k|v, o, residual + RMSNorm
+    + gate/up SiLU, down + residual), final RMSNorm + tied 4-bit lm_head over
+    128256 tokens, argmax -- one HIP graph per token, the token id fed back on
+    the device.  Attention is outside the path: its stand-in is the q rows (a
+    view, no launch).  Random weights: the first 28 of the rotated layer
+    copies, norm weights 1 + 0.1 N(0,1)."""
+    from types import SimpleNamespace
+    from swiftltx_amd.decode import DecodeStep
+    from swiftltx_amd.weights import LayerWeights
+    K, V, L = 3072, 128256, 28
+    norm = lambda: (1.0 + 0.1 * torch.randn(K, generator=gen, device=dev)).float()
+    embed = pkg.Q4Weight(*rand_q4(torch, V, K, gen, dev), K, G)
+    lws = []
+    for lay in layers[:L]:
+        w = lay.w
+        lws.append(LayerWeights(q_proj=None, k_proj=None, v_proj=None, o_proj=w["o_proj"][0],
+                                gate_proj=w["gate_up_proj"][0], up_proj=w["gate_up_proj"][1],
+                                down_proj=w["down_proj"][0], input_norm_weight=norm(),
+                                post_norm_weight=norm(), qkv_proj=w["qkv_proj"][0]))
+    cfg = SimpleNamespace(hidden_size=K, intermediate_size=8192, num_attention_heads=24,
+                          num_key_value_heads=8, head_dim=128, vocab_size=V, rms_norm_eps=1e-5)
+    mw = SimpleNamespace(config=cfg, embed_tokens=embed, lm_head=embed, norm_weight=norm(),
+                         layers=lws)
+    s = torch.cuda.Stream()
+    ds = DecodeStep(mw, stream=s)
+    ds.capture()
+    ds.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        ds.replay()
+    torch.cuda.synchronize()
+    us = 1e6 * (time.perf_counter() - t0) / reps
+    nbytes = (L * (LAYER_BYTES + 2 * K * 4) + gemv_bytes(V, K) + K * 4 + K // 2 + 4 * K // G + 2 * K)
+    return {"us_per_token": round(us, 1), "tokens_per_s": round(1e6 / us, 1),
+            "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes_per_token": nbytes,
+            "launches_per_token": 1 + 4 * L + 1 + 2, "layers": L,
+            "note": "attention (RoPE, KV cache, softmax) is outside the 4-bit path; stand-in = "
+                    "the q rows"}
 
 
 def token_select_leg(pkg, torch, gen, dev, vocab=128256, reps=200):
