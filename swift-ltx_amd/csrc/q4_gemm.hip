@@ -753,12 +753,14 @@ __global__ __launch_bounds__(256) void q4_splitk_reduce_kernel(GemmParams p) {
 }
 
 // Launch plan: block-tile height WM (BM = 64*WM) and K splits, chosen by
-// estimated time on 256 CUs: rounds of blocks x k-tiles per block x the
-// measured time of one k-tile (1.37 us at BM = 192, 0.85 us at BM = 128, a
-// 256-row W tile), plus about 10 us per launch (prologue, epilogue), plus,
-// when split, writing the fp32 partials (~6 TB/s) and the reduce pass
-// reading them back (~4 TB/s, its own launch).  Splits cover an even number
-// of k-tiles (packed weights move two k-tiles at a time).
+// estimated time on 256 CUs: rounds of blocks x (k-tiles per block x the
+// measured time of one k-tile -- 1.37 us at BM = 192, 0.95 us at BM = 128,
+// a 256-row W tile -- plus ~8 us of prologue and epilogue, which every round
+// repeats) + ~2 us per launch, plus, when split, writing the fp32 partials
+// (~6 TB/s) and the reduce pass reading them back (~4 TB/s, its own launch).
+// Measured at M = 750 (lm_head, N = 128256): 664 us at BM = 192 vs 730 us at
+// BM = 128; DiT up (M = 6144, bf16): 318 vs 356 us.  Splits cover an even
+// number of k-tiles (packed weights move two k-tiles at a time).
 struct GemmPlan {
     int wm, tiles_m, tiles_n, splits, split_tiles;
     size_t ws_bytes;
@@ -776,7 +778,7 @@ static GemmPlan plan_gemm(const GemmParams& p, bool allow_split) {
         const int bm = 64 * wm;
         const long tiles_m = (p.M + bm - 1) / bm;
         const long tiles = tiles_m * tiles_n;
-        const double kt_us = wm == 3 ? 1.37 : 0.85;
+        const double kt_us = wm == 3 ? 1.37 : 0.95;
         const int smax = allow_split ? 8 : 1;
         for (int s = 1; s <= smax; ++s) {
             if (s > 1 && nk < 8 * s) break;
@@ -786,7 +788,7 @@ static GemmPlan plan_gemm(const GemmParams& p, bool allow_split) {
             if (s > 1 && s_eff != s) continue;
             const long blocks = tiles * s_eff;
             const long rounds = (blocks + kCUs - 1) / kCUs;
-            double us = (double)rounds * chunk * kt_us + 10.0;
+            double us = (double)rounds * (chunk * kt_us + 8.0) + 2.0;
             if (s_eff > 1) {
                 const double part = (double)s_eff * p.M * nw * 4.0;
                 us += part / 6.0e6 + 3.0 + (part + (double)p.M * p.N * 2.0) / 4.0e6;
