@@ -21,6 +21,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+constexpr int kCUs = 256;   // compute units of an MI355X (8 XCDs x 32)
+
 // fp16 bit pattern of 1024.0: OR-ing a value v < 1024 into its mantissa gives
 // the fp16 number 1024 + v exactly (Kim et al. 2022, "Who Says Elephants
 // Can't Run", int4 -> fp16 conversion by mantissa insertion).

@@ -54,7 +54,6 @@ constexpr int BN = 256, BK = 64;
 constexpr int NW = 8;                  // waves per block (two per SIMD)
 constexpr int kThreads = 64 * NW;
 constexpr int NT = BN / 32 / NW;       // 32-row weight tiles (MFMA N-tiles) per wave
-constexpr int kCUs = 256;
 constexpr int NSA = 4;     // A stages in LDS
 constexpr int GPMAX = 4;   // scale/bias groups per row per 128 k (group size 32)
 

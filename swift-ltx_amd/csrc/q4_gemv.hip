@@ -33,11 +33,13 @@ namespace sltx {
 
 // Prepared x for one chunk of 32 values: 16 fp16 pairs in dot order, plus
 // (-corr, sum).  Stored planar in LDS: xs[j][chunk] holds pairs 4j..4j+3.
+constexpr int kGemvMaxWaves = 16;   // waves per block: 4 .. 16, chosen per launch
+
 template <int NCH>
 struct GemvLds {
     u32x4 xs[4][NCH];
     float2 xc[NCH];
-    float red[4];   // per-wave partial sums of squares (RMS-norm prologue)
+    float red[kGemvMaxWaves];   // per-wave partial sums of squares (RMS-norm prologue)
 };
 
 // Build the dot-order pairs for 8 consecutive x values (one weight word).
@@ -174,22 +176,32 @@ __device__ __forceinline__ void gemv_compute_store(const GemvStage<CPL, NW>& st,
 // kernel carries no loop).  PRO (GemvPro): the input is x, rms_norm(x) or
 // rms_norm(x + xb); each block recomputes the norm of its own copy of the
 // input vector (K values) while its first weight loads are in flight.
+// Largest block (in waves) of one instantiation: a block of w waves leaves a
+// wave 2048 / w VGPRs (4 waves per SIMD at w = 16).  The two-weight-set and
+// pipelined (MULTI) kernels hold two to four times the weight registers, and
+// more than 4 chunks per lane doubles them again; each cap keeps its kernel
+// free of spills.
+template <int CPL, bool SWIGLU, bool MULTI>
+constexpr int gemv_max_waves() { return ((SWIGLU || MULTI) ? 8 : 16) / (CPL > 4 ? 2 : 1); }
+
+// Blocks of 4 to gemv_max_waves() waves (blockDim.x / 64, chosen per launch).
 template <int L, int CPL, bool SWIGLU, bool MULTI, int PRO>
-__global__ __launch_bounds__(256) void q4_gemv_kernel(GemvParams p, int T) {
+__global__ __launch_bounds__((64 * gemv_max_waves<CPL, SWIGLU, MULTI>())) void q4_gemv_kernel(GemvParams p, int T) {
     constexpr int RPI = 64 / L;        // rows per wave-wide instruction
     constexpr int NCH = L * CPL;       // chunks per row (K / 32)
     constexpr int NW = SWIGLU ? 2 : 1; // weight sets
     __shared__ GemvLds<NCH> lds;
 
+    const int NTH = blockDim.x;        // 256 .. 1024 threads
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int kl = lane % L;
     const int sub = lane / L;
-    const int row0 = (blockIdx.x * 4 + wave) * (RPI * T) + sub;
+    const int row0 = (blockIdx.x * (NTH >> 6) + wave) * (RPI * T) + sub;
 
     // x loads first: vmcnt retires in issue order, so x issued after the
     // weights would make the x preparation wait for the HBM latency too.
-    constexpr int XPT = (NCH + 255) / 256;  // x chunks prepared per thread
+    constexpr int XPT = (NCH + 255) / 256;  // x chunks prepared per thread (at most)
     constexpr bool NORM = PRO != kProNone, RES = PRO == kProResidualRms;
     f16x8 xr[XPT][4];
     f16x8 xb[RES ? XPT : 1][4];
@@ -199,8 +211,8 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(GemvParams p, int T) {
         // Waves whose chunks all lie past NCH load nothing (wave-uniform
         // branch): at K = 3072 only 96 of 256 threads own a chunk, and
         // redundant loads would only delay the weight loads queued behind them.
-        if (__builtin_amdgcn_readfirstlane((int)(threadIdx.x & ~63u)) + 256 * u >= NCH) continue;
-        const int c = threadIdx.x + 256 * u;
+        if (__builtin_amdgcn_readfirstlane((int)(threadIdx.x & ~63u)) + NTH * u >= NCH) continue;
+        const int c = threadIdx.x + NTH * u;
         const int cc = c < NCH ? c : NCH - 1;
         const f16x8* xp = reinterpret_cast<const f16x8*>(p.x + (size_t)cc * 32);
 #pragma unroll
@@ -234,7 +246,7 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(GemvParams p, int T) {
         float ss = 0.0f;
 #pragma unroll
         for (int u = 0; u < XPT; ++u) {
-            const int c = threadIdx.x + 256 * u;
+            const int c = threadIdx.x + NTH * u;
             if (c >= NCH) continue;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
@@ -258,7 +270,9 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(GemvParams p, int T) {
         ss = row_reduce<64>(ss);
         if ((threadIdx.x & 63) == 0) lds.red[threadIdx.x >> 6] = ss;
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        const float rms = rsqrtf((lds.red[0] + lds.red[1] + lds.red[2] + lds.red[3]) / (float)p.K + p.eps);
+        float ssum = 0.0f;
+        for (int w = 0; w < (NTH >> 6); ++w) ssum += lds.red[w];
+        const float rms = rsqrtf(ssum / (float)p.K + p.eps);
 #pragma unroll
         for (int u = 0; u < XPT; ++u)
 #pragma unroll
@@ -271,7 +285,7 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(GemvParams p, int T) {
     // Prepare x once per block while the weight loads are in flight.
 #pragma unroll
     for (int u = 0; u < XPT; ++u) {
-        const int c = threadIdx.x + 256 * u;
+        const int c = threadIdx.x + NTH * u;
         if (c < NCH) {
             float corr = 0.0f, sum = 0.0f;
 #pragma unroll
@@ -389,6 +403,18 @@ __global__ __launch_bounds__(256) void q4_gemv_generic_kernel(GemvParams p) {
 
 // ----------------------------------------------------------------- dispatch --
 
+// Waves per block: about one block per CU, 4 to max_w waves.  The input
+// vector is prepared once per block, so fewer, larger blocks prepare fewer
+// copies of it; balanced blocks keep every CU's share equal.  Measured on the
+// decode-layer launches (us, vs 4-wave blocks): down 4.55 vs 4.79 (12 waves),
+// q|k|v 3.78 vs 4.00 (10), q|k|v with the rms_norm prologue 4.31 vs 5.68
+// (10), gate/up 7.03 vs 7.29 (8), gate/up with residual + rms_norm 8.47 vs
+// 9.03 (8).
+static int gemv_block_waves(long waves, int max_w) {
+    long w = (waves + kCUs - 1) / kCUs;
+    return (int)(w < 4 ? 4 : w > max_w ? max_w : w);
+}
+
 template <int L, int CPL, bool SWIGLU>
 static hipError_t launch_lc(const GemvParams& p, hipStream_t st) {
     constexpr int RPI = 64 / L;
@@ -405,23 +431,21 @@ static hipError_t launch_lc(const GemvParams& p, hipStream_t st) {
     if (T < 1) T = 1;
     if (T > 8) T = 8;
     const long waves = (iters + T - 1) / T;
-    const long grid = (waves + 3) / 4;
     // Prologues instantiated: rms_norm for the plain GEMV (q|k|v after
     // input_layernorm), residual + rms_norm for the fused gate/up.
     constexpr int PRO_N = SWIGLU ? kProResidualRms : kProRms;
     const bool norm = p.pro != kProNone;
+    const int wpb = gemv_block_waves(waves, T > 1 ? gemv_max_waves<CPL, SWIGLU, true>()
+                                                   : gemv_max_waves<CPL, SWIGLU, false>());
+    const dim3 grid((unsigned)((waves + wpb - 1) / wpb)), block(64 * wpb);
     if (T > 1 && norm)
-        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, true, PRO_N>), dim3((unsigned)grid), dim3(256),
-                           0, st, p, (int)T);
+        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, true, PRO_N>), grid, block, 0, st, p, (int)T);
     else if (T > 1)
-        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, true, kProNone>), dim3((unsigned)grid),
-                           dim3(256), 0, st, p, (int)T);
+        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, true, kProNone>), grid, block, 0, st, p, (int)T);
     else if (norm)
-        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, false, PRO_N>), dim3((unsigned)grid), dim3(256),
-                           0, st, p, 1);
+        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, false, PRO_N>), grid, block, 0, st, p, 1);
     else
-        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, false, kProNone>), dim3((unsigned)grid),
-                           dim3(256), 0, st, p, 1);
+        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, false, kProNone>), grid, block, 0, st, p, 1);
     return hipGetLastError();
 }
 
