@@ -17,7 +17,7 @@
  *     workspace: fp32 partial sums for GEMMs with too few output tiles to
  *     fill the GPU (split-K, e.g. M=750 x N=3072), the block partials of
  *     sltx_argmax, and the probabilities and candidate list of
- *     sltx_sample_top_p.  There is one per (device, stream),
+ *     sltx_sample_top_p[_state].  There is one per (device, stream),
  *     grown on first need to at least twice its old size; a replaced buffer
  *     is never freed (a graph captured earlier may still use it), so every
  *     buffer lives until the process exits.  A stream being captured into a
@@ -234,6 +234,32 @@ int sltx_argmax(const void* logits, int32_t dtype, int32_t n, int32_t* out_index
 int sltx_sample_top_p(const void* logits, int32_t dtype, int32_t n, float temperature,
                       float top_p, float repetition_penalty, const int32_t* seen,
                       int32_t n_seen, float u, int32_t* out_index, void* stream);
+
+/* Sampler state kept in device memory, so that a sampled decode step takes no
+ * per-token host argument and can be captured once as a HIP graph.  The
+ * reference keeps the same state on the host: seenTokens = the prompt plus
+ * every generated token (LlamaModel.swift:150-161) and Float.random for the
+ * draw (Ops.swift:2092).  All pointers are device pointers, 4-byte aligned. */
+typedef struct sltx_sample_state {
+    int32_t* history;          /* token ids; history[0 .. *history_len) are the seen ids */
+    int32_t* history_len;      /* [1] entries in use; clamped to [0, history_capacity] */
+    int32_t history_capacity;  /* entries history can hold (>= 0) */
+    const float* draws;        /* uniform draws in [0, 1): one per call */
+    int32_t* next_draw;        /* [1] index of the next call's draw, taken modulo draw_count */
+    int32_t draw_count;        /* entries in draws (>= 1) */
+} sltx_sample_state;
+
+/* sltx_sample_top_p with seen = history[0 .. *history_len) and
+ * u = draws[*next_draw mod draw_count] read on the device (a draw outside
+ * [0, 1), or NaN, is clamped into it).  After choosing, the call appends the
+ * token to history (dropped once history_capacity entries are in use) and
+ * sets *next_draw to the following index.  The reference has no separate
+ * entry point for this: it is sample() with the state the reference keeps on
+ * the host moved to device memory.  Calls on one state are ordered only by
+ * their stream; calls that share a state on different streams race. */
+int sltx_sample_top_p_state(const void* logits, int32_t dtype, int32_t n, float temperature,
+                            float top_p, float repetition_penalty,
+                            const sltx_sample_state* state, int32_t* out_index, void* stream);
 
 /* ---- safetensors weights (SafeTensorsFile, SafeTensors.swift:41-118) ----
  * Reads the files swift-ltx's loader reads (ModelWeights.swift:40-154) into

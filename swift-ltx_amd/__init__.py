@@ -58,6 +58,7 @@ EXPORTED = (
     "sltx_matmul_q4_residual",
     "sltx_argmax",
     "sltx_sample_top_p",
+    "sltx_sample_top_p_state",
     "sltx_st_open",
     "sltx_st_close",
     "sltx_st_num_tensors",
@@ -83,6 +84,18 @@ class CQ4Weight(ctypes.Structure):
         ("biases", ctypes.c_void_p),
         ("K", ctypes.c_int32),
         ("group_size", ctypes.c_int32),
+    ]
+
+
+class CSampleState(ctypes.Structure):
+    """sltx_sample_state."""
+    _fields_ = [
+        ("history", ctypes.c_void_p),
+        ("history_len", ctypes.c_void_p),
+        ("history_capacity", ctypes.c_int32),
+        ("draws", ctypes.c_void_p),
+        ("next_draw", ctypes.c_void_p),
+        ("draw_count", ctypes.c_int32),
     ]
 
 
@@ -134,9 +147,11 @@ def lib():
         L.sltx_matmul_q4_residual.argtypes = [P, W, P, P, I32, I32, P]
         L.sltx_argmax.argtypes = [P, I32, I32, P, P]
         L.sltx_sample_top_p.argtypes = [P, I32, I32, F, F, F, P, I32, F, P, P]
+        L.sltx_sample_top_p_state.argtypes = [P, I32, I32, F, F, F,
+                                              ctypes.POINTER(CSampleState), P, P]
         for n in ("sltx_rms_norm", "sltx_residual_rms_norm", "sltx_rmsnorm_matmul_q4",
                   "sltx_residual_rmsnorm_matmul_q4_silu_mul", "sltx_matmul_q4_residual",
-                  "sltx_argmax", "sltx_sample_top_p"):
+                  "sltx_argmax", "sltx_sample_top_p", "sltx_sample_top_p_state"):
             getattr(L, n).restype = ctypes.c_int
         VP = ctypes.c_void_p
         L.sltx_st_open.argtypes = [ctypes.c_char_p, ctypes.POINTER(VP)]
@@ -394,6 +409,68 @@ def sample(logits, temperature=0.7, top_p=0.9, repetition_penalty=1.1, seen_toke
                                   temperature, top_p, repetition_penalty,
                                   _ptr(seen_tokens) if n_seen else None, n_seen, u, _ptr(out),
                                   _stream(stream)))
+    return out
+
+
+class SamplerState:
+    """sltx_sample_state: the sampler's token history and uniform draws in
+    device memory, so a sampled step takes no per-token host argument (the
+    reference keeps both on the host: seenTokens = prompt + generated,
+    LlamaModel.swift:150-161, and Float.random, Ops.swift:2092).
+
+    history: token ids already seen (the prompt); capacity: history entries
+    (the chosen tokens are appended until it is full); draws: uniform draws in
+    [0, 1) used one per call, cyclically (a float32 sequence or a count, in
+    which case they are drawn here with torch's generator)."""
+
+    def __init__(self, capacity, draws=4096, history=(), device="cuda", generator=None):
+        torch = _torch()
+        if capacity < 0:
+            raise ValueError("capacity must be >= 0")
+        self.history = torch.zeros(max(1, capacity), dtype=torch.int32, device=device)
+        self.history_len = torch.zeros(1, dtype=torch.int32, device=device)
+        self.capacity = int(capacity)
+        if isinstance(draws, int):
+            draws = torch.rand(draws, generator=generator, device=device)
+        self.draws = torch.as_tensor(draws, dtype=torch.float32, device=device).contiguous()
+        if self.draws.numel() < 1:
+            raise ValueError("at least one draw")
+        self.next_draw = torch.zeros(1, dtype=torch.int32, device=device)
+        self.set_history(history)
+        self.c = CSampleState(_ptr(self.history), _ptr(self.history_len), self.capacity,
+                              _ptr(self.draws), _ptr(self.next_draw), int(self.draws.numel()))
+
+    def set_history(self, tokens):
+        """Replace the history (e.g. with a new prompt); keeps at most
+        `capacity` ids.  Host-side copy: call outside graph capture."""
+        torch = _torch()
+        t = torch.as_tensor(list(tokens), dtype=torch.int32)[: self.capacity]
+        if t.numel():
+            self.history[: t.numel()].copy_(t)
+        self.history_len.fill_(int(t.numel()))
+
+    def set_draws(self, draws, start=0):
+        """Overwrite the draws in place (same count) and the next index."""
+        torch = _torch()
+        self.draws.copy_(torch.as_tensor(draws, dtype=torch.float32))
+        self.next_draw.fill_(int(start))
+
+    def tokens(self):
+        """The history as a host list."""
+        n = int(self.history_len.item())
+        return self.history[:n].tolist()
+
+
+def sample_with_state(logits, temperature, top_p, repetition_penalty, state, out=None,
+                      stream=None):
+    """sample(...) with seen tokens and the draw taken from `state` (a
+    SamplerState) in device memory; appends the chosen token to the history
+    and advances the draw.  Capturable in a HIP graph (after one eager call
+    on the same stream, which sizes the workspace)."""
+    out = _new((1,), _torch().int32, logits) if out is None else out
+    check(lib().sltx_sample_top_p_state(_ptr(logits), _logits_dtype(logits), int(logits.numel()),
+                                        temperature, top_p, repetition_penalty,
+                                        ctypes.byref(state.c), _ptr(out), _stream(stream)))
     return out
 
 

@@ -216,6 +216,46 @@ int matmul_common(const char* fn, const void* x, const uint32_t* weight, const u
     return run_gemm(fn, x, kF16, w, nullptr, nullptr, kEpiNone, out, y_dtype, M, K, N, st);
 }
 
+// Checks shared by both sampling entry points.
+int check_sample(const char* fn, const void* logits, int dtype, int n, float temperature,
+                 float top_p, float repetition_penalty, const int32_t* out_index) {
+    if (n <= 0) return fail(kErrInvalid, "%s: n must be positive (got %d)", fn, n);
+    if (n > (1 << 24)) return fail(kErrInvalid, "%s: n = %d exceeds 2^24 tokens", fn, n);
+    if (dtype != kF16 && dtype != kF32)
+        return fail(kErrInvalid, "%s: dtype %d must be SLTX_F16 or SLTX_F32", fn, dtype);
+    if (!(temperature > 0.0f) || !(top_p > 0.0f) || !(repetition_penalty > 0.0f))
+        return fail(kErrInvalid, "%s: temperature, top_p and repetition_penalty must be positive", fn);
+    if (!logits || !out_index) return fail(kErrInvalid, "%s: null pointer argument", fn);
+    if (!aligned(logits, dtype == kF32 ? 4 : 2) || !aligned(out_index, 4))
+        return fail(kErrInvalid, "%s: misaligned pointer", fn);
+    return kOk;
+}
+
+int run_sample(const char* fn, SampleParams& p, void* stream) {
+    int rc = ensure_device();
+    if (rc != kOk) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    void* ws = stream_workspace(st, sample_workspace_bytes(p.n));
+    if (!ws)
+        return fail(kErrInvalid,
+                    "%s: no workspace for n = %d on this stream (it is being captured: sample "
+                    "once eagerly on the same stream first)", fn, p.n);
+    return finish(launch_sample(p, ws, st), fn);
+}
+
+SampleParams sample_params(const void* logits, int dtype, int n, float temperature, float top_p,
+                           float repetition_penalty, int32_t* out_index) {
+    SampleParams p = {};
+    p.logits = logits;
+    p.dtype = dtype;
+    p.n = n;
+    p.temperature = temperature;
+    p.top_p = top_p;
+    p.penalty = repetition_penalty;
+    p.out = out_index;
+    return p;
+}
+
 }  // namespace
 }  // namespace sltx
 
@@ -396,39 +436,43 @@ int sltx_sample_top_p(const void* logits, int32_t dtype, int32_t n, float temper
                       float top_p, float repetition_penalty, const int32_t* seen, int32_t n_seen,
                       float u, int32_t* out_index, void* stream) {
     const char* fn = "sltx_sample_top_p";
-    if (n <= 0) return fail(kErrInvalid, "%s: n must be positive (got %d)", fn, n);
-    if (n > (1 << 24)) return fail(kErrInvalid, "%s: n = %d exceeds 2^24 tokens", fn, n);
-    if (dtype != kF16 && dtype != kF32)
-        return fail(kErrInvalid, "%s: dtype %d must be SLTX_F16 or SLTX_F32", fn, dtype);
-    if (!(temperature > 0.0f) || !(top_p > 0.0f) || !(repetition_penalty > 0.0f))
-        return fail(kErrInvalid, "%s: temperature, top_p and repetition_penalty must be positive", fn);
+    int rc = check_sample(fn, logits, dtype, n, temperature, top_p, repetition_penalty, out_index);
+    if (rc != kOk) return rc;
     if (!(u >= 0.0f && u < 1.0f)) return fail(kErrInvalid, "%s: u must lie in [0, 1)", fn);
     if (n_seen < 0) return fail(kErrInvalid, "%s: negative n_seen", fn);
-    if (!logits || !out_index || (n_seen > 0 && !seen))
-        return fail(kErrInvalid, "%s: null pointer argument", fn);
-    if (!aligned(logits, dtype == kF32 ? 4 : 2) || !aligned(out_index, 4) ||
-        (seen && !aligned(seen, 4)))
-        return fail(kErrInvalid, "%s: misaligned pointer", fn);
-    int rc = ensure_device();
-    if (rc != kOk) return rc;
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    void* ws = stream_workspace(st, sample_workspace_bytes(n));
-    if (!ws)
-        return fail(kErrInvalid,
-                    "%s: no workspace for n = %d on this stream (it is being captured: sample "
-                    "once eagerly on the same stream first)", fn, n);
-    SampleParams p;
-    p.logits = logits;
-    p.dtype = dtype;
-    p.n = n;
-    p.temperature = temperature;
-    p.top_p = top_p;
-    p.penalty = repetition_penalty;
+    if (n_seen > 0 && !seen) return fail(kErrInvalid, "%s: null pointer argument", fn);
+    if (seen && !aligned(seen, 4)) return fail(kErrInvalid, "%s: misaligned pointer", fn);
+    SampleParams p = sample_params(logits, dtype, n, temperature, top_p, repetition_penalty, out_index);
     p.u = u;
     p.seen = seen;
     p.n_seen = n_seen;
-    p.out = out_index;
-    return finish(launch_sample(p, ws, st), fn);
+    return run_sample(fn, p, stream);
+}
+
+int sltx_sample_top_p_state(const void* logits, int32_t dtype, int32_t n, float temperature,
+                            float top_p, float repetition_penalty, const sltx_sample_state* state,
+                            int32_t* out_index, void* stream) {
+    const char* fn = "sltx_sample_top_p_state";
+    int rc = check_sample(fn, logits, dtype, n, temperature, top_p, repetition_penalty, out_index);
+    if (rc != kOk) return rc;
+    if (!state) return fail(kErrInvalid, "%s: null state", fn);
+    const sltx_sample_state& s = *state;
+    if (s.history_capacity < 0) return fail(kErrInvalid, "%s: negative history_capacity", fn);
+    if (s.draw_count < 1) return fail(kErrInvalid, "%s: draw_count must be at least 1", fn);
+    if (!s.history_len || !s.draws || !s.next_draw || (s.history_capacity > 0 && !s.history))
+        return fail(kErrInvalid, "%s: null pointer in state", fn);
+    if (!aligned(s.history_len, 4) || !aligned(s.draws, 4) || !aligned(s.next_draw, 4) ||
+        (s.history && !aligned(s.history, 4)))
+        return fail(kErrInvalid, "%s: misaligned pointer in state", fn);
+    SampleParams p = sample_params(logits, dtype, n, temperature, top_p, repetition_penalty, out_index);
+    p.seen = s.history;
+    p.hist = s.history;
+    p.hist_len = s.history_len;
+    p.hist_cap = s.history_capacity;
+    p.u_seq = s.draws;
+    p.u_next = s.next_draw;
+    p.u_count = s.draw_count;
+    return run_sample(fn, p, stream);
 }
 
 int sltx_rms_norm(const void* x, const float* weight, float eps, void* out, int32_t rows,

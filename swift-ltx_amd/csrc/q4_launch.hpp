@@ -78,6 +78,16 @@ struct SampleParams {
     const int32_t* seen;    // [n_seen] token ids (device)
     int n_seen;
     int32_t* out;           // [1] chosen token (device)
+    // Device-resident state (sltx_sample_top_p_state), all null otherwise.
+    // The seen ids are hist[0, *hist_len) (seen == hist), the draw is
+    // u_seq[*u_next], and the select kernel appends the chosen token to the
+    // history and advances u_next.
+    int32_t* hist;          // [hist_cap] token history
+    int32_t* hist_len;      // [1] valid entries
+    int hist_cap;
+    const float* u_seq;     // [u_count] uniform draws
+    int32_t* u_next;        // [1] index of this call's draw
+    int u_count;
     // carved from the workspace by launch_sample
     float* probs;           // [n] scaled logits, then probabilities
     float* mpart;           // block maxima

@@ -87,6 +87,42 @@ __device__ __forceinline__ unsigned long long target_draw(float u, unsigned long
     return (unsigned long long)ceil((double)u * (double)cum);
 }
 
+// Seen-id count: the host argument, or the history length in device memory,
+// clamped to [0, hist_cap].
+__device__ __forceinline__ int seen_count(const SampleParams& p) {
+    if (!p.hist_len) return p.n_seen;
+    const int c = *p.hist_len;
+    return c < 0 ? 0 : c > p.hist_cap ? p.hist_cap : c;
+}
+
+// Index of this call's draw in u_seq (u_next taken modulo u_count).
+__device__ __forceinline__ int draw_index(const SampleParams& p) {
+    const int i = *p.u_next % p.u_count;
+    return i < 0 ? i + p.u_count : i;
+}
+
+// The uniform draw: the host argument, or u_seq[u_next] with values outside
+// [0, 1) (and NaN) clamped into it.
+__device__ __forceinline__ float draw_of(const SampleParams& p) {
+    if (!p.u_seq) return p.u;
+    const float u = p.u_seq[draw_index(p)];
+    return u >= 0.0f ? (u < 1.0f ? u : 0x1.fffffep-1f) : 0.0f;
+}
+
+// One lane: store the chosen token and, with device state, append it to the
+// history (dropped when full) and advance the draw index.
+__device__ __forceinline__ void finish_select(const SampleParams& p, int id) {
+    *p.out = id;
+    if (p.hist_len) {
+        const int c = seen_count(p);
+        if (c < p.hist_cap) {
+            p.hist[c] = id;
+            *p.hist_len = c + 1;
+        }
+    }
+    if (p.u_seq) *p.u_next = (draw_index(p) + 1) % p.u_count;
+}
+
 // Exclusive prefix sum over the block's threads (in thread order).
 template <int NT>
 __device__ unsigned long long block_excl_scan(unsigned long long v, unsigned long long* wsum) {
@@ -341,10 +377,11 @@ __global__ __launch_bounds__(kGridThreads) void sample_scale_kernel(SampleParams
         p.h0mass[b] = 0ull;
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) *p.ccount = 0u;
-    if (p.n_seen > 0) {
+    const int n_seen = seen_count(p);
+    if (n_seen > 0) {
         for (int w = threadIdx.x; w < kSeenWords; w += kGridThreads) seen_bm[w] = 0u;
         __syncthreads();
-        for (int j = threadIdx.x; j < p.n_seen; j += kGridThreads) {
+        for (int j = threadIdx.x; j < n_seen; j += kGridThreads) {
             const int t = p.seen[j];
             if (t < 0 || t >= n) continue;
             const int q = t >> 2, r = q % T;
@@ -359,7 +396,7 @@ __global__ __launch_bounds__(kGridThreads) void sample_scale_kernel(SampleParams
     int k = 0;
     for (int q = blockIdx.x * kGridThreads + threadIdx.x; q < nq; q += T, ++k) {
         const int bit0 = k * (4 * kGridThreads) + threadIdx.x * 4;
-        const uint32_t seen = p.n_seen > 0 ? (seen_bm[bit0 >> 5] >> (bit0 & 31)) & 15u : 0u;
+        const uint32_t seen = n_seen > 0 ? (seen_bm[bit0 >> 5] >> (bit0 & 31)) & 15u : 0u;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int i = 4 * q + e;
@@ -491,11 +528,12 @@ __global__ __launch_bounds__(kGridThreads) void sample_gather_kernel(SampleParam
     scan.load(p.h0cnt, p.h0mass, 0ull, sc);
     scan.find(t1, s1, sc);
     unsigned long long tlo, thi;
+    const float u = draw_of(p);
     if (s1.found) {
-        tlo = target_draw(p.u, t1);
-        thi = target_draw(p.u, s1.incl);
+        tlo = target_draw(u, t1);
+        thi = target_draw(u, s1.incl);
     } else {
-        tlo = thi = target_draw(p.u, s1.total);
+        tlo = thi = target_draw(u, s1.total);
     }
     scan.find(thi, s2, sc);
     const int lo = s2.found ? s2.bin : 0;
@@ -548,6 +586,8 @@ __global__ __launch_bounds__(kSelThreads) void sample_select_kernel(SampleParams
     __shared__ BinSel s1;
     __shared__ int s_id;
     const int C = (int)*p.ccount;
+    // read before the first barrier: thread 0 advances the draw index at the end
+    const float u = draw_of(p);
     const unsigned long long t1 = target_top_p(p.top_p);
     BinScan<kSelThreads> scan0;   // the level-0 histogram
     scan0.load(p.h0cnt, p.h0mass, 0ull, sc);
@@ -601,10 +641,10 @@ __global__ __launch_bounds__(kSelThreads) void sample_select_kernel(SampleParams
             const unsigned long long hit = __ballot(valid && bin == s1.bin && cum >= t1);
             cut = hit ? __shfl(cum, __ffsll((long long)hit) - 1, 64) : s1.incl;
         }
-        const unsigned long long t2 = target_draw(p.u, cut);
+        const unsigned long long t2 = target_draw(u, cut);
         const unsigned long long hit2 = __ballot(valid && cum >= t2);
         const int chosen = __shfl(id, hit2 ? __ffsll((long long)hit2) - 1 : 0, 64);
-        if (lane == 0) *p.out = hit2 ? chosen : 0;
+        if (lane == 0) finish_select(p, hit2 ? chosen : 0);
         return;
     }
 
@@ -623,7 +663,7 @@ __global__ __launch_bounds__(kSelThreads) void sample_select_kernel(SampleParams
             (void)select_in_bin(cand, C, s1.bin, s1.excl, t1, H, sc, bs, cum);
     }
     // the draw
-    const unsigned long long t2 = target_draw(p.u, cum);
+    const unsigned long long t2 = target_draw(u, cum);
     scan0.find(t2, s0, sc);
     int id = -1;
     if (s0.found) {
@@ -634,7 +674,7 @@ __global__ __launch_bounds__(kSelThreads) void sample_select_kernel(SampleParams
             id = select_in_bin(cand, C, s0.bin, s0.excl, t2, H, sc, bs, c2);
         }
     }
-    if (threadIdx.x == 0) *p.out = id < 0 ? 0 : id;
+    if (threadIdx.x == 0) finish_select(p, id < 0 ? 0 : id);
 }
 
 // ------------------------------------------------------------------- host --

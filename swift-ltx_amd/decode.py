@@ -14,9 +14,10 @@ Mirrors LlamaModel.generate / forward / transformerBlock
   argmax / sample                              sltx_argmax / sltx_sample_top_p
 
 The chosen token id stays in device memory and is the next step's input, so a
-greedy step (temperature 0, argmax as the reference uses) can be captured once
-as a HIP graph and replayed per token.  Sampling takes the host's uniform draw
-per call and therefore runs eagerly.
+step can be captured once as a HIP graph and replayed per token: greedy
+(temperature 0, argmax as the reference uses), or sampled with a SamplerState,
+which keeps the seen tokens and the uniform draws in device memory.  Sampling
+with host arguments (seen list, u) runs eagerly.
 
 `attention(layer, qkv)` receives the layer index and the [1, q+k+v] fp16
 projections and returns the [1, heads * head_dim] fp16 attention output (a
@@ -29,7 +30,7 @@ from __future__ import annotations
 import random
 
 from . import (Q4Weight, argmax, embedding_q4, linear, matmul_q4_residual, rmsnorm_matmul_q4,
-               residual_rmsnorm_matmul_q4_silu_mul, sample)
+               residual_rmsnorm_matmul_q4_silu_mul, sample, sample_with_state)
 
 
 def q_rows_attention(q_dim):
@@ -76,10 +77,13 @@ class DecodeStep:
         self.res = torch.empty(1, self.hidden, dtype=f16, device=dev)   # h + attention out
         self.graph = None
 
-    def _select(self, temperature, top_p, repetition_penalty, seen, u):
+    def _select(self, temperature, top_p, repetition_penalty, seen, u, state):
         s = self.stream
         if temperature <= 0:
             argmax(self.logits, out=self.token, stream=s)
+        elif state is not None:
+            sample_with_state(self.logits, temperature, top_p, repetition_penalty, state,
+                              out=self.token, stream=s)
         else:
             sample(self.logits, temperature, top_p, repetition_penalty, seen,
                    random.random() if u is None else u, out=self.token, stream=s)
@@ -102,29 +106,38 @@ class DecodeStep:
         rmsnorm_matmul_q4(self.h, w.norm_weight, eps, w.lm_head, c.vocab_size, out=self.logits,
                           stream=s)
 
-    def step(self, temperature=0.0, top_p=0.9, repetition_penalty=1.1, seen=None, u=None):
-        """Run one step eagerly: self.token -> logits -> next token in self.token."""
+    def step(self, temperature=0.0, top_p=0.9, repetition_penalty=1.1, seen=None, u=None,
+             state=None):
+        """Run one step eagerly: self.token -> logits -> next token in self.token.
+        temperature > 0 samples, with `state` (a SamplerState) if given, else
+        with the host's seen tokens and draw u."""
         self.forward()
-        self._select(temperature, top_p, repetition_penalty, seen, u)
+        self._select(temperature, top_p, repetition_penalty, seen, u, state)
         return self.token
 
-    def capture(self):
-        """Capture one greedy step (argmax) as a HIP graph on self.stream (a
-        torch stream; required), after one eager step there."""
+    def capture(self, temperature=0.0, top_p=0.9, repetition_penalty=1.1, state=None):
+        """Capture one step as a HIP graph on self.stream (a torch stream;
+        required): greedy, or sampled from `state` (a SamplerState, required
+        when temperature > 0).  Runs one eager step there first, which
+        consumes a token, a draw and a history entry like any other step."""
         import torch
         if self.stream is None:
             raise ValueError("capture needs a dedicated stream")
+        if temperature > 0 and state is None:
+            raise ValueError("a sampled step in a graph needs a SamplerState")
+        kw = dict(temperature=temperature, top_p=top_p, repetition_penalty=repetition_penalty,
+                  state=state)
         with torch.cuda.stream(self.stream):
-            self.step()
+            self.step(**kw)
         self.stream.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=self.stream):
-            self.step()
+            self.step(**kw)
         self.graph = g
         return g
 
     def replay(self):
-        """One captured greedy step."""
+        """One captured step."""
         if self.graph is None:
             raise RuntimeError("capture() first")
         self.graph.replay()

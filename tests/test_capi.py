@@ -243,3 +243,37 @@ def test_argmax_and_sample_validation(pkg):
     assert call(out=None) == -1 and "null" in pkg.last_error()
     assert call(out=O + 2) == -1 and "misaligned" in pkg.last_error()
     assert call(seen=A + 1, ns=2) == -1 and "misaligned" in pkg.last_error()
+
+
+def test_sample_state_validation(pkg):
+    """sltx_sample_top_p_state rejects what sltx_sample_top_p rejects, plus a
+    missing or malformed state, before any device work."""
+    L = pkg.lib()
+    A, O = ALIGNED, 0x40000
+    fn = L.sltx_sample_top_p_state
+
+    def state(**kw):
+        f = dict(history=A, history_len=A + 0x100, history_capacity=16, draws=A + 0x200,
+                 next_draw=A + 0x300, draw_count=8)
+        f.update(kw)
+        return pkg.CSampleState(**f)
+
+    def call(st, n=100, dt=0, t=0.7, p=0.9, r=1.1, logits=A, out=O):
+        return fn(logits, dt, n, t, p, r, ctypes.byref(st) if st is not None else None, out, None)
+    good = state()
+    assert call(good, n=0) == -1 and "positive" in pkg.last_error()
+    assert call(good, dt=1) == -1 and "SLTX_F16" in pkg.last_error()
+    assert call(good, t=0.0) == -1 and "must be positive" in pkg.last_error()
+    assert call(good, out=None) == -1 and "null" in pkg.last_error()
+    assert call(None) == -1 and "null state" in pkg.last_error()
+    assert call(state(history_capacity=-1)) == -1 and "history_capacity" in pkg.last_error()
+    assert call(state(draw_count=0)) == -1 and "draw_count" in pkg.last_error()
+    for k in ("history_len", "draws", "next_draw"):
+        assert call(state(**{k: None})) == -1 and "null pointer in state" in pkg.last_error(), k
+    assert call(state(history=None)) == -1 and "null pointer in state" in pkg.last_error()
+    # an empty history needs no buffer
+    for k in ("history", "history_len", "draws", "next_draw"):
+        off = {"history": A + 2, "history_len": A + 0x102, "draws": A + 0x201,
+               "next_draw": A + 0x303}[k]
+        assert call(state(**{k: off})) == -1 and "misaligned" in pkg.last_error(), k
+    assert "sltx_sample_top_p_state" in pkg.EXPORTED

@@ -84,3 +84,49 @@ def test_decode_steps_match_numpy_and_graph(pkg, dev, tmp_path):
         torch.cuda.synchronize()
         replayed.append(int(ds.token.item()))
     assert replayed == tokens
+
+
+def test_decode_sampled_graph_matches_eager(pkg, dev, tmp_path):
+    """A sampled step (temperature 0.9, top-p 0.95, penalty 1.2) with the
+    seen tokens and draws in a SamplerState: each eager step's token is the
+    host-argument sampler's on the same logits with the history so far and
+    that step's draw; a captured step replays the eager sequence exactly
+    from the same start, its history growing on the device."""
+    import torch
+    from swiftltx_amd.decode import DecodeStep
+    from swiftltx_amd.weights import ModelWeights
+    _write_model(tmp_path)
+    mw = ModelWeights.from_directory(str(tmp_path), device=dev)
+    s = torch.cuda.Stream()
+    ds = DecodeStep(mw, stream=s)
+    draws = np.random.default_rng(40).random(16).astype(np.float32)
+    prompt = [7, 3, 7]
+    kw = dict(temperature=0.9, top_p=0.95, repetition_penalty=1.2)
+    st = pkg.SamplerState(32, draws=draws, history=prompt, device=dev)
+    tokens = []
+    with torch.cuda.stream(s):
+        ds.token.fill_(7)
+    for step in range(6):
+        with torch.cuda.stream(s):
+            ds.step(state=st, **kw)
+        s.synchronize()
+        got = int(ds.token.item())
+        seen = torch.tensor(prompt + tokens, dtype=torch.int32, device=dev)
+        host = int(pkg.sample(ds.logits[0], u=float(draws[step]), seen_tokens=seen, **kw).item())
+        assert got == host, (step, got, host)
+        tokens.append(got)
+    assert st.tokens() == prompt + tokens
+    replay_state = pkg.SamplerState(32, draws=draws, history=prompt, device=dev)
+    with torch.cuda.stream(s):
+        ds.token.fill_(7)
+    ds.capture(state=replay_state, **kw)    # one eager step first: 7 -> tokens[0]
+    s.synchronize()
+    replayed = [int(ds.token.item())]
+    for _ in range(5):
+        ds.replay()
+        torch.cuda.synchronize()
+        replayed.append(int(ds.token.item()))
+    assert replayed == tokens
+    assert replay_state.tokens() == prompt + tokens
+    with pytest.raises(ValueError):
+        ds.capture(temperature=0.5)          # sampling in a graph needs a SamplerState

@@ -194,6 +194,124 @@ def test_sample_graph_replay(pkg, dev):
         assert got == eager and got in ok, (rep, got, eager, ref)
 
 
+# ------------------------------------------------- device-resident state --
+
+def _state(pkg, dev, cap, draws, history):
+    return pkg.SamplerState(cap, draws=np.asarray(draws, np.float32), history=history, device=dev)
+
+
+def _lm_logits(rng, n, hist, scale):
+    """Peaked logits whose largest values include the history's tokens, so
+    the repetition penalty changes the draw."""
+    lg = rng.standard_normal(n) * scale
+    lg[np.asarray(hist) % n] += 3 * scale
+    return lg.astype(np.float16)
+
+
+def test_sample_state_matches_host_form(pkg, dev):
+    """sltx_sample_top_p_state reads the seen ids from the device history and
+    the draw from draws[next_draw]; each call appends its token and advances
+    the draw, as the reference's generate loop grows seenTokens
+    (LlamaModel.swift:150-161).  The kernels are the host-argument form's,
+    so the tokens agree exactly, and each lies in the oracle's window."""
+    import torch
+    rng = np.random.default_rng(34)
+    n = 128256
+    draws = [0.13, 0.77, 0.42, 0.91, 0.05]
+    prompt = [5, 17, 99, 17, 128000]
+    st = _state(pkg, dev, 64, draws, prompt)
+    hist = list(prompt)
+    for i in range(12):
+        lg = _lm_logits(rng, n, hist, 2.0 + i % 3)
+        x = _t(lg, dev)
+        got = int(pkg.sample_with_state(x, 0.8, 0.9, 1.3, st).item())
+        u = draws[i % len(draws)]
+        seen_np = np.array(hist, np.int32)
+        host = int(pkg.sample(x, 0.8, 0.9, 1.3, _t(seen_np, dev), u).item())
+        assert got == host, (i, got, host)
+        exact, ok = acceptable(lg, 0.8, 0.9, 1.3, seen_np, u, gpu_sums=True, tol=5e-7, tie=5e-7)
+        assert got in ok, (i, got, exact)
+        hist.append(got)
+        assert st.tokens() == hist, i
+        assert int(st.next_draw.item()) == (i + 1) % len(draws), i
+    torch.cuda.synchronize()
+
+
+def test_sample_state_full_history_and_clamped_draws(pkg, dev):
+    """A full history stops growing (and a length beyond the capacity counts
+    as the capacity); draws outside [0, 1) and NaN are clamped into it; a
+    negative length counts as an empty history."""
+    import torch
+    rng = np.random.default_rng(35)
+    n = 32000
+    top = float(np.float32(1.0) - np.float32(2.0 ** -24))
+    st = _state(pkg, dev, 3, [1.5, -0.25, float("nan"), 0.5], [7, 8])
+    hist = [7, 8]
+    for i, u in enumerate([top, 0.0, 0.0, 0.5, top]):
+        lg = _lm_logits(rng, n, hist, 2.0)
+        x = _t(lg, dev)
+        got = int(pkg.sample_with_state(x, 1.0, 0.95, 1.5, st).item())
+        host = int(pkg.sample(x, 1.0, 0.95, 1.5, _t(np.array(hist, np.int32), dev), u).item())
+        assert got == host, (i, got, host)
+        if len(hist) < 3:
+            hist.append(got)
+        assert st.tokens() == hist, i
+    assert int(st.history_len.item()) == 3
+    # five calls so far: the next draw is draws[1] = -0.25 (-> 0), then NaN (-> 0)
+    assert int(st.next_draw.item()) == 1
+    st.history_len.fill_(1000)            # counts as 3, nothing appended
+    lg = _lm_logits(rng, n, hist, 2.0)
+    x = _t(lg, dev)
+    got = int(pkg.sample_with_state(x, 1.0, 0.95, 1.5, st).item())
+    host = int(pkg.sample(x, 1.0, 0.95, 1.5, _t(np.array(hist, np.int32), dev), 0.0).item())
+    assert got == host and int(st.history_len.item()) == 1000
+    assert st.history[:3].tolist() == hist
+    st.history_len.fill_(-4)              # empty: the token lands at index 0
+    got = int(pkg.sample_with_state(x, 1.0, 0.95, 1.5, st).item())
+    host = int(pkg.sample(x, 1.0, 0.95, 1.5, None, 0.0).item())
+    assert got == host, (got, host)
+    assert int(st.history_len.item()) == 1 and int(st.history[0].item()) == got
+    torch.cuda.synchronize()
+
+
+def test_sample_state_graph_replay(pkg, dev):
+    """One captured state-form call, replayed with new logits copied into its
+    input: each replay takes the next draw and appends to the history, equal
+    to eager calls on a twin state, step by step."""
+    import torch
+    rng = np.random.default_rng(36)
+    n = 128256
+    draws = rng.random(7).astype(np.float32)
+    prompt = [1, 2, 3, 500, 9000]
+    st = _state(pkg, dev, 40, draws, prompt)
+    twin = _state(pkg, dev, 40, draws, prompt)
+    s = torch.cuda.Stream()
+    x = torch.empty(n, dtype=torch.float16, device=dev)
+    out = torch.empty(1, dtype=torch.int32, device=dev)
+    x.copy_(_t(_lm_logits(rng, n, prompt, 3.0), dev))
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        pkg.sample_with_state(x, 0.7, 0.9, 1.2, st, out=out, stream=s)
+    s.synchronize()
+    pkg.sample_with_state(x, 0.7, 0.9, 1.2, twin)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        pkg.sample_with_state(x, 0.7, 0.9, 1.2, st, out=out, stream=s)
+    torch.cuda.synchronize()
+    assert st.tokens() == twin.tokens()   # capture records, it does not run
+    for rep in range(10):
+        x.copy_(_t(_lm_logits(rng, n, twin.tokens(), 2.0 + rep % 4), dev))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = int(out.item())
+        eager = int(pkg.sample_with_state(x, 0.7, 0.9, 1.2, twin).item())
+        torch.cuda.synchronize()
+        assert got == eager, (rep, got, eager)
+        assert st.tokens() == twin.tokens(), rep
+        assert int(st.next_draw.item()) == int(twin.next_draw.item()) == (rep + 2) % 7
+
+
 def test_sample_capture_without_workspace_is_an_error(pkg, dev):
     """A stream that never sampled has no workspace; capture must not
     allocate, so the call fails (and the capture is abandoned)."""
