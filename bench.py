@@ -279,18 +279,23 @@ def fused_layer_leg(pkg, torch, gen, dev, layers, reps):
 
 
 def decode_token_leg(pkg, torch, gen, dev, layers, reps=20):
-    """A greedy Llama-3.2-3B decode step's matmul path (swiftltx_amd.decode):
-    4-bit embedding gather, 28 layers (RMSNorm + q|k|v, o, residual + RMSNorm
-    + gate/up SiLU, down + residual), final RMSNorm + tied 4-bit lm_head over
-    128256 tokens, argmax -- one HIP graph per token, the token id fed back on
-    the device.  Attention is outside the path: its stand-in is the q rows (a
-    view, no launch).  Random weights: the first 28 of the rotated layer
-    copies, norm weights 1 + 0.1 N(0,1)."""
+    """A Llama-3.2-3B decode step's matmul path (swiftltx_amd.decode), greedy
+    and sampled: 4-bit embedding gather, 28 layers (RMSNorm + q|k|v, o,
+    residual + RMSNorm + gate/up SiLU, down + residual), final RMSNorm + tied
+    4-bit lm_head over 128256 tokens, argmax (or top-p sampling) -- one HIP
+    graph per token, the token id fed back on the device.  Attention is
+    outside the path: its stand-in is the q rows (a view, no launch).
+    Random weights: the first 28 of the rotated layer copies; layer norm
+    weights 0.05 (1 + 0.1 N(0,1)), so that the residual stream stays inside
+    fp16 over 28 layers (nothing bounds it without attention: with weights
+    near 1 it overflows and every logit is NaN); final norm weights
+    1 + 0.1 N(0,1), which gives peaked logits like a trained model's."""
     from types import SimpleNamespace
     from swiftltx_amd.decode import DecodeStep
     from swiftltx_amd.weights import LayerWeights
     K, V, L = 3072, 128256, 28
-    norm = lambda: (1.0 + 0.1 * torch.randn(K, generator=gen, device=dev)).float()
+    norm = lambda: (0.05 * (1.0 + 0.1 * torch.randn(K, generator=gen, device=dev))).float()
+    fnorm = lambda: (1.0 + 0.1 * torch.randn(K, generator=gen, device=dev)).float()
     embed = pkg.Q4Weight(*rand_q4(torch, V, K, gen, dev), K, G)
     lws = []
     for lay in layers[:L]:
@@ -301,7 +306,7 @@ def decode_token_leg(pkg, torch, gen, dev, layers, reps=20):
                                 post_norm_weight=norm(), qkv_proj=w["qkv_proj"][0]))
     cfg = SimpleNamespace(hidden_size=K, intermediate_size=8192, num_attention_heads=24,
                           num_key_value_heads=8, head_dim=128, vocab_size=V, rms_norm_eps=1e-5)
-    mw = SimpleNamespace(config=cfg, embed_tokens=embed, lm_head=embed, norm_weight=norm(),
+    mw = SimpleNamespace(config=cfg, embed_tokens=embed, lm_head=embed, norm_weight=fnorm(),
                          layers=lws)
     s = torch.cuda.Stream()
     ds = DecodeStep(mw, stream=s)
@@ -313,10 +318,28 @@ def decode_token_leg(pkg, torch, gen, dev, layers, reps=20):
         ds.replay()
     torch.cuda.synchronize()
     us = 1e6 * (time.perf_counter() - t0) / reps
+    # the same step sampling (temperature 0.7, top-p 0.9, penalty 1.1) from a
+    # SamplerState: 64 prompt ids, the history and the draws on the device
+    state = pkg.SamplerState(4096, draws=4096, generator=gen, device=dev,
+                             history=torch.randint(0, V, (64,), generator=gen,
+                                                   device=dev).tolist())
+    ds2 = DecodeStep(mw, stream=s)
+    ds2.capture(temperature=0.7, top_p=0.9, repetition_penalty=1.1, state=state)
+    ds2.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        ds2.replay()
+    torch.cuda.synchronize()
+    us_s = 1e6 * (time.perf_counter() - t0) / reps
     nbytes = (L * (LAYER_BYTES + 2 * K * 4) + gemv_bytes(V, K) + K * 4 + K // 2 + 4 * K // G + 2 * K)
     return {"us_per_token": round(us, 1), "tokens_per_s": round(1e6 / us, 1),
             "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes_per_token": nbytes,
             "launches_per_token": 1 + 4 * L + 1 + 2, "layers": L,
+            "sampled": {"us_per_token": round(us_s, 1), "tokens_per_s": round(1e6 / us_s, 1),
+                        "launches_per_token": 1 + 4 * L + 1 + 4,
+                        "sampler": "temperature 0.7, top-p 0.9, repetition penalty 1.1, "
+                                   "history and draws in device memory (SamplerState)"},
             "note": "attention (RoPE, KV cache, softmax) is outside the 4-bit path; stand-in = "
                     "the q rows"}
 

@@ -49,6 +49,7 @@ constexpr int kMaxBlocks = 256;
 constexpr int kSelThreads = 1024;   // sample_select
 constexpr int kBins = 4096;         // 12-bit digits
 constexpr int kCandLds = 8192;      // candidates sample_select holds in LDS
+constexpr int kSelUnroll = 8;     // candidates each select thread loads before using them
 constexpr uint32_t kIdMask = 0xFFFFFFu;
 // seen-id bitmap of one scale block: up to 64 quads a thread (n <= 2^24
 // with 256 blocks of 256 threads), 4 bits a quad
@@ -72,6 +73,47 @@ __device__ __forceinline__ unsigned long long mass_of(uint32_t key) {
 
 __device__ __forceinline__ unsigned long long order_key(uint32_t key, uint32_t id) {
     return ((unsigned long long)key << 24) | (kIdMask - id);
+}
+
+// Adds one token (key, mass m) to bin d of an LDS histogram for every lane
+// with ok set; all 64 lanes of the wave call it.  When every such lane has the
+// same bin (tied, uniform or non-finite logits), one lane adds the wave's
+// count and mass sum -- same-address LDS atomics serialise.  Lanes with the
+// same key have the same mass, so a wave of one key adds count * mass; a
+// wave of one bin but several keys sums its masses across the wave.
+// Otherwise each lane adds its own.  Returns the lane that added for the
+// whole wave (-1: each lane added its own).  Masses are integers, so the
+// sums are exact in any order.
+__device__ __forceinline__ int hist_add(bool ok, int d, uint32_t key, unsigned long long m,
+                                        uint32_t* cnt, unsigned long long* mass) {
+    const unsigned long long act = __ballot(ok);
+    if (!act) return -1;
+    const int lane = threadIdx.x & 63;
+    const int lead = __ffsll((long long)act) - 1;
+    const int d0 = __builtin_amdgcn_readlane(d, lead);
+    if (__ballot(ok && d == d0) != act) {
+        if (ok) {
+            atomicAdd(&cnt[d], 1u);
+            if (m) atomicAdd(&mass[d], m);
+        }
+        return -1;
+    }
+    unsigned long long sum;
+    const uint32_t k0 = (uint32_t)__builtin_amdgcn_readlane((int)key, lead);
+    if (__ballot(ok && key == k0) == act) {
+        const unsigned long long m0 =
+            ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(m >> 32), lead) << 32) |
+            (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)m, lead);
+        sum = m0 * (unsigned long long)__popcll(act);
+    } else {
+        sum = ok ? m : 0ull;
+        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    }
+    if (lane == lead) {
+        atomicAdd(&cnt[d0], (uint32_t)__popcll(act));
+        if (sum) atomicAdd(&mass[d0], sum);
+    }
+    return lead;
 }
 
 __device__ __forceinline__ uint32_t lanes_below(unsigned long long mask) {
@@ -247,15 +289,27 @@ __device__ int select_in_bin(const uint2* cand, int C, int bin, unsigned long lo
             H.mass[b] = 0ull;
         }
         __syncthreads();
-        for (int c = tid; c < C; c += kSelThreads) {
-            const uint2 e = cand[c];
-            const unsigned long long D = order_key(e.x, e.y);
-            if ((D & Mk) != P) continue;
-            const int dg = (int)((D >> shift) & wmask);
-            atomicAdd(&H.cnt[dg], 1u);
-            const unsigned long long m = mass_of(e.x);
-            if (m) atomicAdd(&H.mass[dg], m);
-            H.id[dg] = e.y;   // read only when the bin holds one token
+        // Wave-uniform trip count (hist_add needs all 64 lanes); each lane
+        // loads kSelUnroll candidates before using any, so that many memory
+        // latencies overlap when the list is in global memory.
+        for (int c0 = (tid & ~63) * kSelUnroll; c0 < C; c0 += kSelThreads * kSelUnroll) {
+            uint2 ev[kSelUnroll];
+#pragma unroll
+            for (int u = 0; u < kSelUnroll; ++u) {
+                const int c = c0 + u * 64 + (tid & 63);
+                ev[u] = c < C ? cand[c] : make_uint2(0u, 0u);
+            }
+#pragma unroll
+            for (int u = 0; u < kSelUnroll; ++u) {
+                const int c = c0 + u * 64 + (tid & 63);
+                const uint2 e = ev[u];
+                const unsigned long long D = order_key(e.x, e.y);
+                const bool ok = c < C && (D & Mk) == P;
+                const int dg = (int)((D >> shift) & wmask);
+                const int lead = hist_add(ok, dg, e.x, ok ? mass_of(e.x) : 0ull, H.cnt, H.mass);
+                // read only when the bin holds one token
+                if (ok && (lead < 0 || lead == (tid & 63))) H.id[dg] = e.y;
+            }
         }
         __syncthreads();
         BinScan<kSelThreads> scan;
@@ -279,9 +333,16 @@ __device__ int select_in_bin(const uint2* cand, int C, int bin, unsigned long lo
 __device__ int only_in_bin(const uint2* cand, int C, int bin, int* s_id) {
     if (threadIdx.x == 0) *s_id = -1;
     __syncthreads();
-    for (int c = threadIdx.x; c < C; c += kSelThreads) {
-        const uint2 e = cand[c];
-        if ((int)(e.x >> 20) == bin) *s_id = (int)e.y;
+    for (int c0 = threadIdx.x; c0 < C; c0 += kSelThreads * kSelUnroll) {
+        uint2 ev[kSelUnroll];
+#pragma unroll
+        for (int u = 0; u < kSelUnroll; ++u) {
+            const int c = c0 + u * kSelThreads;
+            ev[u] = c < C ? cand[c] : make_uint2(0u, 0xFFFFFFFFu);
+        }
+#pragma unroll
+        for (int u = 0; u < kSelUnroll; ++u)
+            if (c0 + u * kSelThreads < C && (int)(ev[u].x >> 20) == bin) *s_id = (int)ev[u].y;
     }
     __syncthreads();
     const int r = *s_id;
@@ -481,18 +542,21 @@ __global__ __launch_bounds__(kGridThreads) void sample_prob_kernel(SampleParams 
     }
     __syncthreads();
     const float sm = s_sum, mx = s_max;
-    for (int q = blockIdx.x * kGridThreads + threadIdx.x; 4 * q < n; q += T) {
+    // wave-uniform trip count: hist_add needs all 64 lanes
+    const int q_first = blockIdx.x * kGridThreads + threadIdx.x;
+    for (int qw = q_first - (threadIdx.x & 63); 4 * qw < n; qw += T) {
+        const int q = qw + (threadIdx.x & 63);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int i = 4 * q + k;
-            if (i >= n) break;
-            const float pv = expf((q == (int)(blockIdx.x * kGridThreads + threadIdx.x) ? l0[k]
-                                                                             : p.probs[i]) - mx) / sm;
-            p.probs[i] = pv;
+            const bool ok = i < n;
+            float pv = 0.0f;
+            if (ok) {
+                pv = expf((q == q_first ? l0[k] : p.probs[i]) - mx) / sm;
+                p.probs[i] = pv;
+            }
             const uint32_t key = __float_as_uint(pv);
-            atomicAdd(&hc[key >> 20], 1u);
-            const unsigned long long m = mass_of(key);
-            if (m) atomicAdd(&hm[key >> 20], m);
+            hist_add(ok, (int)(key >> 20), key, ok ? mass_of(key) : 0ull, hc, hm);
         }
     }
     __syncthreads();

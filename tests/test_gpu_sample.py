@@ -194,6 +194,26 @@ def test_sample_graph_replay(pkg, dev):
         assert got == eager and got in ok, (rep, got, eager, ref)
 
 
+def test_sample_degenerate_logits(pkg, dev):
+    """All-equal logits (a 128256-way tie, ranked by id at every select
+    level, and the worst case for the select kernel) give exactly the
+    oracle's token with the GPU's sums; all-NaN logits give index 0, as the
+    reference's scan does when every comparison fails (Ops.swift:2082-2097)."""
+    import torch
+    n = 128256
+    for dt in (np.float16, np.float32):
+        eq = np.zeros(n, dt)
+        x = _t(eq, dev)
+        for u in (0.0, 0.3, 0.77, 0.9999):
+            got = int(pkg.sample(x, 0.7, 0.9, 1.1, None, u).item())
+            assert got == o.sample_ref(eq, 0.7, 0.9, 1.1, [], u, gpu_sums=True), (dt, u, got)
+        nan = np.full(n, np.nan, dt)
+        for u in (0.0, 0.5, 0.9999):
+            got = int(pkg.sample(_t(nan, dev), 0.7, 0.9, 1.1, None, u).item())
+            assert got == 0 == o.sample_ref(nan, 0.7, 0.9, 1.1, [], u), (dt, u, got)
+    torch.cuda.synchronize()
+
+
 # ------------------------------------------------- device-resident state --
 
 def _state(pkg, dev, cap, draws, history):
