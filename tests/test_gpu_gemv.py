@@ -41,6 +41,8 @@ SHAPES = [
     (3072, 3072, 64), (1024, 3072, 64), (333, 4096, 64), (3072, 8192, 64), (96, 10240, 64),
     (64, 14336, 128), (40, 16384, 64), (200, 6144, 32), (130, 1536, 64), (70, 7168, 64),
     (33, 3584, 64), (9, 96, 32), (11, 160, 32), (5, 2080, 32), (17, 224, 32),
+    # two row-iterations per wave with 8 chunks per lane (the smallest block cap)
+    (8200, 16384, 64),
 ]
 
 
@@ -104,7 +106,7 @@ def test_golden_swiglu_gemv(pkg, dev, name):
     assert o.max_rel_err(y.cpu().numpy(), t["y_emu"].astype(np.float64)) < 5e-3
 
 
-@pytest.mark.parametrize("N,K", [(64, 3072), (8192, 3072), (300, 8192), (50, 160)])
+@pytest.mark.parametrize("N,K", [(64, 3072), (8192, 3072), (300, 8192), (50, 160), (8200, 10240)])
 def test_swiglu_gemv_shapes(pkg, dev, N, K):
     import torch
     g = 32 if K % 64 else 64
