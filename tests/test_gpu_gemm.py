@@ -67,6 +67,8 @@ SHAPES = [
     (2, 64, 256, 64), (3, 100, 3072, 64), (64, 128, 512, 32), (127, 256, 1024, 128),
     (128, 128, 128, 64), (129, 130, 256, 64), (300, 1000, 768, 64), (17, 96, 96, 32),
     (40, 72, 160, 32), (256, 512, 2048, 64),
+    # M = 1 through the GEMM (the _fast entry points never route to the GEMV)
+    (1, 300, 3072, 64), (1, 64, 96, 32),
 ]
 
 
