@@ -421,7 +421,11 @@ class SamplerState:
     history: token ids already seen (the prompt); capacity: history entries
     (the chosen tokens are appended until it is full); draws: uniform draws in
     [0, 1) used one per call, cyclically (a float32 sequence or a count, in
-    which case they are drawn here with torch's generator)."""
+    which case they are drawn here with torch's generator).
+
+    Setup (the constructor, set_history, set_draws) runs on torch's current
+    stream and waits for it, so a call on any other stream sees the new
+    state."""
 
     def __init__(self, capacity, draws=4096, history=(), device="cuda", generator=None):
         torch = _torch()
@@ -436,7 +440,7 @@ class SamplerState:
         if self.draws.numel() < 1:
             raise ValueError("at least one draw")
         self.next_draw = torch.zeros(1, dtype=torch.int32, device=device)
-        self.set_history(history)
+        self.set_history(history)   # waits for the stream
         self.c = CSampleState(_ptr(self.history), _ptr(self.history_len), self.capacity,
                               _ptr(self.draws), _ptr(self.next_draw), int(self.draws.numel()))
 
@@ -448,12 +452,14 @@ class SamplerState:
         if t.numel():
             self.history[: t.numel()].copy_(t)
         self.history_len.fill_(int(t.numel()))
+        torch.cuda.current_stream(self.history.device).synchronize()
 
     def set_draws(self, draws, start=0):
         """Overwrite the draws in place (same count) and the next index."""
         torch = _torch()
         self.draws.copy_(torch.as_tensor(draws, dtype=torch.float32))
         self.next_draw.fill_(int(start))
+        torch.cuda.current_stream(self.draws.device).synchronize()
 
     def tokens(self):
         """The history as a host list."""

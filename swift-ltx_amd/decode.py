@@ -76,6 +76,8 @@ class DecodeStep:
         self.logits = torch.empty(1, c.vocab_size, dtype=f16, device=dev)
         self.res = torch.empty(1, self.hidden, dtype=f16, device=dev)   # h + attention out
         self.graph = None
+        # the zeroed token must be in place before work on self.stream reads it
+        torch.cuda.current_stream(dev).synchronize()
 
     def _select(self, temperature, top_p, repetition_penalty, seen, u, state):
         s = self.stream
