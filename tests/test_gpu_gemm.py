@@ -69,6 +69,8 @@ SHAPES = [
     (40, 72, 160, 32), (256, 512, 2048, 64),
     # M = 1 through the GEMM (the _fast entry points never route to the GEMV)
     (1, 300, 3072, 64), (1, 64, 96, 32),
+    # K = 32: one partial k-tile
+    (5, 40, 32, 32), (70, 300, 32, 32),
 ]
 
 

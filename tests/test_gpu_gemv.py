@@ -43,6 +43,8 @@ SHAPES = [
     (33, 3584, 64), (9, 96, 32), (11, 160, 32), (5, 2080, 32), (17, 224, 32),
     # two row-iterations per wave with 8 chunks per lane (the smallest block cap)
     (8200, 16384, 64),
+    # K = 32: one chunk per row
+    (3, 32, 32), (500, 32, 32),
 ]
 
 
