@@ -324,15 +324,18 @@ __global__ __launch_bounds__((64 * gemv_max_waves<CPL, SWIGLU, MULTI>())) void q
     }
 }
 
-// Generic fallback for K that no (L, CPL) specialisation covers (K % 32 == 0):
-// one wave per row, x read from LDS per chunk.
+// Generic fallback for K that no (L, CPL) specialisation covers (K % 32 == 0,
+// any size): one wave per row.  x is prepared in LDS kGenSeg chunks at a time
+// and each lane visits its chunks (lane, lane + 64, ...) in increasing order
+// across the segments, so any K fits in a fixed 36 KB.
+constexpr int kGenSeg = 512;   // a multiple of 64
+
 template <bool SWIGLU>
 __global__ __launch_bounds__(256) void q4_gemv_generic_kernel(GemvParams p) {
-    extern __shared__ uint8_t smem[];
+    __shared__ u32x4 xs[4][kGenSeg];
+    __shared__ float2 xcv[kGenSeg];
+    __shared__ float red[4];
     const int nch = p.K / 32;
-    u32x4* xs = reinterpret_cast<u32x4*>(smem);              // [4][nch]
-    float2* xcv = reinterpret_cast<float2*>(xs + 4 * nch);    // [nch]
-    float* red = reinterpret_cast<float*>(xcv + nch);         // [4]
     // Input element i: x, or the (rounded) residual x + xb; rms_norm applied
     // when the prologue asks for it (same formulas as the specialized kernel).
     auto in_val = [&](int i) {
@@ -356,45 +359,58 @@ __global__ __launch_bounds__(256) void q4_gemv_generic_kernel(GemvParams p) {
         __syncthreads();
         rms = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)p.K + p.eps);
     }
-    for (int c = threadIdx.x; c < nch; c += blockDim.x) {
-        const f16x8* xp = reinterpret_cast<const f16x8*>(p.x + (size_t)c * 32);
-        float corr = 0.0f, sum = 0.0f;
-        for (int j = 0; j < 4; ++j) {
-            uint32_t pr[4];
-            f16x8 xv = xp[j];
-            if (p.pro != kProNone)
-                for (int e = 0; e < 8; ++e) {
-                    const int i = c * 32 + j * 8 + e;
-                    xv[e] = (f16)(in_val(i) * rms * p.norm_w[i]);
-                }
-            pair_word(xv, pr, corr, sum);
-            u32x4 v = {pr[0], pr[1], pr[2], pr[3]};
-            xs[j * nch + c] = v;
-        }
-        xcv[c] = make_float2(-corr, sum);
-    }
-    __syncthreads();
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (r >= p.N) return;
+    const bool row_ok = r < p.N;   // wave-uniform; every wave still takes the barriers
     constexpr int NW = SWIGLU ? 2 : 1;
-    float acc[NW];
-    for (int m = 0; m < NW; ++m) {
-        const u32x4* W = reinterpret_cast<const u32x4*>(m == 0 ? p.w0 : p.w1);
-        const uint16_t* S = m == 0 ? p.s0 : p.s1;
-        const uint16_t* B = m == 0 ? p.b0 : p.b1;
-        float a = 0.0f;
-        for (int c = lane; c < nch; c += 64) {
-            u32x4 xq[4];
-            for (int j = 0; j < 4; ++j) xq[j] = xs[j * nch + c];
-            const float2 xc = xcv[c];
-            const float d = chunk_dot(W[(size_t)r * nch + c], xq, xc.x);
-            const size_t gi = (size_t)r * p.groups + (c >> p.gshift);
-            a = fmaf(h2f(S[gi]), d, a);
-            a = fmaf(h2f(B[gi]), xc.y, a);
+    float a[NW];
+#pragma unroll
+    for (int m = 0; m < NW; ++m) a[m] = 0.0f;
+    for (int c0 = 0; c0 < nch; c0 += kGenSeg) {
+        const int cn = min(kGenSeg, nch - c0);
+        if (c0 > 0) __syncthreads();   // the previous segment has been read
+        for (int cl = threadIdx.x; cl < cn; cl += blockDim.x) {
+            const int c = c0 + cl;
+            const f16x8* xp = reinterpret_cast<const f16x8*>(p.x + (size_t)c * 32);
+            float corr = 0.0f, sum = 0.0f;
+            for (int j = 0; j < 4; ++j) {
+                uint32_t pr[4];
+                f16x8 xv = xp[j];
+                if (p.pro != kProNone)
+                    for (int e = 0; e < 8; ++e) {
+                        const int i = c * 32 + j * 8 + e;
+                        xv[e] = (f16)(in_val(i) * rms * p.norm_w[i]);
+                    }
+                pair_word(xv, pr, corr, sum);
+                u32x4 v = {pr[0], pr[1], pr[2], pr[3]};
+                xs[j][cl] = v;
+            }
+            xcv[cl] = make_float2(-corr, sum);
         }
-        acc[m] = row_reduce<64>(a);
+        __syncthreads();
+        if (row_ok) {
+#pragma unroll
+            for (int m = 0; m < NW; ++m) {
+                const u32x4* W = reinterpret_cast<const u32x4*>(m == 0 ? p.w0 : p.w1);
+                const uint16_t* S = m == 0 ? p.s0 : p.s1;
+                const uint16_t* B = m == 0 ? p.b0 : p.b1;
+                for (int cl = lane; cl < cn; cl += 64) {
+                    const int c = c0 + cl;
+                    u32x4 xq[4];
+                    for (int j = 0; j < 4; ++j) xq[j] = xs[j][cl];
+                    const float2 xc = xcv[cl];
+                    const float d = chunk_dot(W[(size_t)r * nch + c], xq, xc.x);
+                    const size_t gi = (size_t)r * p.groups + (c >> p.gshift);
+                    a[m] = fmaf(h2f(S[gi]), d, a[m]);
+                    a[m] = fmaf(h2f(B[gi]), xc.y, a[m]);
+                }
+            }
+        }
     }
+    if (!row_ok) return;
+    float acc[NW];
+#pragma unroll
+    for (int m = 0; m < NW; ++m) acc[m] = row_reduce<64>(a[m]);
     if (lane == 0) {
         float out = SWIGLU ? glu_f32(p.gelu, acc[0], acc[NW - 1]) : acc[0];
         p.y[r] = p.residual ? residual_add_f16(p.residual[r], out) : f2h(out);
@@ -486,13 +502,11 @@ hipError_t launch_gemv(const GemvParams& p, bool swiglu, hipStream_t st) {
     if (L == 64) return swiglu ? launch_l<64, true>(p, cpl, st) : launch_l<64, false>(p, cpl, st);
     if (L == 32) return swiglu ? launch_l<32, true>(p, cpl, st) : launch_l<32, false>(p, cpl, st);
     if (L == 16) return swiglu ? launch_l<16, true>(p, cpl, st) : launch_l<16, false>(p, cpl, st);
-    const size_t shm = (size_t)(p.K / 32) * (4 * sizeof(u32x4) + sizeof(float2)) + 4 * sizeof(float);
-    if (shm > 64 * 1024) return hipErrorInvalidValue;
     const int grid = (p.N + 3) / 4;
     if (swiglu)
-        hipLaunchKernelGGL(q4_gemv_generic_kernel<true>, dim3(grid), dim3(256), shm, st, p);
+        hipLaunchKernelGGL(q4_gemv_generic_kernel<true>, dim3(grid), dim3(256), 0, st, p);
     else
-        hipLaunchKernelGGL(q4_gemv_generic_kernel<false>, dim3(grid), dim3(256), shm, st, p);
+        hipLaunchKernelGGL(q4_gemv_generic_kernel<false>, dim3(grid), dim3(256), 0, st, p);
     return hipGetLastError();
 }
 

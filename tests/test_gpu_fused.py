@@ -71,7 +71,7 @@ def test_residual_rms_norm(pkg, dev, rows, dim):
 # (N, K, g): GEMV specialisations (K=3072 -> 32 lanes x 3, 2048 -> 64 x 1,
 # 8192 -> 64 x 4, 4096 -> 64 x 2), the generic kernel (K=96), all group sizes.
 RMS_SHAPES = [(5120, 3072, 64), (1000, 2048, 128), (257, 8192, 64), (64, 96, 32),
-              (33, 4096, 32)]
+              (33, 4096, 32), (70, 28672, 64)]
 
 
 @pytest.mark.parametrize("N,K,g", RMS_SHAPES)
@@ -107,7 +107,8 @@ def test_rmsnorm_lm_head_full_size(pkg, dev):
     assert_parity(y.cpu().numpy()[:, rows], ref, TOL_GEMV, "rmsnorm lm_head")
 
 
-SWIGLU_SHAPES = [(8192, 3072, 64), (300, 2048, 128), (100, 96, 32), (64, 8192, 64)]
+SWIGLU_SHAPES = [(8192, 3072, 64), (300, 2048, 128), (100, 96, 32), (64, 8192, 64),
+                 (30, 20000, 32)]
 
 
 @pytest.mark.parametrize("N,K,g", SWIGLU_SHAPES)

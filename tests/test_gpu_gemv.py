@@ -45,6 +45,8 @@ SHAPES = [
     (8200, 16384, 64),
     # K = 32: one chunk per row
     (3, 32, 32), (500, 32, 32),
+    # generic kernel over several 512-chunk segments of x (Llama-70B's down K = 28672)
+    (40, 32000, 64), (7, 28672, 64),
 ]
 
 
@@ -108,7 +110,8 @@ def test_golden_swiglu_gemv(pkg, dev, name):
     assert o.max_rel_err(y.cpu().numpy(), t["y_emu"].astype(np.float64)) < 5e-3
 
 
-@pytest.mark.parametrize("N,K", [(64, 3072), (8192, 3072), (300, 8192), (50, 160), (8200, 10240)])
+@pytest.mark.parametrize("N,K", [(64, 3072), (8192, 3072), (300, 8192), (50, 160), (8200, 10240),
+                                 (20, 20000)])
 def test_swiglu_gemv_shapes(pkg, dev, N, K):
     import torch
     g = 32 if K % 64 else 64
