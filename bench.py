@@ -188,7 +188,10 @@ def main():
 
     copy_gbs = stream_copy_ceiling(torch, dev)
     fused = fused_layer_leg(pkg, torch, gen, dev, layers, reps)
-    decode = decode_token_leg(pkg, torch, gen, dev, layers)
+    model = synthetic_llama(pkg, torch, gen, dev, layers)
+    decode = decode_token_leg(pkg, torch, gen, dev, model)
+    prefill = prefill_leg(pkg, torch, gen, dev, model)
+    del model
     select = token_select_leg(pkg, torch, gen, dev)
 
     gemm = {} if args.no_gemm else gemm_legs(pkg, torch, gen, dev)
@@ -225,7 +228,7 @@ def main():
                                           "frac": round(achieved / copy_gbs, 4)}},
         "cpu_baseline": cpu,
         "extra": {"decode_layer_fused_norms": fused, "decode_token_greedy": decode,
-                  "token_select": select, "gemm": gemm,
+                  "prefill_750": prefill, "token_select": select, "gemm": gemm,
                   **({"timing_diag": diag} if diag else {})},
     }
     print(json.dumps(line))
@@ -278,22 +281,17 @@ def fused_layer_leg(pkg, torch, gen, dev, layers, reps):
                     "the projections' kernels"}
 
 
-def decode_token_leg(pkg, torch, gen, dev, layers, reps=20):
-    """A Llama-3.2-3B decode step's matmul path (swiftltx_amd.decode), greedy
-    and sampled: 4-bit embedding gather, 28 layers (RMSNorm + q|k|v, o,
-    residual + RMSNorm + gate/up SiLU, down + residual), final RMSNorm + tied
-    4-bit lm_head over 128256 tokens, argmax (or top-p sampling) -- one HIP
-    graph per token, the token id fed back on the device.  Attention is
-    outside the path: its stand-in is the q rows (a view, no launch).
-    Random weights: the first 28 of the rotated layer copies; layer norm
-    weights 0.05 (1 + 0.1 N(0,1)), so that the residual stream stays inside
-    fp16 over 28 layers (nothing bounds it without attention: with weights
-    near 1 it overflows and every logit is NaN); final norm weights
-    1 + 0.1 N(0,1), which gives peaked logits like a trained model's."""
+def synthetic_llama(pkg, torch, gen, dev, layers, L=28):
+    """Llama-3.2-3B with random 4-bit weights, in ModelWeights' shape (q|k|v
+    concatenated, tied 4-bit embedding / lm_head over 128256 tokens): the
+    first L of the rotated layer copies; layer norm weights 0.05 (1 + 0.1
+    N(0,1)), so that the residual stream stays inside fp16 over 28 layers
+    (nothing bounds it without attention: with weights near 1 it overflows and
+    every logit is NaN); final norm weights 1 + 0.1 N(0,1), which gives peaked
+    logits like a trained model's."""
     from types import SimpleNamespace
-    from swiftltx_amd.decode import DecodeStep
     from swiftltx_amd.weights import LayerWeights
-    K, V, L = 3072, 128256, 28
+    K, V = 3072, 128256
     norm = lambda: (0.05 * (1.0 + 0.1 * torch.randn(K, generator=gen, device=dev))).float()
     fnorm = lambda: (1.0 + 0.1 * torch.randn(K, generator=gen, device=dev)).float()
     embed = pkg.Q4Weight(*rand_q4(torch, V, K, gen, dev), K, G)
@@ -308,6 +306,19 @@ def decode_token_leg(pkg, torch, gen, dev, layers, reps=20):
                           num_key_value_heads=8, head_dim=128, vocab_size=V, rms_norm_eps=1e-5)
     mw = SimpleNamespace(config=cfg, embed_tokens=embed, lm_head=embed, norm_weight=fnorm(),
                          layers=lws)
+    return mw
+
+
+def decode_token_leg(pkg, torch, gen, dev, mw, reps=20):
+    """A Llama-3.2-3B decode step's matmul path (swiftltx_amd.decode), greedy
+    and sampled: 4-bit embedding gather, 28 layers (RMSNorm + q|k|v, o,
+    residual + RMSNorm + gate/up SiLU, down + residual), final RMSNorm + tied
+    4-bit lm_head over 128256 tokens, argmax (or top-p sampling) -- one HIP
+    graph per token, the token id fed back on the device.  Attention is
+    outside the path: its stand-in is the q rows (a view, no launch).  mw:
+    synthetic_llama()."""
+    from swiftltx_amd.decode import DecodeStep
+    K, V, L = mw.config.hidden_size, mw.config.vocab_size, len(mw.layers)
     s = torch.cuda.Stream()
     ds = DecodeStep(mw, stream=s)
     ds.capture()
@@ -342,6 +353,41 @@ def decode_token_leg(pkg, torch, gen, dev, layers, reps=20):
                                    "history and draws in device memory (SamplerState)"},
             "note": "attention (RoPE, KV cache, softmax) is outside the 4-bit path; stand-in = "
                     "the q rows"}
+
+
+def prefill_leg(pkg, torch, gen, dev, mw, S=750, reps=5):
+    """A Llama-3.2-3B prefill of S = 750 prompt tokens (swiftltx_amd.prefill;
+    LlamaModel.swift:168-203): 4-bit embedding gather of S ids, 28 layers of
+    rms_norm, q|k|v GEMM, o GEMM, residual + rms_norm, gate/up GEMM with the
+    SiLU x up epilogue, down GEMM with the residual epilogue, then rms_norm +
+    lm_head on the last row -- one HIP graph per prompt.  Attention is outside
+    the path: its stand-in copies the q columns (a torch copy, inside the
+    timed graph).  flops: the matmuls only, 2 * S * (q|k|v + o + gate + up +
+    down) per layer plus the last row's lm_head."""
+    from swiftltx_amd.prefill import PrefillStep
+    c = mw.config
+    K, F, L = c.hidden_size, c.intermediate_size, len(mw.layers)
+    qkv = (c.num_attention_heads + 2 * c.num_key_value_heads) * c.head_dim
+    q = c.num_attention_heads * c.head_dim
+    s = torch.cuda.Stream()
+    ps = PrefillStep(mw, S, stream=s)
+    ps.tokens.copy_(torch.randint(0, c.vocab_size, (S,), generator=gen, device=dev,
+                                  dtype=torch.int32))
+    torch.cuda.synchronize()
+    ps.capture()
+    ps.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        ps.replay()
+    torch.cuda.synchronize()
+    us = 1e6 * (time.perf_counter() - t0) / reps
+    flops = 2 * S * L * (K * qkv + q * K + 2 * K * F + F * K) + 2 * K * c.vocab_size
+    tf = flops / (us * 1e-6) / 1e12
+    return {"ms_per_prompt": round(us / 1e3, 3), "prompt_tokens_per_s": round(S / (us * 1e-6), 1),
+            "tflops": round(tf, 1), "frac_mfma": round(tf / MFMA_PEAK_TFLOPS, 4),
+            "tokens": S, "layers": L,
+            "note": "matmul flops only; attention stand-in = a copy of the q columns"}
 
 
 def token_select_leg(pkg, torch, gen, dev, vocab=128256, reps=200):

@@ -43,7 +43,8 @@ def _assert_ulp(y, ref, max_ulp=1, max_frac=0.01, what=""):
     assert frac <= max_frac, f"{what}: {frac:.3%} of values differ"
 
 
-@pytest.mark.parametrize("rows,dim", [(1, 3072), (7, 3072), (750, 3072), (3, 100), (2, 8192)])
+@pytest.mark.parametrize("rows,dim", [(1, 3072), (7, 3072), (750, 3072), (3, 100), (2, 8192),
+                                      (3, 16384), (2, 20000)])
 def test_rms_norm(pkg, dev, rows, dim):
     import torch
     rng = np.random.default_rng(rows * 7 + dim)
@@ -54,7 +55,24 @@ def test_rms_norm(pkg, dev, rows, dim):
     _assert_ulp(out.cpu().numpy(), o.rms_norm_ref(x, w, EPS), what=f"rms_norm {rows}x{dim}")
 
 
-@pytest.mark.parametrize("rows,dim", [(1, 3072), (750, 3072), (5, 96)])
+def test_rms_norm_misaligned_rows_take_the_scalar_kernel(pkg, dev):
+    """Rows 2 bytes off a 16-byte boundary cannot use the 16-byte kernel: the
+    scalar kernel gives the same result as an aligned copy."""
+    import torch
+    rng = np.random.default_rng(3)
+    rows, dim = 9, 3072
+    x = (rng.standard_normal((rows, dim)) * 3).astype(np.float16)
+    w = _norm_weight(dim, 7)
+    buf = torch.zeros(rows * dim + 1, dtype=torch.float16, device=dev)
+    buf[1:].copy_(to_dev(x, dev).reshape(-1))
+    xm = buf[1:].view(rows, dim)
+    assert xm.data_ptr() % 16 != 0
+    got = pkg.rms_norm(xm, to_dev(w, dev), EPS, rows, dim)
+    torch.cuda.synchronize()
+    _assert_ulp(got.cpu().numpy(), o.rms_norm_ref(x, w, EPS), what="misaligned rms_norm")
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 3072), (750, 3072), (5, 96), (4, 16384)])
 def test_residual_rms_norm(pkg, dev, rows, dim):
     import torch
     rng = np.random.default_rng(rows + dim)
