@@ -37,6 +37,9 @@
  *     K % group_size == 0, M >= 0, N >= 0 (M == 0 or N == 0 is a no-op).
  *     x and weight must be 16-byte aligned; scales, biases and 16-bit outputs
  *     2-byte aligned; fp32 outputs and bias 4-byte aligned.
+ *   - A matmul's output must not overlap its activation input x (blocks re-read
+ *     x while others store); such calls return SLTX_ERR_INVALID.  Where an
+ *     entry point allows out == residual it says so.
  *   - Thread-safe: no hidden global mutable state beyond a once-per-device init.
  */
 #ifndef SWIFTLTX_Q4_H

@@ -75,6 +75,13 @@ int check_weight(const char* fn, const void* x, const uint32_t* w, const uint16_
     return kOk;
 }
 
+// The output of a matmul must not overlap its activation input: every GEMV
+// block re-reads x, and GEMM blocks read A tiles, while other blocks store.
+int check_out_alias(const char* fn, const void* x, size_t xbytes, const void* out, size_t obytes) {
+    if (overlap(x, xbytes, out, obytes)) return fail(kErrInvalid, "%s: out overlaps x", fn);
+    return kOk;
+}
+
 // Once-per-device readiness check (gfx950 code object present and runnable).
 std::mutex g_init_mu;
 int g_dev_state[64];  // 0 unknown, 1 ok, -1 bad
@@ -209,6 +216,9 @@ int matmul_common(const char* fn, const void* x, const uint32_t* weight, const u
     if (rc != kOk) return rc;
     if (!aligned(out, y_dtype == kF32 ? 4 : 2)) return fail(kErrInvalid, "%s: misaligned out", fn);
     if (M == 0 || N == 0) return kOk;
+    if ((rc = check_out_alias(fn, x, (size_t)M * K * 2, out,
+                              (size_t)M * N * (y_dtype == kF32 ? 4 : 2))) != kOk)
+        return rc;
     if ((rc = ensure_device()) != kOk) return rc;
     const sltx_q4_weight w = {weight, scales, biases, K, g};
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -331,6 +341,7 @@ int sltx_matmul_q4_silu_mul(const void* x, const sltx_q4_weight* gate, const slt
     if (rc != kOk) return rc;
     if (!aligned(out, 2)) return fail(kErrInvalid, "%s: misaligned out", fn);
     if (M == 0 || N == 0) return kOk;
+    if ((rc = check_out_alias(fn, x, (size_t)M * K * 2, out, (size_t)M * N * 2)) != kOk) return rc;
     if ((rc = ensure_device()) != kOk) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (M == 1) return run_gemv(fn, x, *gate, up, out, K, N, st);
@@ -353,6 +364,9 @@ int sltx_matmul_q4_ex(const void* x, int32_t x_dtype, const sltx_q4_weight* w, c
     if (!aligned(out, out_dtype == kF32 ? 4 : 2)) return fail(kErrInvalid, "%s: misaligned out", fn);
     if (bias && !aligned(bias, 4)) return fail(kErrInvalid, "%s: misaligned bias", fn);
     if (M == 0 || N == 0) return kOk;
+    if ((rc = check_out_alias(fn, x, (size_t)M * w->K * 2, out,
+                              (size_t)M * N * (out_dtype == kF32 ? 4 : 2))) != kOk)
+        return rc;
     if ((rc = ensure_device()) != kOk) return rc;
     return run_gemm(fn, x, x_dtype, *w, nullptr, bias, epilogue, out, out_dtype, M, w->K, N,
                     static_cast<hipStream_t>(stream));
@@ -372,6 +386,7 @@ int sltx_matmul_q4_geglu(const void* x, const sltx_q4_weight* gate, const sltx_q
     if (rc != kOk) return rc;
     if (!aligned(out, 2)) return fail(kErrInvalid, "%s: misaligned out", fn);
     if (M == 0 || N == 0) return kOk;
+    if ((rc = check_out_alias(fn, x, (size_t)M * K * 2, out, (size_t)M * N * 2)) != kOk) return rc;
     if ((rc = ensure_device()) != kOk) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (M == 1) {
@@ -524,6 +539,7 @@ int sltx_rmsnorm_matmul_q4(const void* x, const float* norm_weight, float eps,
     if (!norm_weight) return fail(kErrInvalid, "%s: null norm_weight", fn);
     if (!aligned(norm_weight, 16)) return fail(kErrInvalid, "%s: norm_weight must be 16-byte aligned", fn);
     if (!aligned(out, 2)) return fail(kErrInvalid, "%s: misaligned out", fn);
+    if ((rc = check_out_alias(fn, x, (size_t)w->K * 2, out, (size_t)N * 2)) != kOk) return rc;
     if ((rc = ensure_device()) != kOk) return rc;
     GemvFuse fz;
     fz.pro = kProRms;
@@ -556,6 +572,9 @@ int sltx_residual_rmsnorm_matmul_q4_silu_mul(const void* a, const void* b,
     const size_t kb = (size_t)K * 2;
     if (overlap(residual_out, kb, a, kb) || overlap(residual_out, kb, b, kb))
         return fail(kErrInvalid, "%s: residual_out overlaps an input", fn);
+    const size_t ob = (size_t)N * 2;
+    if (overlap(out, ob, a, kb) || overlap(out, ob, b, kb) || overlap(out, ob, residual_out, kb))
+        return fail(kErrInvalid, "%s: out overlaps an input or residual_out", fn);
     if ((rc = ensure_device()) != kOk) return rc;
     GemvFuse fz;
     fz.pro = kProResidualRms;

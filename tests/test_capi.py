@@ -277,3 +277,29 @@ def test_sample_state_validation(pkg):
                "next_draw": A + 0x303}[k]
         assert call(state(**{k: off})) == -1 and "misaligned" in pkg.last_error(), k
     assert "sltx_sample_top_p_state" in pkg.EXPORTED
+
+
+def test_matmul_out_must_not_overlap_x(pkg):
+    """Every GEMV block re-reads x while others store, so an output that
+    overlaps the activation input is rejected before any device work."""
+    L = pkg.lib()
+    A = ALIGNED
+    assert _mm(pkg, x=A, out=A + 64) == -1 and "out overlaps x" in pkg.last_error()
+    assert _mm(pkg, fn="sltx_matmul_q4_fast_f32", M=4, x=A, out=A - 16) == -1
+    assert "out overlaps x" in pkg.last_error()
+    w = _w(pkg)
+    assert L.sltx_matmul_q4_ex(A, 1, ctypes.byref(w), None, 0, A + 32, 2, 8, 64, None) == -1
+    assert "out overlaps x" in pkg.last_error()
+    g, u = _w(pkg), _w(pkg)
+    assert L.sltx_matmul_q4_silu_mul(A, ctypes.byref(g), ctypes.byref(u), A, 2, 3072, 64,
+                                     None) == -1
+    assert "out overlaps x" in pkg.last_error()
+    assert L.sltx_matmul_q4_geglu(A, ctypes.byref(g), ctypes.byref(u), A + 2, 1, 3072, 64,
+                                  None) == -1
+    assert "out overlaps x" in pkg.last_error()
+    assert L.sltx_rmsnorm_matmul_q4(A, 0x30000, 1e-5, ctypes.byref(w), A + 16, 64, None) == -1
+    assert "out overlaps x" in pkg.last_error()
+    fn = L.sltx_residual_rmsnorm_matmul_q4_silu_mul
+    assert fn(A, 0x20000, 0x30000, 1e-5, 0x40000, ctypes.byref(g), ctypes.byref(u), 0x20000,
+              64, None) == -1
+    assert "out overlaps" in pkg.last_error()
