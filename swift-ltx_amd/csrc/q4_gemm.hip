@@ -574,9 +574,10 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
         // while direct-to-LDS copies are in flight, so every LDS wait it
         // emits waits for all of them).  The scheduling-group barriers fix
         // that order: 1 MFMA, half the step's reads, 1 MFMA, the other half,
-        // then MFMAs with four VALU ops each (measured 1-2% faster than one
-        // read per MFMA with three VALU ops, and than all reads after the
-        // first MFMA; four VALU ops help the bf16 dequantization).  Step 0
+        // then MFMAs with up to six VALU ops each, so the dequantization
+        // finishes early in the step (measured 1-3% faster than one read per
+        // MFMA with three VALU ops, and than all reads after the first MFMA;
+        // the bf16 shapes and split down gain most).  Step 0
         // also reads tile kt+1's packed words and scale/bias (used from step 3
         // on).
 #pragma unroll
@@ -607,7 +608,7 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
 #pragma unroll
             for (int q = 2; q < NT * TM; ++q) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
+                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // VALU
             }
             __builtin_amdgcn_sched_barrier(0);
         }
