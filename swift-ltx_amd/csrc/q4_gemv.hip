@@ -201,31 +201,43 @@ __global__ __launch_bounds__((64 * gemv_max_waves<CPL, SWIGLU, MULTI>())) void q
 
     // x loads first: vmcnt retires in issue order, so x issued after the
     // weights would make the x preparation wait for the HBM latency too.
-    constexpr int XPT = (NCH + 255) / 256;  // x chunks prepared per thread (at most)
+    // The vector is prepared in units of G consecutive 8-value words of one
+    // chunk; unit ui = threadIdx.x + NTH * u.  Vectors of up to 512 words take
+    // one word per thread (G = 1): the serial conversion work per thread stays
+    // short, and the four words of a chunk sit in one lane quad, which sums
+    // their (corr, sum).  Longer vectors take a whole chunk per thread (G = 4),
+    // which keeps the unrolled preparation code (one copy per unit a thread
+    // may own) short.  Measured at K = 3072: q|k|v with rms_norm 4.32 -> 4.00
+    // us, gate/up with residual + rms_norm 8.48 -> 8.03 us; at K = 8192 one
+    // word per thread made the down launch slower (4.55 -> 4.88 us).
+    constexpr int NWD = 4 * NCH;                // words in the input vector
+    constexpr int G = NWD <= 512 ? 1 : 4;       // words per unit
+    constexpr int NU = NWD / G;                 // units
+    constexpr int XPU = (NU + 255) / 256;       // units per thread (at most)
+    static_assert(G == 4 || NWD % 64 == 0, "one-word units: every lane of a preparing wave is valid");
     constexpr bool NORM = PRO != kProNone, RES = PRO == kProResidualRms;
-    f16x8 xr[XPT][4];
-    f16x8 xb[RES ? XPT : 1][4];
-    f32x4 nw[NORM ? XPT : 1][8];
+    const int wave_base = __builtin_amdgcn_readfirstlane((int)(threadIdx.x & ~63u));
+    // Waves whose units all lie past the vector skip the preparation
+    // (wave-uniform branch); redundant loads would only delay the weight
+    // loads queued behind them.  Lanes past the vector in a preparing wave
+    // (G = 4 only) load the last unit and store nothing.
+    auto has_units = [&](int u) { return wave_base + NTH * u < NU; };
+    f16x8 xr[XPU][G];
+    f16x8 xb[RES ? XPU : 1][G];
+    f32x4 nw[NORM ? XPU : 1][2 * G];
 #pragma unroll
-    for (int u = 0; u < XPT; ++u) {
-        // Waves whose chunks all lie past NCH load nothing (wave-uniform
-        // branch): at K = 3072 only 96 of 256 threads own a chunk, and
-        // redundant loads would only delay the weight loads queued behind them.
-        if (__builtin_amdgcn_readfirstlane((int)(threadIdx.x & ~63u)) + NTH * u >= NCH) continue;
-        const int c = threadIdx.x + NTH * u;
-        const int cc = c < NCH ? c : NCH - 1;
-        const f16x8* xp = reinterpret_cast<const f16x8*>(p.x + (size_t)cc * 32);
+    for (int u = 0; u < XPU; ++u) {
+        if (!has_units(u)) continue;
+        const int ui = threadIdx.x + NTH * u;
+        const int uc = ui < NU ? ui : NU - 1;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xr[u][j] = xp[j];
-        if constexpr (RES) {
-            const f16x8* bp = reinterpret_cast<const f16x8*>(p.xb + (size_t)cc * 32);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) xb[u][j] = bp[j];
+        for (int g = 0; g < G; ++g) {
+            xr[u][g] = reinterpret_cast<const f16x8*>(p.x)[uc * G + g];
+            if constexpr (RES) xb[u][g] = reinterpret_cast<const f16x8*>(p.xb)[uc * G + g];
         }
         if constexpr (NORM) {
-            const f32x4* wp = reinterpret_cast<const f32x4*>(p.norm_w + (size_t)cc * 32);
 #pragma unroll
-            for (int q = 0; q < 8; ++q) nw[u][q] = wp[q];
+            for (int q = 0; q < 2 * G; ++q) nw[u][q] = reinterpret_cast<const f32x4*>(p.norm_w)[uc * 2 * G + q];
         }
     }
     __builtin_amdgcn_sched_barrier(0);   // keep every x load ahead of the weight loads
@@ -245,25 +257,23 @@ __global__ __launch_bounds__((64 * gemv_max_waves<CPL, SWIGLU, MULTI>())) void q
         // the (rounded) input and rms = rsqrt(mean(v^2) + eps).
         float ss = 0.0f;
 #pragma unroll
-        for (int u = 0; u < XPT; ++u) {
-            const int c = threadIdx.x + NTH * u;
-            if (c >= NCH) continue;
+        for (int u = 0; u < XPU; ++u) {
+            if (!has_units(u)) continue;
+            const int ui = threadIdx.x + NTH * u;
+            if (ui >= NU) continue;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int g = 0; g < G; ++g) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    float v = (float)xr[u][j][e];
+                    float v = (float)xr[u][g][e];
                     if constexpr (RES) {
-                        v += (float)xb[u][j][e];
-                        xr[u][j][e] = (f16)v;
+                        v += (float)xb[u][g][e];
+                        xr[u][g][e] = (f16)v;
                     }
                     ss += v * v;
                 }
-            if constexpr (RES) {
-                if (blockIdx.x == 0) {
-                    f16x8* rp = reinterpret_cast<f16x8*>(p.res_out + (size_t)c * 32);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) rp[j] = xr[u][j];
+                if constexpr (RES) {
+                    if (blockIdx.x == 0) reinterpret_cast<f16x8*>(p.res_out)[ui * G + g] = xr[u][g];
                 }
             }
         }
@@ -274,29 +284,36 @@ __global__ __launch_bounds__((64 * gemv_max_waves<CPL, SWIGLU, MULTI>())) void q
         for (int w = 0; w < (NTH >> 6); ++w) ssum += lds.red[w];
         const float rms = rsqrtf(ssum / (float)p.K + p.eps);
 #pragma unroll
-        for (int u = 0; u < XPT; ++u)
+        for (int u = 0; u < XPU; ++u) {
+            if (!has_units(u)) continue;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int g = 0; g < G; ++g)
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    xr[u][j][e] = (f16)((float)xr[u][j][e] * rms * nw[u][(j * 8 + e) >> 2][e & 3]);
+                    xr[u][g][e] = (f16)((float)xr[u][g][e] * rms * nw[u][2 * g + (e >> 2)][e & 3]);
+        }
     }
 
     // Prepare x once per block while the weight loads are in flight.
 #pragma unroll
-    for (int u = 0; u < XPT; ++u) {
-        const int c = threadIdx.x + NTH * u;
-        if (c < NCH) {
-            float corr = 0.0f, sum = 0.0f;
+    for (int u = 0; u < XPU; ++u) {
+        if (!has_units(u)) continue;
+        const int ui = threadIdx.x + NTH * u;
+        const bool ok = ui < NU;
+        const int c = (ui * G) >> 2, j0 = (ui * G) & 3;
+        float corr = 0.0f, sum = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                uint32_t pr[4];
-                pair_word(xr[u][j], pr, corr, sum);
-                u32x4 v = {pr[0], pr[1], pr[2], pr[3]};
-                lds.xs[j][c] = v;
-            }
-            lds.xc[c] = make_float2(-corr, sum);
+        for (int g = 0; g < G; ++g) {
+            uint32_t pr[4];
+            pair_word(xr[u][g], pr, corr, sum);
+            u32x4 v = {pr[0], pr[1], pr[2], pr[3]};
+            if (ok) lds.xs[j0 + g][c] = v;
         }
+        if constexpr (G == 1) {
+            corr = dpp_add<0x4E>(dpp_add<0xB1>(corr));
+            sum = dpp_add<0x4E>(dpp_add<0xB1>(sum));
+        }
+        if (ok && j0 == 0) lds.xc[c] = make_float2(-corr, sum);
     }
     // LDS-only barrier: __syncthreads() would also wait for every
     // outstanding weight load (its release fence waits on vmcnt(0)).
