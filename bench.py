@@ -358,9 +358,10 @@ def decode_token_leg(pkg, torch, gen, dev, mw, reps=20):
 def prefill_leg(pkg, torch, gen, dev, mw, S=750, reps=5):
     """A Llama-3.2-3B prefill of S = 750 prompt tokens (swiftltx_amd.prefill;
     LlamaModel.swift:168-203): 4-bit embedding gather of S ids, 28 layers of
-    rms_norm, q|k|v GEMM, o GEMM, residual + rms_norm, gate/up GEMM with the
-    SiLU x up epilogue, down GEMM with the residual epilogue, then rms_norm +
-    lm_head on the last row -- one HIP graph per prompt.  Attention is outside
+    q|k|v GEMM, o GEMM + residual + rms_norm (one call), gate/up GEMM with the
+    SiLU x up epilogue, down GEMM + residual + the next layer's rms_norm (one
+    call), then rms_norm + lm_head on the last row -- one HIP graph per prompt
+    (layer 0's input norm is its own launch).  Attention is outside
     the path: its stand-in copies the q columns (a torch copy, inside the
     timed graph).  flops: the matmuls only, 2 * S * (q|k|v + o + gate + up +
     down) per layer plus the last row's lm_head."""

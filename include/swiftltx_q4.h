@@ -15,7 +15,8 @@
  *     frees or keeps them.  Outputs are written, never read.
  *   - Memory: the only device memory the library allocates is a per-stream
  *     workspace: fp32 partial sums for GEMMs with too few output tiles to
- *     fill the GPU (split-K, e.g. M=750 x N=3072), the block partials of
+ *     fill the GPU (split-K, e.g. M=750 x N=3072) and for every
+ *     sltx_matmul_q4_residual_rms_norm, the block partials of
  *     sltx_argmax, and the probabilities and candidate list of
  *     sltx_sample_top_p[_state].  There is one per (device, stream),
  *     grown on first need to at least twice its old size; a replaced buffer
@@ -207,6 +208,30 @@ int sltx_residual_rmsnorm_matmul_q4_silu_mul(const void* a, const void* b,
  * must not otherwise overlap it, nor x. */
 int sltx_matmul_q4_residual(const void* x, const sltx_q4_weight* w, const void* residual,
                             void* out, int32_t M, int32_t N, void* stream);
+
+/* linear + residual add + RMSNorm of the sum, for prefill rows (one call in
+ * place of two or three):
+ *   sum_rounded == 0: linear then residualRmsNorm(residual, o)  (the o_proj
+ *     step, LlamaModel.swift:269-272; Ops.swift:256-279; Kernels.swift:238-290):
+ *     the sum of squares is over the unrounded residual + o;
+ *   sum_rounded != 0: linear, elemAdd, then the next layer's rmsNorm of the
+ *     stored fp16 sum  (the down_proj step and the next input_layernorm,
+ *     LlamaModel.swift:278-279, 233; Ops.swift:8-27, 72-84).
+ * residual_out[M,N] = half(residual + half(x . dequant(W)^T)) and
+ * norm_out = rms_norm(residual_out) with norm_weight (fp32 [N]); both equal,
+ * bit for bit, the unfused sequence of this library's GEMM (M > 1 route) and
+ * sltx_residual_rms_norm / sltx_rms_norm.  Always runs the GEMM (any M >= 1),
+ * whose fp32 partial sums go through the per-stream workspace, then one pass
+ * per row.  N % 8 == 0 and N <= 16384; residual, residual_out, norm_out,
+ * norm_weight 16-byte aligned.  residual_out may be residual (in place);
+ * norm_out must overlap neither, and no output may overlap x.  While the stream
+ * is being captured the workspace must already exist (an eager call of the
+ * same shape on that stream first), else the call fails.
+ * No single reference entry point: it replaces the pairs named above. */
+int sltx_matmul_q4_residual_rms_norm(const void* x, const sltx_q4_weight* w, const void* residual,
+                                     const float* norm_weight, float eps, int32_t M, int32_t N,
+                                     int32_t sum_rounded, void* residual_out, void* norm_out,
+                                     void* stream);
 
 /* ---- Token selection after the lm_head (LlamaModel.swift:153,161) ----
  * Both read n logits (SLTX_F16 or SLTX_F32, device) and write one int32 token

@@ -56,6 +56,7 @@ EXPORTED = (
     "sltx_rmsnorm_matmul_q4",
     "sltx_residual_rmsnorm_matmul_q4_silu_mul",
     "sltx_matmul_q4_residual",
+    "sltx_matmul_q4_residual_rms_norm",
     "sltx_argmax",
     "sltx_sample_top_p",
     "sltx_sample_top_p_state",
@@ -145,12 +146,14 @@ def lib():
         L.sltx_rmsnorm_matmul_q4.argtypes = [P, P, F, W, P, I32, P]
         L.sltx_residual_rmsnorm_matmul_q4_silu_mul.argtypes = [P, P, P, F, P, W, W, P, I32, P]
         L.sltx_matmul_q4_residual.argtypes = [P, W, P, P, I32, I32, P]
+        L.sltx_matmul_q4_residual_rms_norm.argtypes = [P, W, P, P, F, I32, I32, I32, P, P, P]
         L.sltx_argmax.argtypes = [P, I32, I32, P, P]
         L.sltx_sample_top_p.argtypes = [P, I32, I32, F, F, F, P, I32, F, P, P]
         L.sltx_sample_top_p_state.argtypes = [P, I32, I32, F, F, F,
                                               ctypes.POINTER(CSampleState), P, P]
         for n in ("sltx_rms_norm", "sltx_residual_rms_norm", "sltx_rmsnorm_matmul_q4",
                   "sltx_residual_rmsnorm_matmul_q4_silu_mul", "sltx_matmul_q4_residual",
+                  "sltx_matmul_q4_residual_rms_norm",
                   "sltx_argmax", "sltx_sample_top_p", "sltx_sample_top_p_state"):
             getattr(L, n).restype = ctypes.c_int
         VP = ctypes.c_void_p
@@ -353,6 +356,25 @@ def matmul_q4_residual(x, w: Q4Weight, residual, M, N, out=None, stream=None):
     check(lib().sltx_matmul_q4_residual(_ptr(x), ctypes.byref(cw), _ptr(residual), _ptr(out), M,
                                         N, _stream(stream)))
     return out
+
+
+def matmul_q4_residual_rms_norm(x, w: Q4Weight, residual, norm_weight, eps, M, N, sum_rounded,
+                                residual_out=None, norm_out=None, stream=None):
+    """linear + residual add + RMSNorm for prefill rows: residual_out =
+    half(residual + half(x . dequant(W)^T)), norm_out = rms_norm(residual_out)
+    with the sum of squares over the unrounded sum (sum_rounded False: the o_proj
+    step's residualRmsNorm, LlamaModel.swift:269-272) or over residual_out
+    (True: elemAdd then the next layer's rmsNorm, LlamaModel.swift:278-279, 233)
+    -> (residual_out, norm_out), fp16 [M, N]."""
+    torch = _torch()
+    residual_out = _new((M, N), torch.float16, x) if residual_out is None else residual_out
+    norm_out = _new((M, N), torch.float16, x) if norm_out is None else norm_out
+    cw = w.c()
+    check(lib().sltx_matmul_q4_residual_rms_norm(_ptr(x), ctypes.byref(cw), _ptr(residual),
+                                                 _ptr(norm_weight), eps, M, N,
+                                                 1 if sum_rounded else 0, _ptr(residual_out),
+                                                 _ptr(norm_out), _stream(stream)))
+    return residual_out, norm_out
 
 
 def matmul_q4_geglu(x, gate: Q4Weight, up: Q4Weight, M, K, N, out=None, stream=None):

@@ -609,4 +609,62 @@ int sltx_matmul_q4_residual(const void* x, const sltx_q4_weight* w, const void* 
                     residual);
 }
 
+int sltx_matmul_q4_residual_rms_norm(const void* x, const sltx_q4_weight* w, const void* residual,
+                                     const float* norm_weight, float eps, int32_t M, int32_t N,
+                                     int32_t sum_rounded, void* residual_out, void* norm_out,
+                                     void* stream) {
+    const char* fn = "sltx_matmul_q4_residual_rms_norm";
+    if (!w) return fail(kErrInvalid, "%s: null weight descriptor", fn);
+    int rc = check_weight(fn, x, w->weight, w->scales, w->biases, residual_out, M, w->K, N,
+                          w->group_size);
+    if (rc != kOk) return rc;
+    if (M == 0 || N == 0) return kOk;
+    if (!residual || !norm_weight || !norm_out) return fail(kErrInvalid, "%s: null pointer argument", fn);
+    if (N % 8 != 0 || N > 16384)
+        return fail(kErrUnsupported, "%s: N (%d) must be a multiple of 8 and at most 16384", fn, N);
+    if (!aligned(residual, 16) || !aligned(residual_out, 16) || !aligned(norm_out, 16) ||
+        !aligned(norm_weight, 16))
+        return fail(kErrInvalid,
+                    "%s: residual, residual_out, norm_out and norm_weight must be 16-byte aligned", fn);
+    const size_t ob = (size_t)M * N * 2, xb = (size_t)M * w->K * 2;
+    if (residual != residual_out && overlap(residual, ob, residual_out, ob))
+        return fail(kErrInvalid, "%s: residual and residual_out overlap without being equal", fn);
+    if (overlap(norm_out, ob, residual_out, ob) || overlap(norm_out, ob, residual, ob))
+        return fail(kErrInvalid, "%s: norm_out overlaps residual or residual_out", fn);
+    if (overlap(x, xb, residual_out, ob) || overlap(x, xb, norm_out, ob))
+        return fail(kErrInvalid, "%s: an output overlaps x", fn);
+    if ((rc = ensure_device()) != kOk) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    GemmParams p;
+    p.a = x;
+    p.w0 = w->weight;
+    p.s0 = w->scales;
+    p.b0 = w->biases;
+    p.w1 = nullptr;
+    p.s1 = nullptr;
+    p.b1 = nullptr;
+    p.bias = nullptr;
+    p.y = residual_out;   // not written by the GEMM: its output is the fp32 partials
+    p.M = M;
+    p.N = N;
+    p.K = w->K;
+    p.groups = w->K / w->group_size;
+    p.gshift = log2_group(w->group_size);
+    p.tiles_m = p.tiles_n = 0;
+    p.y_dtype = kF16;
+    p.epilogue = kEpiNone;
+    p.residual = static_cast<const uint16_t*>(residual);
+    p.splits = 1;
+    p.split_tiles = 0;
+    p.ws = stream_workspace(st, gemm_partials_workspace_bytes(p));
+    if (!p.ws)
+        return fail(kErrInvalid,
+                    "%s: no workspace on this stream (it is being captured: call it once eagerly "
+                    "on the same stream first)", fn);
+    return finish(launch_gemm_residual_rms_norm(p, false, norm_weight, eps,
+                                                static_cast<uint16_t*>(residual_out),
+                                                static_cast<uint16_t*>(norm_out), sum_rounded != 0, st),
+                  fn);
+}
+
 }  // extern "C"

@@ -760,6 +760,76 @@ __global__ __launch_bounds__(256) void q4_splitk_reduce_kernel(GemmParams p) {
     }
 }
 
+// Split-K reduction fused with the residual add and the RMSNorm of each
+// output row (one block of 256 threads per row, N % 8 == 0):
+//   o = half(sum over splits, in split order)        the projection (linear)
+//   t = float(residual) + float(o);  r = half(t)     elemAdd / residualRmsNorm
+//   rms = rsqrt(mean(q^2) + eps), q = t (sum_rounded == 0, residualRmsNorm,
+//         Kernels.swift:238-290) or q = float(r) (sum_rounded == 1: elemAdd then
+//         rmsNorm of the stored fp16 stream, Kernels.swift:40-86, 121-128)
+//   out = half(float(r) * rms * w)
+// The partial sums follow q4_splitk_reduce_kernel and the row sum of squares
+// follows rms_norm_vec_kernel (thread t: pieces t, t + 256, ... of 8 values;
+// wave trees, then the four waves in order), so the results equal the unfused
+// GEMM + reduce + norm sequence bit for bit.
+template <int VPT>
+__global__ __launch_bounds__(256) void q4_splitk_residual_rms_norm_kernel(
+    GemmParams p, const float* w, float eps, uint16_t* res_out, uint16_t* out, int sum_rounded) {
+    __shared__ float red[4];
+    const int nv = p.N / 8;
+    const size_t m = blockIdx.x;
+    const size_t stride = (size_t)p.M * p.N;
+    const f16x8* R = reinterpret_cast<const f16x8*>(p.residual + m * p.N);
+    f16x8 r[VPT];
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) {
+        const int v = threadIdx.x + 256 * u;
+        if (v >= nv) continue;
+        float a[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] = 0.0f;
+        const float* q = p.ws + m * p.N + (size_t)v * 8;
+        for (int s = 0; s < p.splits; ++s, q += stride) {
+            const f32x4 q0 = reinterpret_cast<const f32x4*>(q)[0];
+            const f32x4 q1 = reinterpret_cast<const f32x4*>(q)[1];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                a[e] += q0[e];
+                a[4 + e] += q1[e];
+            }
+        }
+        const f16x8 h = R[v];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float t = (float)h[e] + h2f(f2h(a[e]));
+            r[u][e] = (f16)t;
+            const float sq = sum_rounded ? (float)r[u][e] : t;
+            ss += sq * sq;
+        }
+        reinterpret_cast<f16x8*>(res_out + m * p.N)[v] = r[u];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float rms = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)p.N + eps);
+    const f32x4* W = reinterpret_cast<const f32x4*>(w);
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) {
+        const int v = threadIdx.x + 256 * u;
+        if (v >= nv) continue;
+        const f32x4 w0 = W[2 * v], w1 = W[2 * v + 1];
+        f16x8 o8;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            o8[e] = (f16)((float)r[u][e] * rms * w0[e]);
+            o8[4 + e] = (f16)((float)r[u][4 + e] * rms * w1[e]);
+        }
+        reinterpret_cast<f16x8*>(out + m * p.N)[v] = o8;
+    }
+}
+
 // Launch plan: block-tile height WM (BM = 64*WM) and K splits, chosen by
 // estimated time on 256 CUs: rounds of blocks x (k-tiles per block x the
 // measured time of one k-tile -- 1.37 us at BM = 192, 0.95 us at BM = 128,
@@ -774,7 +844,10 @@ struct GemmPlan {
     size_t ws_bytes;
 };
 
-static GemmPlan plan_gemm(const GemmParams& p, bool allow_split) {
+// partials: the output goes through the fp32 workspace at every split count
+// (including one), because a row-wise pass follows (the fused residual +
+// RMSNorm), so the unsplit plan pays the partial traffic too.
+static GemmPlan plan_gemm(const GemmParams& p, bool allow_split, bool partials = false) {
     const bool silu = p.epilogue == kEpiSiluMul || p.epilogue == kEpiGeluMul;
     const int bn_out = silu ? BN / 2 : BN;
     const int tiles_n = (p.N + bn_out - 1) / bn_out;
@@ -797,14 +870,15 @@ static GemmPlan plan_gemm(const GemmParams& p, bool allow_split) {
             const long blocks = tiles * s_eff;
             const long rounds = (blocks + kCUs - 1) / kCUs;
             double us = (double)rounds * (chunk * kt_us + 8.0) + 2.0;
-            if (s_eff > 1) {
+            const bool ws = s_eff > 1 || partials;
+            if (ws) {
                 const double part = (double)s_eff * p.M * nw * 4.0;
                 us += part / 6.0e6 + 3.0 + (part + (double)p.M * p.N * 2.0) / 4.0e6;
             }
             if (us < best_us) {
                 best_us = us;
                 best = {wm, (int)tiles_m, tiles_n, s_eff, chunk,
-                        s_eff > 1 ? (size_t)s_eff * p.M * nw * sizeof(float) : 0};
+                        ws ? (size_t)s_eff * p.M * nw * sizeof(float) : 0};
             }
         }
     }
@@ -812,6 +886,7 @@ static GemmPlan plan_gemm(const GemmParams& p, bool allow_split) {
 }
 
 size_t gemm_workspace_bytes(const GemmParams& p) { return plan_gemm(p, true).ws_bytes; }
+size_t gemm_partials_workspace_bytes(const GemmParams& p) { return plan_gemm(p, true, true).ws_bytes; }
 
 template <int WM, bool BF16, bool SPLIT>
 static void launch_wm(const GemmParams& p, bool silu, long grid, hipStream_t st) {
@@ -863,6 +938,37 @@ hipError_t launch_gemm(GemmParams p, bool a_bf16, hipStream_t st) {
     } else {
         launch_dtype<false>(p, a_bf16, silu, grid, plan.wm, st);
     }
+    return hipGetLastError();
+}
+
+// GEMM into fp32 partials (one or more K splits; p.ws holds
+// gemm_partials_workspace_bytes(p)), then the fused reduce + residual +
+// RMSNorm pass.  Requires N % 8 == 0, N <= 16384 and 16-byte aligned rows.
+hipError_t launch_gemm_residual_rms_norm(GemmParams p, bool a_bf16, const float* norm_w, float eps,
+                                         uint16_t* res_out, uint16_t* norm_out, bool sum_rounded,
+                                         hipStream_t st) {
+    if (p.M <= 0 || p.N <= 0) return hipSuccess;
+    if (p.N % 8 != 0 || p.N / 8 > 8 * 256 || !p.ws || !p.residual) return hipErrorInvalidValue;
+    const GemmPlan plan = plan_gemm(p, true, true);
+    p.tiles_m = plan.tiles_m;
+    p.tiles_n = plan.tiles_n;
+    p.splits = plan.splits;
+    p.split_tiles = plan.split_tiles;
+    const long blocks = (long)p.tiles_m * p.tiles_n * p.splits;
+    const long grid = (blocks + 7) / 8 * 8;
+    if (grid > 0x7fffffffL) return hipErrorInvalidValue;
+    launch_dtype<true>(p, a_bf16, false, grid, plan.wm, st);
+    const int vpt = (p.N / 8 + 255) / 256;
+    const dim3 g(p.M), t(256);
+    const int sr = sum_rounded ? 1 : 0;
+    if (vpt == 1)
+        hipLaunchKernelGGL(q4_splitk_residual_rms_norm_kernel<1>, g, t, 0, st, p, norm_w, eps, res_out, norm_out, sr);
+    else if (vpt == 2)
+        hipLaunchKernelGGL(q4_splitk_residual_rms_norm_kernel<2>, g, t, 0, st, p, norm_w, eps, res_out, norm_out, sr);
+    else if (vpt <= 4)
+        hipLaunchKernelGGL(q4_splitk_residual_rms_norm_kernel<4>, g, t, 0, st, p, norm_w, eps, res_out, norm_out, sr);
+    else
+        hipLaunchKernelGGL(q4_splitk_residual_rms_norm_kernel<8>, g, t, 0, st, p, norm_w, eps, res_out, norm_out, sr);
     return hipGetLastError();
 }
 

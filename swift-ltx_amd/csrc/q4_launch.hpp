@@ -110,6 +110,16 @@ size_t gemm_workspace_bytes(const GemmParams& p);
 // Launches the GEMM; splits K only if p.ws is non-null (and then needs
 // gemm_workspace_bytes(p) bytes there).
 hipError_t launch_gemm(GemmParams p, bool a_bf16, hipStream_t st);
+// Bytes of fp32 partials the fused residual + RMSNorm GEMM of `p` uses (its
+// output always goes through the workspace, at one split or more).
+size_t gemm_partials_workspace_bytes(const GemmParams& p);
+// GEMM (no epilogue; p.residual is the residual input) into the workspace
+// p.ws, then one pass per row: res_out = half(residual + half(sum of splits))
+// and norm_out = rms_norm(res_out) with the sum of squares over the unrounded
+// sum (sum_rounded false) or over res_out (true).  N % 8 == 0, N <= 16384.
+hipError_t launch_gemm_residual_rms_norm(GemmParams p, bool a_bf16, const float* norm_w, float eps,
+                                         uint16_t* res_out, uint16_t* norm_out, bool sum_rounded,
+                                         hipStream_t st);
 hipError_t launch_silu_mul(const uint16_t* a, const uint16_t* b, uint16_t* out, long count,
                            hipStream_t st);
 // Row-wise RMS norm, optionally of a + b (then the rounded sum goes to res_out).

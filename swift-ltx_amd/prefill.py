@@ -6,13 +6,15 @@ Mirrors LlamaModel.prefill / transformerBlockBatch (LlamaModel.swift:168-203,
 
   embeddingQ4Batch (Ops.swift:163-185)          sltx_embedding_q4, S device token ids
   per layer:
-    rmsNorm                                     sltx_rms_norm (all S rows)
+    rmsNorm                                     layer 0: sltx_rms_norm (all S rows); later
+                                                layers: the previous down step's call
     q, k, v linear                              sltx_linear, fast (GEMM; q|k|v rows concatenated)
     RoPE, KV cache append, attention            the caller's `attention` (outside this library)
-    o linear                                    sltx_linear, fast (GEMM)
-    residualRmsNorm                             sltx_residual_rms_norm
+    o linear + residualRmsNorm                  sltx_matmul_q4_residual_rms_norm (unrounded sum)
     gate, up linear + siluMul                   sltx_matmul_q4_silu_mul (GEMM, fused epilogue)
-    down linear + elemAdd                       sltx_matmul_q4_residual (GEMM, residual epilogue)
+    down linear + elemAdd (+ next rmsNorm)      sltx_matmul_q4_residual_rms_norm (rounded sum,
+                                                the next layer's input norm); last layer:
+                                                sltx_matmul_q4_residual (GEMM, residual epilogue)
   final rmsNorm + lm_head on the last row       sltx_rmsnorm_matmul_q4 (GEMV)
 
 The reference normalizes all S rows before slicing the last one
@@ -27,8 +29,8 @@ token only.
 """
 from __future__ import annotations
 
-from . import (Q4Weight, embedding_q4, linear, matmul_q4_residual, matmul_q4_silu_mul, rms_norm,
-               residual_rms_norm, rmsnorm_matmul_q4)
+from . import (Q4Weight, embedding_q4, linear, matmul_q4_residual, matmul_q4_residual_rms_norm,
+               matmul_q4_silu_mul, rms_norm, rmsnorm_matmul_q4)
 
 
 def q_columns_attention(q_dim):
@@ -70,7 +72,6 @@ class PrefillStep:
         self.h = torch.empty(S, K, dtype=f16, device=dev)        # residual stream
         self.normed = torch.empty(S, K, dtype=f16, device=dev)
         self.qkv = torch.empty(S, self.qkv_rows, dtype=f16, device=dev)
-        self.o = torch.empty(S, K, dtype=f16, device=dev)
         self.res = torch.empty(S, K, dtype=f16, device=dev)
         self.act = torch.empty(S, F, dtype=f16, device=dev)
         self.logits = torch.empty(1, c.vocab_size, dtype=f16, device=dev)
@@ -82,25 +83,32 @@ class PrefillStep:
         c, w, s = self.c, self.w, self.stream
         S, K, F, eps = self.S, self.hidden, c.intermediate_size, c.rms_norm_eps
         embedding_q4(w.embed_tokens, c.vocab_size, self.tokens, out=self.h, stream=s)
-        for i, lw in enumerate(w.layers):
-            rms_norm(self.h, lw.input_norm_weight, eps, S, K, out=self.normed, stream=s)
+        layers = w.layers
+        rms_norm(self.h, layers[0].input_norm_weight, eps, S, K, out=self.normed, stream=s)
+        for i, lw in enumerate(layers):
             linear(self.normed, lw.qkv_proj, S, K, self.qkv_rows, fast=True, out=self.qkv, stream=s)
             attn = self.attention(i, self.qkv)
-            linear(attn, lw.o_proj, S, self.q_dim, K, fast=True, out=self.o, stream=s)
-            # res = h + o (the residual stream); gate/up read its norm; h = res + down
-            residual_rms_norm(self.h, self.o, lw.post_norm_weight, eps, S, K,
-                              residual_out=self.res, norm_out=self.normed, stream=s)
+            # res = h + o (the residual stream); gate/up read its norm
+            matmul_q4_residual_rms_norm(attn, lw.o_proj, self.h, lw.post_norm_weight, eps, S, K,
+                                        False, residual_out=self.res, norm_out=self.normed,
+                                        stream=s)
             matmul_q4_silu_mul(self.normed, lw.gate_proj, lw.up_proj, S, K, F, out=self.act,
                                stream=s)
-            matmul_q4_residual(self.act, lw.down_proj, self.res, S, K, out=self.h, stream=s)
+            # h = res + down, and the next layer's input norm of h
+            if i + 1 < len(layers):
+                matmul_q4_residual_rms_norm(self.act, lw.down_proj, self.res,
+                                            layers[i + 1].input_norm_weight, eps, S, K, True,
+                                            residual_out=self.h, norm_out=self.normed, stream=s)
+            else:
+                matmul_q4_residual(self.act, lw.down_proj, self.res, S, K, out=self.h, stream=s)
         rmsnorm_matmul_q4(self.h[S - 1:], w.norm_weight, eps, w.lm_head, c.vocab_size,
                           out=self.logits, stream=s)
         return self.logits
 
     def capture(self):
         """Capture forward() as a HIP graph on self.stream (a torch stream;
-        required), after one eager run there (which sizes the split-K
-        workspace the GEMMs use in the graph)."""
+        required), after one eager run there (which sizes the workspace the
+        split-K GEMMs and the fused residual + norm calls use in the graph)."""
         import torch
         if self.stream is None:
             raise ValueError("capture needs a dedicated stream")

@@ -303,3 +303,30 @@ def test_matmul_out_must_not_overlap_x(pkg):
     assert fn(A, 0x20000, 0x30000, 1e-5, 0x40000, ctypes.byref(g), ctypes.byref(u), 0x20000,
               64, None) == -1
     assert "out overlaps" in pkg.last_error()
+
+
+def test_matmul_residual_rms_norm_validation(pkg):
+    """sltx_matmul_q4_residual_rms_norm rejects unsupported widths, misaligned
+    rows and overlapping outputs before any device work."""
+    L = pkg.lib()
+    fn = L.sltx_matmul_q4_residual_rms_norm
+    A, R, O, N_, X = 0x100000, 0x200000, 0x300000, 0x400000, 0x500000
+    w = _w(pkg)
+
+    def call(x=X, wp=ctypes.byref(w), res=R, nw=N_, M=4, N=3072, ro=O, no=0x600000):
+        return fn(x, wp, res, nw, 1e-5, M, N, 0, ro, no, None)
+
+    assert call(M=0) == 0 and call(N=0) == 0           # no-ops
+    assert call(wp=None) == -1 and "null weight" in pkg.last_error()
+    assert call(res=0) == -1 and "null" in pkg.last_error()
+    assert call(N=3076) == -2 and "multiple of 8" in pkg.last_error()
+    assert call(N=16392) == -2
+    assert call(res=R + 2) == -1 and "16-byte aligned" in pkg.last_error()
+    assert call(nw=N_ + 4) == -1 and "16-byte aligned" in pkg.last_error()
+    assert call(ro=R + 16) == -1 and "overlap without being equal" in pkg.last_error()
+    assert call(no=O + 16) == -1 and "norm_out overlaps" in pkg.last_error()
+    assert call(no=R) == -1 and "norm_out overlaps" in pkg.last_error()
+    assert call(ro=X + 64) == -1 and "overlaps x" in pkg.last_error()
+    assert call(no=X) == -1 and "overlaps x" in pkg.last_error()
+    wg = _w(pkg, g=48)
+    assert call(wp=ctypes.byref(wg)) == -2

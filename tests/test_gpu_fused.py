@@ -293,3 +293,75 @@ def test_embedding_q4_full_vocab(pkg, dev):
     idt = torch.from_numpy(ids.astype(np.int64)).to(dev)
     ref = o.embedding_q4_ref(host(w[idt]), host(s[idt]), host(b[idt]), np.arange(len(ids)), g)
     assert np.array_equal(out.cpu().numpy(), ref)
+
+
+# (M, N, K, g): the prefill o (K = 3072) and down (K = 8192) shapes at M = 750,
+# small and multi-row shapes, the generic GEMM (K % 128 != 0), M = 1.
+RRN_SHAPES = [(750, 3072, 3072, 64), (750, 3072, 8192, 64), (33, 192, 256, 64),
+              (1000, 2048, 512, 128), (5, 96, 96, 32), (1, 3072, 3072, 64)]
+
+
+@pytest.mark.parametrize("M,N,K,g", RRN_SHAPES)
+@pytest.mark.parametrize("sum_rounded", [False, True])
+def test_matmul_residual_rms_norm(pkg, dev, M, N, K, g, sum_rounded):
+    """linear + residual add + RMSNorm in one call (LlamaModel.swift:269-272 with
+    the unrounded sum of squares, :278-279 then :233 with the rounded stream)
+    against the oracle: the residual stream within the residual epilogue's
+    bound; the normalized rows within 1 fp16 ulp of half(r * rms * w), with r
+    the GPU's own residual stream and rms from the oracle's fp64 sum of squares
+    (of float(residual) + float(half(y)) unrounded, or of the rounded sum).
+    The oracle's half(y) differs from the GPU's projection in the last fp16 bit
+    on a few elements (within the GEMM bound), which moves one row's sum of
+    squares by ~1e-5 relative: up to 5% of a row's values may then sit on the
+    other side of an fp16 rounding boundary (still within 1 ulp).  The bit-exact
+    test below pins the fused call to the unfused GPU sequence."""
+    import torch
+    x, [(w, s, b)] = o.make_inputs(M, N, K, g, seed=M + N + K)
+    rng = np.random.default_rng(M * N + 1)
+    res = (rng.standard_normal((M, N)) * 6).astype(np.float16)
+    nw = _norm_weight(N, N + 3)
+    y64 = o.matmul_q4_f64(x, w, s, b, g)
+    r_dev, n_dev = pkg.matmul_q4_residual_rms_norm(to_dev(x, dev), q4w(pkg, w, s, b, K, g, dev),
+                                                    to_dev(res, dev), to_dev(nw, dev), EPS, M, N,
+                                                    sum_rounded)
+    torch.cuda.synchronize()
+    got_r, got_n = r_dev.cpu().numpy(), n_dev.cpu().numpy()
+    what = f"M={M} N={N} K={K} g={g} sum_rounded={sum_rounded}"
+    _assert_residual(got_r, res, y64, TOL_GEMM_F16, what)
+    v = res.astype(np.float32) + y64.astype(np.float16).astype(np.float32)
+    q = v.astype(np.float16).astype(np.float64) if sum_rounded else v.astype(np.float64)
+    rms = (1.0 / np.sqrt(np.sum(q * q, axis=-1, keepdims=True) / N + EPS)).astype(np.float32)
+    ref_n = ((got_r.astype(np.float32) * rms) * nw).astype(np.float16)
+    _assert_ulp(got_n, ref_n, max_frac=0.05, what=what)
+
+
+@pytest.mark.parametrize("K", [3072, 8192])
+@pytest.mark.parametrize("sum_rounded", [False, True])
+def test_matmul_residual_rms_norm_equals_unfused(pkg, dev, K, sum_rounded):
+    """At the prefill shapes (M = 750, N = 3072; split-K in both plans) the fused
+    call equals, bit for bit, this library's unfused sequence: the GEMM, then
+    sltx_residual_rms_norm (o_proj step) or the residual GEMM epilogue and
+    sltx_rms_norm (down_proj step and the next input norm).  Also in place
+    (residual_out == residual)."""
+    import torch
+    M, N, g = 750, 3072, 64
+    x, [(w, s, b)] = gpu_inputs(M, N, K, g, seed=K + 7, dev=dev)
+    W = pkg.Q4Weight(w, s, b, K, g)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(K)
+    res = (torch.randn(M, N, generator=gen, device=dev) * 6).half()
+    nw = torch.from_numpy(_norm_weight(N, 5)).to(dev)
+    fr, fn = pkg.matmul_q4_residual_rms_norm(x, W, res, nw, EPS, M, N, sum_rounded)
+    if sum_rounded:
+        ur = pkg.matmul_q4_residual(x, W, res, M, N)
+        un = pkg.rms_norm(ur, nw, EPS, M, N)
+    else:
+        y = pkg.matmul_q4_fast(x, w, s, b, M, K, N, g)
+        ur, un = pkg.residual_rms_norm(res, y, nw, EPS, M, N)
+    inplace = res.clone()
+    ir, inn = pkg.matmul_q4_residual_rms_norm(x, W, inplace, nw, EPS, M, N, sum_rounded,
+                                              residual_out=inplace)
+    torch.cuda.synchronize()
+    assert torch.equal(fr, ur) and torch.equal(fn, un)
+    assert ir.data_ptr() == inplace.data_ptr()
+    assert torch.equal(ir, ur) and torch.equal(inn, un)
