@@ -6,7 +6,8 @@ rows, so every row depends on its own token only):
 
 * the last token's logits within the BASELINE gate (max|d|/max|ref| <= 1e-2)
   of the numpy pipeline, at prompt lengths that take the MFMA GEMM (M > 1,
-  split-K included) and the GEMV (M = 1);
+  split-K included) and the GEMV (M = 1, for q|k|v and gate/up; the fused o
+  and down calls run the GEMM at every M);
 * row independence: the last row's logits do not depend on the other tokens;
 * a captured prefill replays with new token ids exactly as an eager run.
 """
@@ -53,8 +54,8 @@ def test_prefill_last_logits_match_numpy(pkg, dev, tmp_path, S):
 
 def test_prefill_rows_are_independent(pkg, dev, tmp_path):
     """With the attention stand-in, row S-1 sees only its own token: the
-    last logits of [a, b, ..., t] and of [t] agree (one path runs the GEMM,
-    the other the GEMV)."""
+    last logits of [a, b, ..., t] and of [t] agree (one path runs the GEMM
+    throughout, the other the GEMV for q|k|v and gate/up)."""
     src, mw, ps = _prefill(pkg, dev, tmp_path, 40)
     from swiftltx_amd.prefill import PrefillStep
     one = PrefillStep(mw, 1)
