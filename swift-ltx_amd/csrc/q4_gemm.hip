@@ -949,6 +949,7 @@ hipError_t launch_gemm_residual_rms_norm(GemmParams p, bool a_bf16, const float*
                                          hipStream_t st) {
     if (p.M <= 0 || p.N <= 0) return hipSuccess;
     if (p.N % 8 != 0 || p.N / 8 > 8 * 256 || !p.ws || !p.residual) return hipErrorInvalidValue;
+    if ((long)p.M * 256 > 0xffffffffL) return hipErrorInvalidValue;   // one 256-thread block per row
     const GemmPlan plan = plan_gemm(p, true, true);
     p.tiles_m = plan.tiles_m;
     p.tiles_n = plan.tiles_n;

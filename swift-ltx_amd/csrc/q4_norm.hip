@@ -101,6 +101,7 @@ __global__ __launch_bounds__(256) void rms_norm_vec_kernel(const uint16_t* a, co
 hipError_t launch_rms_norm(const uint16_t* a, const uint16_t* b, const float* w, float eps,
                            uint16_t* res_out, uint16_t* out, int rows, int dim, hipStream_t st) {
     if (rows <= 0 || dim <= 0) return hipSuccess;
+    if ((long)rows * 256 > 0xffffffffL) return hipErrorInvalidValue;   // one 256-thread block per row
     auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     const bool vec = dim % 8 == 0 && al16(a) && al16(out) && al16(w) && (!b || (al16(b) && al16(res_out)));
     const int vpt = (dim / 8 + 255) / 256;
