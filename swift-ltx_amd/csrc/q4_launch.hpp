@@ -56,6 +56,7 @@ struct GemmParams {
     float* ws;              // split-K partials [splits][M][N or 2N] (null: no split)
     int splits;             // filled by launch_gemm
     int split_tiles;        // k-tiles per split (even), filled by launch_gemm
+    uint32_t nib_mask;      // 0x0F0F0F0F, set by the launchers (a run-time value: see q4_gemm.hip)
 };
 
 // 4-bit embedding gather (q4_embed.hip).
