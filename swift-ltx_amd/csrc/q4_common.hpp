@@ -31,9 +31,14 @@ constexpr uint32_t kMagic1024x2 = 0x64006400u;
 __device__ __forceinline__ f16x2 as_f16x2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
 __device__ __forceinline__ uint32_t as_u32(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
 
-// v_and_or_b32: (a & mask) | magic
+// v_and_or_b32: (a & mask) | magic.  Written as one instruction: for two
+// 32-bit literal operands the compiler emits v_and_b32 + v_or_b32 (this
+// VOP3 form takes no literal, and at most one scalar operand), so both
+// constants are passed in VGPRs, where they are loop-invariant.
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t orv) {
-    return (a & mask) | orv;
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(mask), "v"(orv));
+    return r;
 }
 
 // v_dot2_f32_f16: a.x*b.x + a.y*b.y + c with fp32 accumulation.
