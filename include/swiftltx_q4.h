@@ -20,9 +20,10 @@
  *     sltx_argmax, and the probabilities and candidate list of
  *     sltx_sample_top_p[_state].  There is one per (device, stream),
  *     grown on first need to at least twice its old size; a replaced buffer
- *     is never freed (a graph captured earlier may still use it), so every
- *     buffer lives until the process exits.  A stream being captured into a
- *     HIP graph never allocates: if its workspace is missing or too small,
+ *     is not freed (a graph captured earlier may still use it): every buffer
+ *     lives until sltx_release_workspace(stream) or the process exits.  A
+ *     stream being captured into a HIP graph never allocates: if its
+ *     workspace is missing or too small,
  *     that GEMM runs unsplit (same results, lower throughput).  Capture after
  *     one eager call on the same stream to get the split kernel into a graph
  *     (with torch, pass that stream to torch.cuda.graph(..., stream=s)).
@@ -90,6 +91,17 @@ int sltx_init(void);
 
 /* Message for the last non-zero status returned on this thread. */
 const char* sltx_last_error(void);
+
+/* Frees the workspace of `stream` on the current device, and every buffer it
+ * replaced, after waiting for the work already queued on that stream.  A
+ * later call on the stream allocates a new one.  Graphs captured on the
+ * stream name the freed buffers: destroy them first (replaying one afterwards
+ * is undefined).  SLTX_OK when the stream has no workspace; SLTX_ERR_INVALID
+ * while the stream is being captured.  Callers that create and destroy
+ * streams call this before hipStreamDestroy, else each stream's buffers stay
+ * allocated until the process ends.  No counterpart in the reference (its
+ * BufferPool, Tensor.swift:47-58, lives as long as the process). */
+int sltx_release_workspace(void* stream);
 
 /* matmulQ4(_:weight:scales:biases:M:K:N:groupSize:) -> Tensor  (Ops.swift:285-305)
  * out[M,N] fp16 = x[M,K] fp16 . dequant(W)^T.  M == 1 runs the HBM-streaming
@@ -169,14 +181,16 @@ int sltx_embedding_q4(const sltx_q4_weight* table, int32_t vocab, const int32_t*
  * fp16 input; the sum of squares runs in fp32 (rms_norm, Kernels.swift:40-86). */
 
 /* rmsNorm(_:weight:eps:dim:) -> Tensor  (Ops.swift:8-27), rows x dim fp16.
- * For M > 1 (prefill); at M = 1 use the fused form below. */
+ * For M > 1 (prefill); at M = 1 use the fused form below.  out may be x
+ * itself (in place) but must not otherwise overlap it. */
 int sltx_rms_norm(const void* x, const float* weight, float eps, void* out, int32_t rows,
                   int32_t dim, void* stream);
 
 /* residualRmsNorm(_:_:weight:eps:dim:) -> (residual, normed)  (Ops.swift:256-279;
  * kernel residual_rms_norm, Kernels.swift:238-290): residual_out = half(a + b);
  * norm_out = rms_norm of it, with the sum of squares over the unrounded a + b.
- * residual_out and norm_out must not overlap. */
+ * residual_out and norm_out must not overlap; either may be a or b itself
+ * (in place, e.g. h = h + o) but must not otherwise overlap them. */
 int sltx_residual_rms_norm(const void* a, const void* b, const float* weight, float eps,
                            void* residual_out, void* norm_out, int32_t rows, int32_t dim,
                            void* stream);

@@ -42,6 +42,7 @@ EXPORTED = (
     "sltx_abi_version",
     "sltx_init",
     "sltx_last_error",
+    "sltx_release_workspace",
     "sltx_matmul_q4",
     "sltx_matmul_q4_fast",
     "sltx_matmul_q4_fast_f32",
@@ -123,6 +124,8 @@ def lib():
         L.sltx_abi_version.restype = ctypes.c_int
         L.sltx_init.restype = ctypes.c_int
         L.sltx_last_error.restype = ctypes.c_char_p
+        L.sltx_release_workspace.argtypes = [P]
+        L.sltx_release_workspace.restype = ctypes.c_int
         mm = [P, P, P, P, P, I32, I32, I32, I32, P]
         for n in ("sltx_matmul_q4", "sltx_matmul_q4_fast", "sltx_matmul_q4_fast_f32"):
             getattr(L, n).argtypes = mm
@@ -188,6 +191,12 @@ def last_error() -> str:
     return lib().sltx_last_error().decode(errors="replace")
 
 
+def release_workspace(stream=None):
+    """Frees the library's workspace for `stream` (default: the current
+    stream) after its queued work; see sltx_release_workspace."""
+    check(lib().sltx_release_workspace(_stream(stream)))
+
+
 # ------------------------------------------------------------ torch glue ---
 
 def _torch():
@@ -242,9 +251,65 @@ def _new(shape, dtype, like):
     return _torch().empty(shape, dtype=dtype, device=like.device)
 
 
+def _need(t, what, count, dtypes=None):
+    """Checks a tensor handed to the library as a raw pointer: a contiguous
+    device tensor of an accepted dtype holding at least `count` elements (the
+    library reads or writes exactly that many from its start).  A strided
+    view or a short buffer would otherwise be read or written out of bounds
+    on the device."""
+    if t is None:
+        raise ValueError(f"{what} is None")
+    if not getattr(t, "is_cuda", False):
+        raise ValueError(f"{what} must be a device tensor")
+    if dtypes is not None and t.dtype not in dtypes:
+        raise ValueError(f"{what} has dtype {t.dtype}, expected one of {dtypes}")
+    if not t.is_contiguous():
+        raise ValueError(f"{what} must be contiguous (got strides {tuple(t.stride())})")
+    if t.numel() < count:
+        raise ValueError(f"{what} holds {t.numel()} elements, {count} needed")
+    return t
+
+
+def _shape_ok(K, g):
+    """The library's shape rules; tensors are checked only for shapes it
+    accepts (it reports the others with its own status code)."""
+    return K > 0 and K % 32 == 0 and g in (32, 64, 128) and K % g == 0
+
+
+def _f16():
+    return (_torch().float16,)
+
+
+def _w_dtypes():
+    torch = _torch()
+    return tuple(d for d in (torch.int32, getattr(torch, "uint32", None)) if d is not None)
+
+
+def _need_w(w, N, K=None, what="weight"):
+    """Q4Weight operands for N rows of K (default w.K) columns."""
+    K = w.K if K is None else K
+    g = int(w.group_size)
+    if g <= 0 or K % g != 0:
+        return   # the library reports the bad shape
+    _need(w.weight, what + ".weight", N * K // 8, _w_dtypes())
+    _need(w.scales, what + ".scales", N * (K // g), _f16())
+    _need(w.biases, what + ".biases", N * (K // g), _f16())
+
+
+def _need_raw(weight, scales, biases, N, K, g):
+    if g > 0 and K % g == 0:
+        _need(weight, "weight", N * K // 8, _w_dtypes())
+        _need(scales, "scales", N * (K // g), _f16())
+        _need(biases, "biases", N * (K // g), _f16())
+
+
 def matmul_q4(x, weight, scales, biases, M, K, N, group_size, out=None, stream=None):
     """matmulQ4 (Ops.swift:285-305): [M,N] fp16 = x[M,K] fp16 . dequant(W)^T."""
     out = _new((M, N), _torch().float16, x) if out is None else out
+    if M > 0 and N > 0 and _shape_ok(K, group_size):
+        _need(x, "x", M * K, _f16())
+        _need_raw(weight, scales, biases, N, K, group_size)
+        _need(out, "out", M * N, (_torch().float16,))
     check(lib().sltx_matmul_q4(_ptr(x), _ptr(weight), _ptr(scales), _ptr(biases), _ptr(out),
                                M, K, N, group_size, _stream(stream)))
     return out
@@ -253,6 +318,10 @@ def matmul_q4(x, weight, scales, biases, M, K, N, group_size, out=None, stream=N
 def matmul_q4_fast(x, weight, scales, biases, M, K, N, group_size, out=None, stream=None):
     """matmulQ4Fast (Ops.swift:312-345): MFMA GEMM, fp16 out."""
     out = _new((M, N), _torch().float16, x) if out is None else out
+    if M > 0 and N > 0 and _shape_ok(K, group_size):
+        _need(x, "x", M * K, _f16())
+        _need_raw(weight, scales, biases, N, K, group_size)
+        _need(out, "out", M * N, (_torch().float16,))
     check(lib().sltx_matmul_q4_fast(_ptr(x), _ptr(weight), _ptr(scales), _ptr(biases), _ptr(out),
                                     M, K, N, group_size, _stream(stream)))
     return out
@@ -261,6 +330,10 @@ def matmul_q4_fast(x, weight, scales, biases, M, K, N, group_size, out=None, str
 def matmul_q4_fast_f32(x, weight, scales, biases, M, K, N, group_size, out=None, stream=None):
     """matmulQ4FastF32 (Ops.swift:348-381): MFMA GEMM, fp32 out."""
     out = _new((M, N), _torch().float32, x) if out is None else out
+    if M > 0 and N > 0 and _shape_ok(K, group_size):
+        _need(x, "x", M * K, _f16())
+        _need_raw(weight, scales, biases, N, K, group_size)
+        _need(out, "out", M * N, (_torch().float32,))
     check(lib().sltx_matmul_q4_fast_f32(_ptr(x), _ptr(weight), _ptr(scales), _ptr(biases),
                                         _ptr(out), M, K, N, group_size, _stream(stream)))
     return out
@@ -269,13 +342,22 @@ def matmul_q4_fast_f32(x, weight, scales, biases, M, K, N, group_size, out=None,
 def silu_mul(a, b, out=None, stream=None):
     """siluMul (Ops.swift:44-56): half(silu(a) * b), fp16."""
     out = _torch().empty_like(a) if out is None else out
-    check(lib().sltx_silu_mul(_ptr(a), _ptr(b), _ptr(out), a.numel(), _stream(stream)))
+    n = a.numel()
+    if n > 0:
+        _need(a, "a", n, _f16())
+        _need(b, "b", n, _f16())
+        _need(out, "out", n, _f16())
+    check(lib().sltx_silu_mul(_ptr(a), _ptr(b), _ptr(out), n, _stream(stream)))
     return out
 
 
 def linear(x, w: Q4Weight, M, K, N, fast=False, out=None, stream=None):
     """linear (Ops.swift:741-752), quantized case: fast && M>1 -> GEMM, else matmul_q4."""
     out = _new((M, N), _torch().float16, x) if out is None else out
+    if M > 0 and N > 0 and _shape_ok(K, w.group_size) and w.K == K:
+        _need(x, "x", M * K, _f16())
+        _need_w(w, N)
+        _need(out, "out", M * N, _f16())
     cw = w.c()
     check(lib().sltx_linear(_ptr(x), ctypes.byref(cw), _ptr(out), M, K, N, 1 if fast else 0,
                             _stream(stream)))
@@ -286,6 +368,11 @@ def matmul_q4_silu_mul(x, gate: Q4Weight, up: Q4Weight, M, K, N, out=None, strea
     """Fused silu(x.Wg^T) * (x.Wu^T) -> fp16 [M, N]; replaces linear(gate),
     linear(up), siluMul (LlamaModel.swift:275-277, :327-329)."""
     out = _new((M, N), _torch().float16, x) if out is None else out
+    if M > 0 and N > 0 and _shape_ok(K, gate.group_size):
+        _need(x, "x", M * K, _f16())
+        _need_w(gate, N, K, "gate")
+        _need_w(up, N, K, "up")
+        _need(out, "out", M * N, _f16())
     g, u = gate.c(), up.c()
     check(lib().sltx_matmul_q4_silu_mul(_ptr(x), ctypes.byref(g), ctypes.byref(u), _ptr(out), M,
                                         K, N, _stream(stream)))
@@ -299,6 +386,12 @@ def matmul_q4_ex(x, w: Q4Weight, M, N, out_dtype=None, bias=None, epilogue=SLTX_
     torch = _torch()
     if out is None:
         out = _new((M, N), out_dtype or torch.float32, x)
+    if M > 0 and N > 0 and _shape_ok(w.K, w.group_size):
+        _need(x, "x", M * w.K, (torch.float16, torch.bfloat16))
+        _need_w(w, N)
+        _need(out, "out", M * N, (torch.float16, torch.bfloat16, torch.float32))
+        if bias is not None:
+            _need(bias, "bias", N, (torch.float32,))
     cw = w.c()
     check(lib().sltx_matmul_q4_ex(_ptr(x), _dtype_code(x.dtype), ctypes.byref(cw), _ptr(bias),
                                   epilogue, _ptr(out), _dtype_code(out.dtype), M, N,
@@ -309,6 +402,10 @@ def matmul_q4_ex(x, w: Q4Weight, M, N, out_dtype=None, bias=None, epilogue=SLTX_
 def rms_norm(x, weight, eps, rows, dim, out=None, stream=None):
     """rmsNorm (Ops.swift:8-27): fp16 [rows, dim], fp32 weight [dim]."""
     out = _new((rows, dim), _torch().float16, x) if out is None else out
+    if rows > 0 and dim > 0:
+        _need(x, "x", rows * dim, _f16())
+        _need(weight, "weight", dim, (_torch().float32,))
+        _need(out, "out", rows * dim, _f16())
     check(lib().sltx_rms_norm(_ptr(x), _ptr(weight), eps, _ptr(out), rows, dim, _stream(stream)))
     return out
 
@@ -319,6 +416,10 @@ def residual_rms_norm(a, b, weight, eps, rows, dim, residual_out=None, norm_out=
     torch = _torch()
     residual_out = _new((rows, dim), torch.float16, a) if residual_out is None else residual_out
     norm_out = _new((rows, dim), torch.float16, a) if norm_out is None else norm_out
+    if rows > 0 and dim > 0:
+        for t, n in ((a, "a"), (b, "b"), (residual_out, "residual_out"), (norm_out, "norm_out")):
+            _need(t, n, rows * dim, _f16())
+        _need(weight, "weight", dim, (torch.float32,))
     check(lib().sltx_residual_rms_norm(_ptr(a), _ptr(b), _ptr(weight), eps, _ptr(residual_out),
                                        _ptr(norm_out), rows, dim, _stream(stream)))
     return residual_out, norm_out
@@ -328,6 +429,11 @@ def rmsnorm_matmul_q4(x, norm_weight, eps, w: Q4Weight, N, out=None, stream=None
     """rms_norm(x) . dequant(W)^T at M = 1 (input_layernorm + q|k|v,
     LlamaModel.swift:288-292) -> fp16 [1, N]."""
     out = _new((1, N), _torch().float16, x) if out is None else out
+    if N > 0 and _shape_ok(w.K, w.group_size):
+        _need(x, "x", w.K, _f16())
+        _need(norm_weight, "norm_weight", w.K, (_torch().float32,))
+        _need_w(w, N)
+        _need(out, "out", N, _f16())
     cw = w.c()
     check(lib().sltx_rmsnorm_matmul_q4(_ptr(x), _ptr(norm_weight), eps, ctypes.byref(cw),
                                        _ptr(out), N, _stream(stream)))
@@ -341,6 +447,13 @@ def residual_rmsnorm_matmul_q4_silu_mul(a, b, norm_weight, eps, gate: Q4Weight, 
     torch = _torch()
     residual_out = _new((1, gate.K), torch.float16, a) if residual_out is None else residual_out
     out = _new((1, N), torch.float16, a) if out is None else out
+    if N > 0 and _shape_ok(gate.K, gate.group_size):
+        for t, n in ((a, "a"), (b, "b"), (residual_out, "residual_out")):
+            _need(t, n, gate.K, _f16())
+        _need(norm_weight, "norm_weight", gate.K, (torch.float32,))
+        _need_w(gate, N, what="gate")
+        _need_w(up, N, what="up")
+        _need(out, "out", N, _f16())
     g, u = gate.c(), up.c()
     check(lib().sltx_residual_rmsnorm_matmul_q4_silu_mul(
         _ptr(a), _ptr(b), _ptr(norm_weight), eps, _ptr(residual_out), ctypes.byref(g),
@@ -352,6 +465,11 @@ def matmul_q4_residual(x, w: Q4Weight, residual, M, N, out=None, stream=None):
     """half(residual + half(x . dequant(W)^T)): linear + elemAdd
     (LlamaModel.swift:330-331) -> fp16 [M, N]."""
     out = _new((M, N), _torch().float16, x) if out is None else out
+    if M > 0 and N > 0 and _shape_ok(w.K, w.group_size):
+        _need(x, "x", M * w.K, _f16())
+        _need_w(w, N)
+        _need(residual, "residual", M * N, _f16())
+        _need(out, "out", M * N, _f16())
     cw = w.c()
     check(lib().sltx_matmul_q4_residual(_ptr(x), ctypes.byref(cw), _ptr(residual), _ptr(out), M,
                                         N, _stream(stream)))
@@ -369,6 +487,13 @@ def matmul_q4_residual_rms_norm(x, w: Q4Weight, residual, norm_weight, eps, M, N
     torch = _torch()
     residual_out = _new((M, N), torch.float16, x) if residual_out is None else residual_out
     norm_out = _new((M, N), torch.float16, x) if norm_out is None else norm_out
+    if M > 0 and N > 0 and _shape_ok(w.K, w.group_size):
+        _need(x, "x", M * w.K, _f16())
+        _need_w(w, N)
+        for t, n in ((residual, "residual"), (residual_out, "residual_out"),
+                     (norm_out, "norm_out")):
+            _need(t, n, M * N, _f16())
+        _need(norm_weight, "norm_weight", N, (torch.float32,))
     cw = w.c()
     check(lib().sltx_matmul_q4_residual_rms_norm(_ptr(x), ctypes.byref(cw), _ptr(residual),
                                                  _ptr(norm_weight), eps, M, N,
@@ -381,6 +506,11 @@ def matmul_q4_geglu(x, gate: Q4Weight, up: Q4Weight, M, K, N, out=None, stream=N
     """gelu_tanh(x.Wg^T) * (x.Wu^T) -> fp16 [M, N]: the T5 encoder FFN's
     gate/up (T5Encoder.swift:191-199)."""
     out = _new((M, N), _torch().float16, x) if out is None else out
+    if M > 0 and N > 0 and _shape_ok(K, gate.group_size):
+        _need(x, "x", M * K, _f16())
+        _need_w(gate, N, K, "gate")
+        _need_w(up, N, K, "up")
+        _need(out, "out", M * N, _f16())
     g, u = gate.c(), up.c()
     check(lib().sltx_matmul_q4_geglu(_ptr(x), ctypes.byref(g), ctypes.byref(u), _ptr(out), M, K,
                                      N, _stream(stream)))
@@ -392,6 +522,10 @@ def embedding_q4(table: Q4Weight, vocab, token_ids, out=None, stream=None):
     4-bit table for int32 device token ids."""
     n = int(token_ids.numel())
     out = _new((n, table.K), _torch().float16, token_ids) if out is None else out
+    if n > 0 and vocab >= 0 and _shape_ok(table.K, table.group_size):
+        _need(token_ids, "token_ids", n, (_torch().int32,))
+        _need_w(table, vocab, what="table")
+        _need(out, "out", n * table.K, _f16())
     cw = table.c()
     check(lib().sltx_embedding_q4(ctypes.byref(cw), vocab, _ptr(token_ids), n, _ptr(out),
                                   _stream(stream)))
@@ -411,6 +545,8 @@ def argmax(logits, out=None, stream=None):
     """argmax (Ops.swift:757-781) on the device: int32 [1] tensor holding the
     first index of the maximum of a contiguous fp16/fp32 vector."""
     out = _new((1,), _torch().int32, logits) if out is None else out
+    _need(logits, "logits", logits.numel())
+    _need(out, "out", 1, (_torch().int32,))
     check(lib().sltx_argmax(_ptr(logits), _logits_dtype(logits), int(logits.numel()), _ptr(out),
                             _stream(stream)))
     return out
@@ -427,6 +563,10 @@ def sample(logits, temperature=0.7, top_p=0.9, repetition_penalty=1.1, seen_toke
         u = random.random()
     out = _new((1,), _torch().int32, logits) if out is None else out
     n_seen = 0 if seen_tokens is None else int(seen_tokens.numel())
+    _need(logits, "logits", logits.numel())
+    _need(out, "out", 1, (_torch().int32,))
+    if n_seen:
+        _need(seen_tokens, "seen_tokens", n_seen, (_torch().int32,))
     check(lib().sltx_sample_top_p(_ptr(logits), _logits_dtype(logits), int(logits.numel()),
                                   temperature, top_p, repetition_penalty,
                                   _ptr(seen_tokens) if n_seen else None, n_seen, u, _ptr(out),
@@ -496,6 +636,8 @@ def sample_with_state(logits, temperature, top_p, repetition_penalty, state, out
     and advances the draw.  Capturable in a HIP graph (after one eager call
     on the same stream, which sizes the workspace)."""
     out = _new((1,), _torch().int32, logits) if out is None else out
+    _need(logits, "logits", logits.numel())
+    _need(out, "out", 1, (_torch().int32,))
     check(lib().sltx_sample_top_p_state(_ptr(logits), _logits_dtype(logits), int(logits.numel()),
                                         temperature, top_p, repetition_penalty,
                                         ctypes.byref(state.c), _ptr(out), _stream(stream)))

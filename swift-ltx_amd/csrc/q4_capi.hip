@@ -155,28 +155,58 @@ int run_gemv(const char* fn, const void* x, const sltx_q4_weight& w0, const sltx
 // current size.  A stream that is being captured into a graph never
 // allocates: if its workspace is missing or too small the GEMM runs unsplit
 // and sampling returns an error.
+// sltx_release_workspace frees one stream's buffers (current and retired).
+struct StreamWs {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    std::vector<void*> retired;
+};
 std::mutex g_ws_mu;
-std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> g_ws;
-std::vector<void*> g_ws_retired;
+std::map<std::pair<int, hipStream_t>, StreamWs> g_ws;
 
 float* stream_workspace(hipStream_t st, size_t need) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
     std::lock_guard<std::mutex> lk(g_ws_mu);
     auto& e = g_ws[{dev, st}];
-    if (e.second >= need) return static_cast<float*>(e.first);
+    if (e.bytes >= need) return static_cast<float*>(e.ptr);
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
         return nullptr;
     void* ptr = nullptr;
-    const size_t bytes = std::max(need + need / 4, 2 * e.second);
+    const size_t bytes = std::max(need + need / 4, 2 * e.bytes);
     if (hipMalloc(&ptr, bytes) != hipSuccess) {
         (void)hipGetLastError();
         return nullptr;
     }
-    if (e.first) g_ws_retired.push_back(e.first);
-    e = {ptr, bytes};
+    if (e.ptr) e.retired.push_back(e.ptr);
+    e.ptr = ptr;
+    e.bytes = bytes;
     return static_cast<float*>(ptr);
+}
+
+int release_workspace(hipStream_t st) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return hip_fail(err, "hipGetDevice");
+    StreamWs e;
+    {
+        std::lock_guard<std::mutex> lk(g_ws_mu);
+        auto it = g_ws.find({dev, st});
+        if (it == g_ws.end()) return kOk;
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+            return fail(kErrInvalid, "sltx_release_workspace: the stream is being captured");
+        e = std::move(it->second);
+        g_ws.erase(it);
+    }
+    // the stream's queued work may still use the buffers
+    err = hipStreamSynchronize(st);
+    if (err != hipSuccess) return hip_fail(err, "hipStreamSynchronize");
+    e.retired.push_back(e.ptr);
+    for (void* p : e.retired)
+        if (p && (err = hipFree(p)) != hipSuccess) return hip_fail(err, "hipFree");
+    return kOk;
 }
 
 int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w0,
@@ -276,6 +306,10 @@ extern "C" {
 int sltx_abi_version(void) { return 1; }
 
 int sltx_init(void) { return ensure_device(); }
+
+int sltx_release_workspace(void* stream) {
+    return release_workspace(static_cast<hipStream_t>(stream));
+}
 
 const char* sltx_last_error(void) { return g_last_error.c_str(); }
 
@@ -498,6 +532,11 @@ int sltx_rms_norm(const void* x, const float* weight, float eps, void* out, int3
     if (!x || !weight || !out) return fail(kErrInvalid, "%s: null pointer argument", fn);
     if (!aligned(x, 2) || !aligned(out, 2) || !aligned(weight, 4))
         return fail(kErrInvalid, "%s: misaligned pointer", fn);
+    // In place (out == x) is safe: each element is read and written by one
+    // thread of its row's block.  Any other overlap races across blocks.
+    const size_t nb = (size_t)rows * dim * 2;
+    if (out != x && overlap(out, nb, x, nb))
+        return fail(kErrInvalid, "%s: out and x overlap without being equal", fn);
     int rc = ensure_device();
     if (rc != kOk) return rc;
     return finish(launch_rms_norm(static_cast<const uint16_t*>(x), nullptr, weight, eps, nullptr,
@@ -520,6 +559,15 @@ int sltx_residual_rms_norm(const void* a, const void* b, const float* weight, fl
     const size_t nb = (size_t)rows * dim * 2;
     if (overlap(residual_out, nb, norm_out, nb))
         return fail(kErrInvalid, "%s: residual_out and norm_out overlap", fn);
+    // Each output may be an input itself (in place, e.g. h = h + o): every
+    // element is read and written by one thread of its row's block.  Any
+    // other overlap races across blocks.
+    for (const void* in : {a, b}) {
+        if (residual_out != in && overlap(residual_out, nb, in, nb))
+            return fail(kErrInvalid, "%s: residual_out overlaps an input without being equal", fn);
+        if (norm_out != in && overlap(norm_out, nb, in, nb))
+            return fail(kErrInvalid, "%s: norm_out overlaps an input without being equal", fn);
+    }
     int rc = ensure_device();
     if (rc != kOk) return rc;
     return finish(launch_rms_norm(static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b),

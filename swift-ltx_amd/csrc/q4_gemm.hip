@@ -902,8 +902,12 @@ size_t gemm_partials_workspace_bytes(const GemmParams& p) { return plan_gemm(p, 
 template <int WM, bool BF16, bool SPLIT>
 static void launch_wm(const GemmParams& p, bool silu, long grid, hipStream_t st) {
     // The fixed-count kernel needs whole 128-k super-stages and group size 64
-    // (scales and biases move as dword pairs of groups).
-    const bool gen = p.K % (2 * BK) != 0 || p.gshift != 1;
+    // (scales and biases move as dword pairs of groups, so their arrays must
+    // also be 4-byte aligned; 2-byte aligned ones take the generic kernel,
+    // which reads them as 16-bit values).
+    const uintptr_t sb_addr = reinterpret_cast<uintptr_t>(p.s0) | reinterpret_cast<uintptr_t>(p.b0) |
+                              reinterpret_cast<uintptr_t>(p.s1) | reinterpret_cast<uintptr_t>(p.b1);
+    const bool gen = p.K % (2 * BK) != 0 || p.gshift != 1 || (sb_addr & 3) != 0;
     if (silu && gen)
         hipLaunchKernelGGL((q4_gemm_kernel<WM, BF16, true, true, SPLIT>), dim3(grid), dim3(kThreads), 0, st, p);
     else if (silu)

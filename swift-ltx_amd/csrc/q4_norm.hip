@@ -32,8 +32,10 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* a, const 
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
     const float rms = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)dim + eps);
+    // r is the stored residual element (written above by this same thread),
+    // as residual_rms_norm reads it back; residual_out may be a or b itself.
     for (int i = threadIdx.x; i < dim; i += 256) {
-        const float r = b ? h2f(f2h(h2f(a[off + i]) + h2f(b[off + i]))) : h2f(a[off + i]);
+        const float r = b ? h2f(res_out[off + i]) : h2f(a[off + i]);
         out[off + i] = f2h(r * rms * w[i]);
     }
 }

@@ -318,7 +318,11 @@ int parse_header(StFile& f, const std::string& hdr) {
             return set_error(kErrInvalid,
                              "%s: tensor '%s': %llu bytes do not match its shape and dtype",
                              f.path.c_str(), kv.first.c_str(), (unsigned long long)info.nbytes);
-        f.tensors[kv.first] = info;
+        // A repeated name is ambiguous (which entry holds the data?): the
+        // file is rejected rather than keeping one of them.
+        if (!f.tensors.emplace(kv.first, info).second)
+            return set_error(kErrInvalid, "%s: duplicate tensor name '%s' in the header",
+                             f.path.c_str(), kv.first.c_str());
         f.names.push_back(kv.first);
     }
     std::sort(f.names.begin(), f.names.end());

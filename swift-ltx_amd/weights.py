@@ -217,6 +217,21 @@ class ModelWeights:
         w = torch.empty((N, K // 8), dtype=torch.int32, device=self.device)
         s = torch.empty((N, K // g), dtype=torch.float16, device=self.device)
         b = torch.empty((N, K // g), dtype=torch.float16, device=self.device)
+        # Every part must have the destination's row layout: packed I32/U32
+        # words of width K/8 and F16 scales/biases with K/g groups, and the
+        # same row count in all three tensors (else its rows would land at
+        # the wrong byte offsets with no error).
+        want = (({"I32", "U32"}, K // 8 * 4), ({"F16"}, K // g * 2), ({"F16"}, K // g * 2))
+        for parts, n in zip(infos, rows):
+            for (f, name), (dtypes, row_bytes) in zip(parts, want):
+                info = f.tensors[name]
+                if info.dtype not in dtypes:
+                    raise ValueError(f"{name}: dtype {info.dtype}, expected {sorted(dtypes)}")
+                if len(info.shape) != 2 or info.shape[0] != n:
+                    raise ValueError(f"{name}: shape {info.shape}, expected {n} rows")
+                if info.byte_count != n * row_bytes:
+                    raise ValueError(f"{name}: {info.byte_count} bytes, expected {n} rows of "
+                                     f"{row_bytes} bytes")
         r0 = 0
         for parts, n in zip(infos, rows):
             for (f, name), t in zip(parts, (w, s, b)):

@@ -171,6 +171,14 @@ def test_rms_norm_validation(pkg):
     assert L.sltx_residual_rms_norm(ALIGNED, ALIGNED, ALIGNED, 1e-5, ALIGNED, ALIGNED + 64, 1,
                                     3072, None) == -1
     assert "overlap" in pkg.last_error()
+    A, B, R, NO = ALIGNED, 2 * ALIGNED, 3 * ALIGNED, 4 * ALIGNED
+    # an output that overlaps an input without being equal to it races
+    assert L.sltx_residual_rms_norm(A, B, ALIGNED, 1e-5, A + 16, NO, 2, 3072, None) == -1
+    assert "residual_out overlaps an input" in pkg.last_error()
+    assert L.sltx_residual_rms_norm(A, B, ALIGNED, 1e-5, R, B + 6144, 2, 3072, None) == -1
+    assert "norm_out overlaps an input" in pkg.last_error()
+    assert L.sltx_rms_norm(A, ALIGNED, 1e-5, A + 6144, 2, 3072, None) == -1
+    assert "overlap" in pkg.last_error()
 
 
 def test_rmsnorm_matmul_validation(pkg):

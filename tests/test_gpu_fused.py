@@ -86,6 +86,47 @@ def test_residual_rms_norm(pkg, dev, rows, dim):
     _assert_ulp(nrm.cpu().numpy(), rnrm, what=f"residual_rms_norm {rows}x{dim}")
 
 
+@pytest.mark.parametrize("rows,dim", [(3, 100), (2, 3072), (1, 20000)])
+@pytest.mark.parametrize("alias", ["a", "b"])
+def test_residual_rms_norm_in_place(pkg, dev, rows, dim, alias):
+    """residual_out may be a or b itself (h = h + o in place).  dim % 8 != 0
+    and dim > 16384 take the scalar kernel, whose second pass reads the stored
+    residual back (recomputing it from a and b would add b twice); dim = 3072
+    takes the 16-byte kernel.  norm_out may also replace an input."""
+    import torch
+    rng = np.random.default_rng(rows * 31 + dim)
+    a = (rng.standard_normal((rows, dim)) * 4).astype(np.float16)
+    b = (rng.standard_normal((rows, dim)) * 2).astype(np.float16)
+    w = _norm_weight(dim, dim + 3)
+    rres, rnrm = o.residual_rms_norm_ref(a, b, w, EPS)
+    ta, tb = to_dev(a, dev), to_dev(b, dev)
+    tgt = ta if alias == "a" else tb
+    res, nrm = pkg.residual_rms_norm(ta, tb, to_dev(w, dev), EPS, rows, dim, residual_out=tgt)
+    torch.cuda.synchronize()
+    assert res.data_ptr() == tgt.data_ptr()
+    assert np.array_equal(res.cpu().numpy(), rres)
+    _assert_ulp(nrm.cpu().numpy(), rnrm, what=f"in-place residual_out={alias} {rows}x{dim}")
+    # norm_out in place of an input (residual_out separate)
+    ta, tb = to_dev(a, dev), to_dev(b, dev)
+    tgt = ta if alias == "a" else tb
+    res2, nrm2 = pkg.residual_rms_norm(ta, tb, to_dev(w, dev), EPS, rows, dim, norm_out=tgt)
+    torch.cuda.synchronize()
+    assert np.array_equal(res2.cpu().numpy(), rres)
+    assert torch.equal(nrm2, nrm)
+
+
+@pytest.mark.parametrize("rows,dim", [(3, 100), (2, 3072)])
+def test_rms_norm_in_place(pkg, dev, rows, dim):
+    import torch
+    rng = np.random.default_rng(rows + 5 * dim)
+    x = (rng.standard_normal((rows, dim)) * 3).astype(np.float16)
+    w = _norm_weight(dim, 11)
+    tx = to_dev(x, dev)
+    out = pkg.rms_norm(tx, to_dev(w, dev), EPS, rows, dim, out=tx)
+    torch.cuda.synchronize()
+    _assert_ulp(out.cpu().numpy(), o.rms_norm_ref(x, w, EPS), what=f"in-place rms_norm {rows}x{dim}")
+
+
 # (N, K, g): GEMV specialisations (K=3072 -> 32 lanes x 3, 2048 -> 64 x 1,
 # 8192 -> 64 x 4, 4096 -> 64 x 2), the generic kernel (K=96), all group sizes.
 RMS_SHAPES = [(5120, 3072, 64), (1000, 2048, 128), (257, 8192, 64), (64, 96, 32),

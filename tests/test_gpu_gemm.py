@@ -350,3 +350,70 @@ def test_unaligned_outputs_match_aligned(pkg, dev, kind, M, N, K):
     torch.cuda.synchronize()
     assert unaligned.data_ptr() % 16 != 0
     assert torch.equal(aligned, unaligned), kind
+
+
+@pytest.mark.parametrize("kind", ["f16", "silu", "bf16"])
+def test_scales_biases_at_2_byte_offset(pkg, dev, kind):
+    """Scales and biases 2 bytes off a 4-byte boundary (allowed: 2-byte
+    alignment) cannot move as dword pairs, so the launcher routes them to the
+    generic kernel; the values must match the aligned run and the oracle."""
+    import torch
+    M, N, K, g = 70, 320, 1024, 64
+    x, sets = gpu_inputs(M, N, K, g, seed=17, dev=dev, n_weights=2,
+                         x_dtype="bf16" if kind == "bf16" else "f16")
+
+    def shifted(t):
+        buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=dev)
+        buf[1:].copy_(t.reshape(-1))
+        v = buf[1:].view(t.shape)
+        assert v.data_ptr() % 4 == 2
+        return v
+
+    Wa = [pkg.Q4Weight(w, s, b, K, g) for w, s, b in sets]
+    Wu = [pkg.Q4Weight(w, shifted(s), shifted(b), K, g) for w, s, b in sets]
+
+    def run(W):
+        if kind == "silu":
+            return pkg.matmul_q4_silu_mul(x, W[0], W[1], M, K, N)
+        if kind == "bf16":
+            return pkg.matmul_q4_ex(x, W[0], M, N, out_dtype=torch.float32)
+        return pkg.linear(x, W[0], M, K, N, fast=True)
+
+    ya, yu = run(Wa), run(Wu)
+    torch.cuda.synchronize()
+    hs = [(host(w), host(s), host(b)) for w, s, b in sets]
+    xh = host(x)
+    if kind == "bf16":
+        ref = o.matmul_q4_f64(o.bf16_bits_to_f32(xh), *hs[0], g)
+        tol = TOL_GEMM_BF16
+    elif kind == "silu":
+        ref = o.silu_mul_f64(o.matmul_q4_f64(xh, *hs[0], g), o.matmul_q4_f64(xh, *hs[1], g))
+        tol = TOL_GEMM_F16
+    else:
+        ref = o.matmul_q4_f64(xh, *hs[0], g)
+        tol = TOL_GEMM_F16
+    assert_parity(yu.float().cpu().numpy(), ref, tol, f"2-byte-offset scales {kind}")
+    assert_parity(ya.float().cpu().numpy(), ref, tol, f"aligned scales {kind}")
+    ok, worst = o.elementwise_ok(yu.float().cpu().numpy(), ya.float().cpu().numpy().astype(np.float64),
+                                 rtol=1e-3, atol_rms=1e-3)
+    assert ok, worst
+
+
+def test_release_workspace(pkg, dev):
+    """A split-K GEMM allocates the stream's workspace; releasing it (after
+    the queued work) and calling again allocates a new one with identical
+    results.  Releasing a stream that has none is a no-op."""
+    import torch
+    M, N, K = 750, 3072, 8192
+    x, [(w, s, b)] = gpu_inputs(M, N, K, 64, seed=5, dev=dev)
+    st = torch.cuda.Stream()
+    pkg.release_workspace(st)   # none yet
+    with torch.cuda.stream(st):
+        y1 = pkg.matmul_q4_fast(x, w, s, b, M, K, N, 64, stream=st)
+    pkg.release_workspace(st)
+    with torch.cuda.stream(st):
+        y2 = pkg.matmul_q4_fast(x, w, s, b, M, K, N, 64, stream=st)
+    st.synchronize()
+    assert torch.equal(y1, y2)
+    pkg.release_workspace(st)
+    pkg.release_workspace(st)

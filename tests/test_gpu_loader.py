@@ -99,7 +99,7 @@ def _q4(rng, N, K, g=64):
     return o.pack_q4(q), s, b
 
 
-def _write_model(root):
+def _write_model(root, bf16_k_scales=False):
     rng = np.random.default_rng(8)
     c = CFG
     h, F, V = c["hidden_size"], c["intermediate_size"], c["vocab_size"]
@@ -130,8 +130,10 @@ def _write_model(root):
     half = len(names) // 2
     for k, part in enumerate((names[:half], names[half:])):
         write_st(root / f"model-0000{k + 1}-of-00002.safetensors",
-                 {n: ("BF16" if n.endswith("post_attention_layernorm.weight") else dt[t[n].dtype],
-                      t[n].shape, t[n].tobytes()) for n in part}, metadata={"format": "mlx"})
+                 {n: ("BF16" if n.endswith("post_attention_layernorm.weight")
+                      or (bf16_k_scales and n == "model.layers.0.self_attn.k_proj.scales")
+                      else dt[t[n].dtype], t[n].shape, t[n].tobytes()) for n in part},
+                 metadata={"format": "mlx"})
     (root / "config.json").write_text(json.dumps(c))
     return t
 
@@ -181,3 +183,13 @@ def test_model_weights_directory(pkg, dev, tmp_path):
     sq = np.concatenate([src[f"model.layers.0.self_attn.{x}_proj.scales"] for x in "qkv"])
     bq = np.concatenate([src[f"model.layers.0.self_attn.{x}_proj.biases"] for x in "qkv"])
     assert_parity(y.cpu().numpy(), o.matmul_q4_f64(xn, wq, sq, bq, 64), TOL_GEMV, "loaded qkv")
+
+
+def test_concat_rejects_mismatched_part(pkg, dev, tmp_path):
+    """q|k|v concatenation reads every part by byte offset into one weight, so
+    a part whose scales are not F16 (here k_proj's tagged BF16) must be
+    rejected, not copied at the wrong row width."""
+    from swiftltx_amd.weights import ModelWeights
+    _write_model(tmp_path, bf16_k_scales=True)
+    with pytest.raises(ValueError, match="k_proj.scales"):
+        ModelWeights.from_directory(str(tmp_path), device=dev)

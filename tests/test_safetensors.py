@@ -134,6 +134,12 @@ def test_corrupt_files_are_rejected(pkg, tmp_path):
     _bad(pkg, tmp_path / "dims.safetensors", "more than 8")
     write_st(tmp_path / "neg.safetensors", {"t": ("U8", (-1,), b"")})
     _bad(pkg, tmp_path / "neg.safetensors", "bad shape")
+    # a name repeated in the header is ambiguous: rejected, not deduplicated
+    hdr = (b'{"t":{"dtype":"F32","shape":[2],"data_offsets":[0,8]},'
+           b'"t":{"dtype":"F32","shape":[2],"data_offsets":[8,16]}}')
+    hdr += b" " * ((8 - len(hdr) % 8) % 8)
+    (tmp_path / "dup.safetensors").write_bytes(struct.pack("<Q", len(hdr)) + hdr + a[:4].tobytes())
+    _bad(pkg, tmp_path / "dup.safetensors", "duplicate tensor name")
 
 
 def test_read_host_capacity_and_names(pkg, tmp_path):
