@@ -277,6 +277,20 @@ int sltx_sample_top_p(const void* logits, int32_t dtype, int32_t n, float temper
                       float top_p, float repetition_penalty, const int32_t* seen,
                       int32_t n_seen, float u, int32_t* out_index, void* stream);
 
+/* sltx_sample_top_p computed in a fixed scratch area instead of the
+ * per-stream workspace: the same arguments, kernels and result, and no device
+ * memory allocated by the call.  No counterpart in the reference (its sampler
+ * runs on the CPU); it is for callers that cannot allocate: code being
+ * captured into a HIP graph on a stream that never ran the sampler eagerly,
+ * tight serving loops, and harnesses that forbid hipMalloc.  Limit:
+ * n <= 262144 logits (SLTX_ERR_INVALID beyond).  The scratch is one
+ * 3,197,184-byte device array per GPU, held until the process ends and
+ * shared by every call on that GPU: calls that overlap on one GPU (on other
+ * streams or threads) race on it and must be ordered by the caller. */
+int sltx_sample_top_p_noalloc(const void* logits, int32_t dtype, int32_t n, float temperature,
+                              float top_p, float repetition_penalty, const int32_t* seen,
+                              int32_t n_seen, float u, int32_t* out_index, void* stream);
+
 /* Sampler state kept in device memory, so that a sampled decode step takes no
  * per-token host argument and can be captured once as a HIP graph.  The
  * reference keeps the same state on the host: seenTokens = the prompt plus

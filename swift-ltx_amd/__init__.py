@@ -60,6 +60,7 @@ EXPORTED = (
     "sltx_matmul_q4_residual_rms_norm",
     "sltx_argmax",
     "sltx_sample_top_p",
+    "sltx_sample_top_p_noalloc",
     "sltx_sample_top_p_state",
     "sltx_st_open",
     "sltx_st_close",
@@ -152,12 +153,14 @@ def lib():
         L.sltx_matmul_q4_residual_rms_norm.argtypes = [P, W, P, P, F, I32, I32, I32, P, P, P]
         L.sltx_argmax.argtypes = [P, I32, I32, P, P]
         L.sltx_sample_top_p.argtypes = [P, I32, I32, F, F, F, P, I32, F, P, P]
+        L.sltx_sample_top_p_noalloc.argtypes = [P, I32, I32, F, F, F, P, I32, F, P, P]
         L.sltx_sample_top_p_state.argtypes = [P, I32, I32, F, F, F,
                                               ctypes.POINTER(CSampleState), P, P]
         for n in ("sltx_rms_norm", "sltx_residual_rms_norm", "sltx_rmsnorm_matmul_q4",
                   "sltx_residual_rmsnorm_matmul_q4_silu_mul", "sltx_matmul_q4_residual",
                   "sltx_matmul_q4_residual_rms_norm",
-                  "sltx_argmax", "sltx_sample_top_p", "sltx_sample_top_p_state"):
+                  "sltx_argmax", "sltx_sample_top_p", "sltx_sample_top_p_noalloc",
+                  "sltx_sample_top_p_state"):
             getattr(L, n).restype = ctypes.c_int
         VP = ctypes.c_void_p
         L.sltx_st_open.argtypes = [ctypes.c_char_p, ctypes.POINTER(VP)]
@@ -571,6 +574,25 @@ def sample(logits, temperature=0.7, top_p=0.9, repetition_penalty=1.1, seen_toke
                                   temperature, top_p, repetition_penalty,
                                   _ptr(seen_tokens) if n_seen else None, n_seen, u, _ptr(out),
                                   _stream(stream)))
+    return out
+
+
+def sample_noalloc(logits, temperature, top_p, repetition_penalty, seen_tokens, u, out=None,
+                   stream=None):
+    """sample(...) through sltx_sample_top_p_noalloc: the same result as
+    sample() with the library allocating nothing (a fixed per-GPU scratch,
+    at most 262144 logits; calls that overlap on one GPU race on it)."""
+    out = _new((1,), _torch().int32, logits) if out is None else out
+    n_seen = 0 if seen_tokens is None else int(seen_tokens.numel())
+    _need(logits, "logits", logits.numel())
+    _need(out, "out", 1, (_torch().int32,))
+    if n_seen:
+        _need(seen_tokens, "seen_tokens", n_seen, (_torch().int32,))
+    check(lib().sltx_sample_top_p_noalloc(_ptr(logits), _logits_dtype(logits),
+                                          int(logits.numel()), temperature, top_p,
+                                          repetition_penalty,
+                                          _ptr(seen_tokens) if n_seen else None, n_seen, u,
+                                          _ptr(out), _stream(stream)))
     return out
 
 

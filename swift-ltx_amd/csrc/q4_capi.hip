@@ -84,13 +84,13 @@ int check_out_alias(const char* fn, const void* x, size_t xbytes, const void* ou
 
 // Once-per-device readiness check (gfx950 code object present and runnable).
 std::mutex g_init_mu;
-int g_dev_state[64];  // 0 unknown, 1 ok, -1 bad
+int g_dev_state[kMaxDevices];  // 0 unknown, 1 ok, -1 bad
 
 int ensure_device() {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
-    if (dev < 0 || dev >= 64) return fail(kErrHip, "device index %d out of range", dev);
+    if (dev < 0 || dev >= kMaxDevices) return fail(kErrHip, "device index %d out of range", dev);
     std::lock_guard<std::mutex> lk(g_init_mu);
     if (g_dev_state[dev] == 1) return kOk;
     hipDeviceProp_t prop;
@@ -101,6 +101,9 @@ int ensure_device() {
         return fail(kErrUnsupported, "device %d is %s; this library is built for gfx950 only", dev,
                     prop.gcnArchName);
     }
+    // the allocation-free sampler's scratch address on this device
+    const int rc = sample_noalloc_scratch_init(dev);
+    if (rc != kOk) return rc;
     g_dev_state[dev] = 1;
     return kOk;
 }
@@ -496,6 +499,32 @@ int sltx_sample_top_p(const void* logits, int32_t dtype, int32_t n, float temper
     p.seen = seen;
     p.n_seen = n_seen;
     return run_sample(fn, p, stream);
+}
+
+int sltx_sample_top_p_noalloc(const void* logits, int32_t dtype, int32_t n, float temperature,
+                              float top_p, float repetition_penalty, const int32_t* seen,
+                              int32_t n_seen, float u, int32_t* out_index, void* stream) {
+    const char* fn = "sltx_sample_top_p_noalloc";
+    int rc = check_sample(fn, logits, dtype, n, temperature, top_p, repetition_penalty, out_index);
+    if (rc != kOk) return rc;
+    if (n > kSampleNoAllocMaxN)
+        return fail(kErrInvalid, "%s: n = %d exceeds the %d logits its fixed scratch holds", fn, n,
+                    kSampleNoAllocMaxN);
+    if (!(u >= 0.0f && u < 1.0f)) return fail(kErrInvalid, "%s: u must lie in [0, 1)", fn);
+    if (n_seen < 0) return fail(kErrInvalid, "%s: negative n_seen", fn);
+    if (n_seen > 0 && !seen) return fail(kErrInvalid, "%s: null pointer argument", fn);
+    if (seen && !aligned(seen, 4)) return fail(kErrInvalid, "%s: misaligned pointer", fn);
+    if ((rc = ensure_device()) != kOk) return rc;
+    int dev = 0;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    void* ws = sample_noalloc_scratch(dev);
+    if (!ws) return fail(kErrHip, "%s: no scratch address for device %d", fn, dev);
+    SampleParams p = sample_params(logits, dtype, n, temperature, top_p, repetition_penalty, out_index);
+    p.u = u;
+    p.seen = seen;
+    p.n_seen = n_seen;
+    return finish(launch_sample(p, ws, static_cast<hipStream_t>(stream)), fn);
 }
 
 int sltx_sample_top_p_state(const void* logits, int32_t dtype, int32_t n, float temperature,

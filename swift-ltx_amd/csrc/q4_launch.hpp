@@ -106,6 +106,15 @@ size_t argmax_workspace_bytes();
 hipError_t launch_argmax(const void* logits, int dtype, int n, int32_t* out, void* ws,
                          hipStream_t st);
 hipError_t launch_sample(SampleParams p, void* ws, hipStream_t st);
+// Largest vocabulary sltx_sample_top_p_noalloc accepts; its scratch holds
+// sample_workspace_bytes(kSampleNoAllocMaxN) bytes per GPU.
+constexpr int kSampleNoAllocMaxN = 262144;
+constexpr int kMaxDevices = 64;
+// Resolves the device address of that scratch on device `dev` (the current
+// device); called once per device by the library's init.  Status code.
+int sample_noalloc_scratch_init(int dev);
+// The address resolved for `dev`, or null before sample_noalloc_scratch_init.
+void* sample_noalloc_scratch(int dev);
 // Bytes of split-K workspace the launch of `p` would use (0: it does not split).
 size_t gemm_workspace_bytes(const GemmParams& p);
 // Launches the GEMM; splits K only if p.ws is non-null (and then needs

@@ -38,6 +38,8 @@
 //                   wave's registers and scanned; more go through levels 1-4
 //                   (in LDS when they fit), a level stopping once its bin
 //                   holds a single token
+#include <mutex>
+
 #include "q4_common.hpp"
 #include "q4_launch.hpp"
 
@@ -756,9 +758,46 @@ size_t up256(size_t b) { return (b + 255) / 256 * 256; }
 
 size_t argmax_workspace_bytes() { return 2 * kMaxBlocks * 4; }
 
-size_t sample_workspace_bytes(int n) {
-    return up256((size_t)n * 4) + 2 * up256(kMaxBlocks * 4) +
-           up256(kBins * 4) + up256(kBins * 8) + 256 + up256((size_t)n * 8);
+constexpr size_t sample_ws_bytes(size_t n) {
+    return (n * 4 + 255) / 256 * 256 + 2 * ((kMaxBlocks * 4 + 255) / 256 * 256) +
+           (kBins * 4 + 255) / 256 * 256 + (kBins * 8 + 255) / 256 * 256 + 256 +
+           (n * 8 + 255) / 256 * 256;
+}
+
+size_t sample_workspace_bytes(int n) { return sample_ws_bytes((size_t)n); }
+
+// Scratch of sltx_sample_top_p_noalloc: the sampler's workspace for up to
+// kSampleNoAllocMaxN logits (3,197,184 bytes), in a file-scope device array,
+// so that entry point allocates nothing.  Each GPU holds its own copy until
+// the process ends, and every call on that GPU shares it (the scale kernel
+// clears the counters each call; the other regions are written before they
+// are read).  In host code `scratch` only names the symbol: kernels are given
+// the device address resolved per device below.
+static_assert(sample_ws_bytes(kSampleNoAllocMaxN) == 3197184, "noalloc scratch size");
+static __device__ __align__(256) unsigned char scratch[sample_ws_bytes(kSampleNoAllocMaxN)];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+}  // namespace
+
+int sample_noalloc_scratch_init(int dev) {
+    if (dev < 0 || dev >= kMaxDevices) return set_error(kErrHip, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[dev]) return kOk;
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+        return set_error(kErrHip, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                         hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+    return kOk;
+}
+
+void* sample_noalloc_scratch(int dev) {
+    if (dev < 0 || dev >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    return g_scratch_ptr[dev];
 }
 
 hipError_t launch_argmax(const void* logits, int dtype, int n, int32_t* out, void* ws,

@@ -253,6 +253,25 @@ def test_argmax_and_sample_validation(pkg):
     assert call(seen=A + 1, ns=2) == -1 and "misaligned" in pkg.last_error()
 
 
+def test_sample_noalloc_validation(pkg):
+    """sltx_sample_top_p_noalloc rejects what sltx_sample_top_p rejects, and
+    vocabularies past its fixed scratch (262144 logits), before any HIP call."""
+    L = pkg.lib()
+    A, O = ALIGNED, 0x40000
+    fn = L.sltx_sample_top_p_noalloc
+
+    def call(n=100, dt=0, t=0.7, p=0.9, r=1.1, seen=None, ns=0, u=0.5, logits=A, out=O):
+        return fn(logits, dt, n, t, p, r, seen, ns, u, out, None)
+    assert call(n=262145) == -1 and "262144" in pkg.last_error()
+    assert call(n=(1 << 24)) == -1 and "262144" in pkg.last_error()
+    assert call(n=0) == -1 and "positive" in pkg.last_error()
+    assert call(dt=1) == -1 and "SLTX_F16" in pkg.last_error()
+    assert call(t=0.0) == -1 and "must be positive" in pkg.last_error()
+    assert call(u=1.0) == -1 and "[0, 1)" in pkg.last_error()
+    assert call(ns=3, seen=None) == -1 and "null" in pkg.last_error()
+    assert call(out=O + 2) == -1 and "misaligned" in pkg.last_error()
+
+
 def test_sample_state_validation(pkg):
     """sltx_sample_top_p_state rejects what sltx_sample_top_p rejects, plus a
     missing or malformed state, before any device work."""
