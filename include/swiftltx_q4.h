@@ -247,6 +247,54 @@ int sltx_matmul_q4_residual_rms_norm(const void* x, const sltx_q4_weight* w, con
                                      int32_t sum_rounded, void* residual_out, void* norm_out,
                                      void* stream);
 
+/* One decode layer after attention, in a single launch: the four dependent
+ * projections of transformerBlock that follow attention and the next layer's
+ * input norm + q|k|v (LlamaModel.swift:324-331, then :288-292 of the next
+ * layer), which the reference encodes as separate dispatches into one command
+ * buffer (MetalContext.swift:109-134):
+ *   o            = half(attn . Wo^T)
+ *   h1           = half(residual + o)
+ *   act          = half(silu(n . Wg^T) * (n . Wu^T)),  n = rms_norm(h1; post_norm)
+ *                  with the sum of squares over the unrounded residual + o
+ *                  (residualRmsNorm, Kernels.swift:238-290)
+ *   residual_out = half(h1 + half(act . Wd^T))
+ *   next_qkv_out = half(rms_norm(residual_out; next_norm) . Wqkv^T)  (if next_qkv)
+ * The same values as sltx_matmul_q4, sltx_residual_rmsnorm_matmul_q4_silu_mul,
+ * sltx_matmul_q4_residual and sltx_rmsnorm_matmul_q4 called in sequence, up
+ * to the order of the sums of squares.  Pass next_qkv = NULL for the last
+ * layer.  o_proj is [hidden, hidden] (K = hidden: the attention width must
+ * equal hidden), gate/up [ffn, hidden], down [hidden, ffn], next_qkv
+ * [next_qkv_rows, hidden]; one group_size for all.  Built for hidden 3072 /
+ * ffn 8192 (Llama-3.2-3B) and 2048 / 8192 (Llama-3.2-1B) with up to 8192
+ * q|k|v rows on a 256-CU MI355X; other shapes return SLTX_ERR_UNSUPPORTED
+ * (use the per-projection entry points), as do group sizes whose scales
+ * take more than 128 halves per row-iteration (group 32 at hidden 3072).
+ * attn, residual, residual_out, post_norm and next_norm 16-byte aligned;
+ * every weight's scales and biases 8-byte aligned.  The outputs may overlap attn or
+ * residual (every block has read its inputs before any output is written)
+ * but not each other.  One block per CU must be resident at once: the launch
+ * is refused when the occupancy does not allow it, and work running
+ * concurrently on other streams can delay blocks past the kernel's bounded
+ * waits (then the results are wrong and sltx_decode_layer_faults reports it).
+ * Uses a per-stream sync area (about 4 * (2 hidden + ffn) bytes, zeroed when
+ * allocated, freed by sltx_release_workspace): under graph capture call it
+ * once eagerly on that stream first.  Calls sharing a stream's sync area are
+ * ordered by the stream; a graph replayed on another stream must not overlap
+ * them.  No single reference entry point: it replaces the sequence named
+ * above. */
+int sltx_decode_layer_q4(const void* attn, const void* residual, const sltx_q4_weight* o_proj,
+                         const float* post_norm, const sltx_q4_weight* gate,
+                         const sltx_q4_weight* up, const sltx_q4_weight* down,
+                         const float* next_norm, const sltx_q4_weight* next_qkv,
+                         int32_t next_qkv_rows, int32_t hidden, int32_t ffn, float eps,
+                         void* residual_out, void* next_qkv_out, void* stream);
+
+/* Waits of sltx_decode_layer_q4 calls on `stream` that gave up since the last
+ * query (0 when every call's blocks were co-resident), read after the
+ * stream's queued work and reset.  Not under capture.  No counterpart in the
+ * reference. */
+int sltx_decode_layer_faults(void* stream, int32_t* faults);
+
 /* ---- Token selection after the lm_head (LlamaModel.swift:153,161) ----
  * Both read n logits (SLTX_F16 or SLTX_F32, device) and write one int32 token
  * id to device memory, so the next step's embedding gather can consume it

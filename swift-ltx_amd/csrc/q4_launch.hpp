@@ -99,6 +99,46 @@ struct SampleParams {
     uint2* cand;            // [n] (probability bits, id)
 };
 
+// One decode layer after attention in a single launch (q4_decode.hip): o,
+// residual + rms_norm, gate/up + SiLU, down + residual, and (wq non-null) the
+// next layer's rms_norm + q|k|v.  Weights as GemvParams; sync and the three
+// exchange vectors live in a zeroed per-stream area of
+// decode_layer_sync_bytes(H, F) bytes.
+struct DecodeLayerParams {
+    const uint16_t* attn;        // [H] o_proj input
+    const uint16_t* h;           // [H] residual stream in
+    const uint32_t* wo;          // [H, H/8]
+    const uint16_t *so, *bo;
+    const float* post_norm;      // [H]
+    const uint32_t *wg, *wu;     // [F, H/8]
+    const uint16_t *sg, *bg, *su, *bu;
+    const uint32_t* wd;          // [H, F/8]
+    const uint16_t *sd, *bd;
+    const float* next_norm;      // [H] (with wq)
+    const uint32_t* wq;          // [nq, H/8] or null (last layer)
+    const uint16_t *sq, *bq;
+    uint16_t* h_out;             // [H] residual stream out
+    uint16_t* qkv_out;           // [nq]
+    uint32_t* sync;              // [0] epoch, [1] timed-out waits
+    uint32_t *xo, *xa, *xd;      // exchanged vectors, [H], [F], [H] tagged words
+    float eps;
+    int H, F, nq;
+    int groups_h, groups_f;      // H / g, F / g
+    int gshift;                  // log2(g / 32)
+    int spin_limit;              // polls before a wait gives up
+};
+
+// Polls a wait of the single-launch decode layer makes before it gives up
+// (about 0.1 s; a grid that is not all resident, e.g. beside another
+// kernel, is the only way to reach it).
+constexpr int kDecodeSpinLimit = 1 << 16;
+size_t decode_layer_sync_bytes(int H, int F);
+// 1 if a kernel is built for these shapes on a grid of G blocks.
+int decode_layer_supported(const DecodeLayerParams& p, int G);
+// 1 if G blocks of that kernel can all be resident on `cus` CUs.
+int decode_layer_resident(const DecodeLayerParams& p, int G, int cus);
+hipError_t launch_decode_layer(const DecodeLayerParams& p, int G, hipStream_t st);
+
 hipError_t launch_gemv(const GemvParams& p, bool swiglu, hipStream_t st);
 hipError_t launch_embedding_q4(const EmbedParams& p, int n, hipStream_t st);
 size_t sample_workspace_bytes(int n);
