@@ -365,6 +365,15 @@ int sltx_sample_top_p_state(const void* logits, int32_t dtype, int32_t n, float 
                             float top_p, float repetition_penalty,
                             const sltx_sample_state* state, int32_t* out_index, void* stream);
 
+/* ---- Measurement ----
+ * The HBM read ceiling the weight streams are judged against: reads `bytes`
+ * (a multiple of 16) from src with 16-byte loads over the whole GPU and
+ * writes, per block, the XOR of the 32-bit words it read to sink (which holds
+ * sltx_hbm_read_blocks() words), so the reads cannot be elided and can be
+ * checked.  No counterpart in the reference. */
+int sltx_hbm_read_blocks(void);
+int sltx_hbm_read(const void* src, uint64_t bytes, uint32_t* sink, void* stream);
+
 /* ---- safetensors weights (SafeTensorsFile, SafeTensors.swift:41-118) ----
  * Reads the files swift-ltx's loader reads (ModelWeights.swift:40-154) into
  * caller-allocated device memory.  The header (8-byte LE length, JSON object,

@@ -25,6 +25,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(HERE, "_build")
 LIB_PATH = os.path.join(LIB_DIR, "libq4oracle.so")
+CPU_LIB_PATH = os.path.join(LIB_DIR, "libq4cpu.so")
 
 
 # --------------------------------------------------------------- packing ---
@@ -336,7 +337,62 @@ def build_c(force: bool = False) -> str:
     subprocess.run(["gcc", "-O2", "-fPIC", "-shared", "-std=c11", "-ffp-contract=off",
                     "-o", tmp, src, "-lm", "-lpthread"], check=True)
     os.replace(tmp, LIB_PATH)
+    # The CPU baselines (q4_cpu_baseline.c): vectorized for AVX2 + FMA (every
+    # x86-64-v3 host, the GPU boxes' EPYCs included), fp contraction allowed.
+    src2 = os.path.join(HERE, "q4_cpu_baseline.c")
+    tmp2 = CPU_LIB_PATH + ".tmp%d" % os.getpid()
+    subprocess.run(["gcc", "-O3", "-mavx2", "-mfma", "-fPIC", "-shared", "-std=gnu11", "-o", tmp2,
+                    src2, "-lpthread"], check=True)
+    os.replace(tmp2, CPU_LIB_PATH)
     return LIB_PATH
+
+
+_cpu_lib = None
+
+
+def cpu_lib():
+    """ctypes handle of the CPU baselines (q4_cpu_baseline.c)."""
+    global _cpu_lib
+    if _cpu_lib is None:
+        if not os.path.exists(CPU_LIB_PATH):
+            build_c(force=True)
+        L = ctypes.CDLL(CPU_LIB_PATH)
+        P, I64 = ctypes.c_void_p, ctypes.c_int64
+        L.cpu_q4_scalar.argtypes = [P, P, P, P, P, I64, I64, I64, I64]
+        L.cpu_q4_scalar.restype = None
+        L.cpu_q4_simd.argtypes = [P, P, P, P, P, I64, I64, I64, I64, ctypes.c_int]
+        L.cpu_q4_simd.restype = ctypes.c_int
+        _cpu_lib = L
+    return _cpu_lib
+
+
+def _q4_args(x, w, s, b):
+    x = np.ascontiguousarray(x, dtype=np.float16).view(np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.uint32)
+    s = np.ascontiguousarray(s, dtype=np.float16).view(np.uint16)
+    b = np.ascontiguousarray(b, dtype=np.float16).view(np.uint16)
+    return x, w, s, b
+
+
+def cpu_q4_scalar(x, w, s, b, group) -> np.ndarray:
+    """Single-thread scalar baseline (matmulCPU's loop shape,
+    LlamaModel.swift:478-493, with the 4-bit dequant inline)."""
+    x, w, s, b = _q4_args(x, w, s, b)
+    M, K = x.shape
+    y = np.empty((M, w.shape[0]), dtype=np.uint16)
+    cpu_lib().cpu_q4_scalar(_p(x), _p(w), _p(s), _p(b), _p(y), M, w.shape[0], K, group)
+    return y.view(np.float16)
+
+
+def cpu_q4_simd(x, w, s, b, group, threads=1) -> np.ndarray:
+    """8-wide fp32 (SIMD8<Float>) baseline over `threads` pthreads."""
+    x, w, s, b = _q4_args(x, w, s, b)
+    M, K = x.shape
+    y = np.empty((M, w.shape[0]), dtype=np.uint16)
+    rc = cpu_lib().cpu_q4_simd(_p(x), _p(w), _p(s), _p(b), _p(y), M, w.shape[0], K, group, threads)
+    if rc < 0:
+        raise RuntimeError("cpu_q4_simd failed")
+    return y.view(np.float16)
 
 
 _lib = None

@@ -60,6 +60,8 @@ EXPORTED = (
     "sltx_matmul_q4_residual_rms_norm",
     "sltx_decode_layer_q4",
     "sltx_decode_layer_faults",
+    "sltx_hbm_read_blocks",
+    "sltx_hbm_read",
     "sltx_argmax",
     "sltx_sample_top_p",
     "sltx_sample_top_p_noalloc",
@@ -157,6 +159,10 @@ def lib():
         L.sltx_decode_layer_q4.restype = ctypes.c_int
         L.sltx_decode_layer_faults.argtypes = [P, P]
         L.sltx_decode_layer_faults.restype = ctypes.c_int
+        L.sltx_hbm_read_blocks.argtypes = []
+        L.sltx_hbm_read_blocks.restype = ctypes.c_int
+        L.sltx_hbm_read.argtypes = [P, ctypes.c_uint64, P, P]
+        L.sltx_hbm_read.restype = ctypes.c_int
         L.sltx_argmax.argtypes = [P, I32, I32, P, P]
         L.sltx_sample_top_p.argtypes = [P, I32, I32, F, F, F, P, I32, F, P, P]
         L.sltx_sample_top_p_noalloc.argtypes = [P, I32, I32, F, F, F, P, I32, F, P, P]
@@ -553,6 +559,20 @@ def decode_layer_faults(stream=None) -> int:
     n = ctypes.c_int32(0)
     check(lib().sltx_decode_layer_faults(_stream(stream), ctypes.byref(n)))
     return int(n.value)
+
+
+def hbm_read(src, sink=None, stream=None):
+    """Streams the bytes of device tensor `src` (contiguous, size a multiple of
+    16) through the GPU's loads; returns the per-block XOR words (int32
+    device tensor of sltx_hbm_read_blocks() entries)."""
+    torch = _torch()
+    if sink is None:
+        sink = torch.empty(lib().sltx_hbm_read_blocks(), dtype=torch.int32, device=src.device)
+    _need(src, "src", src.numel())
+    _need(sink, "sink", lib().sltx_hbm_read_blocks(), (torch.int32,))
+    check(lib().sltx_hbm_read(_ptr(src), src.numel() * src.element_size(), _ptr(sink),
+                              _stream(stream)))
+    return sink
 
 
 def matmul_q4_geglu(x, gate: Q4Weight, up: Q4Weight, M, K, N, out=None, stream=None):

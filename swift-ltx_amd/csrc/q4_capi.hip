@@ -872,6 +872,20 @@ int sltx_decode_layer_q4(const void* attn, const void* residual, const sltx_q4_w
     return finish(launch_decode_layer(p, cus, st), fn);
 }
 
+int sltx_hbm_read_blocks(void) { return hbm_read_blocks(); }
+
+int sltx_hbm_read(const void* src, uint64_t bytes, uint32_t* sink, void* stream) {
+    const char* fn = "sltx_hbm_read";
+    if (bytes == 0) return kOk;
+    if (!src || !sink) return fail(kErrInvalid, "%s: null pointer argument", fn);
+    if (bytes % 16 != 0 || !aligned(src, 16) || !aligned(sink, 4))
+        return fail(kErrInvalid, "%s: bytes must be a multiple of 16, src 16-byte aligned", fn);
+    int rc = ensure_device();
+    if (rc != kOk) return rc;
+    return finish(launch_hbm_read(src, (long)(bytes / 16), sink, static_cast<hipStream_t>(stream)),
+                  fn);
+}
+
 int sltx_decode_layer_faults(void* stream, int32_t* faults) {
     const char* fn = "sltx_decode_layer_faults";
     if (!faults) return fail(kErrInvalid, "%s: null pointer argument", fn);

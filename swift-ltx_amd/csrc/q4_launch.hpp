@@ -170,6 +170,9 @@ size_t gemm_partials_workspace_bytes(const GemmParams& p);
 hipError_t launch_gemm_residual_rms_norm(GemmParams p, bool a_bf16, const float* norm_w, float eps,
                                          uint16_t* res_out, uint16_t* norm_out, bool sum_rounded,
                                          hipStream_t st);
+// HBM read ceiling (q4_probe.hip): sink holds hbm_read_blocks() words.
+int hbm_read_blocks();
+hipError_t launch_hbm_read(const void* src, long n16, uint32_t* sink, hipStream_t st);
 hipError_t launch_silu_mul(const uint16_t* a, const uint16_t* b, uint16_t* out, long count,
                            hipStream_t st);
 // Row-wise RMS norm, optionally of a + b (then the rounded sum goes to res_out).

@@ -472,3 +472,26 @@ def test_sample_ref_gpu_sums_agree_with_reference_sums():
         c = np.cumsum(info["probs"].astype(np.float64))
         assert c[pos] >= info["r"] - 1e-5 and (pos == 0 or c[pos - 1] <= info["r"] + 1e-5)
     assert agree >= 190
+
+
+@pytest.mark.parametrize("M,N,K,g", [(1, 96, 256, 64), (3, 40, 512, 32), (5, 64, 1024, 128),
+                                     (1, 257, 3072, 64)])
+def test_cpu_baselines_match_the_closed_form(oracle, M, N, K, g):
+    """The CPU baselines timed beside the GPU (q4_cpu_baseline.c: scalar in
+    matmulCPU's loop shape, 8-wide SIMD over threads) compute the reference
+    semantics: within the GEMV bound of the fp64 closed form, the SIMD result
+    independent of the thread count, and both exactly 0 for all-8 codes with
+    b = -8s."""
+    x, [(w, s, b)] = oracle.make_inputs(M, N, K, g, seed=M * 7 + N)
+    ref = oracle.matmul_q4_f64(x, w, s, b, g)
+    ys = oracle.cpu_q4_scalar(x, w, s, b, g).astype(np.float64)
+    y1 = oracle.cpu_q4_simd(x, w, s, b, g, 1)
+    y3 = oracle.cpu_q4_simd(x, w, s, b, g, 3)
+    for y, what in ((ys, "scalar"), (y1.astype(np.float64), "simd")):
+        ok, worst = oracle.elementwise_ok(y, ref, rtol=6e-4, atol_rms=1e-4)
+        assert ok, (what, worst)
+    assert np.array_equal(y1, y3)
+    w8 = np.full_like(w, 0x88888888)
+    b8 = (-8.0 * s.astype(np.float32)).astype(np.float16)
+    assert not np.any(oracle.cpu_q4_scalar(x, w8, s, b8, g).astype(np.float64))
+    assert not np.any(oracle.cpu_q4_simd(x, w8, s, b8, g, 2).astype(np.float64))
