@@ -2,31 +2,46 @@
 """Benchmark of the MI355X 4-bit dequant matmul path (one GPU).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
+    python bench.py --summarize-trace DIR     (a rocprofv3 output folder of this script)
 
 Workload: one Llama-3.2-3B decode layer's projections at
 M = 1 with MLX 4-bit group-64 weights -- q/o [3072x3072], k/v [1024x3072],
 gate+up [8192x3072] fused with SiLU x up, down [3072x8192].  A step is one
 layer: 4 launches (q/k/v rows concatenated at load time into one [5120x3072]
-weight, o, gate/up+SiLU, down), down consuming the gate/up output.  Steps rotate over --copies distinct layers (default 40,
-2.27 GB of weights) so the 256 MB MALL cannot hold the working set, and the
-timed region replays a HIP graph of one rotation (graph capture removes the
-host launch cost, as a decode loop would).
+weight, o, gate/up+SiLU, down), down consuming the gate/up output.  Step i
+uses layer copy i mod --copies (default 40 copies, 2.27 GB of weights), so the
+256 MB MALL cannot hold the working set.
 
-value = algorithmic bytes of all K steps / wall time of the K steps
-        (GB/s; bytes = N*K/2 + 4*N*K/64 + 2*K + 2*N per weight set).
-roofline = the dominant kernel (fused gate/up GEMV, 28.33 MB per launch):
-        bytes / its average duration, timed with HIP events inside the timed
-        region, against the 8 TB/s HBM peak.
-extra.gemm = the M > 1 MFMA GEMM legs in TFLOP/s
-        against the 2.5 PFLOP/s dense fp16/bf16 peak.
-cpu_baseline = the C restatement in oracle/ (the "port" CPU baseline, same
-        dequant-matmul, fp32 accumulate) timed on this host's cores on a bounded
-        sample of decode layers.
+value      = algorithmic bytes of exactly K steps / wall time of those K
+             steps: W warm-up steps and then K timed steps, each a HIP graph
+             of that many steps (graph replay removes the host launch cost, as
+             a decode loop would), bracketed by torch.cuda.synchronize().
+stats      = the same layer over >= 50 replays (and >= 200 ms) of a graph of
+             one rotation over the copies, an event after each replay:
+             median and quartiles of the time per step.
+roofline   = the dominant kernel (fused gate/up GEMV, 28.33 MB per launch):
+             a graph of its 40 rotated launches alone, >= 50 replays with an
+             event after each; avg_us = the median over replays of the time
+             per launch.  `--summarize-trace` computes the same statistic from
+             a kernel trace (the median over replays of the replay's mean
+             kernel duration).  measured_ceiling: a read-only stream
+             (sltx_hbm_read) and a device copy, same replay method.
+extra      = the other BASELINE configs and the paths around the GEMV, each
+             by the same replay method: config 1 (q_proj GEMV over >= 2 GB of
+             rotated copies), config 4a (lm_head GEMV over 10 rotated copies,
+             2.2 GB), the fused-norm and single-launch decode layers, the
+             decode token (greedy / sampled), the 750-token prefill, token
+             selection, small M (2..128) and the M > 1 MFMA GEMMs (configs 3,
+             4b, 5) against the 2.5 PFLOP/s dense fp16/bf16 peak.
+cpu_baseline = C restatements of the same dequant matmul (Swift, the
+             reference's host language, is not installed): single-thread
+             scalar and all-cores 8-wide SIMD, median of 5 runs per config.
 """
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -38,9 +53,13 @@ METRIC = "4-bit GEMV HBM GB/s + GEMM TFLOP/s (% roofline) at Llama-3.2-3B shapes
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0  # dense fp16 / bf16
 G = 64
+MIN_REPLAYS = 50
+MIN_MS = 200.0
 
 
 def gemv_bytes(N, K, nsets=1, M=1, g=G):
+    """Algorithmic bytes of a 4-bit matmul: packed codes, fp16 scales and
+    biases of each weight set, fp16 x [M, K] and y [M, N]."""
     return nsets * (N * K // 2 + 4 * N * (K // g)) + 2 * M * K + 2 * M * N
 
 
@@ -51,6 +70,7 @@ DECODE = [("qkv_proj", 5120, 3072, 1), ("o_proj", 3072, 3072, 1),
           ("gate_up_proj", 8192, 3072, 2), ("down_proj", 3072, 8192, 1)]
 LAYER_BYTES = sum(gemv_bytes(N, K, n) for _, N, K, n in DECODE)  # 56,696,832
 DOMINANT = "gate_up_proj"
+DOMINANT_KERNEL = "q4_gemv_kernel<32, 3, true, false, 0>"
 DOMINANT_BYTES = gemv_bytes(8192, 3072, 2)  # 28,334,080
 
 
@@ -60,18 +80,79 @@ def parse():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=80)
     ap.add_argument("--copies", type=int, default=40)
-    ap.add_argument("--no-gemm", action="store_true", help="skip the M>1 GEMM legs")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the M>1 GEMM and small-M legs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--diag", action="store_true", help="print timing-method diagnostics")
     ap.add_argument("--traffic", action="store_true",
                     help="only: 24 launches of the dominant kernel over 12 weight copies, then a "
                          "256 MiB torch copy (the calibration kernel), for rocprofv3 --pmc runs")
     ap.add_argument("--gemm-pmc", action="store_true",
                     help="only: 10 launches each of the M=750 prefill gate/up (SiLU) and down "
                          "GEMMs, for rocprofv3 --pmc MFMA-utilisation runs")
+    ap.add_argument("--summarize-trace", metavar="DIR",
+                    help="print a markdown summary of a rocprofv3 --kernel-trace output folder "
+                         "(rocpd .db or kernel_trace.csv) of this script; no GPU needed")
     return ap.parse_args()
 
+
+# --------------------------------------------------------------- timing ---
+
+def replay_stats(torch, replay, units, min_reps=MIN_REPLAYS, min_ms=MIN_MS, max_reps=20000):
+    """Times `replay` (enqueues one graph replay, or one eager sequence, on
+    the current stream): one untimed call, then at least min_reps calls and
+    at least min_ms of GPU time, an event recorded on the same stream after
+    each.  Returns us per unit (units = launches or steps per call): median,
+    25th / 75th percentiles, and the count."""
+    import numpy as np
+    replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    replay()
+    e1.record()
+    torch.cuda.synchronize()
+    one = max(e0.elapsed_time(e1), 1e-3)
+    reps = int(min(max_reps, max(min_reps, math.ceil(min_ms / one))))
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    evs[0].record()
+    for i in range(reps):
+        replay()
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    per = np.array([evs[i].elapsed_time(evs[i + 1]) for i in range(reps)]) * 1e3 / units
+    q25, q50, q75 = np.percentile(per, [25, 50, 75])
+    return {"median_us": round(float(q50), 3), "p25_us": round(float(q25), 3),
+            "p75_us": round(float(q75), 3), "replays": reps, "units_per_replay": units,
+            "timed_ms": round(float(per.sum() * units / 1e3), 1)}
+
+
+def capture(torch, fn, stream, warm=None):
+    """A HIP graph of fn() captured on `stream`, after warm() (default fn)
+    has run there eagerly once: the library sizes per-stream workspaces on
+    first use and never allocates while a stream is being captured."""
+    with torch.cuda.stream(stream):
+        (warm or fn)()
+    stream.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def rate(st, nbytes=None, flops=None):
+    """Adds GB/s (HBM fraction) or TFLOP/s (MFMA fraction) of the median."""
+    us = st["median_us"]
+    if nbytes:
+        gbs = nbytes / (us * 1e-6) / 1e9
+        st.update({"gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                   "bytes": nbytes})
+    if flops:
+        tf = flops / (us * 1e-6) / 1e12
+        st.update({"tflops": round(tf, 1), "frac_mfma": round(tf / MFMA_PEAK_TFLOPS, 4)})
+    return st
+
+
+# ----------------------------------------------------------------- data ---
 
 def rand_q4(torch, N, K, gen, dev):
     w = torch.randint(-2**31, 2**31 - 1, (N, K // 8), generator=gen, device=dev,
@@ -81,20 +162,35 @@ def rand_q4(torch, N, K, gen, dev):
     return w, s, b
 
 
+def q4(pkg, torch, N, K, gen, dev):
+    return pkg.Q4Weight(*rand_q4(torch, N, K, gen, dev), K, G)
+
+
 class Layer:
     def __init__(self, pkg, torch, gen, dev):
         self.w = {}
         for name, N, K, n in DECODE:
-            sets = [pkg.Q4Weight(*rand_q4(torch, N, K, gen, dev), K, G) for _ in range(n)]
-            self.w[name] = sets
+            self.w[name] = [q4(pkg, torch, N, K, gen, dev) for _ in range(n)]
 
+
+def _wsb(q):
+    return q.weight, q.scales, q.biases
+
+
+# ----------------------------------------------------------------- main ---
 
 def main():
     args = parse()
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace, args.copies))
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(no sharding or collectives); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 1 or args.warmup < 0 or args.copies < 1:
+        print("--steps must be >= 1, --warmup >= 0, --copies >= 1", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -113,14 +209,16 @@ def main():
         gemm_pmc_run(pkg, torch, gen, dev)
         return
 
-    layers = [Layer(pkg, torch, gen, dev) for _ in range(args.copies)]
+    C = args.copies
+    layers = [Layer(pkg, torch, gen, dev) for _ in range(C)]
     x = torch.randn(1, 3072, generator=gen, device=dev).half()
     attn = torch.randn(1, 3072, generator=gen, device=dev).half()
     x2 = torch.randn(1, 3072, generator=gen, device=dev).half()
     outs = {name: torch.empty(1, N, device=dev, dtype=torch.float16) for name, N, _, _ in DECODE}
+    cap = torch.cuda.Stream()
 
-    def step(L):
-        w = L.w
+    def step(i):
+        w = layers[i % C].w
         pkg.matmul_q4(x, *_wsb(w["qkv_proj"][0]), 1, 3072, 5120, G, out=outs["qkv_proj"])
         pkg.matmul_q4(attn, *_wsb(w["o_proj"][0]), 1, 3072, 3072, G, out=outs["o_proj"])
         pkg.matmul_q4_silu_mul(x2, w["gate_up_proj"][0], w["gate_up_proj"][1], 1, 3072, 8192,
@@ -128,83 +226,75 @@ def main():
         pkg.matmul_q4(outs["gate_up_proj"], *_wsb(w["down_proj"][0]), 1, 8192, 3072, G,
                       out=outs["down_proj"])
 
-    # eager warm-up (initialises the library's per-device state before capture)
-    for L in layers:
-        step(L)
+    # The library's per-device state is set up by a call that is not a step
+    # (a 16-byte read), so that no step runs outside the warm-up and the timed
+    # region.  Steps 0..W-1 are the warm-up graph, W..W+K-1 the timed graph.
+    pkg.hbm_read(torch.zeros(4, device=dev, dtype=torch.int32))
     torch.cuda.synchronize()
 
-    # one rotation over all copies, captured as a HIP graph
-    nrot = args.copies
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for L in layers:
-            step(L)
-    torch.cuda.synchronize()
+    def graph_of(first, n):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap):
+            for i in range(first, first + n):
+                step(i)
+        return g
 
-    reps_w = max(1, args.warmup // nrot)
-    reps = max(1, (args.steps + nrot - 1) // nrot)
-    steps = reps * nrot
-    for _ in range(reps_w):
-        graph.replay()
+    g_warm = graph_of(0, args.warmup) if args.warmup > 0 else None
+    g_timed = graph_of(args.warmup, args.steps)
     torch.cuda.synchronize()
-
-    # timed region: K steps as graph replays, bracketed by synchronize
+    if g_warm is not None:
+        g_warm.replay()
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(reps):
-        graph.replay()
+    g_timed.replay()
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    wall = t1 - t0
+    wall = time.perf_counter() - t0
+    value = args.steps * LAYER_BYTES / wall / 1e9
+    del g_warm, g_timed
 
-    # dominant kernel: HIP cannot report elapsed time between event nodes
-    # captured inside a graph, so the gate/up launches of the same rotation
-    # are captured alone and their replays bracketed by events on the stream
-    # they run on; duration = elapsed / launches (inter-launch gaps included)
-    g2 = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g2):
-        for L in layers:
-            w = L.w["gate_up_proj"]
-            pkg.matmul_q4_silu_mul(x2, w[0], w[1], 1, 3072, 8192, out=outs["gate_up_proj"])
-    g2.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    r2 = max(1, reps // 2)
-    e0.record()
-    for _ in range(r2):
-        g2.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    dom_ms = [e0.elapsed_time(e1) / (r2 * nrot)]
-    timing = (f"HIP events around {r2} replays of a graph of the {nrot} rotated gate/up "
-              "launches")
+    # the same layer, >= 50 replays of one rotation: median and quartiles
+    g_rot = graph_of(0, C)
+    layer_st = rate(replay_stats(torch, g_rot.replay, C), nbytes=LAYER_BYTES)
+    del g_rot
 
-    dom_us = 1e3 * sum(dom_ms) / len(dom_ms)
+    # dominant kernel: its C rotated launches alone
+    def gate_up(i):
+        w = layers[i % C].w["gate_up_proj"]
+        pkg.matmul_q4_silu_mul(x2, w[0], w[1], 1, 3072, 8192, out=outs["gate_up_proj"])
+
+    g_dom = capture(torch, lambda: [gate_up(i) for i in range(C)], cap, warm=lambda: gate_up(0))
+    dom = replay_stats(torch, g_dom.replay, C)
+    del g_dom
+    dom_us = dom["median_us"]
     achieved = DOMINANT_BYTES / (dom_us * 1e-6) / 1e9
-    value = steps * LAYER_BYTES / wall / 1e9
 
-    diag = {}
-    if args.diag:
-        diag = timing_diagnostics(pkg, torch, layers, x2, outs, reps)
-
-    copy_gbs = stream_copy_ceiling(torch, dev)
-    fused = fused_layer_leg(pkg, torch, gen, dev, layers, reps)
+    ceilings = hbm_ceilings(pkg, torch, dev, cap)
+    legs = {}
+    legs["config1_q_proj_gemv_m1"] = config1_leg(pkg, torch, gen, dev, cap)
+    legs["lm_head_gemv_m1_cold"] = lm_head_cold_leg(pkg, torch, gen, dev, cap)
+    legs["decode_layer_fused_norms"] = fused_layer_leg(pkg, torch, gen, dev, layers, cap)
+    legs["decode_layer_single_launch"] = single_launch_layer_leg(pkg, torch, gen, dev, layers,
+                                                                 cap)
     model = synthetic_llama(pkg, torch, gen, dev, layers)
-    decode = decode_token_leg(pkg, torch, gen, dev, model)
-    prefill = prefill_leg(pkg, torch, gen, dev, model)
+    legs["decode_token_greedy"] = decode_token_leg(pkg, torch, gen, dev, model)
+    legs["prefill_750"] = prefill_leg(pkg, torch, gen, dev, model)
     del model
-    select = token_select_leg(pkg, torch, gen, dev)
-
-    gemm = {} if args.no_gemm else gemm_legs(pkg, torch, gen, dev)
-    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    legs["token_select"] = token_select_leg(pkg, torch, gen, dev)
+    del layers, outs
+    torch.cuda.empty_cache()
+    if not args.no_gemm:
+        legs["gemm"] = gemm_legs(pkg, torch, gen, dev, cap)
+        legs["small_m"] = small_m_legs(pkg, torch, gen, dev, cap)
+    cpu = None if args.no_cpu else cpu_baseline()
 
     line = {
         "metric": METRIC,
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": steps,
-        "warmup": reps_w * nrot,
-        "ms_per_step": round(1e3 * wall / steps, 5),
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 * wall / args.steps, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -213,32 +303,98 @@ def main():
                 "scales |N(0,0.02)| fp16, biases -8*scale)",
         "config": {"workload": "Llama-3.2-3B decode layer projections, M=1, MLX 4-bit g64 "
                                "(q,k,v rows concatenated at load, o, gate+up fused SiLU*up, "
-                               f"down); {args.copies} distinct layer copies rotated",
+                               f"down); {C} distinct layer copies rotated",
                    "bytes_per_step": LAYER_BYTES, "launches_per_step": len(DECODE),
-                   "graph": "one rotation captured as a HIP graph"},
+                   "timed": f"one HIP graph of exactly {args.steps} steps after one of "
+                            f"{args.warmup} warm-up steps, wall clock between synchronizes"},
+        "stats": {**layer_st, "ms_per_step_median": round(layer_st["median_us"] / 1e3, 5),
+                  "what": f"per step, over replays of a graph of one {C}-copy rotation"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profiles(),
-                     "kernel": "q4_gemv_kernel<32,3,true,false,0> (gate/up fused SiLU*up)",
-                     "avg_us": round(dom_us, 3), "bytes_per_launch": DOMINANT_BYTES,
-                     "timing": timing,
-                     "measured_ceiling": {"gbs": copy_gbs,
-                                          "what": "1 GiB device copy (torch copy_) in a graph, "
-                                                  "bytes read + written per second",
-                                          "frac": round(achieved / copy_gbs, 4)}},
+                     "kernel": f"{DOMINANT_KERNEL} (gate/up fused SiLU*up)",
+                     "avg_us": dom_us, "p25_us": dom["p25_us"], "p75_us": dom["p75_us"],
+                     "replays": dom["replays"], "bytes_per_launch": DOMINANT_BYTES,
+                     "timing": f"median over {dom['replays']} replays of a graph of the {C} "
+                               "rotated gate/up launches of the time per launch (an event "
+                               "after each replay, on the stream the graph runs on)",
+                     "measured_ceiling": {**ceilings,
+                                          "frac_of_read": round(achieved / ceilings["read_gbs"],
+                                                                4)}},
         "cpu_baseline": cpu,
-        "extra": {"decode_layer_fused_norms": fused, "decode_token_greedy": decode,
-                  "prefill_750": prefill, "token_select": select, "gemm": gemm,
-                  **({"timing_diag": diag} if diag else {})},
+        "extra": legs,
     }
     print(json.dumps(line))
 
 
-def fused_layer_leg(pkg, torch, gen, dev, layers, reps):
+# ------------------------------------------------------------ ceilings ---
+
+def hbm_ceilings(pkg, torch, dev, cap, read_gib=4, copy_gib=1):
+    """Measured HBM ceilings: a read-only stream of read_gib GiB
+    (sltx_hbm_read: 16-byte nontemporal loads over the whole GPU, XOR-reduced)
+    and a device copy of copy_gib GiB (torch copy_, bytes read + written)."""
+    src = torch.empty(read_gib * 2 ** 30 // 4, device=dev, dtype=torch.int32)
+    src.random_()
+    sink = torch.empty(pkg.lib().sltx_hbm_read_blocks(), device=dev, dtype=torch.int32)
+    g = capture(torch, lambda: pkg.hbm_read(src, sink), cap)
+    rd = rate(replay_stats(torch, g.replay, 1), nbytes=src.numel() * 4)
+    del g, src
+    n = copy_gib * 2 ** 30 // 2
+    a = torch.empty(n, device=dev, dtype=torch.float16).normal_()
+    b = torch.empty_like(a)
+    g = capture(torch, lambda: b.copy_(a), cap)
+    cp = rate(replay_stats(torch, g.replay, 1), nbytes=2 * n * 2)
+    del g, a, b
+    torch.cuda.empty_cache()
+    return {"read_gbs": rd["gbs"], "read_frac_of_peak": rd["frac_hbm"],
+            "read_what": f"sltx_hbm_read of {read_gib} GiB, median of {rd['replays']} replays",
+            "copy_gbs": cp["gbs"],
+            "copy_what": f"{copy_gib} GiB device copy (read + written), median of "
+                         f"{cp['replays']} replays"}
+
+
+# --------------------------------------------------------- config legs ---
+
+def config1_leg(pkg, torch, gen, dev, cap, copies=400):
+    """one q_proj GEMV [3072 x 3072], M = 1, rotated over
+    `copies` weight copies (400 x 5.31 MB = 2.12 GB)."""
+    ws = [q4(pkg, torch, 3072, 3072, gen, dev) for _ in range(copies)]
+    xx = torch.randn(1, 3072, generator=gen, device=dev).half()
+    y = torch.empty(1, 3072, device=dev, dtype=torch.float16)
+    run = lambda w: pkg.matmul_q4(xx, *_wsb(w), 1, 3072, 3072, G, out=y)
+    g = capture(torch, lambda: [run(w) for w in ws], cap, warm=lambda: run(ws[0]))
+    st = rate(replay_stats(torch, g.replay, copies), nbytes=gemv_bytes(3072, 3072))
+    del g, ws
+    torch.cuda.empty_cache()
+    st["copies"] = copies
+    st["working_set_gb"] = round(copies * gemv_bytes(3072, 3072) / 1e9, 2)
+    return st
+
+
+def lm_head_cold_leg(pkg, torch, gen, dev, cap, copies=10):
+    """BASELINE config 4a: the tied lm_head GEMV [128256 x 3072], M = 1,
+    rotated over `copies` weight copies (10 x 222.6 MB = 2.23 GB, beyond the
+    256 MB MALL)."""
+    V = 128256
+    ws = [q4(pkg, torch, V, 3072, gen, dev) for _ in range(copies)]
+    xx = torch.randn(1, 3072, generator=gen, device=dev).half()
+    y = torch.empty(1, V, device=dev, dtype=torch.float16)
+    run = lambda w: pkg.matmul_q4(xx, *_wsb(w), 1, 3072, V, G, out=y)
+    g = capture(torch, lambda: [run(w) for w in ws], cap, warm=lambda: run(ws[0]))
+    st = rate(replay_stats(torch, g.replay, copies), nbytes=gemv_bytes(V, 3072))
+    del g, ws
+    torch.cuda.empty_cache()
+    st["copies"] = copies
+    st["working_set_gb"] = round(copies * gemv_bytes(V, 3072) / 1e9, 2)
+    return st
+
+
+def fused_layer_leg(pkg, torch, gen, dev, layers, cap):
     """The same decode layer with the operators around the projections fused
     in (LlamaModel.swift:288-331): rms_norm -> q|k|v, o, residual add +
     rms_norm -> gate/up + SiLU x up, down + residual add.  Still 4 launches;
-    the norm weights (fp32) and the residual vectors add a few KB per layer."""
+    the norm weights (fp32) and the residual vectors add a few KB per layer.
+    Rotated over the layer copies."""
     K, F = 3072, 8192
     n1 = (1.0 + 0.1 * torch.randn(K, generator=gen, device=dev)).float()
     n2 = (1.0 + 0.1 * torch.randn(K, generator=gen, device=dev)).float()
@@ -259,26 +415,47 @@ def fused_layer_leg(pkg, torch, gen, dev, layers, reps):
                                                 out=act)
         pkg.matmul_q4_residual(act, w["down_proj"][0], res, 1, K, out=out)
 
-    for L in layers:
-        step(L)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for L in layers:
-            step(L)
-    g.replay()
-    torch.cuda.synchronize()
-    r = max(1, reps)
-    t0 = time.perf_counter()
-    for _ in range(r):
-        g.replay()
-    torch.cuda.synchronize()
-    us = 1e6 * (time.perf_counter() - t0) / (r * len(layers))
+    g = capture(torch, lambda: [step(L) for L in layers], cap, warm=lambda: step(layers[0]))
     nbytes = LAYER_BYTES + 2 * K * 4 + 5 * 2 * K
-    return {"us_per_layer": round(us, 3), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
-            "bytes_per_layer": nbytes, "launches_per_layer": 4,
-            "note": "rms_norm, residual add + rms_norm and the final residual add run inside "
-                    "the projections' kernels"}
+    st = rate(replay_stats(torch, g.replay, len(layers)), nbytes=nbytes)
+    del g
+    st.update({"launches_per_layer": 4,
+               "note": "rms_norm, residual add + rms_norm and the final residual add run inside "
+                       "the projections' kernels"})
+    return st
+
+
+def single_launch_layer_leg(pkg, torch, gen, dev, layers, cap):
+    """The same fused layer as one launch (sltx_decode_layer_q4): o_proj,
+    residual + rms_norm, gate/up + SiLU x up, down + residual, then the next
+    layer's rms_norm + q|k|v (layer i's o/gate/up/down with layer i+1's q|k|v:
+    the same weights per layer as the 4-launch form).  Rotated over the copies."""
+    K = 3072
+    n1 = (1.0 + 0.1 * torch.randn(K, generator=gen, device=dev)).float()
+    n2 = (1.0 + 0.1 * torch.randn(K, generator=gen, device=dev)).float()
+    h = (0.1 * torch.randn(1, K, generator=gen, device=dev)).half()
+    attn = (0.1 * torch.randn(1, K, generator=gen, device=dev)).half()
+    res = torch.empty(1, K, device=dev, dtype=torch.float16)
+    qkv = torch.empty(1, 5120, device=dev, dtype=torch.float16)
+    n = len(layers)
+
+    def call(i):
+        w, wn = layers[i].w, layers[(i + 1) % n].w
+        pkg.decode_layer(attn, h, w["o_proj"][0], n2, w["gate_up_proj"][0],
+                         w["gate_up_proj"][1], w["down_proj"][0], 1e-5, next_norm=n1,
+                         next_qkv=wn["qkv_proj"][0], residual_out=res, next_qkv_out=qkv,
+                         stream=cap)
+
+    g = capture(torch, lambda: [call(i) for i in range(n)], cap, warm=lambda: call(0))
+    nbytes = LAYER_BYTES + 2 * K * 4 + 5 * 2 * K
+    st = rate(replay_stats(torch, g.replay, n), nbytes=nbytes)
+    del g
+    faults = pkg.decode_layer_faults(cap)
+    st.update({"launches_per_layer": 1, "bounded_wait_faults": faults,
+               "note": "phases hand over through tagged words in device memory; slower than the "
+                       "4-launch form on this GPU (the hand-off under full HBM load costs more "
+                       "than a launch)"})
+    return st
 
 
 def synthetic_llama(pkg, torch, gen, dev, layers, L=28):
@@ -294,7 +471,7 @@ def synthetic_llama(pkg, torch, gen, dev, layers, L=28):
     K, V = 3072, 128256
     norm = lambda: (0.05 * (1.0 + 0.1 * torch.randn(K, generator=gen, device=dev))).float()
     fnorm = lambda: (1.0 + 0.1 * torch.randn(K, generator=gen, device=dev)).float()
-    embed = pkg.Q4Weight(*rand_q4(torch, V, K, gen, dev), K, G)
+    embed = q4(pkg, torch, V, K, gen, dev)
     lws = []
     for lay in layers[:L]:
         w = lay.w
@@ -304,12 +481,11 @@ def synthetic_llama(pkg, torch, gen, dev, layers, L=28):
                                 post_norm_weight=norm(), qkv_proj=w["qkv_proj"][0]))
     cfg = SimpleNamespace(hidden_size=K, intermediate_size=8192, num_attention_heads=24,
                           num_key_value_heads=8, head_dim=128, vocab_size=V, rms_norm_eps=1e-5)
-    mw = SimpleNamespace(config=cfg, embed_tokens=embed, lm_head=embed, norm_weight=fnorm(),
-                         layers=lws)
-    return mw
+    return SimpleNamespace(config=cfg, embed_tokens=embed, lm_head=embed, norm_weight=fnorm(),
+                           layers=lws)
 
 
-def decode_token_leg(pkg, torch, gen, dev, mw, reps=20):
+def decode_token_leg(pkg, torch, gen, dev, mw):
     """A Llama-3.2-3B decode step's matmul path (swiftltx_amd.decode), greedy
     and sampled: 4-bit embedding gather, 28 layers (RMSNorm + q|k|v, o,
     residual + RMSNorm + gate/up SiLU, down + residual), final RMSNorm + tied
@@ -322,32 +498,21 @@ def decode_token_leg(pkg, torch, gen, dev, mw, reps=20):
     s = torch.cuda.Stream()
     ds = DecodeStep(mw, stream=s)
     ds.capture()
-    ds.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        ds.replay()
-    torch.cuda.synchronize()
-    us = 1e6 * (time.perf_counter() - t0) / reps
+    st = replay_stats(torch, ds.replay, 1)
     # the same step sampling (temperature 0.7, top-p 0.9, penalty 1.1) from a
     # SamplerState: 64 prompt ids, the history and the draws on the device
-    state = pkg.SamplerState(4096, draws=4096, generator=gen, device=dev,
+    state = pkg.SamplerState(8192, draws=8192, generator=gen, device=dev,
                              history=torch.randint(0, V, (64,), generator=gen,
                                                    device=dev).tolist())
     ds2 = DecodeStep(mw, stream=s)
     ds2.capture(temperature=0.7, top_p=0.9, repetition_penalty=1.1, state=state)
-    ds2.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        ds2.replay()
-    torch.cuda.synchronize()
-    us_s = 1e6 * (time.perf_counter() - t0) / reps
-    nbytes = (L * (LAYER_BYTES + 2 * K * 4) + gemv_bytes(V, K) + K * 4 + K // 2 + 4 * K // G + 2 * K)
-    return {"us_per_token": round(us, 1), "tokens_per_s": round(1e6 / us, 1),
-            "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes_per_token": nbytes,
+    st2 = replay_stats(torch, ds2.replay, 1, max_reps=4000)
+    nbytes = (L * (LAYER_BYTES + 2 * K * 4) + gemv_bytes(V, K) + K * 4 + K // 2 + 4 * K // G
+              + 2 * K)
+    us, us_s = st["median_us"], st2["median_us"]
+    return {**rate(st, nbytes=nbytes), "tokens_per_s": round(1e6 / us, 1),
             "launches_per_token": 1 + 4 * L + 1 + 2, "layers": L,
-            "sampled": {"us_per_token": round(us_s, 1), "tokens_per_s": round(1e6 / us_s, 1),
+            "sampled": {**st2, "tokens_per_s": round(1e6 / us_s, 1),
                         "launches_per_token": 1 + 4 * L + 1 + 4,
                         "sampler": "temperature 0.7, top-p 0.9, repetition penalty 1.1, "
                                    "history and draws in device memory (SamplerState)"},
@@ -355,7 +520,7 @@ def decode_token_leg(pkg, torch, gen, dev, mw, reps=20):
                     "the q rows"}
 
 
-def prefill_leg(pkg, torch, gen, dev, mw, S=750, reps=5):
+def prefill_leg(pkg, torch, gen, dev, mw, S=750):
     """A Llama-3.2-3B prefill of S = 750 prompt tokens (swiftltx_amd.prefill;
     LlamaModel.swift:168-203): 4-bit embedding gather of S ids, 28 layers of
     q|k|v GEMM, o GEMM + residual + rms_norm (one call), gate/up GEMM with the
@@ -376,61 +541,144 @@ def prefill_leg(pkg, torch, gen, dev, mw, S=750, reps=5):
                                   dtype=torch.int32))
     torch.cuda.synchronize()
     ps.capture()
-    ps.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        ps.replay()
-    torch.cuda.synchronize()
-    us = 1e6 * (time.perf_counter() - t0) / reps
+    st = replay_stats(torch, ps.replay, 1)
     flops = 2 * S * L * (K * qkv + q * K + 2 * K * F + F * K) + 2 * K * c.vocab_size
-    tf = flops / (us * 1e-6) / 1e12
-    return {"ms_per_prompt": round(us / 1e3, 3), "prompt_tokens_per_s": round(S / (us * 1e-6), 1),
-            "tflops": round(tf, 1), "frac_mfma": round(tf / MFMA_PEAK_TFLOPS, 4),
-            "tokens": S, "layers": L,
-            "note": "matmul flops only; attention stand-in = a copy of the q columns"}
+    rate(st, flops=flops)
+    st.update({"ms_per_prompt": round(st["median_us"] / 1e3, 3),
+               "prompt_tokens_per_s": round(S / (st["median_us"] * 1e-6), 1),
+               "tokens": S, "layers": L,
+               "note": "matmul flops only; attention stand-in = a copy of the q columns"})
+    return st
 
 
-def token_select_leg(pkg, torch, gen, dev, vocab=128256, reps=200):
+def token_select_leg(pkg, torch, gen, dev, vocab=128256):
     """Token selection after the lm_head (LlamaModel.swift:153,161): argmax
     and temperature 0.7 / top-p 0.9 / repetition penalty 1.1 sampling over
-    Llama 3.2's 128256 fp16 logits (N(0, 3^2): a nucleus of a few tokens, as
-    for a trained model) with 64 seen ids.  Each is captured as a HIP graph on
-    its own stream (after one eager call there, which sizes the workspace) and
-    replayed; us per call includes the graph's launch gaps."""
-    logits = (3.0 * torch.randn(vocab, generator=gen, device=dev)).half()
+    Llama 3.2's 128256 fp16 logits with 64 seen ids, for N(0, 3^2) logits (a
+    nucleus of a few tokens, as for a trained model) and for flat logits
+    (every token tied: the nucleus is the whole vocabulary).  Each is a graph
+    of 10 calls on its own stream (after one eager call there, which sizes the
+    workspace); us per call includes the graph's launch gaps."""
+    peaked = (3.0 * torch.randn(vocab, generator=gen, device=dev)).half()
+    flat = torch.zeros(vocab, device=dev, dtype=torch.float16)
     seen = torch.randint(0, vocab, (64,), generator=gen, device=dev, dtype=torch.int32)
     out = torch.empty(1, device=dev, dtype=torch.int32)
     res = {}
-    for name, fn in (("argmax", lambda s: pkg.argmax(logits, out=out, stream=s)),
-                     ("sample_top_p", lambda s: pkg.sample(logits, 0.7, 0.9, 1.1, seen, 0.5,
-                                                           out=out, stream=s))):
+    cases = (("argmax", lambda s: pkg.argmax(peaked, out=out, stream=s)),
+             ("sample_top_p", lambda s: pkg.sample(peaked, 0.7, 0.9, 1.1, seen, 0.5, out=out,
+                                                   stream=s)),
+             ("sample_top_p_flat", lambda s: pkg.sample(flat, 0.7, 0.9, 1.1, seen, 0.5, out=out,
+                                                        stream=s)))
+    for name, fn in cases:
         s = torch.cuda.Stream()
-        with torch.cuda.stream(s):
-            fn(s)
-        s.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=s):
-            for _ in range(10):
-                fn(s)
-        g.replay()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(reps // 10):
-            g.replay()
-        torch.cuda.synchronize()
-        res[name + "_us"] = round(1e6 * (time.perf_counter() - t0) / (reps // 10 * 10), 2)
+        g = capture(torch, lambda: [fn(s) for _ in range(10)], s, warm=lambda: fn(s))
+        res[name] = replay_stats(torch, g.replay, 10)
+        del g
     res["vocab"] = vocab
     res["launches"] = {"argmax": 2, "sample_top_p": 4}
     return res
 
 
+# ---------------------------------------------------------------- GEMMs ---
+
+def gemm_legs(pkg, torch, gen, dev, cap):
+    """BASELINE configs 3 (M = 750 prefill gate/up + SiLU and down), 4b
+    (lm_head M = 750) and 5 (LTX DiT FFN, M = 6144 bf16): graphs of R launches
+    on one resident weight (compute-bound: each weight is re-read once per
+    tile row, not once per launch)."""
+    res = {}
+
+    def leg(fn, flops, reps):
+        g = capture(torch, lambda: [fn() for _ in range(reps)], cap, warm=fn)
+        st = rate(replay_stats(torch, g.replay, reps), flops=flops)
+        del g
+        return st
+
+    M = 750
+    xa = torch.randn(M, 3072, generator=gen, device=dev).half()
+    gu = [q4(pkg, torch, 8192, 3072, gen, dev) for _ in range(2)]
+    h = torch.empty(M, 8192, device=dev, dtype=torch.float16)
+    res["prefill_gate_up_silu_m750"] = leg(
+        lambda: pkg.matmul_q4_silu_mul(xa, gu[0], gu[1], M, 3072, 8192, out=h),
+        2 * 2 * M * 8192 * 3072, 10)
+    dw = q4(pkg, torch, 3072, 8192, gen, dev)
+    y = torch.empty(M, 3072, device=dev, dtype=torch.float16)
+    res["prefill_down_m750"] = leg(
+        lambda: pkg.matmul_q4_fast(h, *_wsb(dw), M, 8192, 3072, G, out=y),
+        2 * M * 3072 * 8192, 10)
+    del gu, dw
+    lm = q4(pkg, torch, 128256, 3072, gen, dev)
+    yl = torch.empty(M, 128256, device=dev, dtype=torch.float16)
+    res["lm_head_gemm_m750"] = leg(
+        lambda: pkg.matmul_q4_fast(xa, *_wsb(lm), M, 3072, 128256, G, out=yl),
+        2 * M * 128256 * 3072, 5)
+    del lm, yl
+    Md = 6144
+    xd = torch.randn(Md, 2048, generator=gen, device=dev).bfloat16()
+    up = q4(pkg, torch, 8192, 2048, gen, dev)
+    down = q4(pkg, torch, 2048, 8192, gen, dev)
+    hd = torch.empty(Md, 8192, device=dev, dtype=torch.bfloat16)
+    yd = torch.empty(Md, 2048, device=dev, dtype=torch.float32)
+    res["dit_ffn_up_gelu_m6144_bf16"] = leg(
+        lambda: pkg.matmul_q4_ex(xd, up, Md, 8192, out=hd, epilogue=pkg.SLTX_EPI_GELU_TANH),
+        2 * Md * 8192 * 2048, 5)
+    res["dit_ffn_down_m6144_bf16"] = leg(
+        lambda: pkg.matmul_q4_ex(hd, down, Md, 2048, out=yd), 2 * Md * 2048 * 8192, 5)
+    del xd, up, down, hd, yd
+    torch.cuda.empty_cache()
+    return res
+
+
+SMALL_M = (2, 8, 32, 128)
+
+
+def small_m_legs(pkg, torch, gen, dev, cap, min_gb=2.0):
+    """Small M (T5 encoder layers at S <= 128, T5Encoder.swift:140-205, and
+    short prompts): the Llama gate/up + SiLU shape and the T5-XXL shapes
+    (K = 4096: q/k/v/o [4096 x 4096], gelu FFN wi_0/wi_1 [10240 x 4096] in
+    one launch, wo [4096 x 10240]) at M in 2, 8, 32, 128, each over weight
+    copies rotated to >= min_gb GB.  GB/s = weight + activation bytes per
+    launch / median time; bound: HBM (every weight byte read once per launch)."""
+    shapes = (("llama_gate_up_silu", 8192, 3072, 2, "silu"),
+              ("t5_attn_proj", 4096, 4096, 1, None),
+              ("t5_ffn_wi_gelu", 10240, 4096, 2, "gelu"),
+              ("t5_ffn_wo", 4096, 10240, 1, None))
+    res = {}
+    for name, N, K, nsets, epi in shapes:
+        per = gemv_bytes(N, K, nsets, M=0)
+        copies = max(1, math.ceil(min_gb * 1e9 / per))
+        ws = [[q4(pkg, torch, N, K, gen, dev) for _ in range(nsets)] for _ in range(copies)]
+        row = {"N": N, "K": K, "weight_sets": nsets, "copies": copies}
+        for M in SMALL_M:
+            xx = torch.randn(M, K, generator=gen, device=dev).half()
+            y = torch.empty(M, N, device=dev, dtype=torch.float16)
+
+            def run(w, xx=xx, y=y, M=M):
+                if epi == "silu":
+                    pkg.matmul_q4_silu_mul(xx, w[0], w[1], M, K, N, out=y)
+                elif epi == "gelu":
+                    pkg.matmul_q4_geglu(xx, w[0], w[1], M, K, N, out=y)
+                else:
+                    pkg.matmul_q4(xx, *_wsb(w[0]), M, K, N, G, out=y)
+
+            g = capture(torch, lambda: [run(w) for w in ws], cap, warm=lambda: run(ws[0]))
+            st = rate(replay_stats(torch, g.replay, copies),
+                      nbytes=gemv_bytes(N, K, nsets, M=M), flops=2 * M * N * K * nsets)
+            del g
+            row[f"m{M}"] = st
+        res[name] = row
+        del ws
+        torch.cuda.empty_cache()
+    return res
+
+
+# ------------------------------------------------------------ PMC modes ---
+
 def traffic_run(pkg, torch, gen, dev):
     """Workload for the FETCH_SIZE / WRITE_SIZE passes: the dominant kernel
     (fused gate/up GEMV) 24 times over 12 distinct weight copies, then one
     256 MiB copy_ whose counters give the bytes-per-count calibration."""
-    sets = [[pkg.Q4Weight(*rand_q4(torch, 8192, 3072, gen, dev), 3072, G) for _ in range(2)]
-            for _ in range(12)]
+    sets = [[q4(pkg, torch, 8192, 3072, gen, dev) for _ in range(2)] for _ in range(12)]
     x = torch.randn(1, 3072, generator=gen, device=dev).half()
     y = torch.empty(1, 8192, device=dev, dtype=torch.float16)
     for _ in range(2):
@@ -445,14 +693,14 @@ def traffic_run(pkg, torch, gen, dev):
 
 def gemm_pmc_run(pkg, torch, gen, dev):
     """Workload for the MFMA-utilisation passes: the M=750 prefill GEMMs
-    (gate/up with SiLU x up, and down, split-K) 10 times each, after one
-    warm-up launch each."""
+    (gate/up with SiLU x up, and down) 10 times each, after one warm-up
+    launch each."""
     M, K, F = 750, 3072, 8192
     x = torch.randn(M, K, generator=gen, device=dev).half()
     a = torch.randn(M, F, generator=gen, device=dev).half()
-    gate = pkg.Q4Weight(*rand_q4(torch, F, K, gen, dev), K, G)
-    up = pkg.Q4Weight(*rand_q4(torch, F, K, gen, dev), K, G)
-    down = pkg.Q4Weight(*rand_q4(torch, K, F, gen, dev), F, G)
+    gate = q4(pkg, torch, F, K, gen, dev)
+    up = q4(pkg, torch, F, K, gen, dev)
+    down = q4(pkg, torch, K, F, gen, dev)
     y = torch.empty(M, F, device=dev, dtype=torch.float16)
     z = torch.empty(M, K, device=dev, dtype=torch.float16)
     for _ in range(11):
@@ -461,192 +709,6 @@ def gemm_pmc_run(pkg, torch, gen, dev):
         pkg.linear(a, down, M, F, K, fast=True, out=z)
     torch.cuda.synchronize()
     print("gemm pmc run done", flush=True)
-
-
-def _wsb(q):
-    return q.weight, q.scales, q.biases
-
-
-def timing_diagnostics(pkg, torch, layers, x2, outs, reps):
-    """Dominant-kernel duration by three methods (for cross-checking rocprof)."""
-    out = {}
-    # (a) eager, per-launch events
-    es = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in layers]
-    for (a, b), L in zip(es, layers):
-        w = L.w["gate_up_proj"]
-        a.record()
-        pkg.matmul_q4_silu_mul(x2, w[0], w[1], 1, 3072, 8192, out=outs["gate_up_proj"])
-        b.record()
-    torch.cuda.synchronize()
-    out["eager_event_us"] = round(1e3 * sum(a.elapsed_time(b) for a, b in es) / len(es), 3)
-    # (b) graph of dominant launches only
-    g2 = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g2):
-        for L in layers:
-            w = L.w["gate_up_proj"]
-            pkg.matmul_q4_silu_mul(x2, w[0], w[1], 1, 3072, 8192, out=outs["gate_up_proj"])
-    g2.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(10):
-        g2.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    out["graph_only_us"] = round(1e3 * e0.elapsed_time(e1) / (10 * len(layers)), 3)
-    return out
-
-
-def gemm_legs(pkg, torch, gen, dev):
-    """BASELINE configs 3-5 (M > 1, MFMA GEMM) and 4a (lm_head GEMV), each timed
-    over a graph of R launches bracketed by events."""
-    res = {}
-
-    # the library keeps its split-K workspace per stream and never allocates
-    # while a stream is being captured: warm up on the stream the graph is
-    # captured on
-    cap = torch.cuda.Stream()
-
-    def timed(fn, flops=None, nbytes=None, reps=20):
-        with torch.cuda.stream(cap):
-            fn()
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=cap):
-            for _ in range(reps):
-                fn()
-        g.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(3):
-            g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        us = 1e3 * e0.elapsed_time(e1) / (3 * reps)
-        r = {"us": round(us, 2)}
-        if flops:
-            tf = flops / (us * 1e-6) / 1e12
-            r.update({"tflops": round(tf, 1), "frac_mfma": round(tf / MFMA_PEAK_TFLOPS, 4)})
-        if nbytes:
-            gbs = nbytes / (us * 1e-6) / 1e9
-            r.update({"gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
-        return r
-
-    M = 750
-    xa = torch.randn(M, 3072, generator=gen, device=dev).half()
-    gu = [pkg.Q4Weight(*rand_q4(torch, 8192, 3072, gen, dev), 3072, G) for _ in range(2)]
-    h = torch.empty(M, 8192, device=dev, dtype=torch.float16)
-    res["prefill_gate_up_silu_m750"] = timed(
-        lambda: pkg.matmul_q4_silu_mul(xa, gu[0], gu[1], M, 3072, 8192, out=h),
-        flops=2 * 2 * M * 8192 * 3072)
-    dw = pkg.Q4Weight(*rand_q4(torch, 3072, 8192, gen, dev), 8192, G)
-    y = torch.empty(M, 3072, device=dev, dtype=torch.float16)
-    res["prefill_down_m750"] = timed(
-        lambda: pkg.matmul_q4_fast(h, dw.weight, dw.scales, dw.biases, M, 8192, 3072, G, out=y),
-        flops=2 * M * 3072 * 8192)
-    del gu, dw
-    lm = pkg.Q4Weight(*rand_q4(torch, 128256, 3072, gen, dev), 3072, G)
-    x1 = xa[:1].contiguous()
-    y1 = torch.empty(1, 128256, device=dev, dtype=torch.float16)
-    # lm_head (222 MB) fits the 256 MB MALL when repeated, so this GEMV leg is
-    # an upper bound; the decode rotation above is the HBM-honest number
-    res["lm_head_gemv_m1"] = timed(
-        lambda: pkg.matmul_q4(x1, lm.weight, lm.scales, lm.biases, 1, 3072, 128256, G, out=y1),
-        nbytes=gemv_bytes(128256, 3072), reps=10)
-    yl = torch.empty(M, 128256, device=dev, dtype=torch.float16)
-    res["lm_head_gemm_m750"] = timed(
-        lambda: pkg.matmul_q4_fast(xa, lm.weight, lm.scales, lm.biases, M, 3072, 128256, G,
-                                   out=yl),
-        flops=2 * M * 128256 * 3072, reps=5)
-    del lm, yl
-    Md = 6144
-    xd = torch.randn(Md, 2048, generator=gen, device=dev).bfloat16()
-    up = pkg.Q4Weight(*rand_q4(torch, 8192, 2048, gen, dev), 2048, G)
-    down = pkg.Q4Weight(*rand_q4(torch, 2048, 8192, gen, dev), 8192, G)
-    hd = torch.empty(Md, 8192, device=dev, dtype=torch.bfloat16)
-    yd = torch.empty(Md, 2048, device=dev, dtype=torch.float32)
-    res["dit_ffn_up_gelu_m6144_bf16"] = timed(
-        lambda: pkg.matmul_q4_ex(xd, up, Md, 8192, out=hd, epilogue=pkg.SLTX_EPI_GELU_TANH),
-        flops=2 * Md * 8192 * 2048, reps=5)
-    res["dit_ffn_down_m6144_bf16"] = timed(
-        lambda: pkg.matmul_q4_ex(hd, down, Md, 2048, out=yd), flops=2 * Md * 2048 * 8192,
-        reps=5)
-    return res
-
-
-def cpu_baseline(seconds):
-    """The oracle's C dequant-matmul (port of the same semantics, fp32
-    accumulate, pthreads over rows) on a bounded sample: whole decode layers
-    (7 projections: gate and up unfused, plus silu_mul) repeated for about
-    `seconds`."""
-    import numpy as np
-    from oracle import q4_oracle as o
-    o.lib()
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        cores = os.cpu_count() or 1
-    threads = max(1, min(cores, 16))
-    projs = [("q_proj", 3072, 3072), ("k_proj", 1024, 3072), ("v_proj", 1024, 3072),
-             ("o_proj", 3072, 3072), ("gate_proj", 8192, 3072), ("up_proj", 8192, 3072),
-             ("down_proj", 3072, 8192)]
-    data = {}
-    for i, (name, N, K) in enumerate(projs):
-        x, [(w, s, b)] = o.make_inputs(1, N, K, G, seed=100 + i)
-        data[name] = (x, w, s, b)
-    layers = 0
-    t0 = time.perf_counter()
-    while True:
-        ys = {n: o.c_cpu_matmul_q4(*data[n], G, threads) for n, _, _ in projs}
-        o.c_silu_mul(ys["gate_proj"], ys["up_proj"])
-        layers += 1
-        if time.perf_counter() - t0 >= seconds and layers >= 2:
-            break
-    dt = time.perf_counter() - t0
-    # single-thread scalar run of the same layer, about a quarter of the time
-    layers1 = 0
-    t1 = time.perf_counter()
-    while True:
-        ys = {n: o.c_cpu_matmul_q4(*data[n], G, 1) for n, _, _ in projs}
-        o.c_silu_mul(ys["gate_proj"], ys["up_proj"])
-        layers1 += 1
-        if time.perf_counter() - t1 >= seconds / 4 and layers1 >= 1:
-            break
-    dt1 = time.perf_counter() - t1
-    return {"value": round(layers * LAYER_BYTES / dt / 1e9, 4), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{layers} decode layers (same 7 projections + silu_mul, {LAYER_BYTES} "
-                      f"algorithmic bytes each) in {dt:.1f} s, {threads} threads",
-            "host_cpus": cores,
-            "single_thread": {"value": round(layers1 * LAYER_BYTES / dt1 / 1e9, 4),
-                              "unit": "GB/s",
-                              "sample": f"{layers1} decode layers in {dt1:.1f} s, 1 thread"}}
-
-
-def stream_copy_ceiling(torch, dev, gib=1, reps=10):
-    """Measured HBM ceiling: a device-to-device copy of `gib` GiB (torch
-    copy_), captured in a graph and replayed; bytes read + written per second."""
-    n = gib * 2 ** 30 // 2
-    src = torch.empty(n, device=dev, dtype=torch.float16).normal_()
-    dst = torch.empty_like(src)
-    dst.copy_(src)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        dst.copy_(src)
-    g.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        g.replay()
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / reps
-    gbs = 2 * n * 2 / dt / 1e9
-    del src, dst
-    torch.cuda.empty_cache()
-    return round(gbs, 1)
 
 
 def traffic_from_profiles():
@@ -662,6 +724,163 @@ def traffic_from_profiles():
             except ValueError:
                 return None
     return None
+
+
+# --------------------------------------------------------- CPU baseline ---
+
+def cpu_baseline(runs=5):
+    """BASELINE's CPU plan: the same dequant matmul (w = s*q + b, group 64,
+    fp32 accumulate, fp16 out; gate/up with SiLU x up) as C restatements in
+    oracle/q4_cpu_baseline.c -- a substitute for Swift, which is not
+    installed: single-thread scalar (matmulCPU's loop order,
+    LlamaModel.swift:478-493) and all-cores 8-wide SIMD (SIMD8<Float>), the
+    median of `runs` wall-clock runs per config.  Config 3's scalar figure is
+    timed on the first rows of x and scaled to 750 rows (the scalar loop's
+    cost is linear in the rows)."""
+    import numpy as np
+    from oracle import q4_oracle as o
+    o.cpu_lib()
+    try:
+        host = len(os.sched_getaffinity(0))
+    except AttributeError:
+        host = os.cpu_count() or 1
+    threads = max(1, min(host, 16))
+    configs = {
+        "config1_q_proj_m1": (1, [("q_proj", 3072, 3072)], False),
+        "config2_decode_layer_m1": (1, [("q_proj", 3072, 3072), ("k_proj", 1024, 3072),
+                                        ("v_proj", 1024, 3072), ("o_proj", 3072, 3072),
+                                        ("gate_proj", 8192, 3072), ("up_proj", 8192, 3072),
+                                        ("down_proj", 3072, 8192)], True),
+        "config3_prefill_m750": (750, [("gate_proj", 8192, 3072), ("up_proj", 8192, 3072),
+                                       ("down_proj", 3072, 8192)], True),
+    }
+    out = {}
+    for cname, (M, projs, silu) in configs.items():
+        jobs = []
+        for i, (name, N, K) in enumerate(projs):
+            xx, [(w, s, b)] = o.make_inputs(M, N, K, G, seed=200 + i)
+            jobs.append(o.CpuQ4(xx, w, s, b, G))
+        rows = M if M == 1 else 4
+        nbytes = sum(gemv_bytes(j.N, j.K, M=M) for j in jobs)
+        flops = sum(2 * M * j.N * j.K for j in jobs)
+        res = {"M": M, "matmuls": [n for n, _, _ in projs], "bytes": nbytes, "flops": flops}
+        for kind in ("scalar", "simd"):
+            ts = []
+            for _ in range(runs):
+                t0 = time.perf_counter()
+                ys = [j.scalar(rows) if kind == "scalar" else j.simd(threads) for j in jobs]
+                if silu:
+                    o.c_silu_mul(ys[-3], ys[-2])
+                ts.append(time.perf_counter() - t0)
+            t = float(np.median(ts)) * (M / rows if kind == "scalar" else 1.0)
+            res[kind] = {"us": round(t * 1e6, 1), "gbs": round(nbytes / t / 1e9, 3),
+                         "gflops": round(flops / t / 1e9, 2),
+                         "threads": 1 if kind == "scalar" else threads, "runs": runs,
+                         **({"rows_timed": rows} if kind == "scalar" and rows != M else {})}
+        out[cname] = res
+    c2 = out["config2_decode_layer_m1"]["simd"]
+    return {"value": c2["gbs"], "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"BASELINE config 2 decode layer (7 projections + silu_mul, "
+                      f"{out['config2_decode_layer_m1']['bytes']} algorithmic bytes), 8-wide "
+                      f"SIMD C on {threads} threads, median of {runs} runs",
+            "substitute": "C restatement of the Swift scalar / SIMD8<Float> CPU plan (no Swift "
+                          "toolchain on the box)",
+            "host_cpus": host, "per_config": out}
+
+
+# --------------------------------------------------------- trace summary ---
+
+def _trace_rows(folder):
+    """(name, start_ns, end_ns, blocks, threads, vgpr, agpr, lds) of every
+    kernel dispatch in a rocprofv3 output folder, in start order."""
+    import csv
+    import glob
+    import sqlite3
+    dbs = sorted(glob.glob(os.path.join(folder, "**", "*.db"), recursive=True))
+    rows = []
+    if dbs:
+        for db in dbs:
+            c = sqlite3.connect(db)
+            for r in c.execute("select name, start, end, grid_x, workgroup_x, vgpr_count, "
+                               "accum_vgpr_count, lds_size from kernels"):
+                rows.append((r[0], int(r[1]), int(r[2]), int(r[3]) // max(1, int(r[4])),
+                             int(r[4]), r[5], r[6], r[7]))
+    else:
+        for f in sorted(glob.glob(os.path.join(folder, "**", "*kernel_trace.csv"),
+                                  recursive=True)):
+            for r in csv.DictReader(open(f)):
+                wg = int(r.get("Workgroup_Size_X", r.get("Workgroup_Size", 1)) or 1)
+                gr = int(r.get("Grid_Size_X", r.get("Grid_Size", 1)) or 1)
+                rows.append((r["Kernel_Name"], int(r["Start_Timestamp"]),
+                             int(r["End_Timestamp"]), gr // max(1, wg), wg,
+                             r.get("Arch_VGPR_Count", ""), r.get("Accum_VGPR_Count", ""),
+                             r.get("LDS_Block_Size", r.get("Group_Segment_Size", ""))))
+    rows.sort(key=lambda r: r[1])
+    return rows
+
+
+def _short(name):
+    n = name[5:] if name.startswith("void ") else name
+    n = n.replace("sltx::", "")
+    i = n.find("(")
+    if i > 0 and not n.startswith("at::"):
+        n = n[:i]
+    return n if len(n) <= 90 else n[:87] + "..."
+
+
+def summarize_trace(folder, copies=40):
+    """Markdown summary of a kernel trace of this script: every kernel
+    (median / mean / min / max duration per launch shape) and the dominant
+    kernel's replay statistic, computed the way the bench computes avg_us:
+    the trace's runs of `copies` back-to-back dominant launches (the gate/up
+    graph's replays) -> the mean kernel duration of each replay -> the median
+    over replays."""
+    import numpy as np
+    rows = _trace_rows(folder)
+    if not rows:
+        return f"no kernel dispatches found under {folder}"
+    groups = {}
+    for r in rows:
+        groups.setdefault((_short(r[0]), r[3], r[4]), []).append(r)
+    out = ["| kernel | blocks x threads | calls | median us | mean us | min us | max us | "
+           "VGPR | AGPR | LDS B |", "|---|---|---|---|---|---|---|---|---|---|"]
+    order = sorted(groups.items(), key=lambda kv: -sum(r[2] - r[1] for r in kv[1]))
+    for (name, blocks, thr), rs in order[:40]:
+        d = np.array([(r[2] - r[1]) / 1e3 for r in rs])
+        out.append(f"| `{name}` | {blocks} x {thr} | {len(rs)} | {np.median(d):.3f} | "
+                   f"{d.mean():.3f} | {d.min():.3f} | {d.max():.3f} | {rs[0][5]} | {rs[0][6]} | "
+                   f"{rs[0][7]} |")
+    # dominant kernel: maximal runs of consecutive dominant launches
+    runs, cur = [], []
+    for r in rows:
+        if DOMINANT_KERNEL in r[0]:
+            cur.append(r)
+        else:
+            if len(cur) >= copies:
+                runs.append(cur)
+            cur = []
+    if len(cur) >= copies:
+        runs.append(cur)
+    reps = []
+    for run in runs:
+        for i in range(0, len(run) - copies + 1, copies):
+            chunk = run[i:i + copies]
+            reps.append(np.mean([(r[2] - r[1]) / 1e3 for r in chunk]))
+    out.append("")
+    if reps:
+        med = float(np.median(reps))
+        p25, p75 = np.percentile(reps, [25, 75])
+        gbs = DOMINANT_BYTES / (med * 1e-6) / 1e9
+        out += [f"dominant kernel `{DOMINANT_KERNEL}`: {len(reps)} replays of {copies} "
+                f"back-to-back launches",
+                f"replay_median_us: {med:.3f}",
+                f"replay_p25_us: {p25:.3f}",
+                f"replay_p75_us: {p75:.3f}",
+                f"achieved_gbs: {gbs:.1f}",
+                f"frac_of_8000_gbs: {gbs / HBM_PEAK_GBS:.4f}"]
+    else:
+        out.append(f"no run of {copies} back-to-back `{DOMINANT_KERNEL}` launches in the trace")
+    return "\n".join(out)
 
 
 if __name__ == "__main__":

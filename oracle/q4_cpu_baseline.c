@@ -1,5 +1,6 @@
 /* q4_cpu_baseline.c -- CPU baselines of the 4-bit dequant matmul (test and
  * benchmark infrastructure: timed beside the GPU path, never shipped).
+ * Built with -mavx2 -mfma -mf16c: fp16 <-> fp32 are the F16C instructions.
  *
  * Semantics of swift-ltx's matmul_q4 (Kernels.swift:444-620): w[n,k] =
  * s[n,k/g] * q[n,k] + b[n,k/g] (Kernels.swift:392-395), nibble k of row n =
@@ -8,8 +9,9 @@
  *
  *   cpu_q4_scalar  one thread, the loop shape of the reference's only CPU
  *                  matmul (matmulCPU, LlamaModel.swift:478-493: for m, for n,
- *                  for k, one fp32 sum) with the weight dequantized inline;
- *                  built without auto-vectorization.
+ *                  for k, one fp32 sum over an fp32 copy of the x row) with
+ *                  the weight dequantized inline, the group's scale and bias
+ *                  read once per group; built without auto-vectorization.
  *   cpu_q4_simd    the same product with an explicit 8-wide fp32 vector
  *                  (Swift's SIMD8<Float>): each packed word is dequantized as
  *                  one 8-lane vector (shift, mask, convert, fma with the
@@ -26,7 +28,13 @@
 typedef float f8 __attribute__((vector_size(32)));
 typedef int32_t i8v __attribute__((vector_size(32)));
 
-static float f16_to_f32(uint16_t h) {
+#if defined(__F16C__)
+#include <immintrin.h>
+/* hardware conversions (x86 F16C), as Swift's Float(Float16) compiles to */
+static inline float f16_to_f32(uint16_t h) { return _cvtsh_ss(h); }
+static inline uint16_t f32_to_f16(float f) { return (uint16_t)_cvtss_sh(f, 0); }   /* nearest even */
+#else
+static inline float f16_to_f32(uint16_t h) {
     const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
     const uint32_t exp = (h >> 10) & 0x1fu, man = h & 0x3ffu;
     uint32_t bits;
@@ -49,7 +57,7 @@ static float f16_to_f32(uint16_t h) {
     return f;
 }
 
-static uint16_t f32_to_f16(float f) {   /* round to nearest even */
+static inline uint16_t f32_to_f16(float f) {   /* round to nearest even */
     uint32_t x;
     memcpy(&x, &f, 4);
     const uint32_t sign = (x >> 16) & 0x8000u;
@@ -70,6 +78,7 @@ static uint16_t f32_to_f16(float f) {   /* round to nearest even */
     if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) ++r;
     return (uint16_t)(sign | r);
 }
+#endif
 
 /* ------------------------------------------------------------- scalar --- */
 
@@ -77,17 +86,24 @@ __attribute__((optimize("no-tree-vectorize")))
 void cpu_q4_scalar(const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b,
                    uint16_t* y, int64_t M, int64_t N, int64_t K, int64_t g) {
     const int64_t packed = K / 8, groups = K / g;
-    for (int64_t m = 0; m < M; ++m)
+    float* xf = (float*)malloc(sizeof(float) * (size_t)K);
+    if (!xf) return;
+    for (int64_t m = 0; m < M; ++m) {
+        for (int64_t k = 0; k < K; ++k) xf[k] = f16_to_f32(x[m * K + k]);   /* the fp32 row */
         for (int64_t n = 0; n < N; ++n) {
             const uint32_t* wr = w + n * packed;
             float sum = 0.0f;
-            for (int64_t k = 0; k < K; ++k) {
-                const float q = (float)((wr[k >> 3] >> (4 * (k & 7))) & 0xfu);
-                const float wk = q * f16_to_f32(s[n * groups + k / g]) + f16_to_f32(b[n * groups + k / g]);
-                sum += f16_to_f32(x[m * K + k]) * wk;
+            for (int64_t gi = 0; gi < groups; ++gi) {   /* k in order, one group at a time */
+                const float sc = f16_to_f32(s[n * groups + gi]), bi = f16_to_f32(b[n * groups + gi]);
+                for (int64_t k = gi * g; k < (gi + 1) * g; ++k) {
+                    const float q = (float)((wr[k >> 3] >> (4 * (k & 7))) & 0xfu);
+                    sum += xf[k] * (q * sc + bi);
+                }
             }
             y[m * N + n] = f32_to_f16(sum);
         }
+    }
+    free(xf);
 }
 
 /* --------------------------------------------------------------- SIMD --- */

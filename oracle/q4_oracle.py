@@ -329,8 +329,10 @@ def elementwise_ok(y, ref, rtol: float, atol_rms: float) -> tuple[bool, float]:
 def build_c(force: bool = False) -> str:
     """Compile q4_oracle.c into _build/libq4oracle.so with gcc."""
     src = os.path.join(HERE, "q4_oracle.c")
-    if (not force and os.path.exists(LIB_PATH)
-            and os.path.getmtime(LIB_PATH) >= os.path.getmtime(src)):
+    src2 = os.path.join(HERE, "q4_cpu_baseline.c")
+    if (not force and all(os.path.exists(p) for p in (LIB_PATH, CPU_LIB_PATH))
+            and min(os.path.getmtime(LIB_PATH), os.path.getmtime(CPU_LIB_PATH))
+            >= max(os.path.getmtime(src), os.path.getmtime(src2))):
         return LIB_PATH
     os.makedirs(LIB_DIR, exist_ok=True)
     tmp = LIB_PATH + ".tmp%d" % os.getpid()
@@ -339,9 +341,8 @@ def build_c(force: bool = False) -> str:
     os.replace(tmp, LIB_PATH)
     # The CPU baselines (q4_cpu_baseline.c): vectorized for AVX2 + FMA (every
     # x86-64-v3 host, the GPU boxes' EPYCs included), fp contraction allowed.
-    src2 = os.path.join(HERE, "q4_cpu_baseline.c")
     tmp2 = CPU_LIB_PATH + ".tmp%d" % os.getpid()
-    subprocess.run(["gcc", "-O3", "-mavx2", "-mfma", "-fPIC", "-shared", "-std=gnu11", "-o", tmp2,
+    subprocess.run(["gcc", "-O3", "-mavx2", "-mfma", "-mf16c", "-fPIC", "-shared", "-std=gnu11", "-o", tmp2,
                     src2, "-lpthread"], check=True)
     os.replace(tmp2, CPU_LIB_PATH)
     return LIB_PATH
@@ -374,25 +375,43 @@ def _q4_args(x, w, s, b):
     return x, w, s, b
 
 
+class CpuQ4:
+    """Inputs of one dequant matmul converted once for the CPU baselines, so
+    that timing a run times only the C call."""
+
+    def __init__(self, x, w, s, b, group):
+        self.x, self.w, self.s, self.b = _q4_args(x, w, s, b)
+        self.M, self.K = self.x.shape
+        self.N = self.w.shape[0]
+        self.group = group
+        self.y = np.empty((self.M, self.N), dtype=np.uint16)
+
+    def scalar(self, rows=None) -> np.ndarray:
+        """Single-thread scalar baseline (matmulCPU's loop shape,
+        LlamaModel.swift:478-493, with the 4-bit dequant inline) over the first
+        `rows` rows of x (all by default)."""
+        m = self.M if rows is None else rows
+        cpu_lib().cpu_q4_scalar(_p(self.x), _p(self.w), _p(self.s), _p(self.b), _p(self.y), m,
+                                self.N, self.K, self.group)
+        return self.y[:m].view(np.float16)
+
+    def simd(self, threads=1) -> np.ndarray:
+        """8-wide fp32 (SIMD8<Float>) baseline over `threads` pthreads."""
+        rc = cpu_lib().cpu_q4_simd(_p(self.x), _p(self.w), _p(self.s), _p(self.b), _p(self.y),
+                                   self.M, self.N, self.K, self.group, threads)
+        if rc < 0:
+            raise RuntimeError("cpu_q4_simd failed")
+        return self.y.view(np.float16)
+
+
 def cpu_q4_scalar(x, w, s, b, group) -> np.ndarray:
-    """Single-thread scalar baseline (matmulCPU's loop shape,
-    LlamaModel.swift:478-493, with the 4-bit dequant inline)."""
-    x, w, s, b = _q4_args(x, w, s, b)
-    M, K = x.shape
-    y = np.empty((M, w.shape[0]), dtype=np.uint16)
-    cpu_lib().cpu_q4_scalar(_p(x), _p(w), _p(s), _p(b), _p(y), M, w.shape[0], K, group)
-    return y.view(np.float16)
+    """CpuQ4(...).scalar() on a copy of the output."""
+    return CpuQ4(x, w, s, b, group).scalar().copy()
 
 
 def cpu_q4_simd(x, w, s, b, group, threads=1) -> np.ndarray:
-    """8-wide fp32 (SIMD8<Float>) baseline over `threads` pthreads."""
-    x, w, s, b = _q4_args(x, w, s, b)
-    M, K = x.shape
-    y = np.empty((M, w.shape[0]), dtype=np.uint16)
-    rc = cpu_lib().cpu_q4_simd(_p(x), _p(w), _p(s), _p(b), _p(y), M, w.shape[0], K, group, threads)
-    if rc < 0:
-        raise RuntimeError("cpu_q4_simd failed")
-    return y.view(np.float16)
+    """CpuQ4(...).simd(threads) on a copy of the output."""
+    return CpuQ4(x, w, s, b, group).simd(threads).copy()
 
 
 _lib = None
