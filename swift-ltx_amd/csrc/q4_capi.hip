@@ -274,6 +274,8 @@ int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w
     p.ws = nullptr;
     p.splits = 1;
     p.split_tiles = 0;
+    SkinnyPlan sp;
+    if (skinny_plan(p, x_dtype == kBF16, &sp)) return finish(launch_skinny(p, sp, st), fn);
     const size_t need = gemm_workspace_bytes(p);
     if (need > 0) p.ws = stream_workspace(st, need);
     return finish(launch_gemm(p, x_dtype == kBF16, st), fn);

@@ -155,6 +155,15 @@ constexpr int kMaxDevices = 64;
 int sample_noalloc_scratch_init(int dev);
 // The address resolved for `dev`, or null before sample_noalloc_scratch_init.
 void* sample_noalloc_scratch(int dev);
+// Small-M route (q4_skinny.hip): W waves split K into STEPS 128-wide steps
+// each, MT tiles of 16 activation rows, RT tiles of 16 weight rows per block.
+// skinny_plan returns false when the shape or epilogue is not covered (the
+// GEMM then runs).
+struct SkinnyPlan {
+    int W, MT, STEPS, RT;
+};
+bool skinny_plan(const GemmParams& p, bool a_bf16, SkinnyPlan* out);
+hipError_t launch_skinny(const GemmParams& p, const SkinnyPlan& pl, hipStream_t st);
 // Bytes of split-K workspace the launch of `p` would use (0: it does not split).
 size_t gemm_workspace_bytes(const GemmParams& p);
 // Launches the GEMM; splits K only if p.ws is non-null (and then needs

@@ -1,0 +1,359 @@
+// q4_skinny.hip -- 4-bit dequant matmul for small M (1..32 activation rows:
+// short prompts, the T5 encoder's S <= 128 layers, batched decode) on CDNA4
+// MFMA, as a weight stream.
+//
+// Same product as q4_gemm.hip, Y[M,N] = X[M,K] . dequant(W)[N,K]^T with fp32
+// accumulation (matmulQ4Fast, Ops.swift:312-381).  At small M each weight
+// byte feeds only M multiply-adds, so the kernel is bound by the weight
+// stream, like the GEMV: the block tile of the large-M GEMM (128 or 192
+// activation rows, LDS-staged weights) would pad M and re-stage weights for
+// nothing.  Here:
+//  * A block owns 16 * RT weight rows (of each weight set: gate and up for
+//    the gated epilogues) and all K; its W waves split K into equal slices of
+//    128 * STEPS.  In wave w, lane l covers row l % 16 of each 16-row tile
+//    and, in each 128-wide k-step, the 32 k at offset 32 * (l / 16): one
+//    16-byte load of packed words, four lanes reading 64 contiguous bytes of
+//    a row.  Every load of a wave is issued before the first MFMA, in the
+//    order of use.
+//  * The block's scales and biases (one contiguous slab per array) are
+//    copied to LDS with direct 16-byte global -> LDS loads, issued first.
+//  * The wave's slice of X (all M rows, 16 per MFMA tile) stays in
+//    registers for the whole kernel, read through a buffer resource of
+//    M * K fp16 so that rows past M read as zeros without a branch.
+//  * Each word is dequantized in registers without leaving fp16: its
+//    nibbles are spread to bytes (q0 q2 q4 q6 and q1 q3 q5 q7), and
+//    v_cvt_scalef32_pk_f16_fp8 turns two bytes into two fp16 at a time: read
+//    as fp8 e4m3, a byte b < 16 is b * 2^-9 exactly (the subnormals and the
+//    first binade share one spacing), and the instruction's scale, of which
+//    only the exponent counts, is 2^9.  One v_pk_fma_f16 per pair then gives
+//    s * q + b with the GEMM's single rounding.  The k order inside a word
+//    is 0,2,1,3,4,6,5,7; X is permuted alike when it is loaded, once per
+//    wave.  Four MFMAs per 16-byte load accumulate into the tile's
+//    accumulators directly.
+//  * The partial tiles of the W waves are summed through LDS once, then the
+//    epilogue (gated SiLU / GELU-tanh pair, bias, GELU-tanh, residual add)
+//    runs on the fp32 sums.
+#include "q4_common.hpp"
+#include "q4_launch.hpp"
+
+namespace sltx {
+
+namespace {
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt
+// 6:4, lgkmcnt 11:8; a field at its maximum does not wait)
+__host__ __device__ constexpr int vmcnt_only(int n) {
+    return (n & 0xF) | (0x7 << 4) | (0xF << 8) | (((n >> 4) & 0x3) << 14);
+}
+
+// 16-byte pieces of one array's scale / bias slab (rows x groups fp16), and
+// the pieces reserved per slab in LDS (whole waves of 64).
+__host__ __device__ constexpr int slab_pieces(int rows, int groups) { return rows * groups / 8; }
+__host__ __device__ constexpr int slab_alloc(int rows, int groups) {
+    return (slab_pieces(rows, groups) + 63) / 64 * 64;
+}
+
+// x[k .. k+7] as four fp16 pairs (x0,x1) (x2,x3) (x4,x5) (x6,x7) -> the
+// pairs (x0,x2) (x1,x3) (x4,x6) (x5,x7) of the dequantized word's order.
+__device__ __forceinline__ u32x4 permute_x(u32x4 r) {
+    u32x4 a;
+    a[0] = __builtin_amdgcn_perm(r[1], r[0], 0x05040100u);
+    a[1] = __builtin_amdgcn_perm(r[1], r[0], 0x07060302u);
+    a[2] = __builtin_amdgcn_perm(r[3], r[2], 0x05040100u);
+    a[3] = __builtin_amdgcn_perm(r[3], r[2], 0x07060302u);
+    return a;
+}
+
+// One packed word -> 8 fp16 s*q+b in the order q0,q2,q1,q3,q4,q6,q5,q7.
+__device__ __forceinline__ u32x4 dequant_word(uint32_t w, f16x2 s2, f16x2 b2) {
+    const uint32_t lo = w & 0x0F0F0F0Fu;          // bytes q0 q2 q4 q6
+    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;   // bytes q1 q3 q5 q7
+    const float k512 = 512.0f;                    // 2^9: fp8 byte b -> b
+    f16x2 q[4];
+    q[0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, k512, false);   // q0, q2
+    q[1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, k512, false);   // q1, q3
+    q[2] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, k512, true);    // q4, q6
+    q[3] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, k512, true);    // q5, q7
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = as_u32(__builtin_elementwise_fma(q[e], s2, b2));
+    return o;
+}
+
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ void store_one(const GemmParams& p, size_t o, float v) {
+    if (p.y_dtype == kF32)
+        reinterpret_cast<float*>(p.y)[o] = v;
+    else if (p.y_dtype == kBF16)
+        reinterpret_cast<uint16_t*>(p.y)[o] = f2bf(v);
+    else
+        reinterpret_cast<uint16_t*>(p.y)[o] = f2h(v);
+}
+
+// W waves, MT tiles of 16 activation rows, STEPS 128-wide k-steps per wave,
+// PAIR: two weight sets (gate, up) and a gated epilogue, RT tiles of 16
+// weight rows per block.  OCC: blocks per CU the register budget is sized for.
+template <int W, int MT, int STEPS, bool PAIR, int RT, int OCC>
+__global__ __launch_bounds__(64 * W, OCC) void q4_skinny_kernel(GemmParams p) {
+    constexpr int NS = PAIR ? 2 : 1;
+    constexpr int ROWS = 16 * RT;
+    __shared__ f32x4 red[W][RT][NS][MT][64];
+    extern __shared__ u32x4 sb_lds[];   // [2 * NS slabs][ROWS][groups] fp16
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int n0 = blockIdx.x * ROWS;
+    const int K = p.K, groups = p.groups;
+    const int kw0 = wave * (128 * STEPS) + 32 * kq;   // this lane's first k
+
+    // ---- scales and biases -> LDS (slab a: s0, b0[, s1, b1]) ----
+    const int pieces = slab_pieces(ROWS, groups), alloc = slab_alloc(ROWS, groups);
+    const int valid = min(ROWS, p.N - n0) * groups * 2;   // slab bytes inside the arrays
+    constexpr int RA = (RT * STEPS + 7) / 8;              // rounds per slab (groups <= K/32)
+#pragma unroll
+    for (int a = 0; a < 2 * NS; ++a) {
+        const uint16_t* arr = a == 0 ? p.s0 : a == 1 ? p.b0 : a == 2 ? p.s1 : p.b1;
+        const char* src = reinterpret_cast<const char*>(arr + (size_t)n0 * groups);
+#pragma unroll
+        for (int r = 0; r < RA; ++r) {
+            const int c0 = r * 64 * W + 64 * wave;   // wave-uniform
+            if (c0 < pieces) {
+                int off = (c0 + lane) * 16;
+                if (off >= valid) off = 0;          // a spare copy of piece 0
+                __builtin_amdgcn_global_load_lds((const void*)(src + off),
+                                                 (lds_ptr_t)(sb_lds + a * alloc + c0), 16, 0, 0);
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- the wave's slice of X: fragment r of step t is x[k .. k+7] with
+    // k = kw0 + 128 t + 8 r, the k of word r of the lane's packed load ----
+    u32x4 xa[MT][STEPS][4];
+    {
+        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<void*>(p.a), (short)0, p.M * K * 2, 0x00020000);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int xrow = ((mt * 16 + r16) * K + kw0) * 2;
+#pragma unroll
+            for (int t = 0; t < STEPS; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    xa[mt][t][r] = __builtin_bit_cast(
+                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xrow + 256 * t + 16 * r, 0, 0));
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- packed words, step by step ----
+    u32x4 wq[STEPS][RT][NS];
+#pragma unroll
+    for (int t = 0; t < STEPS; ++t)
+#pragma unroll
+        for (int i = 0; i < RT; ++i)
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const int row = min(n0 + 16 * i + r16, p.N - 1);
+                const uint32_t* wr = (s ? p.w1 : p.w0) + (size_t)row * (K / 8) + kw0 / 8;
+                wq[t][i][s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + 16 * t));
+            }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // The slabs are complete once at most the X and weight loads issued after
+    // them are outstanding (every wave issues all of those).  Both waits are
+    // builtins: with a wait in inline assembly the compiler loses its count
+    // of the loads in flight and waits for all of them at the next use.  The
+    // barrier is assembly with a memory clobber, so that no LDS read moves
+    // above it.
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(MT * STEPS * 4 + STEPS * RT * NS));
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < STEPS; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) xa[mt][t][r] = permute_x(xa[mt][t][r]);
+
+    const uint16_t* sbl = reinterpret_cast<const uint16_t*>(sb_lds);
+    const int gshift = 5 + p.gshift;   // log2(group size)
+    f32x4 acc[RT][NS][MT];
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[i][s][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < STEPS; ++t)
+#pragma unroll
+        for (int i = 0; i < RT; ++i)
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                // the lane's 32 k lie in one group (group sizes 32, 64, 128)
+                const int gi = (kw0 + 128 * t) >> gshift;
+                const uint16_t* srow = sbl + (size_t)(2 * s) * alloc * 8 + (16 * i + r16) * groups;
+                const uint32_t sv = srow[gi], bv = srow[alloc * 8 + gi];
+                const f16x2 s2 = as_f16x2(sv | (sv << 16));
+                const f16x2 b2 = as_f16x2(bv | (bv << 16));
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const u32x4 b = dequant_word(wq[t][i][s][r], s2, b2);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+                        acc[i][s][mt] = mfma16(xa[mt][t][r], b, acc[i][s][mt]);
+                }
+            }
+
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) red[wave][i][s][mt][lane] = acc[i][s][mt];
+    __syncthreads();
+
+    // one output per thread: D[m][n] of a 16x16 tile sits in lane
+    // 16 * (m / 4) + n, element m % 4
+    for (int o = threadIdx.x; o < RT * MT * 256; o += 64 * W) {
+        const int i = o / (MT * 256), mt = (o >> 8) % MT, ml = (o >> 4) & 15, nl = o & 15;
+        const int m = mt * 16 + ml, n = n0 + 16 * i + nl;
+        if (m >= p.M || n >= p.N) continue;
+        const int src = 16 * (ml >> 2) + nl, e = ml & 3;
+        float v[NS];
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            float a = 0.0f;
+#pragma unroll
+            for (int w = 0; w < W; ++w) a += red[w][i][s][mt][src][e];
+            v[s] = a;
+        }
+        float out;
+        if constexpr (PAIR) {
+            out = glu_f32(p.epilogue == kEpiGeluMul, v[0], v[NS - 1]);
+        } else {
+            out = v[0];
+            if (p.bias) out += p.bias[n];
+            if (p.epilogue == kEpiGeluTanh) out = gelu_tanh_f32(out);
+        }
+        const size_t oi = (size_t)m * p.N + n;
+        if (!PAIR && p.epilogue == kEpiResidual)
+            reinterpret_cast<uint16_t*>(p.y)[oi] = residual_add_f16(p.residual[oi], out);
+        else
+            store_one(p, oi, out);
+    }
+}
+
+// Registers of a configuration, roughly: X fragments, the packed words in
+// flight, accumulators, and about 40 for the rest.
+constexpr int skinny_vgprs(int mt, int steps, int ns, int rt) {
+    return 16 * mt * steps + 4 * rt * ns * steps + 4 * rt * ns * mt + 40;
+}
+constexpr int kSkinnyMaxVgprs = 224;   // of the 256 one block of 8 waves may use
+
+template <int W, int MT, int STEPS, bool PAIR, int RT>
+hipError_t launch_cfg(const GemmParams& p, hipStream_t st) {
+    // two blocks per CU when a wave fits in 128 VGPRs
+    constexpr int OCC = (W == 8 && skinny_vgprs(MT, STEPS, PAIR ? 2 : 1, RT) <= 120) ? 2 : 1;
+    const dim3 grid((unsigned)((p.N + 16 * RT - 1) / (16 * RT))), block(64 * W);
+    const size_t lds = (size_t)(PAIR ? 4 : 2) * slab_alloc(16 * RT, p.groups) * 16;
+    hipLaunchKernelGGL((q4_skinny_kernel<W, MT, STEPS, PAIR, RT, OCC>), grid, block, lds, st, p);
+    return hipGetLastError();
+}
+
+template <int W, int MT, int STEPS>
+hipError_t launch_steps(const GemmParams& p, const SkinnyPlan& pl, hipStream_t st) {
+    const bool pair = p.w1 != nullptr;
+    if (pl.RT == 2) {
+        if constexpr (W == 8 && skinny_vgprs(MT, STEPS, 2, 2) <= kSkinnyMaxVgprs)
+            return pair ? launch_cfg<W, MT, STEPS, true, 2>(p, st)
+                        : launch_cfg<W, MT, STEPS, false, 2>(p, st);
+        return hipErrorInvalidValue;
+    }
+    if (pair) {
+        // a gated pair of 5 steps does not fit the 128 VGPRs of 16 waves
+        if constexpr (W == 16 && STEPS == 5) return hipErrorInvalidValue;
+        else return launch_cfg<W, MT, STEPS, true, 1>(p, st);
+    }
+    return launch_cfg<W, MT, STEPS, false, 1>(p, st);
+}
+
+}  // namespace
+
+bool skinny_plan(const GemmParams& p, bool a_bf16, SkinnyPlan* out) {
+    if (a_bf16 || p.M < 1 || p.M > 32 || p.N < 1 || p.K <= 0) return false;
+    if (p.gshift < 0 || p.gshift > 2) return false;
+    if ((long)p.M * p.K * 2 > 0x7fffffffL) return false;   // X buffer offsets are 32-bit
+    const bool pair = p.w1 != nullptr;
+    if (pair && p.epilogue != kEpiSiluMul && p.epilogue != kEpiGeluMul) return false;
+    if (!pair && p.epilogue != kEpiNone && p.epilogue != kEpiGeluTanh &&
+        p.epilogue != kEpiResidual)
+        return false;
+    const int mt = p.M <= 16 ? 1 : 2;
+    SkinnyPlan pl{0, mt, 0, 1};
+    // 8 waves of 1..6 steps (1..4 with 32 activation rows), else 16 waves of
+    // 1..5 steps (1..4 for a gated pair; 16 activation rows)
+    if (p.K % 1024 == 0 && p.K / 1024 <= (mt == 1 ? 6 : 4)) {
+        pl.W = 8;
+        pl.STEPS = p.K / 1024;
+    } else if (mt == 1 && p.K % 2048 == 0 && p.K / 2048 <= (pair ? 4 : 5)) {
+        // (a gated pair of 5 steps does not fit the 128 VGPRs of 16 waves)
+        pl.W = 16;
+        pl.STEPS = p.K / 2048;
+    } else {
+        return false;
+    }
+    // Two row tiles per block (the X slice serves twice the weight rows) when
+    // that still leaves one block per CU, with 8 waves.
+    if (pl.W == 8 && p.M > 4 && (p.N + 31) / 32 >= kCUs &&
+        skinny_vgprs(mt, pl.STEPS, 2, 2) <= kSkinnyMaxVgprs)
+        pl.RT = 2;
+    // scales and biases are staged with 16-byte loads
+    const uintptr_t sb = reinterpret_cast<uintptr_t>(p.s0) | reinterpret_cast<uintptr_t>(p.b0) |
+                         (pair ? reinterpret_cast<uintptr_t>(p.s1) | reinterpret_cast<uintptr_t>(p.b1)
+                               : 0);
+    if ((sb & 15) != 0) return false;
+    *out = pl;
+    return true;
+}
+
+hipError_t launch_skinny(const GemmParams& p, const SkinnyPlan& pl, hipStream_t st) {
+    if (pl.W == 8 && pl.MT == 1) {
+        switch (pl.STEPS) {
+            case 1: return launch_steps<8, 1, 1>(p, pl, st);
+            case 2: return launch_steps<8, 1, 2>(p, pl, st);
+            case 3: return launch_steps<8, 1, 3>(p, pl, st);
+            case 4: return launch_steps<8, 1, 4>(p, pl, st);
+            case 5: return launch_steps<8, 1, 5>(p, pl, st);
+            case 6: return launch_steps<8, 1, 6>(p, pl, st);
+        }
+    } else if (pl.W == 8 && pl.MT == 2) {
+        switch (pl.STEPS) {
+            case 1: return launch_steps<8, 2, 1>(p, pl, st);
+            case 2: return launch_steps<8, 2, 2>(p, pl, st);
+            case 3: return launch_steps<8, 2, 3>(p, pl, st);
+            case 4: return launch_steps<8, 2, 4>(p, pl, st);
+        }
+    } else if (pl.W == 16 && pl.MT == 1) {
+        switch (pl.STEPS) {
+            case 1: return launch_steps<16, 1, 1>(p, pl, st);
+            case 2: return launch_steps<16, 1, 2>(p, pl, st);
+            case 3: return launch_steps<16, 1, 3>(p, pl, st);
+            case 4: return launch_steps<16, 1, 4>(p, pl, st);
+            case 5: return launch_steps<16, 1, 5>(p, pl, st);
+        }
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace sltx
