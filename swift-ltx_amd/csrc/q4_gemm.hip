@@ -67,23 +67,24 @@ __device__ __forceinline__ int swz(int row, int col16) {
 }
 
 // One 32-bit word (8 nibbles, k order) -> 8 fp16 values s*q+b.  Nibbles are
-// spread to bytes, paired with v_perm_b32, turned into 1024+q by mantissa
-// insertion, reduced to q exactly, then one fp16 FMA q*s+b (one rounding).
+// spread to bytes and interleaved back into k order with v_perm_b32; then
+// v_cvt_scalef32_pk_f16_fp8 turns two bytes into two exact fp16 integers (an
+// fp8 e4m3 byte b < 16 is b * 2^-9, and the instruction's scale, of which only
+// the exponent counts, is 2^9) and one fp16 FMA q*s+b rounds once.
 __device__ __forceinline__ u32x4 dequant_word_f16(uint32_t w, f16x2 s2, f16x2 b2) {
-    const f16x2 m1024 = {(f16)-1024.0f, (f16)-1024.0f};
     const uint32_t lo = w & 0x0F0F0F0Fu;          // bytes q6 q4 q2 q0
     const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;   // bytes q7 q5 q3 q1
-    uint32_t pr[4];
-    pr[0] = __builtin_amdgcn_perm(hi, lo, 0x0C040C00u) | kMagic1024x2;  // q0, q1
-    pr[1] = __builtin_amdgcn_perm(hi, lo, 0x0C050C01u) | kMagic1024x2;  // q2, q3
-    pr[2] = __builtin_amdgcn_perm(hi, lo, 0x0C060C02u) | kMagic1024x2;  // q4, q5
-    pr[3] = __builtin_amdgcn_perm(hi, lo, 0x0C070C03u) | kMagic1024x2;  // q6, q7
+    const uint32_t q03 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);   // bytes q3 q2 q1 q0
+    const uint32_t q47 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);   // bytes q7 q6 q5 q4
+    const float k512 = 512.0f;
+    f16x2 q[4];
+    q[0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(q03, k512, false);   // q0, q1
+    q[1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(q03, k512, true);    // q2, q3
+    q[2] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(q47, k512, false);   // q4, q5
+    q[3] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(q47, k512, true);    // q6, q7
     u32x4 o;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const f16x2 q = as_f16x2(pr[e]) + m1024;               // exact small integers
-        o[e] = as_u32(__builtin_elementwise_fma(q, s2, b2));    // v_pk_fma_f16
-    }
+    for (int e = 0; e < 4; ++e) o[e] = as_u32(__builtin_elementwise_fma(q[e], s2, b2));   // v_pk_fma_f16
     return o;
 }
 
