@@ -555,27 +555,41 @@ def token_select_leg(pkg, torch, gen, dev, vocab=128256):
     """Token selection after the lm_head (LlamaModel.swift:153,161): argmax
     and temperature 0.7 / top-p 0.9 / repetition penalty 1.1 sampling over
     Llama 3.2's 128256 fp16 logits with 64 seen ids, for N(0, 3^2) logits (a
-    nucleus of a few tokens, as for a trained model) and for flat logits
-    (every token tied: the nucleus is the whole vocabulary).  Each is a graph
+    nucleus of a few tokens, as for a trained model) and for the degenerate
+    distributions that are the sampler's worst cases: flat (every token tied:
+    the nucleus is the whole vocabulary), two tied levels (half the tokens at
+    each of two probabilities), near-flat (N(0, 1e-3^2) logits: one level-0
+    bin of 128256 distinct-ish keys) and two dense clusters.  Each is a graph
     of 10 calls on its own stream (after one eager call there, which sizes the
-    workspace); us per call includes the graph's launch gaps."""
+    workspace); us per call includes the graph's launch gaps.  "worst_us" is
+    the largest sampling median."""
     peaked = (3.0 * torch.randn(vocab, generator=gen, device=dev)).half()
     flat = torch.zeros(vocab, device=dev, dtype=torch.float16)
+    half = torch.rand(vocab, generator=gen, device=dev) < 0.5
+    two_levels = torch.where(half, 0.0, 1.0).half()
+    near_flat = (1e-3 * torch.randn(vocab, generator=gen, device=dev)).half()
+    clusters = (torch.where(half, 0.0, 0.3) +
+                1e-3 * torch.randn(vocab, generator=gen, device=dev)).half()
     seen = torch.randint(0, vocab, (64,), generator=gen, device=dev, dtype=torch.int32)
     out = torch.empty(1, device=dev, dtype=torch.int32)
     res = {}
+
+    def samp(lg):
+        return lambda s: pkg.sample(lg, 0.7, 0.9, 1.1, seen, 0.5, out=out, stream=s)
+
     cases = (("argmax", lambda s: pkg.argmax(peaked, out=out, stream=s)),
-             ("sample_top_p", lambda s: pkg.sample(peaked, 0.7, 0.9, 1.1, seen, 0.5, out=out,
-                                                   stream=s)),
-             ("sample_top_p_flat", lambda s: pkg.sample(flat, 0.7, 0.9, 1.1, seen, 0.5, out=out,
-                                                        stream=s)))
+             ("sample_top_p", samp(peaked)), ("sample_top_p_flat", samp(flat)),
+             ("sample_top_p_two_levels", samp(two_levels)),
+             ("sample_top_p_near_flat", samp(near_flat)),
+             ("sample_top_p_two_clusters", samp(clusters)))
     for name, fn in cases:
         s = torch.cuda.Stream()
         g = capture(torch, lambda: [fn(s) for _ in range(10)], s, warm=lambda: fn(s))
         res[name] = replay_stats(torch, g.replay, 10)
         del g
+    res["worst_us"] = max(v["median_us"] for k, v in res.items() if k.startswith("sample_"))
     res["vocab"] = vocab
-    res["launches"] = {"argmax": 2, "sample_top_p": 4}
+    res["launches"] = {"argmax": 2, "sample_top_p": 5}
     return res
 
 

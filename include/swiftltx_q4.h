@@ -332,7 +332,7 @@ int sltx_sample_top_p(const void* logits, int32_t dtype, int32_t n, float temper
  * captured into a HIP graph on a stream that never ran the sampler eagerly,
  * tight serving loops, and harnesses that forbid hipMalloc.  Limit:
  * n <= 262144 logits (SLTX_ERR_INVALID beyond).  The scratch is one
- * 3,197,184-byte device array per GPU, held until the process ends and
+ * 3,315,968-byte device array per GPU, held until the process ends and
  * shared by every call on that GPU: calls that overlap on one GPU (on other
  * streams or threads) race on it and must be ordered by the caller. */
 int sltx_sample_top_p_noalloc(const void* logits, int32_t dtype, int32_t n, float temperature,

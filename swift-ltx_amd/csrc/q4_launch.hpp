@@ -71,6 +71,26 @@ struct EmbedParams {
 };
 
 // Token selection after the lm_head (q4_sample.hip).
+// Written by the sampler's gather kernel (and, mode 1, its narrow kernel)
+// for the kernels after it.  mode 0: the buckets are level-0
+// bins (key >> 20) and the gather kernel compacted the candidates; mode 1:
+// the candidate bins held too many tokens, and a range histogram splits them
+// into finer buckets -- segment A, level-0 bin a_bin in 2048 buckets of 2^9
+// keys, and segment B, bins [b_lo, b_hi] (empty if b_lo > b_hi) in 2048
+// buckets of 2^b_shift keys.  Tied buckets (one key) get per-chunk counts of
+// their key (up to 4: tkey).
+struct SampleCtl {
+    uint32_t ccount;              // compacted candidates
+    int mode;
+    int cut_found;                // the top-p target lies within the total mass
+    int a_bin, b_lo, b_hi, b_shift;
+    int ntied;
+    uint32_t tkey[4];
+    unsigned long long above;     // mode 1: mass of the keys above the range
+    unsigned long long gap;       // mode 1: mass of the bins between the segments
+    unsigned long long total;     // mass of all tokens
+};
+
 struct SampleParams {
     const void* logits;     // [n] fp16 or fp32
     int dtype;              // kF16 / kF32
@@ -95,7 +115,14 @@ struct SampleParams {
     float* spart;           // block exp-sums (relative to the block maxima)
     uint32_t* h0cnt;        // level-0 histogram (4096 bins)
     unsigned long long* h0mass;
-    uint32_t* ccount;       // compacted candidates
+    uint32_t* h0min;        // smallest and largest key (probability bits) of each
+    uint32_t* h0max;        // level-0 bin: a bin of equal keys is all tied
+    uint32_t* h1cnt;        // range histogram (4096 buckets), same fields
+    unsigned long long* h1mass;
+    uint32_t* h1min;
+    uint32_t* h1max;
+    SampleCtl* ctl;         // candidate count and where the candidates come from
+    uint32_t* tcnt;         // [4][ceil(n / 1024)] tied-key counts per 1024-token chunk
     uint2* cand;            // [n] (probability bits, id)
 };
 

@@ -26,18 +26,28 @@
 // weighted radix selects over D, 12 bits a level:
 //   sample_scale    l = penalised logit / temperature (the block's seen ids
 //                   marked in an LDS bitmap); block max and exp-sum; clears
-//                   the level-0 histogram
+//                   the level-0 and range histograms
 //   sample_prob     p = exp(l - max) / sum; level-0 histogram (p bits
 //                   31..20: count and mass per bin)
 //   sample_gather   each block finds, from the histogram, the bin holding the
-//                   cutoff and the bins the draw can reach, and compacts their
-//                   tokens (no grid-wide fence or last-block hand-off: on a
-//                   chip whose XCDs have separate L2s those cost more than
-//                   re-reading the 48 KB histogram per block)
+//                   cutoff and the bins the draw can reach; if their untied
+//                   tokens fit the select kernel's LDS it compacts them
+//                   (mode 0), otherwise it builds a range histogram over
+//                   their keys in finer buckets (mode 1).  Bins and buckets
+//                   of one key (ties) are never compacted: their tokens are
+//                   found by rank, from counts of the tied key per 1024-token
+//                   chunk kept during compaction.  (No grid-wide fence or
+//                   last-block hand-off: on a chip whose XCDs have separate
+//                   L2s those cost more than re-reading the 48 KB histogram
+//                   per block.)
+//   sample_narrow   mode 1: the same from the range histogram, compacting
+//                   the untied tokens of the buckets that matter
 //   sample_select   one workgroup: up to 64 candidates are sorted in one
-//                   wave's registers and scanned; more go through levels 1-4
-//                   (in LDS when they fit), a level stopping once its bin
-//                   holds a single token
+//                   wave's registers and scanned; more go through the levels
+//                   below their bucket, 12 bits of D a level (in LDS when
+//                   they fit), until a level's bin holds at most 64 tokens,
+//                   which one wave sorts
+#include <algorithm>
 #include <mutex>
 
 #include "q4_common.hpp"
@@ -51,11 +61,62 @@ constexpr int kMaxBlocks = 256;
 constexpr int kSelThreads = 1024;   // sample_select
 constexpr int kBins = 4096;         // 12-bit digits
 constexpr int kCandLds = 8192;      // candidates sample_select holds in LDS
-constexpr int kSelUnroll = 8;     // candidates each select thread loads before using them
+constexpr int kSelUnroll = 8;      // candidates each select thread loads before using them
+constexpr int kNthUnroll = 16;     // 16-byte key loads a lane has in flight in nth_with_key
+constexpr int kTiedSlots = 4;      // tied keys with per-chunk counts
 constexpr uint32_t kIdMask = 0xFFFFFFu;
 // seen-id bitmap of one scale block: up to 64 quads a thread (n <= 2^24
 // with 256 blocks of 256 threads), 4 bits a quad
 constexpr int kSeenWords = 64 * 4 * kGridThreads / 32;
+
+// Wave-wide inclusive prefix sums in lane order through DPP: row shifts by
+// 1, 2, 4, 8 (out-of-row sources read 0), then the last lane of rows 0 / 2
+// added to rows 1 / 3 and lane 31 to rows 2-3 -- six steps at VALU latency
+// instead of LDS-routed shuffles.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_move(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xF, true);
+}
+
+__device__ __forceinline__ uint32_t wave_incl_sum(uint32_t x) {
+    x += dpp_move<0x111, 0xF>(x);
+    x += dpp_move<0x112, 0xF>(x);
+    x += dpp_move<0x114, 0xF>(x);
+    x += dpp_move<0x118, 0xF>(x);
+    x += dpp_move<0x142, 0xA>(x);
+    x += dpp_move<0x143, 0xC>(x);
+    return x;
+}
+
+template <int CTRL, int ROWS>
+__device__ __forceinline__ unsigned long long dpp_move(unsigned long long v) {
+    const uint32_t lo = dpp_move<CTRL, ROWS>((uint32_t)v);
+    const uint32_t hi = dpp_move<CTRL, ROWS>((uint32_t)(v >> 32));
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+__device__ __forceinline__ unsigned long long wave_incl_sum(unsigned long long x) {
+    x += dpp_move<0x111, 0xF>(x);
+    x += dpp_move<0x112, 0xF>(x);
+    x += dpp_move<0x114, 0xF>(x);
+    x += dpp_move<0x118, 0xF>(x);
+    x += dpp_move<0x142, 0xA>(x);
+    x += dpp_move<0x143, 0xC>(x);
+    return x;
+}
+
+// The whole wave's sum, in every lane.
+template <class T>
+__device__ __forceinline__ T wave_sum(T x) {
+    const T s = wave_incl_sum(x);
+    if constexpr (sizeof(T) == 8) {
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)s, 63);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(s >> 32), 63);
+        return (T)(((unsigned long long)hi << 32) | lo);
+    } else {
+        return (T)__builtin_amdgcn_readlane((int)s, 63);
+    }
+}
 
 __device__ __forceinline__ float load_logit(const void* p, int dtype, int i) {
     if (dtype == kF32) return reinterpret_cast<const float*>(p)[i];
@@ -108,14 +169,102 @@ __device__ __forceinline__ int hist_add(bool ok, int d, uint32_t key, unsigned l
             (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)m, lead);
         sum = m0 * (unsigned long long)__popcll(act);
     } else {
-        sum = ok ? m : 0ull;
-        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+        sum = wave_sum(ok ? m : 0ull);
     }
     if (lane == lead) {
         atomicAdd(&cnt[d0], (uint32_t)__popcll(act));
         if (sum) atomicAdd(&mass[d0], sum);
     }
     return lead;
+}
+
+// Smallest and largest key of bin d for the lanes with ok set, kept in LDS
+// next to the histogram (lead: hist_add's result, the lane that added for
+// the whole wave, which then holds every active lane in one bin).
+__device__ __forceinline__ void key_minmax(bool ok, int d, uint32_t key, int lead, uint32_t* kmin,
+                                           uint32_t* kmax) {
+    if (lead < 0) {
+        if (ok) {
+            atomicMin(&kmin[d], key);
+            atomicMax(&kmax[d], key);
+        }
+        return;
+    }
+    const unsigned long long act = __ballot(ok);
+    const uint32_t k0 = (uint32_t)__builtin_amdgcn_readlane((int)key, lead);
+    uint32_t lo = k0, hi = k0;
+    if (__ballot(ok && key == k0) != act) {
+        lo = ok ? key : 0xFFFFFFFFu;
+        hi = ok ? key : 0u;
+        for (int o = 32; o > 0; o >>= 1) {
+            lo = min(lo, (uint32_t)__shfl_xor((int)lo, o, 64));
+            hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, 64));
+        }
+    }
+    if ((int)(threadIdx.x & 63) == lead) {
+        atomicMin(&kmin[d], lo);
+        atomicMax(&kmax[d], hi);
+    }
+}
+
+// The buckets the select positions are found in.  Mode 0: level-0 bins,
+// key >> 20.  Mode 1 (the range histogram): segment A, keys of level-0 bin
+// a_bin in buckets [0, kSplit) of 2^9 keys; segment B, keys of bins
+// [b_lo, b_hi] in buckets [kSplit, kBins) of 2^b_shift keys; the bins
+// between the segments are in no bucket (their mass, `gap`, is added to
+// segment A's running mass) and no candidate can lie there.
+constexpr int kSplit = kBins / 2;
+
+struct Buckets {
+    const uint32_t* cnt;
+    const unsigned long long* mass;
+    const uint32_t* kmin;
+    const uint32_t* kmax;
+    int ranged;
+    uint32_t a_base, b_base;
+    unsigned long long b_lim;
+    int b_shift;
+    unsigned long long gap;
+
+    // bucket of a key, kBins if none
+    __device__ int of(uint32_t key) const {
+        if (!ranged) return (int)(key >> 20);
+        if (key - a_base < (1u << 20)) return (int)((key - a_base) >> 9);
+        if (key >= b_base && (unsigned long long)key < b_lim)
+            return kSplit + (int)((key - b_base) >> b_shift);
+        return kBins;
+    }
+    // bits of the order key D below bucket b's key prefix, and that prefix
+    __device__ int low_bits(int b) const { return !ranged ? 44 : b < kSplit ? 33 : b_shift + 24; }
+    __device__ unsigned long long prefix(int b) const {
+        if (!ranged) return (unsigned long long)b << 44;
+        if (b < kSplit) return (unsigned long long)((a_base >> 9) + (uint32_t)b) << 33;
+        return (unsigned long long)((b_base >> b_shift) + (uint32_t)(b - kSplit)) << (b_shift + 24);
+    }
+};
+
+__device__ __forceinline__ Buckets level0_buckets(const SampleParams& p) {
+    return Buckets{p.h0cnt, p.h0mass, p.h0min, p.h0max, 0, 0u, 0u, 0ull, 20, 0ull};
+}
+
+// Segments A = bin a, B = bins [blo, bhi] (b_shift <= 20: buckets aligned).
+__device__ __forceinline__ Buckets range_buckets(const SampleParams& p, int a, int blo, int bhi,
+                                                 int b_shift, unsigned long long gap) {
+    const bool b_empty = blo > bhi;
+    return Buckets{p.h1cnt, p.h1mass, p.h1min, p.h1max, 1, (uint32_t)a << 20,
+                   b_empty ? 0u : (uint32_t)blo << 20,
+                   b_empty ? 0ull : (unsigned long long)(bhi + 1) << 20, b_shift, gap};
+}
+
+__device__ __forceinline__ Buckets range_buckets(const SampleParams& p, const SampleCtl& c) {
+    return range_buckets(p, c.a_bin, c.b_lo, c.b_hi, c.b_shift, c.gap);
+}
+
+// Bucket b holds more than one token and all share one key (LDS bitmap of
+// BinScan::load_tied): in the order (p descending, id ascending) its tokens
+// follow each other by id, each adding the same mass.
+__device__ __forceinline__ bool is_tied(const uint32_t* tied_bm, int b) {
+    return b >= 0 && b < kBins && ((tied_bm[b >> 5] >> (b & 31)) & 1u);
 }
 
 __device__ __forceinline__ uint32_t lanes_below(unsigned long long mask) {
@@ -171,19 +320,11 @@ __device__ __forceinline__ void finish_select(const SampleParams& p, int id) {
 template <int NT>
 __device__ unsigned long long block_excl_scan(unsigned long long v, unsigned long long* wsum) {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    unsigned long long x = v;
-    for (int o = 1; o < 64; o <<= 1) {
-        const unsigned long long y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
-    }
+    const unsigned long long x = wave_incl_sum(v);
     if (lane == 63) wsum[wid] = x;
     __syncthreads();
     if (wid == 0) {
-        unsigned long long w = lane < NT / 64 ? wsum[lane] : 0ull;
-        for (int o = 1; o < NT / 64; o <<= 1) {
-            const unsigned long long y = __shfl_up(w, o, 64);
-            if (lane >= o) w += y;
-        }
+        const unsigned long long w = wave_incl_sum(lane < NT / 64 ? wsum[lane] : 0ull);
         if (lane < NT / 64) wsum[lane] = w;
     }
     __syncthreads();
@@ -201,21 +342,24 @@ struct BinSel {
 struct SelScratch {
     unsigned long long wsum[16];
     int best;
+    int chunk;                 // nth_in_chunks: the chunk; select_in_bin: the id
+    int nfew;
+    unsigned long long rem;    // nth_in_chunks: rank left; select_in_bin: inclusive mass
 };
 
-// kBins bins in descending bin order, after `above` mass, spread over the
-// block (BPT consecutive bins a thread).  load() reads the bins and scans
-// their masses; find(target) gives the highest non-empty bin whose inclusive
-// running mass reaches target (found), its exclusive / inclusive mass and
-// count, and the total.  Whole block; cnt and mass may be global or LDS.
-// Both end synchronised.
+// kBins buckets in descending order, after `above` mass, spread over the
+// block (BPT consecutive buckets a thread).  load() reads the buckets and
+// scans their masses; find(target) gives the highest non-empty bucket whose
+// inclusive running mass reaches target (found), its exclusive / inclusive
+// mass and count, and the total.  Whole block; cnt and mass may be global or
+// LDS.  Both end synchronised.
 template <int NT>
 struct BinScan {
     static constexpr int BPT = kBins / NT;
     uint32_t c[BPT];
     unsigned long long m[BPT];
     unsigned long long excl, tot;
-    int top;   // this thread's bins: top, top-1, ..., top-BPT+1
+    int top;   // this thread's buckets: top, top-1, ..., top-BPT+1
 
     __device__ void load(const uint32_t* cnt, const unsigned long long* mass,
                          unsigned long long above, SelScratch& sc) {
@@ -230,6 +374,34 @@ struct BinScan {
         excl = above + block_excl_scan<NT>(tot, sc.wsum);
     }
 
+    // load() over a histogram with key extremes: also marks the tied buckets
+    // in tied_bm (kBins bits, LDS; written whole), and in mode 1 adds the
+    // mass between the segments to segment A's running mass.
+    __device__ void load_tied(const Buckets& bk, unsigned long long above, SelScratch& sc,
+                              uint32_t* tied_bm) {
+        top = kBins - 1 - (int)threadIdx.x * BPT;
+        tot = 0ull;
+        uint32_t lo[BPT], hi[BPT];
+#pragma unroll
+        for (int k = 0; k < BPT; ++k) {
+            c[k] = bk.cnt[top - k];
+            m[k] = bk.mass[top - k];
+            lo[k] = bk.kmin[top - k];
+            hi[k] = bk.kmax[top - k];
+        }
+        uint32_t t = 0u;
+#pragma unroll
+        for (int k = 0; k < BPT; ++k) {
+            tot += m[k];
+            if (c[k] > 1u && lo[k] == hi[k]) t |= 1u << ((top - k) & 31);
+        }
+        // the 32 / BPT consecutive threads of one bitmap word
+        for (int o = 1; o < 32 / BPT; o <<= 1) t |= (uint32_t)__shfl_xor((int)t, o, 64);
+        if ((threadIdx.x & (32 / BPT - 1)) == 0) tied_bm[top >> 5] = t;
+        excl = above + block_excl_scan<NT>(tot, sc.wsum) +
+               (bk.ranged && top < kSplit ? bk.gap : 0ull);
+    }
+
     __device__ void find(unsigned long long target, BinSel& out, SelScratch& sc) {
         if (threadIdx.x == 0) sc.best = -1;
         __syncthreads();
@@ -240,7 +412,11 @@ struct BinScan {
             run += m[k];
             if (best < 0 && c[k] && run >= target) best = top - k;
         }
-        if (best >= 0) atomicMax(&sc.best, best);
+        // buckets descend with the thread index: the wave's first hit holds
+        // its highest, so one LDS atomic a wave (same-address atomics
+        // serialise)
+        const unsigned long long hit = __ballot(best >= 0);
+        if (hit && (int)(threadIdx.x & 63) == __ffsll((long long)hit) - 1) atomicMax(&sc.best, best);
         __syncthreads();
         const int B = sc.best;
         if ((int)threadIdx.x == NT - 1) {
@@ -273,46 +449,58 @@ struct LevelHist {
     uint32_t id[kBins];
 };
 
-// Levels 1-4 of the weighted select inside level-0 bin `bin` (exclusive mass
-// `above`): the token whose inclusive running mass first reaches target.
-// Whole block; returns the id (-1 only for non-finite input) and sets cum_out
-// to its inclusive mass.
-__device__ int select_in_bin(const uint2* cand, int C, int bin, unsigned long long above,
-                             unsigned long long target, LevelHist& H, SelScratch& sc, BinSel& bs,
+// Calls f(c, e) for every candidate index c < C (e = cand[c]) in a
+// wave-uniform loop (hist_add needs all 64 lanes): candidate c goes to wave
+// (c / 64) % 16, each lane loading kSelUnroll candidates before using any
+// (memory latencies overlap when the list is in global memory); lanes past
+// C get c >= C.
+template <class F>
+__device__ __forceinline__ void for_each_cand(const uint2* cand, int C, F f) {
+    const int lane = threadIdx.x & 63;
+    for (int c0 = (int)(threadIdx.x & ~63u); c0 < C; c0 += kSelThreads * kSelUnroll) {
+        uint2 ev[kSelUnroll];
+#pragma unroll
+        for (int u = 0; u < kSelUnroll; ++u) {
+            const int c = c0 + u * kSelThreads + lane;
+            ev[u] = c < C ? cand[c] : make_uint2(0u, 0u);
+        }
+#pragma unroll
+        for (int u = 0; u < kSelUnroll; ++u) f(c0 + u * kSelThreads + lane, ev[u]);
+    }
+}
+
+// The levels below bucket `bucket` (exclusive mass `above`) of the weighted
+// select over the 56-bit order key D: 12 bits a level (fewer for the last);
+// once a level's bin holds at most 64 tokens, one wave sorts them.  The
+// token whose inclusive running mass first reaches target.  Whole block;
+// returns the id (-1 only for non-finite input) and sets cum_out to its
+// inclusive mass.
+__device__ int select_in_bin(const uint2* cand, int C, const Buckets& bk, int bucket,
+                             uint32_t count, unsigned long long above, unsigned long long target,
+                             LevelHist& H, SelScratch& sc, BinSel& bs,
                              unsigned long long& cum_out) {
-    const int tid = threadIdx.x;
-    unsigned long long P = (unsigned long long)bin << 44;
-    unsigned long long Mk = 0xFFFull << 44;
-    for (int lev = 1; lev <= 4; ++lev) {
-        const int shift = lev == 1 ? 32 : lev == 2 ? 20 : lev == 3 ? 8 : 0;
-        const unsigned long long wmask = lev == 4 ? 0xFFull : 0xFFFull;
+    const int tid = threadIdx.x, lane = tid & 63;
+    int pos = bk.low_bits(bucket);
+    unsigned long long P = bk.prefix(bucket);
+    unsigned long long Mk = (0xFFFFFFFFFFFFFFull >> pos) << pos;
+    uint32_t left = count;   // tokens under the prefix
+    while (left > 64u && pos > 0) {
+        const int shift = pos > 12 ? pos - 12 : 0;
+        const unsigned long long wmask = (1ull << (pos - shift)) - 1ull;
+        pos = shift;
         for (int b = tid; b < kBins; b += kSelThreads) {
             H.cnt[b] = 0u;
             H.mass[b] = 0ull;
         }
         __syncthreads();
-        // Wave-uniform trip count (hist_add needs all 64 lanes); each lane
-        // loads kSelUnroll candidates before using any, so that many memory
-        // latencies overlap when the list is in global memory.
-        for (int c0 = (tid & ~63) * kSelUnroll; c0 < C; c0 += kSelThreads * kSelUnroll) {
-            uint2 ev[kSelUnroll];
-#pragma unroll
-            for (int u = 0; u < kSelUnroll; ++u) {
-                const int c = c0 + u * 64 + (tid & 63);
-                ev[u] = c < C ? cand[c] : make_uint2(0u, 0u);
-            }
-#pragma unroll
-            for (int u = 0; u < kSelUnroll; ++u) {
-                const int c = c0 + u * 64 + (tid & 63);
-                const uint2 e = ev[u];
-                const unsigned long long D = order_key(e.x, e.y);
-                const bool ok = c < C && (D & Mk) == P;
-                const int dg = (int)((D >> shift) & wmask);
-                const int lead = hist_add(ok, dg, e.x, ok ? mass_of(e.x) : 0ull, H.cnt, H.mass);
-                // read only when the bin holds one token
-                if (ok && (lead < 0 || lead == (tid & 63))) H.id[dg] = e.y;
-            }
-        }
+        for_each_cand(cand, C, [&](int c, uint2 e) {
+            const unsigned long long D = order_key(e.x, e.y);
+            const bool ok = c < C && (D & Mk) == P;
+            const int dg = (int)((D >> shift) & wmask);
+            const int lead = hist_add(ok, dg, e.x, ok ? mass_of(e.x) : 0ull, H.cnt, H.mass);
+            // read only when the bin holds one token
+            if (ok && (lead < 0 || lead == lane)) H.id[dg] = e.y;
+        });
         __syncthreads();
         BinScan<kSelThreads> scan;
         scan.load(H.cnt, H.mass, above, sc);
@@ -327,12 +515,50 @@ __device__ int select_in_bin(const uint2* cand, int C, int bin, unsigned long lo
             __syncthreads();
             return id;
         }
+        left = bs.cnt;
     }
-    return -1;   // not reached: the full key is unique
+    // at most 64 tokens left under the prefix: gather them (H.id is free),
+    // and wave 0 sorts them by D and scans their masses after `above`
+    if (tid == 0) sc.nfew = 0;
+    __syncthreads();
+    for_each_cand(cand, C, [&](int c, uint2 e) {
+        if (c < C && (order_key(e.x, e.y) & Mk) == P) {
+            const int slot = atomicAdd(&sc.nfew, 1);
+            if (slot < 64) {
+                H.id[2 * slot] = e.x;
+                H.id[2 * slot + 1] = e.y;
+            }
+        }
+    });
+    __syncthreads();
+    if (tid < 64) {
+        const bool v = lane < sc.nfew;
+        const uint32_t kx = v ? H.id[2 * lane] : 0u, ky = v ? H.id[2 * lane + 1] : 0u;
+        unsigned long long sk = v ? (1ull << 63) | order_key(kx, ky) : 0ull;
+        for (int k = 2; k <= 64; k <<= 1) {
+            for (int j = k >> 1; j > 0; j >>= 1) {
+                const unsigned long long o = __shfl_xor(sk, j, 64);
+                const bool take_max = ((lane & j) == 0) == ((lane & k) == 0);
+                sk = take_max ? (sk > o ? sk : o) : (sk < o ? sk : o);
+            }
+        }
+        const bool valid = (sk >> 63) != 0ull;
+        const unsigned long long S = wave_incl_sum(valid ? mass_of((uint32_t)(sk >> 24)) : 0ull);
+        const unsigned long long hit = __ballot(valid && above + S >= target);
+        if (lane == (hit ? __ffsll((long long)hit) - 1 : 0)) {
+            sc.rem = hit ? above + S : 0ull;
+            sc.chunk = hit ? (int)(kIdMask - (uint32_t)(sk & kIdMask)) : -1;
+        }
+    }
+    __syncthreads();
+    const int id = sc.chunk;
+    cum_out = sc.rem;
+    __syncthreads();
+    return id;
 }
 
-// The single token of level-0 bin `bin` among the candidates.
-__device__ int only_in_bin(const uint2* cand, int C, int bin, int* s_id) {
+// The single token of bucket `bin` among the candidates.
+__device__ int only_in_bin(const uint2* cand, int C, const Buckets& bk, int bin, int* s_id) {
     if (threadIdx.x == 0) *s_id = -1;
     __syncthreads();
     for (int c0 = threadIdx.x; c0 < C; c0 += kSelThreads * kSelUnroll) {
@@ -344,7 +570,7 @@ __device__ int only_in_bin(const uint2* cand, int C, int bin, int* s_id) {
         }
 #pragma unroll
         for (int u = 0; u < kSelUnroll; ++u)
-            if (c0 + u * kSelThreads < C && (int)(ev[u].x >> 20) == bin) *s_id = (int)ev[u].y;
+            if (c0 + u * kSelThreads < C && bk.of(ev[u].x) == bin) *s_id = (int)ev[u].y;
     }
     __syncthreads();
     const int r = *s_id;
@@ -438,8 +664,14 @@ __global__ __launch_bounds__(kGridThreads) void sample_scale_kernel(SampleParams
     for (int b = blockIdx.x * kGridThreads + threadIdx.x; b < kBins; b += T) {
         p.h0cnt[b] = 0u;
         p.h0mass[b] = 0ull;
+        p.h0min[b] = 0xFFFFFFFFu;
+        p.h0max[b] = 0u;
+        p.h1cnt[b] = 0u;
+        p.h1mass[b] = 0ull;
+        p.h1min[b] = 0xFFFFFFFFu;
+        p.h1max[b] = 0u;
     }
-    if (blockIdx.x == 0 && threadIdx.x == 0) *p.ccount = 0u;
+    if (blockIdx.x == 0 && threadIdx.x == 0) p.ctl->ccount = 0u;
     const int n_seen = seen_count(p);
     if (n_seen > 0) {
         for (int w = threadIdx.x; w < kSeenWords; w += kGridThreads) seen_bm[w] = 0u;
@@ -506,12 +738,15 @@ __global__ __launch_bounds__(kGridThreads) void sample_scale_kernel(SampleParams
 __global__ __launch_bounds__(kGridThreads) void sample_prob_kernel(SampleParams p) {
     __shared__ uint32_t hc[kBins];
     __shared__ unsigned long long hm[kBins];
+    __shared__ uint32_t hlo[kBins], hhi[kBins];
     __shared__ float s_sum, s_max, wred[kGridThreads / 64];
     const int n = p.n;
     const int T = gridDim.x * kGridThreads;
     for (int b = threadIdx.x; b < kBins; b += kGridThreads) {
         hc[b] = 0u;
         hm[b] = 0ull;
+        hlo[b] = 0xFFFFFFFFu;
+        hhi[b] = 0u;
     }
     // this thread's first quad, requested before the fold below
     float l0[4];
@@ -558,111 +793,501 @@ __global__ __launch_bounds__(kGridThreads) void sample_prob_kernel(SampleParams 
                 p.probs[i] = pv;
             }
             const uint32_t key = __float_as_uint(pv);
-            hist_add(ok, (int)(key >> 20), key, ok ? mass_of(key) : 0ull, hc, hm);
+            const int d = (int)(key >> 20);
+            const int lead = hist_add(ok, d, key, ok ? mass_of(key) : 0ull, hc, hm);
+            key_minmax(ok, d, key, lead, hlo, hhi);
         }
     }
     __syncthreads();
     for (int b = threadIdx.x; b < kBins; b += kGridThreads) {
-        if (hc[b]) atomicAdd(&p.h0cnt[b], hc[b]);
+        if (hc[b]) {
+            atomicAdd(&p.h0cnt[b], hc[b]);
+            atomicMin(&p.h0min[b], hlo[b]);
+            atomicMax(&p.h0max[b], hhi[b]);
+        }
         if (hm[b]) atomicAdd(&p.h0mass[b], hm[b]);
     }
 }
 
-// Compacts the tokens of the cutoff's level-0 bin and of every bin the draw
-// can land in: its target lies in [ceil(u * T1), ceil(u * incl(cutoff bin))]
-// since the cutoff token's inclusive mass is at least T1 and at most its
-// bin's.
-__global__ __launch_bounds__(kGridThreads) void sample_gather_kernel(SampleParams p) {
-    constexpr int kWaves = kGridThreads / 64;
-    __shared__ uint32_t offs[kWaves * 4];   // per wave and sub-step: slot offset in the block
-    __shared__ uint32_t s_base;
-    __shared__ SelScratch sc;
-    __shared__ BinSel s1, s2;
-    const int n = p.n;
-    const int T = gridDim.x * kGridThreads;
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    // this thread's first quad, requested before the histogram scan so the
-    // two memory latencies overlap
-    uint32_t key0[4];
-    {
-        const int q = blockIdx.x * kGridThreads + (int)threadIdx.x;
+namespace {
+
+// Rank inside a tied bucket: the tokens of mass m after `excl` reach target
+// t at the j-th one, j = ceil((t - excl) / m) (at least 1).
+__device__ __forceinline__ unsigned long long tied_rank(unsigned long long excl,
+                                                        unsigned long long t,
+                                                        unsigned long long m) {
+    if (m == 0ull || t <= excl) return 1ull;
+    return (t - excl + m - 1ull) / m;
+}
+
+// The mass of each token of a tied bucket found by BinScan::find.
+__device__ __forceinline__ unsigned long long tied_mass(const BinSel& s) {
+    return (s.incl - s.excl) / s.cnt;
+}
+
+__device__ __forceinline__ int ceil_log2(int v) {
+    int l = 0;
+    while ((1 << l) < v) ++l;
+    return l;
+}
+
+// The first quad of this thread's grid-stride walk (NT threads a block),
+// requested early so its latency overlaps the histogram scans.
+template <int NT>
+__device__ __forceinline__ void first_quad(const SampleParams& p, uint32_t (&key0)[4]) {
+    const int q = blockIdx.x * NT + (int)threadIdx.x;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) key0[k] = 4 * q + k < n ? __float_as_uint(p.probs[4 * q + k]) : 0u;
-    }
-    const unsigned long long t1 = target_top_p(p.top_p);
-    BinScan<kGridThreads> scan;
-    scan.load(p.h0cnt, p.h0mass, 0ull, sc);
-    scan.find(t1, s1, sc);
-    unsigned long long tlo, thi;
-    const float u = draw_of(p);
-    if (s1.found) {
+    for (int k = 0; k < 4; ++k) key0[k] = 4 * q + k < p.n ? __float_as_uint(p.probs[4 * q + k]) : 0u;
+}
+
+// Draw-target bounds from the cutoff's bucket: the draw's target lies in
+// [ceil(u * T1), ceil(u * incl)] since the cutoff token's inclusive mass is
+// at least T1 and at most its bucket's; a bucket of one token or of one key
+// fixes the cutoff's mass, so both bounds are the exact target.
+__device__ __forceinline__ void draw_bounds(const BinSel& s1, const uint32_t* tied_bm, float u,
+                                            unsigned long long t1, unsigned long long total,
+                                            unsigned long long& tlo, unsigned long long& thi) {
+    if (!s1.found) {
+        tlo = thi = target_draw(u, total);
+    } else if (s1.cnt == 1u) {
+        tlo = thi = target_draw(u, s1.incl);
+    } else if (is_tied(tied_bm, s1.bin)) {
+        const unsigned long long m = tied_mass(s1);
+        tlo = thi = target_draw(u, s1.excl + tied_rank(s1.excl, t1, m) * m);
+    } else {
         tlo = target_draw(u, t1);
         thi = target_draw(u, s1.incl);
-    } else {
-        tlo = thi = target_draw(u, s1.total);
     }
-    scan.find(thi, s2, sc);
-    const int lo = s2.found ? s2.bin : 0;
-    scan.find(tlo, s2, sc);
-    const int hi = s2.found ? s2.bin : kBins - 1;
-    const int b1 = s1.found ? s1.bin : -1;
-    // block-uniform loop; one atomic a block reserves its slots
-    for (int qb = blockIdx.x * kGridThreads; 4 * qb < n; qb += T) {
+}
+
+// The keys of the first kTiedSlots tied buckets of [lo, hi], from the top,
+// into tkey (LDS); their number into *ntied.  Whole block (NT >= 128).
+template <int NT>
+__device__ void pick_tied(const Buckets& bk, const uint32_t* tied_bm, int lo, int hi,
+                          uint32_t* tkey, int* ntied, SelScratch& sc) {
+    const int t = threadIdx.x;
+    const int w = kBins / 32 - 1 - t;   // words from the top
+    uint32_t bits = 0u;
+    if (t < kBins / 32 && lo <= hi && w >= (lo >> 5) && w <= (hi >> 5)) {
+        bits = tied_bm[w];
+        if (w == (hi >> 5) && (hi & 31) != 31) bits &= (2u << (hi & 31)) - 1u;
+        if (w == (lo >> 5)) bits &= ~0u << (lo & 31);
+    }
+    if (!__syncthreads_or(bits != 0u)) {   // block-uniform: no tied bucket in range
+        if (t == 0) *ntied = 0;
+        __syncthreads();
+        return;
+    }
+    const unsigned long long before = block_excl_scan<NT>((unsigned long long)__popc(bits), sc.wsum);
+    if (t == NT - 1) {
+        const unsigned long long all = before + __popc(bits);
+        *ntied = all < kTiedSlots ? (int)all : kTiedSlots;
+    }
+    for (unsigned long long k = before; bits && k < kTiedSlots; ++k) {
+        const int b = 31 - __clz(bits);
+        bits &= ~(1u << b);
+        tkey[k] = bk.kmin[(w << 5) + b];
+    }
+    __syncthreads();
+}
+
+// Tokens of the block's quads (4 consecutive tokens a thread, NT threads,
+// block-uniform loop) for which want(key) holds go to p.cand: one atomic a
+// block and iteration reserves the slots (wave 0 scans the per-wave,
+// per-sub-step counts).  For each of the ntied keys in tkey, the count of its
+// tokens in each 1024-token chunk goes to p.tcnt.  key0: the block's first
+// quad, already loaded.
+template <int NT, class Want>
+__device__ void compact(const SampleParams& p, const uint32_t (&key0)[4], Want want,
+                        const uint32_t* tkey, int ntied, uint32_t* offs, uint32_t* tsum) {
+    constexpr int kWaves = NT / 64;
+    static_assert(kWaves * 4 <= 64, "one wave scans the slot counts");
+    const int n = p.n;
+    const int T = gridDim.x * NT;
+    const int nchunk = (n + 1023) >> 10;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    for (int qb = blockIdx.x * NT; 4 * qb < n; qb += T) {
         const int q = qb + (int)threadIdx.x;
         uint32_t key[4];
         unsigned long long bal[4];
+        uint32_t tc[kTiedSlots] = {0u, 0u, 0u, 0u};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int i = 4 * q + k;
-            key[k] = qb == (int)(blockIdx.x * kGridThreads) ? key0[k]
+            key[k] = qb == (int)(blockIdx.x * NT) ? key0[k]
                      : i < n ? __float_as_uint(p.probs[i]) : 0u;
-            const int b = (int)(key[k] >> 20);
-            bal[k] = __ballot(i < n && (b == b1 || (b >= lo && b <= hi)));
+            bal[k] = __ballot(i < n && want(key[k]));
+#pragma unroll
+            for (int s = 0; s < kTiedSlots; ++s)
+                if (s < ntied) tc[s] += (uint32_t)__popcll(__ballot(i < n && key[k] == tkey[s]));
         }
         if (lane == 0) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) offs[wid * 4 + k] = (uint32_t)__popcll(bal[k]);
+#pragma unroll
+            for (int s = 0; s < kTiedSlots; ++s) tsum[wid * kTiedSlots + s] = tc[s];
         }
         __syncthreads();
-        if (threadIdx.x == 0) {
-            uint32_t tot = 0u;
-            for (int j = 0; j < kWaves * 4; ++j) {
-                const uint32_t c = offs[j];
-                offs[j] = tot;
-                tot += c;
-            }
-            s_base = tot ? atomicAdd(p.ccount, tot) : 0u;
+        if (wid == 0) {
+            const uint32_t v = lane < kWaves * 4 ? offs[lane] : 0u;
+            const uint32_t incl = wave_incl_sum(v);
+            const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+            uint32_t base = 0u;
+            if (lane == 0 && tot) base = atomicAdd(&p.ctl->ccount, tot);
+            base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+            if (lane < kWaves * 4) offs[lane] = base + incl - v;
+        } else if (ntied && (int)threadIdx.x - 64 < (NT / 256) * kTiedSlots) {
+            // chunk g of this iteration (4 waves, 1024 tokens), slot s
+            const int t = (int)threadIdx.x - 64;
+            const int g = t / kTiedSlots, s = t % kTiedSlots;
+            const int chunk = (qb >> 8) + g;
+            if (s < ntied && chunk < nchunk)
+                p.tcnt[s * nchunk + chunk] = tsum[(4 * g) * kTiedSlots + s] +
+                                             tsum[(4 * g + 1) * kTiedSlots + s] +
+                                             tsum[(4 * g + 2) * kTiedSlots + s] +
+                                             tsum[(4 * g + 3) * kTiedSlots + s];
         }
         __syncthreads();
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             if ((bal[k] >> lane) & 1ull)
-                p.cand[s_base + offs[wid * 4 + k] + lanes_below(bal[k])] =
+                p.cand[offs[wid * 4 + k] + lanes_below(bal[k])] =
                     make_uint2(key[k], (uint32_t)(4 * q + k));
         }
         __syncthreads();
     }
 }
 
+}  // namespace
+
+// Finds, from the level-0 histogram, the bin holding the cutoff and the bins
+// the draw can land in.  When their untied tokens fit the select kernel's
+// LDS (mode 0) it compacts them; otherwise (mode 1) it builds the range
+// histogram over the keys of those bins (segment A: the cutoff's bin,
+// segment B: the draw's bins), which the select kernel's blocks then narrow
+// and compact.  No grid-wide fence or last-block hand-off here: on a chip
+// whose XCDs have separate L2s those cost more than re-reading the 48 KB
+// histogram per block.
+__global__ __launch_bounds__(kGridThreads) void sample_gather_kernel(SampleParams p) {
+    constexpr int kWaves = kGridThreads / 64;
+    __shared__ uint32_t offs[kWaves * 4];   // per wave and sub-step: slot offset in the block
+    __shared__ uint32_t tsum[kWaves * kTiedSlots];
+    __shared__ uint32_t tied_bm[kBins / 32];
+    __shared__ uint32_t s_tkey[kTiedSlots], s_cnt[kWaves];
+    __shared__ int s_ntied;
+    __shared__ SelScratch sc;
+    __shared__ BinSel s1, s2;
+    __shared__ uint32_t hc[kBins], hlo[kBins], hhi[kBins];
+    __shared__ unsigned long long hm[kBins];
+    const int n = p.n;
+    const int T = gridDim.x * kGridThreads;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    uint32_t key0[4];
+    first_quad<kGridThreads>(p, key0);
+    const Buckets bk = level0_buckets(p);
+    const unsigned long long t1 = target_top_p(p.top_p);
+    BinScan<kGridThreads> scan;
+    scan.load_tied(bk, 0ull, sc, tied_bm);
+    scan.find(t1, s1, sc);
+    unsigned long long tlo, thi;
+    draw_bounds(s1, tied_bm, draw_of(p), t1, s1.total, tlo, thi);
+    scan.find(thi, s2, sc);
+    const int lo = s2.found ? s2.bin : 0;
+    scan.find(tlo, s2, sc);
+    const int hi = s2.found ? s2.bin : kBins - 1;
+    const unsigned long long above_hi = s2.found ? s2.excl : 0ull;
+    const int b1 = s1.found ? s1.bin : -1;
+    auto want = [&](int b) { return (b == b1 || (b >= lo && b <= hi)) && !is_tied(tied_bm, b); };
+    // segment A: the cutoff's bin (else the draw's first); B: the draw's
+    // bins above it; the untied candidates and the mass between A and B
+    const int a = b1 >= 0 ? b1 : lo;
+    const int blo = max(lo, a + 1);
+    uint32_t mine = 0u;
+    unsigned long long gapm = 0ull;
+#pragma unroll
+    for (int k = 0; k < BinScan<kGridThreads>::BPT; ++k) {
+        const int b = scan.top - k;
+        if (want(b)) mine += scan.c[k];
+        if (b > a && b < blo) gapm += scan.m[k];
+    }
+    mine = wave_sum(mine);
+    gapm = wave_sum(gapm);
+    if (lane == 0) {
+        s_cnt[wid] = mine;
+        sc.wsum[wid] = gapm;
+    }
+    __syncthreads();
+    uint32_t C = 0u;
+    unsigned long long gap = 0ull;
+    for (int w = 0; w < kWaves; ++w) {
+        C += s_cnt[w];
+        gap += sc.wsum[w];
+    }
+    __syncthreads();   // sc.wsum is rewritten below
+    const int b_shift = 9 + (blo <= hi ? ceil_log2(hi - blo + 1) : 0);
+    const bool ranged = C > (uint32_t)kCandLds && b_shift <= 20;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        SampleCtl& c = *p.ctl;
+        c.mode = ranged ? 1 : 0;
+        c.cut_found = s1.found;
+        c.a_bin = a;
+        c.b_lo = blo;
+        c.b_hi = hi;
+        c.b_shift = b_shift;
+        c.above = above_hi;
+        c.gap = gap;
+        c.total = s1.total;
+    }
+    if (!ranged) {
+        pick_tied<kGridThreads>(bk, tied_bm, lo, hi, s_tkey, &s_ntied, sc);
+        const int nt = s_ntied;
+        if (blockIdx.x == 0 && threadIdx.x < kTiedSlots) {
+            if (threadIdx.x == 0) p.ctl->ntied = nt;
+            if ((int)threadIdx.x < nt) p.ctl->tkey[threadIdx.x] = s_tkey[threadIdx.x];
+        }
+        compact<kGridThreads>(p, key0, [&](uint32_t key) { return want((int)(key >> 20)); },
+                              s_tkey, nt, offs, tsum);
+        return;
+    }
+    // the range histogram: counts, masses and key extremes of its buckets
+    const Buckets rb = range_buckets(p, a, blo, hi, b_shift, gap);
+    for (int b = threadIdx.x; b < kBins; b += kGridThreads) {
+        hc[b] = 0u;
+        hm[b] = 0ull;
+        hlo[b] = 0xFFFFFFFFu;
+        hhi[b] = 0u;
+    }
+    __syncthreads();
+    const int q_first = blockIdx.x * kGridThreads + threadIdx.x;
+    for (int qw = q_first - lane; 4 * qw < n; qw += T) {   // wave-uniform: hist_add
+        const int q = qw + lane;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = 4 * q + k;
+            const uint32_t key = q == q_first ? key0[k] : i < n ? __float_as_uint(p.probs[i]) : 0u;
+            const int d0 = rb.of(key);
+            const bool ok = i < n && d0 < kBins;
+            const int d = ok ? d0 : 0;
+            const int lead = hist_add(ok, d, key, ok ? mass_of(key) : 0ull, hc, hm);
+            key_minmax(ok, d, key, lead, hlo, hhi);
+        }
+    }
+    __syncthreads();
+    for (int b = threadIdx.x; b < kBins; b += kGridThreads) {
+        if (hc[b]) {
+            atomicAdd(&p.h1cnt[b], hc[b]);
+            atomicMin(&p.h1min[b], hlo[b]);
+            atomicMax(&p.h1max[b], hhi[b]);
+        }
+        if (hm[b]) atomicAdd(&p.h1mass[b], hm[b]);
+    }
+}
+
+namespace {
+
+// This lane's matches of key K among tokens [a, b) (a a multiple of 4): 4
+// consecutive tokens a lane, kNthUnroll 16-byte loads in flight.  The keys
+// are read in whole quads: the probability region is padded to 256 bytes.
+__device__ __forceinline__ uint32_t count_key(const uint32_t* kb, int a, int b, uint32_t K) {
+    const int lane = threadIdx.x & 63;
+    uint32_t c = 0u;
+    for (int i0 = a + 4 * lane; i0 < b; i0 += 256 * kNthUnroll) {
+        uint4 v[kNthUnroll];
+#pragma unroll
+        for (int u = 0; u < kNthUnroll; ++u) {
+            const int i = i0 + 256 * u;
+            v[u] = i < b ? *reinterpret_cast<const uint4*>(kb + i) : make_uint4(~K, ~K, ~K, ~K);
+        }
+#pragma unroll
+        for (int u = 0; u < kNthUnroll; ++u) {
+            const int i = i0 + 256 * u;
+            c += (uint32_t)(v[u].x == K) + (uint32_t)(v[u].y == K && i + 1 < b) +
+                 (uint32_t)(v[u].z == K && i + 2 < b) + (uint32_t)(v[u].w == K && i + 3 < b);
+        }
+    }
+    return c;
+}
+
+// The j-th (1-based) token in index order whose key is K, or -1, without
+// per-chunk counts (a tied bucket beyond the kTiedSlots counted): rounds of
+// 16-way narrowing (the range splits into 16 parts of whole quads, a wave
+// counts each, and the part holding the j-th becomes the range) until at
+// most 256 tokens are left, which one wave finishes.  Whole block.
+__device__ int nth_with_key(const float* probs, int n, uint32_t K, unsigned long long j,
+                            SelScratch& sc, int* s_id) {
+    constexpr int NW = kSelThreads / 64;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const uint32_t* kb = reinterpret_cast<const uint32_t*>(probs);
+    int lo = 0, hi = n;
+    unsigned long long r = j;
+    if (threadIdx.x == 0) *s_id = -1;
+    while (hi - lo > 256) {
+        const int per = ((hi - lo + NW - 1) / NW + 3) & ~3;
+        const int a = min(hi, lo + wid * per), b = min(hi, a + per);
+        uint32_t c = count_key(kb, a, b, K);
+        c = wave_sum(c);
+        if (lane == 0) sc.wsum[wid] = c;
+        __syncthreads();
+        unsigned long long before = 0ull;
+        int part = -1;
+        for (int w = 0; w < NW; ++w) {
+            const unsigned long long cw = sc.wsum[w];
+            if (part < 0) {
+                if (r <= before + cw) part = w;
+                else before += cw;
+            }
+        }
+        __syncthreads();   // wsum is written again next round
+        if (part < 0) return -1;   // block-uniform: fewer than j such tokens
+        lo = min(hi, lo + part * per);
+        hi = min(hi, lo + per);
+        r -= before;
+    }
+    if (wid == 0) {
+        const int i = lo + 4 * lane;
+        const uint4 v = i < hi ? *reinterpret_cast<const uint4*>(kb + i)
+                               : make_uint4(~K, ~K, ~K, ~K);
+        const uint32_t m = (uint32_t)(v.x == K) | (uint32_t)(v.y == K && i + 1 < hi) << 1 |
+                           (uint32_t)(v.z == K && i + 2 < hi) << 2 |
+                           (uint32_t)(v.w == K && i + 3 < hi) << 3;
+        const uint32_t c = (uint32_t)__popc(m);
+        const uint32_t S = wave_incl_sum(c);
+        if ((unsigned long long)(S - c) < r && r <= (unsigned long long)S) {
+            uint32_t k = (uint32_t)(r - (S - c)), e = 0u;   // the k-th set bit of m
+            for (; e < 4u; ++e)
+                if (((m >> e) & 1u) && --k == 0u) break;
+            *s_id = i + (int)e;
+        }
+    }
+    __syncthreads();
+    const int id = *s_id;
+    __syncthreads();
+    return id;
+}
+
+// The j-th (1-based) token in index order whose key is K, from the
+// per-chunk counts of its slot: a block scan over the chunk counts finds
+// the chunk, and one token a thread (1024 threads: one chunk) finds the
+// token in it.  Whole block; -1 if fewer than j.
+__device__ int nth_in_chunks(const SampleParams& p, int slot, uint32_t K, unsigned long long j,
+                             SelScratch& sc, int* s_id) {
+    const int n = p.n, nchunk = (n + 1023) >> 10;
+    const uint32_t* cnt = p.tcnt + slot * nchunk;
+    if (threadIdx.x == 0) {
+        sc.chunk = -1;
+        *s_id = -1;
+    }
+    __syncthreads();
+    unsigned long long base = 0ull;
+    for (int c0 = 0; c0 < nchunk; c0 += kSelThreads) {   // block-uniform
+        const int c = c0 + (int)threadIdx.x;
+        const uint32_t v = c < nchunk ? cnt[c] : 0u;
+        const unsigned long long ex = base + block_excl_scan<kSelThreads>(v, sc.wsum);
+        if (v && ex < j && j <= ex + v) {
+            sc.chunk = c;
+            sc.rem = j - ex;
+        }
+        base += sc.wsum[kSelThreads / 64 - 1];
+        __syncthreads();
+    }
+    const int chunk = sc.chunk;
+    if (chunk < 0) return -1;   // block-uniform
+    const unsigned long long r = sc.rem;
+    const int i = (chunk << 10) + (int)threadIdx.x;
+    const uint32_t hit = i < n && __float_as_uint(p.probs[i]) == K ? 1u : 0u;
+    const unsigned long long ex = block_excl_scan<kSelThreads>(hit, sc.wsum);
+    if (hit && ex + 1ull == r) *s_id = i;
+    __syncthreads();
+    const int id = *s_id;
+    __syncthreads();
+    return id;
+}
+
+}  // namespace
+
+// Mode 1 only: the range histogram narrowed as the gather kernel did the
+// level-0 one -- the bucket of the cutoff and the buckets the draw can
+// reach -- and their untied tokens compacted (one quad a thread).
+__global__ __launch_bounds__(kSelThreads) void sample_narrow_kernel(SampleParams p) {
+    constexpr int kWaves = kSelThreads / 64;
+    __shared__ SelScratch sc;
+    __shared__ BinSel s1, s2;
+    __shared__ uint32_t tied_bm[kBins / 32];
+    __shared__ uint32_t offs[kWaves * 4], tsum[kWaves * kTiedSlots], s_tkey[kTiedSlots];
+    __shared__ int s_ntied;
+    SampleCtl& ctl = *p.ctl;
+    if (ctl.mode == 0) return;
+    uint32_t key0[4];
+    first_quad<kSelThreads>(p, key0);
+    const Buckets bk = range_buckets(p, ctl);
+    const unsigned long long t1 = target_top_p(p.top_p);
+    BinScan<kSelThreads> scan;
+    scan.load_tied(bk, ctl.above, sc, tied_bm);
+    if (ctl.cut_found) {
+        scan.find(t1, s1, sc);
+    } else {
+        if (threadIdx.x == 0) s1.found = 0;
+        __syncthreads();
+    }
+    unsigned long long tlo, thi;
+    draw_bounds(s1, tied_bm, draw_of(p), t1, ctl.total, tlo, thi);
+    scan.find(thi, s2, sc);
+    const int lo = s2.found ? s2.bin : 0;
+    scan.find(tlo, s2, sc);
+    const int hi = s2.found ? s2.bin : kBins - 1;
+    const int b1 = s1.found ? s1.bin : -1;
+    pick_tied<kSelThreads>(bk, tied_bm, lo, hi, s_tkey, &s_ntied, sc);
+    const int nt = s_ntied;
+    if (blockIdx.x == 0 && threadIdx.x < kTiedSlots) {
+        if (threadIdx.x == 0) ctl.ntied = nt;
+        if ((int)threadIdx.x < nt) ctl.tkey[threadIdx.x] = s_tkey[threadIdx.x];
+    }
+    compact<kSelThreads>(p, key0, [&](uint32_t key) {
+        const int b = bk.of(key);
+        return (b == b1 || (b >= lo && b <= hi)) && b < kBins && !is_tied(tied_bm, b);
+    }, s_tkey, nt, offs, tsum);
+}
+
+// Positions of the cutoff (its inclusive mass) and of the draw (its token)
+// in the gather kernel's buckets, each: a bucket of one token (read off the
+// histogram / the candidates), a tied bucket (by rank: the cutoff's mass
+// directly, the draw's token from the per-chunk counts), at most 64
+// candidates (one wave sorts them), or the levels below the bucket over its
+// candidates (in LDS when they fit).  One workgroup.
 __global__ __launch_bounds__(kSelThreads) void sample_select_kernel(SampleParams p) {
     __shared__ uint2 lc[kCandLds];
     __shared__ LevelHist H;
     __shared__ SelScratch sc;
-    __shared__ BinSel s0, bs;
-    __shared__ BinSel s1;
+    __shared__ BinSel s0, s1, bs;
+    __shared__ uint32_t tied_bm[kBins / 32];
     __shared__ int s_id;
-    const int C = (int)*p.ccount;
+    __shared__ unsigned long long s_cum;
+    const SampleCtl& ctl = *p.ctl;
+    const int mode = ctl.mode;
+    const Buckets bk = mode ? range_buckets(p, ctl) : level0_buckets(p);
     // read before the first barrier: thread 0 advances the draw index at the end
     const float u = draw_of(p);
     const unsigned long long t1 = target_top_p(p.top_p);
-    BinScan<kSelThreads> scan0;   // the level-0 histogram
-    scan0.load(p.h0cnt, p.h0mass, 0ull, sc);
-    scan0.find(t1, s1, sc);       // the cutoff's bin
+    BinScan<kSelThreads> scan0;
+    scan0.load_tied(bk, mode ? ctl.above : 0ull, sc, tied_bm);
+    if (ctl.cut_found) {
+        scan0.find(t1, s1, sc);       // the cutoff's bucket
+    } else {
+        if (threadIdx.x == 0) s1.found = 0;
+        __syncthreads();
+    }
+    const int C = (int)ctl.ccount;
 
-    if (C <= 64) {
-        // Few candidates (the usual nucleus of a peaked distribution): one
-        // wave sorts them by key and scans their masses.  First the mass of
-        // all bins above each bin, into H.mass.
+    // Few candidates (the usual nucleus of a peaked distribution): wave 0
+    // sorts them by key and gives each its inclusive running mass (the mass
+    // of all buckets above its bucket, from the histogram, plus the running
+    // mass inside its bucket).
+    const bool few = C <= 64;
+    const int lane = threadIdx.x & 63;
+    int w_id = 0, w_bin = -1;
+    unsigned long long w_cum = 0ull;
+    bool w_valid = false;
+    if (few) {
         {
             unsigned long long run = scan0.excl;
 #pragma unroll
@@ -672,72 +1297,89 @@ __global__ __launch_bounds__(kSelThreads) void sample_select_kernel(SampleParams
             }
         }
         __syncthreads();
-        if (threadIdx.x >= 64) return;
-        const int lane = threadIdx.x;
-        const uint2 e = lane < C ? p.cand[lane] : make_uint2(0u, 0u);
-        unsigned long long sk = lane < C ? (1ull << 63) | order_key(e.x, e.y) : 0ull;
-        // bitonic sort, descending, across the wave
-        for (int k = 2; k <= 64; k <<= 1) {
-            for (int j = k >> 1; j > 0; j >>= 1) {
-                const unsigned long long o = __shfl_xor(sk, j, 64);
-                const bool take_max = ((lane & j) == 0) == ((lane & k) == 0);
-                sk = take_max ? (sk > o ? sk : o) : (sk < o ? sk : o);
+        if (threadIdx.x < 64) {
+            const uint2 e = lane < C ? p.cand[lane] : make_uint2(0u, 0u);
+            unsigned long long sk = lane < C ? (1ull << 63) | order_key(e.x, e.y) : 0ull;
+            // bitonic sort, descending, across the wave
+            for (int k = 2; k <= 64; k <<= 1) {
+                for (int j = k >> 1; j > 0; j >>= 1) {
+                    const unsigned long long o = __shfl_xor(sk, j, 64);
+                    const bool take_max = ((lane & j) == 0) == ((lane & k) == 0);
+                    sk = take_max ? (sk > o ? sk : o) : (sk < o ? sk : o);
+                }
             }
+            w_valid = (sk >> 63) != 0ull;
+            const uint32_t key = (uint32_t)(sk >> 24);
+            w_id = (int)(kIdMask - (uint32_t)(sk & kIdMask));
+            w_bin = w_valid ? bk.of(key) : -1;
+            if (w_bin >= kBins) w_bin = -1;   // not a candidate's key: never taken
+            const unsigned long long m = w_valid ? mass_of(key) : 0ull;
+            // inclusive running mass inside each bucket (buckets are contiguous runs)
+            const unsigned long long S = wave_incl_sum(m);
+            const int prev_bin = __shfl_up(w_bin, 1, 64);
+            const bool head = w_valid && (lane == 0 || prev_bin != w_bin);
+            const unsigned long long heads = __ballot(head) & ((2ull << lane) - 1ull);
+            const int start = heads ? 63 - __clzll((long long)heads) : 0;
+            const unsigned long long before = __shfl(S, start > 0 ? start - 1 : 0, 64);
+            w_cum = (w_bin >= 0 ? H.mass[w_bin] : 0ull) + S - (start > 0 ? before : 0ull);
         }
-        const bool valid = (sk >> 63) != 0ull;
-        const uint32_t key = (uint32_t)(sk >> 24);
-        const int id = (int)(kIdMask - (uint32_t)(sk & kIdMask));
-        const int bin = valid ? (int)(key >> 20) : -1;
-        const unsigned long long m = valid ? mass_of(key) : 0ull;
-        // inclusive running mass inside each bin (bins are contiguous runs)
-        unsigned long long S = m;
-        for (int o = 1; o < 64; o <<= 1) {
-            const unsigned long long y = __shfl_up(S, o, 64);
-            if (lane >= o) S += y;
-        }
-        const int prev_bin = __shfl_up(bin, 1, 64);
-        const bool head = valid && (lane == 0 || prev_bin != bin);
-        const unsigned long long heads = __ballot(head) & ((2ull << lane) - 1ull);
-        const int start = heads ? 63 - __clzll((long long)heads) : 0;
-        const unsigned long long before = __shfl(S, start > 0 ? start - 1 : 0, 64);
-        const unsigned long long cum =
-            (valid ? H.mass[bin] : 0ull) + S - (start > 0 ? before : 0ull);
-        unsigned long long cut = s1.total;
-        if (s1.found) {
-            const unsigned long long hit = __ballot(valid && bin == s1.bin && cum >= t1);
-            cut = hit ? __shfl(cum, __ffsll((long long)hit) - 1, 64) : s1.incl;
-        }
-        const unsigned long long t2 = target_draw(u, cut);
-        const unsigned long long hit2 = __ballot(valid && cum >= t2);
-        const int chosen = __shfl(id, hit2 ? __ffsll((long long)hit2) - 1 : 0, 64);
-        if (lane == 0) finish_select(p, hit2 ? chosen : 0);
-        return;
     }
-
     const uint2* cand = p.cand;
-    if (C <= kCandLds) {
+    if (!few && C <= kCandLds) {
         for (int c = threadIdx.x; c < C; c += kSelThreads) lc[c] = p.cand[c];
         cand = lc;
     }
     __syncthreads();
+
     // the cutoff: its inclusive mass
-    unsigned long long cum = s1.total;
+    unsigned long long cum = ctl.total;
     if (s1.found) {
-        if (s1.cnt == 1u)
+        if (s1.cnt == 1u) {
             cum = s1.incl;
-        else
-            (void)select_in_bin(cand, C, s1.bin, s1.excl, t1, H, sc, bs, cum);
+        } else if (is_tied(tied_bm, s1.bin)) {
+            const unsigned long long m = tied_mass(s1);
+            cum = s1.excl + tied_rank(s1.excl, t1, m) * m;
+        } else if (few) {
+            if (threadIdx.x < 64) {
+                const unsigned long long hit = __ballot(w_valid && w_bin == s1.bin && w_cum >= t1);
+                const unsigned long long c = hit ? __shfl(w_cum, __ffsll((long long)hit) - 1, 64)
+                                                 : s1.incl;
+                if (threadIdx.x == 0) s_cum = c;
+            }
+            __syncthreads();
+            cum = s_cum;
+        } else {
+            (void)select_in_bin(cand, C, bk, s1.bin, s1.cnt, s1.excl, t1, H, sc, bs, cum);
+        }
     }
     // the draw
     const unsigned long long t2 = target_draw(u, cum);
     scan0.find(t2, s0, sc);
     int id = -1;
     if (s0.found) {
-        if (s0.cnt == 1u) {
-            id = only_in_bin(cand, C, s0.bin, &s_id);
+        if (is_tied(tied_bm, s0.bin)) {
+            const uint32_t K = bk.kmin[s0.bin];
+            const unsigned long long j = tied_rank(s0.excl, t2, tied_mass(s0));
+            int slot = -1;
+            for (int s = 0; s < ctl.ntied && s < kTiedSlots; ++s)
+                if (slot < 0 && ctl.tkey[s] == K) slot = s;
+            id = slot >= 0 ? nth_in_chunks(p, slot, K, j, sc, &s_id)
+                           : nth_with_key(p.probs, p.n, K, j, sc, &s_id);
+        } else if (few) {
+            if (threadIdx.x == 0) s_id = -1;
+            __syncthreads();
+            if (threadIdx.x < 64) {
+                const unsigned long long hit2 = __ballot(w_valid && w_cum >= t2);
+                const int chosen = __shfl(w_id, hit2 ? __ffsll((long long)hit2) - 1 : 0, 64);
+                if (threadIdx.x == 0 && hit2) s_id = chosen;
+            }
+            __syncthreads();
+            id = s_id;
+        } else if (s0.cnt == 1u) {
+            id = only_in_bin(cand, C, bk, s0.bin, &s_id);
         } else {
             unsigned long long c2 = 0ull;
-            id = select_in_bin(cand, C, s0.bin, s0.excl, t2, H, sc, bs, c2);
+            id = select_in_bin(cand, C, bk, s0.bin, s0.cnt, s0.excl, t2, H, sc, bs, c2);
         }
     }
     if (threadIdx.x == 0) finish_select(p, id < 0 ? 0 : id);
@@ -758,22 +1400,25 @@ size_t up256(size_t b) { return (b + 255) / 256 * 256; }
 
 size_t argmax_workspace_bytes() { return 2 * kMaxBlocks * 4; }
 
+// probabilities, block maxima and exp-sums, the level-0 and range
+// histograms (count, mass, key min and max), the control block, the tied-key
+// chunk counts, candidates
 constexpr size_t sample_ws_bytes(size_t n) {
     return (n * 4 + 255) / 256 * 256 + 2 * ((kMaxBlocks * 4 + 255) / 256 * 256) +
-           (kBins * 4 + 255) / 256 * 256 + (kBins * 8 + 255) / 256 * 256 + 256 +
-           (n * 8 + 255) / 256 * 256;
+           2 * (3 * ((kBins * 4 + 255) / 256 * 256) + (kBins * 8 + 255) / 256 * 256) + 256 +
+           (kTiedSlots * 4 * ((n + 1023) / 1024) + 255) / 256 * 256 + (n * 8 + 255) / 256 * 256;
 }
 
 size_t sample_workspace_bytes(int n) { return sample_ws_bytes((size_t)n); }
 
 // Scratch of sltx_sample_top_p_noalloc: the sampler's workspace for up to
-// kSampleNoAllocMaxN logits (3,197,184 bytes), in a file-scope device array,
+// kSampleNoAllocMaxN logits (3,315,968 bytes), in a file-scope device array,
 // so that entry point allocates nothing.  Each GPU holds its own copy until
 // the process ends, and every call on that GPU shares it (the scale kernel
 // clears the counters each call; the other regions are written before they
 // are read).  In host code `scratch` only names the symbol: kernels are given
 // the device address resolved per device below.
-static_assert(sample_ws_bytes(kSampleNoAllocMaxN) == 3197184, "noalloc scratch size");
+static_assert(sample_ws_bytes(kSampleNoAllocMaxN) == 3315968, "noalloc scratch size");
 static __device__ __align__(256) unsigned char scratch[sample_ws_bytes(kSampleNoAllocMaxN)];
 
 namespace {
@@ -825,13 +1470,30 @@ hipError_t launch_sample(SampleParams p, void* ws, hipStream_t st) {
     w += up256(kBins * 4);
     p.h0mass = reinterpret_cast<unsigned long long*>(w);
     w += up256(kBins * 8);
-    p.ccount = reinterpret_cast<uint32_t*>(w);
+    p.h0min = reinterpret_cast<uint32_t*>(w);
+    w += up256(kBins * 4);
+    p.h0max = reinterpret_cast<uint32_t*>(w);
+    w += up256(kBins * 4);
+    p.h1cnt = reinterpret_cast<uint32_t*>(w);
+    w += up256(kBins * 4);
+    p.h1mass = reinterpret_cast<unsigned long long*>(w);
+    w += up256(kBins * 8);
+    p.h1min = reinterpret_cast<uint32_t*>(w);
+    w += up256(kBins * 4);
+    p.h1max = reinterpret_cast<uint32_t*>(w);
+    w += up256(kBins * 4);
+    static_assert(sizeof(SampleCtl) <= 256, "control block");
+    p.ctl = reinterpret_cast<SampleCtl*>(w);
     w += 256;
+    p.tcnt = reinterpret_cast<uint32_t*>(w);
+    w += up256((size_t)kTiedSlots * 4 * ((n + 1023) / 1024));
     p.cand = reinterpret_cast<uint2*>(w);
     const int G = grid_blocks(p.n);
     hipLaunchKernelGGL(sample_scale_kernel, dim3(G), dim3(kGridThreads), 0, st, p);
     hipLaunchKernelGGL(sample_prob_kernel, dim3(G), dim3(kGridThreads), 0, st, p);
     hipLaunchKernelGGL(sample_gather_kernel, dim3(G), dim3(kGridThreads), 0, st, p);
+    const int Gn = std::min(kMaxBlocks, (p.n + 4 * kSelThreads - 1) / (4 * kSelThreads));
+    hipLaunchKernelGGL(sample_narrow_kernel, dim3(Gn), dim3(kSelThreads), 0, st, p);
     hipLaunchKernelGGL(sample_select_kernel, dim3(1), dim3(kSelThreads), 0, st, p);
     return hipGetLastError();
 }

@@ -131,6 +131,49 @@ def test_sample_matches_oracle(pkg, dev, n, kind):
     torch.cuda.synchronize()
 
 
+def _dense(kind, n, rng):
+    if kind == "near_flat":      # one level-0 bin: the range histogram narrows it
+        return rng.standard_normal(n) * 1e-3
+    if kind == "two_clusters":   # two dense bins; the draw lands in either
+        return np.where(rng.random(n) < 0.5, 0.0, 0.3) + rng.standard_normal(n) * 1e-3
+    if kind == "half_tied":      # a tied bucket inside a dense bin
+        v = rng.standard_normal(n) * 1e-3
+        v[rng.random(n) < 0.5] = 0.0
+        return v
+    return rng.standard_normal(n) * 2e-6   # "one_bucket": keys within one range bucket
+
+
+@pytest.mark.parametrize("kind,dt", [("near_flat", np.float16), ("near_flat", np.float32),
+                                     ("two_clusters", np.float32), ("half_tied", np.float32),
+                                     ("half_tied", np.float16), ("one_bucket", np.float32)])
+def test_sample_dense_nucleus(pkg, dev, kind, dt):
+    """Nuclei of tens of thousands of nearly equal probabilities: more
+    candidates than the select kernel holds in LDS, so the gather kernel
+    builds the range histogram and the narrow kernel compacts only the
+    buckets the cutoff and the draw can reach ("one_bucket": every key in
+    one bucket, the select kernel's levels over the candidates in HBM).
+    Checked against the oracle as in test_sample_matches_oracle."""
+    import torch
+    n = 128256
+    rng = np.random.default_rng(hash(kind) % 1000 + dt(0).itemsize)
+    lg = _dense(kind, n, rng).astype(dt)
+    x = _t(lg, dev)
+    seen_np = rng.integers(0, n, 40).astype(np.int32)
+    seen = _t(seen_np, dev)
+    for T, top_p, pen in ((0.7, 0.9, 1.1), (1.0, 0.5, 1.0), (1.3, 1.0, 1.0), (0.7, 2.0, 1.1)):
+        for u in (0.0, 0.173, 0.5, 0.9999):
+            got = int(pkg.sample(x, T, top_p, pen, seen, u).item())
+            case = (kind, dt.__name__, T, top_p, pen, u, got)
+            exact, ok = acceptable(lg, T, top_p, pen, seen_np, u, gpu_sums=True, tol=5e-7,
+                                   tie=5e-7)
+            assert got in ok, case + (exact,)
+            if len(ok) == 1:
+                assert got == exact, case + (exact,)
+            ref, ok = acceptable(lg, T, top_p, pen, seen_np, u)
+            assert got in ok, case + (ref,)
+    torch.cuda.synchronize()
+
+
 def test_sample_tiny_top_p_is_argmax_of_penalised(pkg, dev):
     rng = np.random.default_rng(31)
     n = 128256
