@@ -88,6 +88,10 @@ def parse():
     ap.add_argument("--gemm-pmc", action="store_true",
                     help="only: 10 launches each of the M=750 prefill gate/up (SiLU) and down "
                          "GEMMs, for rocprofv3 --pmc MFMA-utilisation runs")
+    ap.add_argument("--token-select", action="store_true",
+                    help="only: the token-selection leg (graphs), then TRACE_CALLS eager calls of "
+                         "each sampling case, for rocprofv3 --kernel-trace; with "
+                         "--summarize-trace: summarize such a trace per case and kernel")
     ap.add_argument("--summarize-trace", metavar="DIR",
                     help="print a markdown summary of a rocprofv3 --kernel-trace output folder "
                          "(rocpd .db or kernel_trace.csv) of this script; no GPU needed")
@@ -182,7 +186,10 @@ def _wsb(q):
 def main():
     args = parse()
     if args.summarize_trace:
-        print(summarize_trace(args.summarize_trace, args.copies))
+        if args.token_select:
+            print(summarize_token_select_trace(args.summarize_trace))
+        else:
+            print(summarize_trace(args.summarize_trace, args.copies))
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -207,6 +214,16 @@ def main():
         return
     if args.gemm_pmc:
         gemm_pmc_run(pkg, torch, gen, dev)
+        return
+    if args.token_select:
+        print(json.dumps(token_select_leg(pkg, torch, gen, dev)), flush=True)
+        for name, fn in token_select_cases(pkg, torch, gen, dev):
+            if name.startswith("sample_"):
+                s = torch.cuda.Stream()
+                for _ in range(TRACE_CALLS):
+                    fn(s)
+                torch.cuda.synchronize()
+        print("eager trace section:", ", ".join(SAMPLE_CASES), flush=True)
         return
 
     C = args.copies
@@ -551,18 +568,15 @@ def prefill_leg(pkg, torch, gen, dev, mw, S=750):
     return st
 
 
-def token_select_leg(pkg, torch, gen, dev, vocab=128256):
-    """Token selection after the lm_head (LlamaModel.swift:153,161): argmax
-    and temperature 0.7 / top-p 0.9 / repetition penalty 1.1 sampling over
-    Llama 3.2's 128256 fp16 logits with 64 seen ids, for N(0, 3^2) logits (a
-    nucleus of a few tokens, as for a trained model) and for the degenerate
-    distributions that are the sampler's worst cases: flat (every token tied:
-    the nucleus is the whole vocabulary), two tied levels (half the tokens at
-    each of two probabilities), near-flat (N(0, 1e-3^2) logits: one level-0
-    bin of 128256 distinct-ish keys) and two dense clusters.  Each is a graph
-    of 10 calls on its own stream (after one eager call there, which sizes the
-    workspace); us per call includes the graph's launch gaps.  "worst_us" is
-    the largest sampling median."""
+SAMPLE_CASES = ("sample_top_p", "sample_top_p_flat", "sample_top_p_two_levels",
+                "sample_top_p_near_flat", "sample_top_p_two_clusters")
+SAMPLE_KERNELS = ("scale", "prob", "gather", "narrow", "select")
+TRACE_CALLS = 20
+
+
+def token_select_cases(pkg, torch, gen, dev, vocab=128256):
+    """(name, fn(stream)) for argmax and the sampling cases of
+    token_select_leg, over fresh seeded logits."""
     peaked = (3.0 * torch.randn(vocab, generator=gen, device=dev)).half()
     flat = torch.zeros(vocab, device=dev, dtype=torch.float16)
     half = torch.rand(vocab, generator=gen, device=dev) < 0.5
@@ -572,24 +586,38 @@ def token_select_leg(pkg, torch, gen, dev, vocab=128256):
                 1e-3 * torch.randn(vocab, generator=gen, device=dev)).half()
     seen = torch.randint(0, vocab, (64,), generator=gen, device=dev, dtype=torch.int32)
     out = torch.empty(1, device=dev, dtype=torch.int32)
-    res = {}
 
     def samp(lg):
         return lambda s: pkg.sample(lg, 0.7, 0.9, 1.1, seen, 0.5, out=out, stream=s)
 
-    cases = (("argmax", lambda s: pkg.argmax(peaked, out=out, stream=s)),
-             ("sample_top_p", samp(peaked)), ("sample_top_p_flat", samp(flat)),
-             ("sample_top_p_two_levels", samp(two_levels)),
-             ("sample_top_p_near_flat", samp(near_flat)),
-             ("sample_top_p_two_clusters", samp(clusters)))
-    for name, fn in cases:
+    return (("argmax", lambda s: pkg.argmax(peaked, out=out, stream=s)),
+            ("sample_top_p", samp(peaked)), ("sample_top_p_flat", samp(flat)),
+            ("sample_top_p_two_levels", samp(two_levels)),
+            ("sample_top_p_near_flat", samp(near_flat)),
+            ("sample_top_p_two_clusters", samp(clusters)))
+
+
+def token_select_leg(pkg, torch, gen, dev, vocab=128256):
+    """Token selection after the lm_head (LlamaModel.swift:153,161): argmax
+    and temperature 0.7 / top-p 0.9 / repetition penalty 1.1 sampling (u =
+    0.5) over Llama 3.2's 128256 fp16 logits with 64 seen ids, for N(0, 3^2)
+    logits (a nucleus of a few tokens, as for a trained model) and for the
+    degenerate distributions that are the sampler's worst cases: flat (every
+    token tied: the nucleus is the whole vocabulary), two tied levels (half
+    the tokens at each of two probabilities), near-flat (N(0, 1e-3^2) logits:
+    one level-0 bin of 128256 near-equal keys) and two dense clusters.  Each
+    is a graph of 10 calls on its own stream (after one eager call there,
+    which sizes the workspace); us per call includes the graph's launch gaps.
+    "worst_us" is the largest sampling median."""
+    res = {}
+    for name, fn in token_select_cases(pkg, torch, gen, dev, vocab):
         s = torch.cuda.Stream()
         g = capture(torch, lambda: [fn(s) for _ in range(10)], s, warm=lambda: fn(s))
         res[name] = replay_stats(torch, g.replay, 10)
         del g
     res["worst_us"] = max(v["median_us"] for k, v in res.items() if k.startswith("sample_"))
     res["vocab"] = vocab
-    res["launches"] = {"argmax": 2, "sample_top_p": 5}
+    res["launches"] = {"argmax": 2, "sample_top_p": len(SAMPLE_KERNELS)}
     return res
 
 
@@ -894,6 +922,32 @@ def summarize_trace(folder, copies=40):
                 f"frac_of_8000_gbs: {gbs / HBM_PEAK_GBS:.4f}"]
     else:
         out.append(f"no run of {copies} back-to-back `{DOMINANT_KERNEL}` launches in the trace")
+    return "\n".join(out)
+
+
+def summarize_token_select_trace(folder):
+    """Markdown table of a kernel trace of `bench.py --token-select`: the
+    median duration of each sampler kernel per case, over the eager section's
+    TRACE_CALLS calls of each case (the trace's last sampler dispatches, in
+    SAMPLE_CASES order)."""
+    import numpy as np
+    rows = [r for r in _trace_rows(folder) if "sample_" in r[0] and "_kernel" in r[0]]
+    per_call = len(SAMPLE_KERNELS)
+    need = len(SAMPLE_CASES) * TRACE_CALLS * per_call
+    if len(rows) < need:
+        return f"expected {need} sampler dispatches in the eager section, found {len(rows)}"
+    rows = rows[-need:]
+    out = ["| case | " + " | ".join(f"{k} us" for k in SAMPLE_KERNELS) + " | sum us |",
+           "|---|" + "---|" * (per_call + 1)]
+    for ci, case in enumerate(SAMPLE_CASES):
+        seg = rows[ci * TRACE_CALLS * per_call:(ci + 1) * TRACE_CALLS * per_call]
+        meds = []
+        for k, kname in enumerate(SAMPLE_KERNELS):
+            ks = seg[k::per_call]
+            assert all(f"sample_{kname}_kernel" in r[0] for r in ks), (case, kname)
+            meds.append(float(np.median([(r[2] - r[1]) / 1e3 for r in ks])))
+        out.append(f"| {case} | " + " | ".join(f"{m:.1f}" for m in meds) +
+                   f" | {sum(meds):.1f} |")
     return "\n".join(out)
 
 
