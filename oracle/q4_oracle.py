@@ -23,7 +23,10 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_DIR = os.path.join(HERE, "_build")
+# SLTX_ORACLE_LIB_DIR selects prebuilt libraries (the sanitized build of
+# build_c_sanitized, for the CPU tests); they are never rebuilt there.
+PREBUILT_DIR = os.environ.get("SLTX_ORACLE_LIB_DIR")
+LIB_DIR = PREBUILT_DIR or os.path.join(HERE, "_build")
 LIB_PATH = os.path.join(LIB_DIR, "libq4oracle.so")
 CPU_LIB_PATH = os.path.join(LIB_DIR, "libq4cpu.so")
 
@@ -328,6 +331,8 @@ def elementwise_ok(y, ref, rtol: float, atol_rms: float) -> tuple[bool, float]:
 
 def build_c(force: bool = False) -> str:
     """Compile q4_oracle.c into _build/libq4oracle.so with gcc."""
+    if PREBUILT_DIR:
+        return LIB_PATH
     src = os.path.join(HERE, "q4_oracle.c")
     src2 = os.path.join(HERE, "q4_cpu_baseline.c")
     if (not force and all(os.path.exists(p) for p in (LIB_PATH, CPU_LIB_PATH))
@@ -346,6 +351,23 @@ def build_c(force: bool = False) -> str:
                     src2, "-lpthread"], check=True)
     os.replace(tmp2, CPU_LIB_PATH)
     return LIB_PATH
+
+
+def build_c_sanitized(out_dir: str) -> None:
+    """q4_oracle.c and q4_cpu_baseline.c built with clang's AddressSanitizer
+    and UndefinedBehaviorSanitizer into out_dir (same file names and flags as
+    build_c, plus the sanitizers; the process that loads them must preload
+    clang's ASan runtime)."""
+    clang = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "llvm", "bin", "clang")
+    san = ["-fsanitize=address,undefined", "-fno-sanitize-recover=undefined",
+           "-fno-omit-frame-pointer", "-g", "-shared-libsan"]
+    os.makedirs(out_dir, exist_ok=True)
+    subprocess.run([clang, "-O2", "-fPIC", "-shared", "-std=c11", "-ffp-contract=off", *san,
+                    "-o", os.path.join(out_dir, "libq4oracle.so"),
+                    os.path.join(HERE, "q4_oracle.c"), "-lm", "-lpthread"], check=True)
+    subprocess.run([clang, "-O3", "-mavx2", "-mfma", "-mf16c", "-fPIC", "-shared", "-std=gnu11",
+                    *san, "-o", os.path.join(out_dir, "libq4cpu.so"),
+                    os.path.join(HERE, "q4_cpu_baseline.c"), "-lpthread"], check=True)
 
 
 _cpu_lib = None

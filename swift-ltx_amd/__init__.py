@@ -23,7 +23,9 @@ import os
 from dataclasses import dataclass
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PKG_DIR, "lib", "libswiftltx_q4.so")
+# SLTX_LIB_PATH selects another build of the same library (the sanitized
+# host-only build of build_sanitized.py, for the CPU tests).
+LIB_PATH = os.environ.get("SLTX_LIB_PATH") or os.path.join(PKG_DIR, "lib", "libswiftltx_q4.so")
 
 SLTX_OK = 0
 SLTX_ERR_INVALID = -1
