@@ -88,6 +88,10 @@ def parse():
     ap.add_argument("--gemm-pmc", action="store_true",
                     help="only: 10 launches each of the M=750 prefill gate/up (SiLU) and down "
                          "GEMMs, for rocprofv3 --pmc MFMA-utilisation runs")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="only: the probes of what bounds the kernels -- launch floor, "
+                         "register-only MFMA rate and clock, grid hand-off cost by block count, "
+                         "GEMV marginal rate, hipBLASLt dense fp16 at the M=750 shapes")
     ap.add_argument("--token-select", action="store_true",
                     help="only: the token-selection leg (graphs), then TRACE_CALLS eager calls of "
                          "each sampling case, for rocprofv3 --kernel-trace; with "
@@ -214,6 +218,9 @@ def main():
         return
     if args.gemm_pmc:
         gemm_pmc_run(pkg, torch, gen, dev)
+        return
+    if args.ceilings:
+        ceilings_run(pkg, torch, gen, dev)
         return
     if args.token_select:
         print(json.dumps(token_select_leg(pkg, torch, gen, dev)), flush=True)
@@ -566,6 +573,126 @@ def prefill_leg(pkg, torch, gen, dev, mw, S=750):
                "tokens": S, "layers": L,
                "note": "matmul flops only; attention stand-in = a copy of the q columns"})
     return st
+
+
+# ------------------------------------------------------------ ceilings ---
+
+def _event_us(torch, fn, reps=7):
+    """Median over reps of one eager call's event-timed duration (us)."""
+    import numpy as np
+    out = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out.append(e0.elapsed_time(e1) * 1e3)
+    return float(np.median(out))
+
+
+def ceilings_run(pkg, torch, gen, dev):
+    """The probes behind the bounds the kernels are judged against; prints
+    one JSON object per probe (also read by rocprofv3 --kernel-trace runs)."""
+    import numpy as np
+    import torch.nn.functional as F
+
+    def emit(name, obj):
+        print(json.dumps({"probe": name, **obj}), flush=True)
+
+    # launch floor: a graph of 200 dependent empty launches
+    s = torch.cuda.Stream()
+    g = capture(torch, lambda: [pkg.probe_empty(stream=s) for _ in range(200)], s,
+                warm=lambda: pkg.probe_empty(stream=s))
+    with torch.cuda.stream(s):
+        st = replay_stats(torch, g.replay, 200)
+    emit("launch_floor", {"us_per_launch": st, "launches_per_graph": 200})
+    del g
+
+    # register-only MFMA rate and clock: 1 and 2 waves per SIMD
+    ab = torch.randn(256, 8, generator=gen, device=dev).half()
+    kcu = 256
+    for blocks in (kcu, 2 * kcu):
+        iters = 40000
+        sink = torch.empty(blocks * 256, device=dev)
+        clocks = torch.zeros(blocks, 2, dtype=torch.int64, device=dev)
+        pkg.probe_mfma(ab, blocks, 100, sink, clocks)
+        us = _event_us(torch, lambda: pkg.probe_mfma(ab, blocks, iters, sink, clocks), reps=5)
+        c = clocks.cpu().numpy().astype(np.float64)
+        mhz = np.median(c[:, 0] / np.maximum(c[:, 1], 1)) * 100.0
+        flops = blocks * 4 * iters * 4 * 2 * 32 * 32 * 16
+        emit("mfma_register_only", {"blocks": blocks, "waves_per_simd": blocks * 4 // (4 * kcu),
+                                    "iters": iters, "us": round(us, 1),
+                                    "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+                                    "frac_of_2500": round(flops / (us * 1e-6) / 1e12 / 2500, 4),
+                                    "shader_clock_mhz": round(float(mhz), 1)})
+
+    # grid-wide hand-off inside one launch, by block count
+    faults = torch.zeros(1, dtype=torch.int32, device=dev)
+    R = 200
+    for mode, mname in ((0, "one counter"), (1, "per-XCD counters"), (2, "tagged words"),
+                        (3, "per-XCD counters + 16 data words a block")):
+        for fence in ((0, 1) if mode < 3 else (0,)):
+            rows = []
+            for blocks in (8, 32, 64, 128, 256, 512, 1024):
+                sync = torch.zeros(pkg.probe_sync_words(blocks), dtype=torch.int32, device=dev)
+
+                def one(rounds):
+                    sync.zero_()   # a fresh buffer every launch (both sides of the difference)
+                    pkg.probe_sync(mode, fence, blocks, rounds, sync, faults)
+
+                def run(rounds):
+                    return _event_us(torch, lambda: one(rounds), reps=5)
+                try:
+                    t0, t1 = run(0), run(R)
+                except pkg.SltxError as e:
+                    rows.append({"blocks": blocks, "error": str(e)})
+                    continue
+                rows.append({"blocks": blocks, "us_per_barrier": round((t1 - t0) / R, 3)})
+            emit("grid_handoff", {"mode": mname, "fence": bool(fence), "rounds": R,
+                                  "by_blocks": rows,
+                                  "faults": int(faults.item())})
+            faults.zero_()
+
+    # GEMV marginal rate: M = 1, K = 3072, cold weights (rotated over >= 2 GB)
+    pts = []
+    for N in (3072, 8192, 16384, 32768, 65536, 131072):
+        nb = gemv_bytes(N, 3072)
+        copies = max(2, min(800, -(-2 * 2 ** 30 // nb)))
+        ws = [q4(pkg, torch, N, 3072, gen, dev) for _ in range(copies)]
+        x = torch.randn(1, 3072, generator=gen, device=dev).half()
+        y = torch.empty(1, N, device=dev, dtype=torch.float16)
+        cap = torch.cuda.Stream()
+        gr = capture(torch, lambda: [pkg.matmul_q4(x, *_wsb(w), 1, 3072, N, G, out=y,
+                                                   stream=cap) for w in ws], cap)
+        with torch.cuda.stream(cap):
+            st = replay_stats(torch, gr.replay, copies)
+        pts.append((nb, st["median_us"]))
+        emit("gemv_size", {"N": N, "K": 3072, "bytes": nb, "copies": copies, "us": st})
+        del gr, ws
+        torch.cuda.empty_cache()
+    b = np.array([p[0] for p in pts], dtype=np.float64)
+    t = np.array([p[1] for p in pts], dtype=np.float64)
+    big = b >= gemv_bytes(16384, 3072)
+    slope, icpt = np.polyfit(b[big], t[big], 1)
+    emit("gemv_marginal", {"fit_over_bytes": [int(v) for v in b[big]],
+                           "marginal_gbs": round(1e-3 / slope, 1),
+                           "frac_of_8000": round(1e-3 / slope / HBM_PEAK_GBS, 4),
+                           "fixed_us": round(float(icpt), 2)})
+
+    # hipBLASLt through torch: dense fp16 at the M = 750 shapes and 4096^3
+    for name, M, K, N in (("gate_up_m750_dense", 750, 3072, 16384),
+                          ("down_m750_dense", 750, 8192, 3072),
+                          ("square_4096", 4096, 4096, 4096)):
+        xa = torch.randn(M, K, generator=gen, device=dev).half()
+        wb = torch.randn(N, K, generator=gen, device=dev).half()
+        out = torch.empty(M, N, device=dev, dtype=torch.float16)
+        cap = torch.cuda.Stream()
+        gr = capture(torch, lambda: [torch.matmul(xa, wb.t(), out=out) for _ in range(10)], cap)
+        with torch.cuda.stream(cap):
+            st = rate(replay_stats(torch, gr.replay, 10), flops=2 * M * N * K)
+        emit("hipblaslt_fp16", {"shape": name, "M": M, "K": K, "N": N, "us": st})
+        del gr
 
 
 SAMPLE_CASES = ("sample_top_p", "sample_top_p_flat", "sample_top_p_two_levels",

@@ -374,6 +374,30 @@ int sltx_sample_top_p_state(const void* logits, int32_t dtype, int32_t n, float 
 int sltx_hbm_read_blocks(void);
 int sltx_hbm_read(const void* src, uint64_t bytes, uint32_t* sink, void* stream);
 
+/* Probes of what bounds the kernels (no counterpart in the reference):
+ * - sltx_probe_empty: one launch of an empty one-wave kernel (the launch
+ *   floor, timed in a graph of many);
+ * - sltx_probe_mfma: `blocks` blocks of 256 threads, each wave running
+ *   `iters` x 4 independent v_mfma_f32_32x32x16_f16 on register operands
+ *   taken from ab (256 x 16 bytes, 16-byte aligned); sink gets 256 floats a
+ *   block (the sums, so nothing is elided), clocks 2 words a block: shader
+ *   clock cycles and 100 MHz wall ticks of the loop;
+ * - sltx_probe_sync: `rounds` grid-wide barriers among `blocks` one-wave
+ *   blocks (at most what the device holds at once: SLTX_ERR_INVALID
+ *   beyond), arrival by mode 0 one agent-scope counter, 1 per-XCD counters
+ *   then one global counter, 2 tagged words polled by every block, 3 as 1
+ *   after storing 16 data words a block (agent scope, completion awaited),
+ *   which every block reads back after the wait; `fence`
+ *   adds agent-scope release / acquire fences around each.  sync holds
+ *   sltx_probe_sync_words(blocks) zeroed words (64-byte aligned); a wait
+ *   that runs out of polls adds one to *faults and the kernel finishes. */
+int sltx_probe_empty(void* stream);
+int sltx_probe_mfma(const void* ab, int32_t blocks, int32_t iters, float* sink, uint64_t* clocks,
+                    void* stream);
+int sltx_probe_sync_words(int32_t blocks);
+int sltx_probe_sync(int32_t mode, int32_t fence, int32_t blocks, int32_t rounds, uint32_t* sync,
+                    int32_t* faults, void* stream);
+
 /* ---- safetensors weights (SafeTensorsFile, SafeTensors.swift:41-118) ----
  * Reads the files swift-ltx's loader reads (ModelWeights.swift:40-154) into
  * caller-allocated device memory.  The header (8-byte LE length, JSON object,

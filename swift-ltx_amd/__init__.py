@@ -64,6 +64,10 @@ EXPORTED = (
     "sltx_decode_layer_faults",
     "sltx_hbm_read_blocks",
     "sltx_hbm_read",
+    "sltx_probe_empty",
+    "sltx_probe_mfma",
+    "sltx_probe_sync_words",
+    "sltx_probe_sync",
     "sltx_argmax",
     "sltx_sample_top_p",
     "sltx_sample_top_p_noalloc",
@@ -165,6 +169,14 @@ def lib():
         L.sltx_hbm_read_blocks.restype = ctypes.c_int
         L.sltx_hbm_read.argtypes = [P, ctypes.c_uint64, P, P]
         L.sltx_hbm_read.restype = ctypes.c_int
+        L.sltx_probe_empty.argtypes = [P]
+        L.sltx_probe_empty.restype = ctypes.c_int
+        L.sltx_probe_mfma.argtypes = [P, I32, I32, P, P, P]
+        L.sltx_probe_mfma.restype = ctypes.c_int
+        L.sltx_probe_sync_words.argtypes = [I32]
+        L.sltx_probe_sync_words.restype = ctypes.c_int
+        L.sltx_probe_sync.argtypes = [I32, I32, I32, I32, P, P, P]
+        L.sltx_probe_sync.restype = ctypes.c_int
         L.sltx_argmax.argtypes = [P, I32, I32, P, P]
         L.sltx_sample_top_p.argtypes = [P, I32, I32, F, F, F, P, I32, F, P, P]
         L.sltx_sample_top_p_noalloc.argtypes = [P, I32, I32, F, F, F, P, I32, F, P, P]
@@ -575,6 +587,36 @@ def hbm_read(src, sink=None, stream=None):
     check(lib().sltx_hbm_read(_ptr(src), src.numel() * src.element_size(), _ptr(sink),
                               _stream(stream)))
     return sink
+
+
+def probe_empty(stream=None):
+    """One launch of an empty kernel (sltx_probe_empty)."""
+    check(lib().sltx_probe_empty(_stream(stream)))
+
+
+def probe_mfma(ab, blocks, iters, sink, clocks, stream=None):
+    """Register-only MFMA loop (sltx_probe_mfma): ab fp16 [256, 8], sink
+    float32 [blocks * 256], clocks int64 [blocks, 2]."""
+    torch = _torch()
+    _need(ab, "ab", 256 * 8, (torch.float16,))
+    _need(sink, "sink", blocks * 256, (torch.float32,))
+    _need(clocks, "clocks", blocks * 2, (torch.int64,))
+    check(lib().sltx_probe_mfma(_ptr(ab), blocks, iters, _ptr(sink), _ptr(clocks),
+                                _stream(stream)))
+
+
+def probe_sync_words(blocks):
+    return int(lib().sltx_probe_sync_words(blocks))
+
+
+def probe_sync(mode, fence, blocks, rounds, sync, faults, stream=None):
+    """rounds grid barriers among `blocks` one-wave blocks (sltx_probe_sync);
+    sync: zeroed int32 [probe_sync_words(blocks)], faults: int32 [1]."""
+    torch = _torch()
+    _need(sync, "sync", probe_sync_words(blocks), (torch.int32,))
+    _need(faults, "faults", 1, (torch.int32,))
+    check(lib().sltx_probe_sync(mode, fence, blocks, rounds, _ptr(sync), _ptr(faults),
+                                _stream(stream)))
 
 
 def matmul_q4_geglu(x, gate: Q4Weight, up: Q4Weight, M, K, N, out=None, stream=None):

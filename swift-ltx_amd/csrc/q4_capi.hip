@@ -888,6 +888,47 @@ int sltx_hbm_read(const void* src, uint64_t bytes, uint32_t* sink, void* stream)
                   fn);
 }
 
+int sltx_probe_empty(void* stream) {
+    int rc = ensure_device();
+    if (rc != kOk) return rc;
+    return finish(launch_probe_empty(static_cast<hipStream_t>(stream)), "sltx_probe_empty");
+}
+
+int sltx_probe_mfma(const void* ab, int32_t blocks, int32_t iters, float* sink, uint64_t* clocks,
+                    void* stream) {
+    const char* fn = "sltx_probe_mfma";
+    if (!ab || !sink || !clocks) return fail(kErrInvalid, "%s: null pointer argument", fn);
+    if (blocks < 1 || blocks > 65536 || iters < 0)
+        return fail(kErrInvalid, "%s: blocks must be in [1, 65536], iters >= 0", fn);
+    if (!aligned(ab, 16) || !aligned(sink, 4) || !aligned(clocks, 8))
+        return fail(kErrInvalid, "%s: misaligned pointer", fn);
+    int rc = ensure_device();
+    if (rc != kOk) return rc;
+    return finish(launch_probe_mfma(ab, blocks, iters, sink,
+                                    reinterpret_cast<unsigned long long*>(clocks),
+                                    static_cast<hipStream_t>(stream)), fn);
+}
+
+int sltx_probe_sync_words(int32_t blocks) { return blocks < 1 ? 0 : probe_sync_words(blocks); }
+
+int sltx_probe_sync(int32_t mode, int32_t fence, int32_t blocks, int32_t rounds, uint32_t* sync,
+                    int32_t* faults, void* stream) {
+    const char* fn = "sltx_probe_sync";
+    if (!sync || !faults) return fail(kErrInvalid, "%s: null pointer argument", fn);
+    if (mode < 0 || mode > 3 || rounds < 0 || blocks < 1)
+        return fail(kErrInvalid, "%s: mode must be 0 to 3, rounds >= 0, blocks >= 1", fn);
+    if (!aligned(sync, 64) || !aligned(faults, 4))
+        return fail(kErrInvalid, "%s: sync must be 64-byte aligned", fn);
+    int rc = ensure_device();
+    if (rc != kOk) return rc;
+    const int cap = probe_sync_max_blocks();
+    if (blocks > cap)
+        return fail(kErrInvalid, "%s: %d blocks exceed the %d this device holds at once", fn,
+                    blocks, cap);
+    return finish(launch_probe_sync(mode, fence, blocks, rounds, sync, faults,
+                                    static_cast<hipStream_t>(stream)), fn);
+}
+
 int sltx_decode_layer_faults(void* stream, int32_t* faults) {
     const char* fn = "sltx_decode_layer_faults";
     if (!faults) return fail(kErrInvalid, "%s: null pointer argument", fn);

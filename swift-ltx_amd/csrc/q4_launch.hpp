@@ -209,6 +209,14 @@ hipError_t launch_gemm_residual_rms_norm(GemmParams p, bool a_bf16, const float*
 // HBM read ceiling (q4_probe.hip): sink holds hbm_read_blocks() words.
 int hbm_read_blocks();
 hipError_t launch_hbm_read(const void* src, long n16, uint32_t* sink, hipStream_t st);
+// launch floor, register-only MFMA and grid hand-off probes (q4_probe.hip)
+hipError_t launch_probe_empty(hipStream_t st);
+hipError_t launch_probe_mfma(const void* ab, int blocks, int iters, float* sink,
+                             unsigned long long* clocks, hipStream_t st);
+int probe_sync_words(int blocks);
+int probe_sync_max_blocks();
+hipError_t launch_probe_sync(int mode, int fence, int blocks, int rounds, uint32_t* sync,
+                             int* faults, hipStream_t st);
 hipError_t launch_silu_mul(const uint16_t* a, const uint16_t* b, uint16_t* out, long count,
                            hipStream_t st);
 // Row-wise RMS norm, optionally of a + b (then the rounded sum goes to res_out).
