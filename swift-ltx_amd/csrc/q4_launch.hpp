@@ -188,6 +188,7 @@ void* sample_noalloc_scratch(int dev);
 // GEMM then runs).
 struct SkinnyPlan {
     int W, MT, STEPS, RT;
+    bool XL;   // X staged in LDS (one 16-row tile, M * K * 2 bytes that fit)
 };
 bool skinny_plan(const GemmParams& p, bool a_bf16, SkinnyPlan* out);
 hipError_t launch_skinny(const GemmParams& p, const SkinnyPlan& pl, hipStream_t st);

@@ -18,8 +18,16 @@
 //  * The block's scales and biases (one contiguous slab per array) are
 //    copied to LDS with direct 16-byte global -> LDS loads, issued first.
 //  * The wave's slice of X (all M rows, 16 per MFMA tile) stays in
-//    registers for the whole kernel, read through a buffer resource of
-//    M * K fp16 so that rows past M read as zeros without a branch.
+//    registers for the whole kernel.  With one 16-row tile and M * K * 2
+//    bytes that fit (XL), the block first copies the M real rows to LDS
+//    (rows padded by 16 bytes: the 16 rows of a fragment read hit distinct
+//    banks), before its weight loads, and each wave reads its fragments from
+//    there, with zeros for rows past M: every 16-byte load through the
+//    vector memory path costs that path 16 cycles whatever its lanes hold,
+//    so fragments loaded from memory for all 16 rows (zeros past M) cost
+//    the CU more load issue than its weights at small M.  Otherwise the
+//    fragments are read through a buffer resource of M * K fp16, so that
+//    rows past M read as zeros without a branch.
 //  * Each word is dequantized in registers without leaving fp16: its
 //    nibbles are spread to bytes (q0 q2 q4 q6 and q1 q3 q5 q7), and
 //    v_cvt_scalef32_pk_f16_fp8 turns two bytes into two fp16 at a time: read
@@ -100,12 +108,14 @@ __device__ __forceinline__ void store_one(const GemmParams& p, size_t o, float v
 // W waves, MT tiles of 16 activation rows, STEPS 128-wide k-steps per wave,
 // PAIR: two weight sets (gate, up) and a gated epilogue, RT tiles of 16
 // weight rows per block.  OCC: blocks per CU the register budget is sized for.
-template <int W, int MT, int STEPS, bool PAIR, int RT, int OCC>
+template <int W, int MT, int STEPS, bool PAIR, int RT, int OCC, bool XL>
 __global__ __launch_bounds__(64 * W, OCC) void q4_skinny_kernel(GemmParams p) {
     constexpr int NS = PAIR ? 2 : 1;
     constexpr int ROWS = 16 * RT;
+    static_assert(!XL || MT == 1, "LDS X holds one 16-row tile");
     __shared__ f32x4 red[W][RT][NS][MT][64];
-    extern __shared__ u32x4 sb_lds[];   // [2 * NS slabs][ROWS][groups] fp16
+    // [2 * NS slabs][ROWS][groups] fp16, then (XL) X rows [M][K + 8] fp16
+    extern __shared__ u32x4 sb_lds[];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, kq = lane >> 4;
@@ -132,12 +142,25 @@ __global__ __launch_bounds__(64 * W, OCC) void q4_skinny_kernel(GemmParams p) {
             }
         }
     }
+    // ---- XL: X rows [0, M) -> LDS, 1 KB (one wave-wide copy) at a time ----
+    const int xrow16 = K / 8 + 1;   // LDS row stride in 16-byte units (one of padding)
+    u32x4* const xl = sb_lds + 2 * NS * alloc;
+    if constexpr (XL) {
+        const int per_row = K / 512;   // 1 KB chunks per row (K % 1024 == 0)
+        for (int c = wave; c < p.M * per_row; c += W) {   // wave-uniform
+            const int m = c / per_row, j = c - m * per_row;
+            const char* src = reinterpret_cast<const char*>(p.a) + (size_t)m * K * 2 +
+                              j * 1024 + lane * 16;
+            __builtin_amdgcn_global_load_lds((const void*)src,
+                                             (lds_ptr_t)(xl + m * xrow16 + j * 64), 16, 0, 0);
+        }
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- the wave's slice of X: fragment r of step t is x[k .. k+7] with
     // k = kw0 + 128 t + 8 r, the k of word r of the lane's packed load ----
     u32x4 xa[MT][STEPS][4];
-    {
+    if constexpr (!XL) {
         const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<void*>(p.a), (short)0, p.M * K * 2, 0x00020000);
 #pragma unroll
@@ -173,10 +196,23 @@ __global__ __launch_bounds__(64 * W, OCC) void q4_skinny_kernel(GemmParams p) {
     // of the loads in flight and waits for all of them at the next use.  The
     // barrier is assembly with a memory clobber, so that no LDS read moves
     // above it.
-    __builtin_amdgcn_s_waitcnt(vmcnt_only(MT * STEPS * 4 + STEPS * RT * NS));
+    __builtin_amdgcn_s_waitcnt(vmcnt_only((XL ? 0 : MT * STEPS * 4) + STEPS * RT * NS));
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
     asm volatile("s_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
+
+    if constexpr (XL) {   // rows past M read row 0 and are replaced by zeros
+        const bool live = r16 < p.M;
+        const u32x4* xr = xl + (live ? r16 : 0) * xrow16 + kw0 / 8;
+        const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int t = 0; t < STEPS; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const u32x4 v = xr[16 * t + r];
+                xa[0][t][r] = live ? v : zero;
+            }
+    }
 
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -261,14 +297,28 @@ constexpr int skinny_vgprs(int mt, int steps, int ns, int rt) {
 }
 constexpr int kSkinnyMaxVgprs = 224;   // of the 256 one block of 8 waves may use
 
-template <int W, int MT, int STEPS, bool PAIR, int RT>
+// Dynamic LDS of a launch: the scale / bias slabs, then (XL) X's rows.
+size_t skinny_lds(const GemmParams& p, int rt, bool pair, bool xl) {
+    return (size_t)(pair ? 4 : 2) * slab_alloc(16 * rt, p.groups) * 16 +
+           (xl ? (size_t)p.M * (p.K / 8 + 1) * 16 : 0);
+}
+
+template <int W, int MT, int STEPS, bool PAIR, int RT, bool XL>
 hipError_t launch_cfg(const GemmParams& p, hipStream_t st) {
     // two blocks per CU when a wave fits in 128 VGPRs
     constexpr int OCC = (W == 8 && skinny_vgprs(MT, STEPS, PAIR ? 2 : 1, RT) <= 120) ? 2 : 1;
     const dim3 grid((unsigned)((p.N + 16 * RT - 1) / (16 * RT))), block(64 * W);
-    const size_t lds = (size_t)(PAIR ? 4 : 2) * slab_alloc(16 * RT, p.groups) * 16;
-    hipLaunchKernelGGL((q4_skinny_kernel<W, MT, STEPS, PAIR, RT, OCC>), grid, block, lds, st, p);
+    const size_t lds = skinny_lds(p, RT, PAIR, XL);
+    hipLaunchKernelGGL((q4_skinny_kernel<W, MT, STEPS, PAIR, RT, OCC, XL>), grid, block, lds, st, p);
     return hipGetLastError();
+}
+
+template <int W, int MT, int STEPS, bool PAIR, int RT>
+hipError_t launch_xl(const GemmParams& p, bool xl, hipStream_t st) {
+    if constexpr (MT == 1) {
+        if (xl) return launch_cfg<W, MT, STEPS, PAIR, RT, true>(p, st);
+    }
+    return launch_cfg<W, MT, STEPS, PAIR, RT, false>(p, st);
 }
 
 template <int W, int MT, int STEPS>
@@ -276,16 +326,16 @@ hipError_t launch_steps(const GemmParams& p, const SkinnyPlan& pl, hipStream_t s
     const bool pair = p.w1 != nullptr;
     if (pl.RT == 2) {
         if constexpr (W == 8 && skinny_vgprs(MT, STEPS, 2, 2) <= kSkinnyMaxVgprs)
-            return pair ? launch_cfg<W, MT, STEPS, true, 2>(p, st)
-                        : launch_cfg<W, MT, STEPS, false, 2>(p, st);
+            return pair ? launch_xl<W, MT, STEPS, true, 2>(p, pl.XL, st)
+                        : launch_xl<W, MT, STEPS, false, 2>(p, pl.XL, st);
         return hipErrorInvalidValue;
     }
     if (pair) {
         // a gated pair of 5 steps does not fit the 128 VGPRs of 16 waves
         if constexpr (W == 16 && STEPS == 5) return hipErrorInvalidValue;
-        else return launch_cfg<W, MT, STEPS, true, 1>(p, st);
+        else return launch_xl<W, MT, STEPS, true, 1>(p, pl.XL, st);
     }
-    return launch_cfg<W, MT, STEPS, false, 1>(p, st);
+    return launch_xl<W, MT, STEPS, false, 1>(p, pl.XL, st);
 }
 
 }  // namespace
@@ -300,7 +350,7 @@ bool skinny_plan(const GemmParams& p, bool a_bf16, SkinnyPlan* out) {
         p.epilogue != kEpiResidual)
         return false;
     const int mt = p.M <= 16 ? 1 : 2;
-    SkinnyPlan pl{0, mt, 0, 1};
+    SkinnyPlan pl{0, mt, 0, 1, false};
     // 8 waves of 1..6 steps (1..4 with 32 activation rows), else 16 waves of
     // 1..5 steps (1..4 for a gated pair; 16 activation rows)
     if (p.K % 1024 == 0 && p.K / 1024 <= (mt == 1 ? 6 : 4)) {
@@ -318,6 +368,9 @@ bool skinny_plan(const GemmParams& p, bool a_bf16, SkinnyPlan* out) {
     if (pl.W == 8 && p.M > 4 && (p.N + 31) / 32 >= kCUs &&
         skinny_vgprs(mt, pl.STEPS, 2, 2) <= kSkinnyMaxVgprs)
         pl.RT = 2;
+    // X in LDS: one 16-row tile whose rows fit beside the slabs, so that a
+    // block still gets its share of the CU's LDS
+    pl.XL = mt == 1 && skinny_lds(p, pl.RT, pair, true) <= (size_t)(pl.RT == 2 ? 128 : 64) * 1024;
     // scales and biases are staged with 16-byte loads
     const uintptr_t sb = reinterpret_cast<uintptr_t>(p.s0) | reinterpret_cast<uintptr_t>(p.b0) |
                          (pair ? reinterpret_cast<uintptr_t>(p.s1) | reinterpret_cast<uintptr_t>(p.b1)
