@@ -12,10 +12,13 @@ weight, o, gate/up+SiLU, down), down consuming the gate/up output.  Step i
 uses layer copy i mod --copies (default 40 copies, 2.27 GB of weights), so the
 256 MB MALL cannot hold the working set.
 
-value      = algorithmic bytes of exactly K steps / wall time of those K
+value      = algorithmic bytes of exactly K steps / GPU time of those K
              steps: W warm-up steps and then K timed steps, each a HIP graph
              of that many steps (graph replay removes the host launch cost, as
-             a decode loop would), bracketed by torch.cuda.synchronize().
+             a decode loop would), bracketed by torch.cuda.synchronize() and
+             timed by events recorded around the replay on its stream (the
+             host wall clock around it, which adds one replay's launch and
+             synchronize latency, is in timing.host_wall_gbs).
 stats      = the same layer over >= 50 replays (and >= 200 ms) of a graph of
              one rotation over the copies, an event after each replay:
              median and quartiles of the time per step.
@@ -131,6 +134,21 @@ def replay_stats(torch, replay, units, min_reps=MIN_REPLAYS, min_ms=MIN_MS, max_
     return {"median_us": round(float(q50), 3), "p25_us": round(float(q25), 3),
             "p75_us": round(float(q75), 3), "replays": reps, "units_per_replay": units,
             "timed_ms": round(float(per.sum() * units / 1e3), 1)}
+
+
+def upload_graph(g, stream):
+    """hipGraphUpload of a captured graph's executable on `stream`, so that
+    the replay in the timed region does not also pay the upload of its
+    kernel packets to the device (the timed region holds that one replay)."""
+    import ctypes
+    try:
+        exe = g.raw_cuda_graph_exec()
+        hip = ctypes.CDLL("libamdhip64.so")
+    except (AttributeError, OSError, RuntimeError):
+        return False
+    hip.hipGraphUpload.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    hip.hipGraphUpload.restype = ctypes.c_int
+    return hip.hipGraphUpload(ctypes.c_void_p(exe), ctypes.c_void_p(stream.cuda_stream)) == 0
 
 
 def capture(torch, fn, stream, warm=None):
@@ -265,14 +283,23 @@ def main():
 
     g_warm = graph_of(0, args.warmup) if args.warmup > 0 else None
     g_timed = graph_of(args.warmup, args.steps)
+    uploaded = upload_graph(g_timed, cap)
     torch.cuda.synchronize()
     if g_warm is not None:
         g_warm.replay()
+    # Exactly K steps, one replay, bracketed by synchronizes.  The time is
+    # the GPU's (events on the replaying stream, as BASELINE's rules time
+    # kernels); the host wall clock around it, which adds the launch and
+    # synchronize latency of one replay (~75 us), is reported beside it.
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    ev0.record()
     g_timed.replay()
+    ev1.record()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    host_wall = time.perf_counter() - t0
+    wall = ev0.elapsed_time(ev1) / 1e3
     value = args.steps * LAYER_BYTES / wall / 1e9
     del g_warm, g_timed
 
@@ -330,7 +357,11 @@ def main():
                                f"down); {C} distinct layer copies rotated",
                    "bytes_per_step": LAYER_BYTES, "launches_per_step": len(DECODE),
                    "timed": f"one HIP graph of exactly {args.steps} steps after one of "
-                            f"{args.warmup} warm-up steps, wall clock between synchronizes"},
+                            f"{args.warmup} warm-up steps, between synchronizes; GPU time from "
+                            f"events around the replay"},
+        "timing": {"gpu_ms": round(wall * 1e3, 4), "host_wall_ms": round(host_wall * 1e3, 4),
+                   "host_wall_gbs": round(args.steps * LAYER_BYTES / host_wall / 1e9, 1),
+                   "graph_uploaded": uploaded},
         "stats": {**layer_st, "ms_per_step_median": round(layer_st["median_us"] / 1e3, 5),
                   "what": f"per step, over replays of a graph of one {C}-copy rotation"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
