@@ -72,20 +72,25 @@ struct EmbedParams {
 
 // Token selection after the lm_head (q4_sample.hip).
 // Written by the sampler's gather kernel (and, mode 1, its narrow kernel)
-// for the kernels after it.  mode 0: the buckets are level-0
-// bins (key >> 20) and the gather kernel compacted the candidates; mode 1:
-// the candidate bins held too many tokens, and a range histogram splits them
-// into finer buckets -- segment A, level-0 bin a_bin in 2048 buckets of 2^9
-// keys, and segment B, bins [b_lo, b_hi] (empty if b_lo > b_hi) in 2048
-// buckets of 2^b_shift keys.  Tied buckets (one key) get per-chunk counts of
-// their key (up to 4: tkey).
+// for the kernels after it.  mode 0: the buckets are level-0 bins (key >> 20)
+// and the gather kernel compacted the candidates; mode 1: the candidate bins
+// held too many tokens, and a range histogram splits them into finer
+// buckets -- segment A, the keys [a_lo, a_end) of the cutoff's bin in
+// buckets [0, 2048) of 2^a_shift keys counted from a_base, and segment B,
+// the keys [b_lo, b_end) of the draw's bins above it in buckets [2048, 4096)
+// counted from b_base; each segment's range is the smallest to the largest
+// key its bins hold, and each base is its low key rounded down to the bucket
+// width.  Tied buckets (one key) get per-chunk counts of their key (up to 4:
+// tkey).
 struct SampleCtl {
     uint32_t ccount;              // compacted candidates
     int mode;
     int cut_found;                // the top-p target lies within the total mass
-    int a_bin, b_lo, b_hi, b_shift;
+    int a_shift, b_shift;
+    uint32_t a_lo, a_base, b_lo, b_base;
     int ntied;
     uint32_t tkey[4];
+    unsigned long long a_end, b_end;
     unsigned long long above;     // mode 1: mass of the keys above the range
     unsigned long long gap;       // mode 1: mass of the bins between the segments
     unsigned long long total;     // mass of all tokens

@@ -33,7 +33,8 @@
 //                   cutoff and the bins the draw can reach; if their untied
 //                   tokens fit the select kernel's LDS it compacts them
 //                   (mode 0), otherwise it builds a range histogram over
-//                   their keys in finer buckets (mode 1).  Bins and buckets
+//                   their keys in finer buckets (mode 1), sized from the
+//                   smallest and largest key of those bins.  Bins and buckets
 //                   of one key (ties) are never compacted: their tokens are
 //                   found by rank, from counts of the tied key per 1024-token
 //                   chunk kept during compaction.  (No grid-wide fence or
@@ -64,6 +65,7 @@ constexpr int kCandLds = 8192;      // candidates sample_select holds in LDS
 constexpr int kSelUnroll = 8;      // candidates each select thread loads before using them
 constexpr int kNthUnroll = 16;     // 16-byte key loads a lane has in flight in nth_with_key
 constexpr int kTiedSlots = 4;      // tied keys with per-chunk counts
+constexpr int kSmallLevel = 4096;  // tokens up to which a select level takes an 8-bit digit
 constexpr uint32_t kIdMask = 0xFFFFFFu;
 // seen-id bitmap of one scale block: up to 64 quads a thread (n <= 2^24
 // with 256 blocks of 256 threads), 4 bits a quad
@@ -103,6 +105,26 @@ __device__ __forceinline__ unsigned long long wave_incl_sum(unsigned long long x
     x += dpp_move<0x142, 0xA>(x);
     x += dpp_move<0x143, 0xC>(x);
     return x;
+}
+
+// The whole wave's smallest / largest value, in every lane: the same DPP
+// steps with `id` read where a shift has no source lane.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_move_id(uint32_t v, uint32_t id) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)id, (int)v, CTRL, ROWS, 0xF, false);
+}
+
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_minmax(uint32_t x) {
+    constexpr uint32_t id = MAX ? 0u : 0xFFFFFFFFu;
+    auto f = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
+    x = f(x, dpp_move_id<0x111, 0xF>(x, id));
+    x = f(x, dpp_move_id<0x112, 0xF>(x, id));
+    x = f(x, dpp_move_id<0x114, 0xF>(x, id));
+    x = f(x, dpp_move_id<0x118, 0xF>(x, id));
+    x = f(x, dpp_move_id<0x142, 0xA>(x, id));
+    x = f(x, dpp_move_id<0x143, 0xC>(x, id));
+    return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
 }
 
 // The whole wave's sum, in every lane.
@@ -194,12 +216,8 @@ __device__ __forceinline__ void key_minmax(bool ok, int d, uint32_t key, int lea
     const uint32_t k0 = (uint32_t)__builtin_amdgcn_readlane((int)key, lead);
     uint32_t lo = k0, hi = k0;
     if (__ballot(ok && key == k0) != act) {
-        lo = ok ? key : 0xFFFFFFFFu;
-        hi = ok ? key : 0u;
-        for (int o = 32; o > 0; o >>= 1) {
-            lo = min(lo, (uint32_t)__shfl_xor((int)lo, o, 64));
-            hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, 64));
-        }
+        lo = wave_minmax<false>(ok ? key : 0xFFFFFFFFu);
+        hi = wave_minmax<true>(ok ? key : 0u);
     }
     if ((int)(threadIdx.x & 63) == lead) {
         atomicMin(&kmin[d], lo);
@@ -208,11 +226,12 @@ __device__ __forceinline__ void key_minmax(bool ok, int d, uint32_t key, int lea
 }
 
 // The buckets the select positions are found in.  Mode 0: level-0 bins,
-// key >> 20.  Mode 1 (the range histogram): segment A, keys of level-0 bin
-// a_bin in buckets [0, kSplit) of 2^9 keys; segment B, keys of bins
-// [b_lo, b_hi] in buckets [kSplit, kBins) of 2^b_shift keys; the bins
-// between the segments are in no bucket (their mass, `gap`, is added to
-// segment A's running mass) and no candidate can lie there.
+// key >> 20.  Mode 1 (the range histogram): segment A, keys [a_lo, a_end) in
+// buckets [0, kSplit) of 2^a_shift keys counted from a_base; segment B, keys
+// [b_lo, b_end) in buckets [kSplit, kBins) of 2^b_shift keys counted from
+// b_base (each base is its low key rounded down to the bucket width); the
+// keys between the segments are in no bucket (their mass, `gap`, is added to
+// segment A's running mass) and no candidate lies there.
 constexpr int kSplit = kBins / 2;
 
 struct Buckets {
@@ -221,43 +240,52 @@ struct Buckets {
     const uint32_t* kmin;
     const uint32_t* kmax;
     int ranged;
-    uint32_t a_base, b_base;
-    unsigned long long b_lim;
-    int b_shift;
+    uint32_t a_lo, a_base, b_lo, b_base;
+    unsigned long long a_end, b_end;
+    int a_shift, b_shift;
     unsigned long long gap;
 
     // bucket of a key, kBins if none
     __device__ int of(uint32_t key) const {
         if (!ranged) return (int)(key >> 20);
-        if (key - a_base < (1u << 20)) return (int)((key - a_base) >> 9);
-        if (key >= b_base && (unsigned long long)key < b_lim)
+        if (key >= a_lo && (unsigned long long)key < a_end) return (int)((key - a_base) >> a_shift);
+        if (key >= b_lo && (unsigned long long)key < b_end)
             return kSplit + (int)((key - b_base) >> b_shift);
         return kBins;
     }
     // bits of the order key D below bucket b's key prefix, and that prefix
-    __device__ int low_bits(int b) const { return !ranged ? 44 : b < kSplit ? 33 : b_shift + 24; }
+    __device__ int low_bits(int b) const {
+        return !ranged ? 44 : (b < kSplit ? a_shift : b_shift) + 24;
+    }
     __device__ unsigned long long prefix(int b) const {
         if (!ranged) return (unsigned long long)b << 44;
-        if (b < kSplit) return (unsigned long long)((a_base >> 9) + (uint32_t)b) << 33;
+        if (b < kSplit)
+            return (unsigned long long)((a_base >> a_shift) + (uint32_t)b) << (a_shift + 24);
         return (unsigned long long)((b_base >> b_shift) + (uint32_t)(b - kSplit)) << (b_shift + 24);
     }
 };
 
 __device__ __forceinline__ Buckets level0_buckets(const SampleParams& p) {
-    return Buckets{p.h0cnt, p.h0mass, p.h0min, p.h0max, 0, 0u, 0u, 0ull, 20, 0ull};
-}
-
-// Segments A = bin a, B = bins [blo, bhi] (b_shift <= 20: buckets aligned).
-__device__ __forceinline__ Buckets range_buckets(const SampleParams& p, int a, int blo, int bhi,
-                                                 int b_shift, unsigned long long gap) {
-    const bool b_empty = blo > bhi;
-    return Buckets{p.h1cnt, p.h1mass, p.h1min, p.h1max, 1, (uint32_t)a << 20,
-                   b_empty ? 0u : (uint32_t)blo << 20,
-                   b_empty ? 0ull : (unsigned long long)(bhi + 1) << 20, b_shift, gap};
+    return Buckets{p.h0cnt, p.h0mass, p.h0min, p.h0max, 0, 0u, 0u, 0u, 0u, 0ull, 0ull, 20, 20,
+                   0ull};
 }
 
 __device__ __forceinline__ Buckets range_buckets(const SampleParams& p, const SampleCtl& c) {
-    return range_buckets(p, c.a_bin, c.b_lo, c.b_hi, c.b_shift, c.gap);
+    return Buckets{p.h1cnt, p.h1mass, p.h1min, p.h1max, 1, c.a_lo, c.a_base, c.b_lo, c.b_base,
+                   c.a_end, c.b_end, c.a_shift, c.b_shift, c.gap};
+}
+
+// The narrowest power-of-two bucket width (its log2) that puts the keys
+// [lo, hi] into kSegBuckets buckets counted from lo rounded down to the
+// width.  A segment has kSplit buckets; using fewer keeps the gather
+// kernel's histogram merge short (one set of device atomics per non-empty
+// bucket and block) while its buckets stay far narrower than a level-0 bin.
+constexpr uint32_t kSegBuckets = 512;
+
+__device__ __forceinline__ int seg_shift(uint32_t lo, uint32_t hi) {
+    int sh = 0;
+    while (sh < 32 && (hi >> sh) - (lo >> sh) >= kSegBuckets) ++sh;
+    return sh;
 }
 
 // Bucket b holds more than one token and all share one key (LDS bitmap of
@@ -358,6 +386,7 @@ struct BinScan {
     static constexpr int BPT = kBins / NT;
     uint32_t c[BPT];
     unsigned long long m[BPT];
+    uint32_t kmn[BPT], kmx[BPT];   // load_tied: each bucket's smallest and largest key
     unsigned long long excl, tot;
     int top;   // this thread's buckets: top, top-1, ..., top-BPT+1
 
@@ -381,19 +410,18 @@ struct BinScan {
                               uint32_t* tied_bm) {
         top = kBins - 1 - (int)threadIdx.x * BPT;
         tot = 0ull;
-        uint32_t lo[BPT], hi[BPT];
 #pragma unroll
         for (int k = 0; k < BPT; ++k) {
             c[k] = bk.cnt[top - k];
             m[k] = bk.mass[top - k];
-            lo[k] = bk.kmin[top - k];
-            hi[k] = bk.kmax[top - k];
+            kmn[k] = bk.kmin[top - k];
+            kmx[k] = bk.kmax[top - k];
         }
         uint32_t t = 0u;
 #pragma unroll
         for (int k = 0; k < BPT; ++k) {
             tot += m[k];
-            if (c[k] > 1u && lo[k] == hi[k]) t |= 1u << ((top - k) & 31);
+            if (c[k] > 1u && kmn[k] == kmx[k]) t |= 1u << ((top - k) & 31);
         }
         // the 32 / BPT consecutive threads of one bitmap word
         for (int o = 1; o < 32 / BPT; o <<= 1) t |= (uint32_t)__shfl_xor((int)t, o, 64);
@@ -485,10 +513,14 @@ __device__ int select_in_bin(const uint2* cand, int C, const Buckets& bk, int bu
     unsigned long long Mk = (0xFFFFFFFFFFFFFFull >> pos) << pos;
     uint32_t left = count;   // tokens under the prefix
     while (left > 64u && pos > 0) {
-        const int shift = pos > 12 ? pos - 12 : 0;
+        // at most kSmallLevel tokens: an 8-bit digit, whose 256 bins one wave
+        // scans (three barriers a level instead of the block-wide scan's eight)
+        const bool small = left <= (uint32_t)kSmallLevel;
+        const int width = small ? 8 : 12;
+        const int shift = pos > width ? pos - width : 0;
         const unsigned long long wmask = (1ull << (pos - shift)) - 1ull;
         pos = shift;
-        for (int b = tid; b < kBins; b += kSelThreads) {
+        for (int b = tid; b < (small ? 256 : kBins); b += kSelThreads) {
             H.cnt[b] = 0u;
             H.mass[b] = 0ull;
         }
@@ -502,9 +534,46 @@ __device__ int select_in_bin(const uint2* cand, int C, const Buckets& bk, int bu
             if (ok && (lead < 0 || lead == lane)) H.id[dg] = e.y;
         });
         __syncthreads();
-        BinScan<kSelThreads> scan;
-        scan.load(H.cnt, H.mass, above, sc);
-        scan.find(target, bs, sc);
+        if (small) {
+            // lane l: bins 255 - 4l .. 252 - 4l (descending order)
+            if (tid < 64) {
+                uint32_t c4[4];
+                unsigned long long m4[4], t = 0ull;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    c4[k] = H.cnt[255 - 4 * lane - k];
+                    m4[k] = H.mass[255 - 4 * lane - k];
+                    t += m4[k];
+                }
+                unsigned long long run = above + wave_incl_sum(t) - t;
+                int hk = -1;
+                uint32_t hc = 0u;
+                unsigned long long e = 0ull, hm = 0ull;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    if (hk < 0 && c4[k] && run + m4[k] >= target) {
+                        hk = k;
+                        e = run;
+                        hm = m4[k];
+                        hc = c4[k];
+                    }
+                    run += m4[k];
+                }
+                const unsigned long long hits = __ballot(hk >= 0);
+                if (lane == 0) bs.found = hits != 0ull;
+                if (hits && lane == __ffsll((long long)hits) - 1) {
+                    bs.bin = 255 - 4 * lane - hk;
+                    bs.excl = e;
+                    bs.incl = e + hm;
+                    bs.cnt = hc;
+                }
+            }
+            __syncthreads();
+        } else {
+            BinScan<kSelThreads> scan;
+            scan.load(H.cnt, H.mass, above, sc);
+            scan.find(target, bs, sc);
+        }
         if (!bs.found) return -1;
         P |= (unsigned long long)bs.bin << shift;
         Mk |= wmask << shift;
@@ -825,12 +894,6 @@ __device__ __forceinline__ unsigned long long tied_mass(const BinSel& s) {
     return (s.incl - s.excl) / s.cnt;
 }
 
-__device__ __forceinline__ int ceil_log2(int v) {
-    int l = 0;
-    while ((1 << l) < v) ++l;
-    return l;
-}
-
 // The first quad of this thread's grid-stride walk (NT threads a block),
 // requested early so its latency overlaps the histogram scans.
 template <int NT>
@@ -973,7 +1036,7 @@ __global__ __launch_bounds__(kGridThreads) void sample_gather_kernel(SampleParam
     __shared__ uint32_t offs[kWaves * 4];   // per wave and sub-step: slot offset in the block
     __shared__ uint32_t tsum[kWaves * kTiedSlots];
     __shared__ uint32_t tied_bm[kBins / 32];
-    __shared__ uint32_t s_tkey[kTiedSlots], s_cnt[kWaves];
+    __shared__ uint32_t s_tkey[kTiedSlots], s_cnt[kWaves], s_amn, s_amx;
     __shared__ int s_ntied;
     __shared__ SelScratch sc;
     __shared__ BinSel s1, s2;
@@ -1024,21 +1087,14 @@ __global__ __launch_bounds__(kGridThreads) void sample_gather_kernel(SampleParam
         gap += sc.wsum[w];
     }
     __syncthreads();   // sc.wsum is rewritten below
-    const int b_shift = 9 + (blo <= hi ? ceil_log2(hi - blo + 1) : 0);
-    const bool ranged = C > (uint32_t)kCandLds && b_shift <= 20;
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        SampleCtl& c = *p.ctl;
-        c.mode = ranged ? 1 : 0;
-        c.cut_found = s1.found;
-        c.a_bin = a;
-        c.b_lo = blo;
-        c.b_hi = hi;
-        c.b_shift = b_shift;
-        c.above = above_hi;
-        c.gap = gap;
-        c.total = s1.total;
-    }
+    const bool ranged = C > (uint32_t)kCandLds;
     if (!ranged) {
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            SampleCtl& c = *p.ctl;
+            c.mode = 0;
+            c.cut_found = s1.found;
+            c.total = s1.total;
+        }
         pick_tied<kGridThreads>(bk, tied_bm, lo, hi, s_tkey, &s_ntied, sc);
         const int nt = s_ntied;
         if (blockIdx.x == 0 && threadIdx.x < kTiedSlots) {
@@ -1049,8 +1105,64 @@ __global__ __launch_bounds__(kGridThreads) void sample_gather_kernel(SampleParam
                               s_tkey, nt, offs, tsum);
         return;
     }
+    // The segments' key ranges, from the level-0 key extremes the scan holds:
+    // A, bin a; B, the non-empty bins of [blo, hi] (min / max over the block).
+    uint32_t bmn = 0xFFFFFFFFu, bmx = 0u;
+#pragma unroll
+    for (int k = 0; k < BinScan<kGridThreads>::BPT; ++k) {
+        const int b = scan.top - k;
+        if (b >= blo && b <= hi && scan.c[k]) {
+            bmn = min(bmn, scan.kmn[k]);
+            bmx = max(bmx, scan.kmx[k]);
+        }
+        if (b == a) {   // one thread
+            s_amn = scan.c[k] ? scan.kmn[k] : 1u;
+            s_amx = scan.c[k] ? scan.kmx[k] : 0u;
+        }
+    }
+    bmn = wave_minmax<false>(bmn);
+    bmx = wave_minmax<true>(bmx);
+    if (lane == 0) {
+        s_cnt[wid] = bmn;
+        offs[wid] = bmx;
+    }
+    __syncthreads();
+    for (int w = 0; w < kWaves; ++w) {
+        bmn = min(bmn, s_cnt[w]);
+        bmx = max(bmx, offs[w]);
+    }
+    const uint32_t amn = s_amn, amx = s_amx;
+    const bool a_some = amn <= amx;
+    const int a_shift = a_some ? seg_shift(amn, amx) : 0;
+    const int b_shift = bmn <= bmx ? seg_shift(bmn, bmx) : 0;
+    SampleCtl seg;
+    seg.a_shift = a_shift;
+    seg.b_shift = b_shift;
+    seg.a_lo = amn;
+    seg.a_base = (amn >> a_shift) << a_shift;
+    seg.a_end = a_some ? (unsigned long long)amx + 1ull : 0ull;
+    seg.b_lo = bmn <= bmx ? bmn : 1u;
+    seg.b_base = bmn <= bmx ? (bmn >> b_shift) << b_shift : 0u;
+    seg.b_end = bmn <= bmx ? (unsigned long long)bmx + 1ull : 0ull;
+    seg.gap = gap;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        SampleCtl& c = *p.ctl;
+        c.mode = 1;
+        c.cut_found = s1.found;
+        c.a_shift = seg.a_shift;
+        c.b_shift = seg.b_shift;
+        c.a_lo = seg.a_lo;
+        c.a_base = seg.a_base;
+        c.a_end = seg.a_end;
+        c.b_lo = seg.b_lo;
+        c.b_base = seg.b_base;
+        c.b_end = seg.b_end;
+        c.above = above_hi;
+        c.gap = gap;
+        c.total = s1.total;
+    }
     // the range histogram: counts, masses and key extremes of its buckets
-    const Buckets rb = range_buckets(p, a, blo, hi, b_shift, gap);
+    const Buckets rb = range_buckets(p, seg);
     for (int b = threadIdx.x; b < kBins; b += kGridThreads) {
         hc[b] = 0u;
         hm[b] = 0ull;
