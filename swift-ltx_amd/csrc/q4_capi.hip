@@ -274,8 +274,17 @@ int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w
     p.ws = nullptr;
     p.splits = 1;
     p.split_tiles = 0;
+    // M <= 4: the narrow route (4x4x4 MFMA blocks, whole-line loads).  M <= 8:
+    // the narrow route too when the small-M route's grid would not be
+    // resident at once; measured on the Llama and T5 shapes, the small-M
+    // route is faster otherwise.
+    NarrowPlan np;
     SkinnyPlan sp;
-    if (skinny_plan(p, x_dtype == kBF16, &sp)) return finish(launch_skinny(p, sp, st), fn);
+    const bool narrow = narrow_plan(p, x_dtype == kBF16, &np);
+    const bool skinny = skinny_plan(p, x_dtype == kBF16, &sp);
+    if (narrow && (p.M <= 4 || !skinny || skinny_rounds(p, sp) > 1))
+        return finish(launch_narrow(p, np, st), fn);
+    if (skinny) return finish(launch_skinny(p, sp, st), fn);
     const size_t need = gemm_workspace_bytes(p);
     if (need > 0) p.ws = stream_workspace(st, need);
     return finish(launch_gemm(p, x_dtype == kBF16, st), fn);

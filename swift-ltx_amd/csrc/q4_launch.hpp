@@ -187,6 +187,16 @@ constexpr int kMaxDevices = 64;
 int sample_noalloc_scratch_init(int dev);
 // The address resolved for `dev`, or null before sample_noalloc_scratch_init.
 void* sample_noalloc_scratch(int dev);
+// Narrow-M route (q4_narrow.hip, M <= 8): a wave owns 4 rows of each weight
+// set and 1/S of K's 512-k runs on 4x4x4 MFMA blocks; RG row groups (S waves
+// each) per block, MB A blocks of 4 activation rows.  narrow_plan returns
+// false when the shape or epilogue is not covered (the small-M route is
+// tried next).
+struct NarrowPlan {
+    int S, RG, MB;
+};
+bool narrow_plan(const GemmParams& p, bool a_bf16, NarrowPlan* out);
+hipError_t launch_narrow(const GemmParams& p, const NarrowPlan& pl, hipStream_t st);
 // Small-M route (q4_skinny.hip): W waves split K into STEPS 128-wide steps
 // each, MT tiles of 16 activation rows, RT tiles of 16 weight rows per block.
 // skinny_plan returns false when the shape or epilogue is not covered (the
@@ -197,6 +207,8 @@ struct SkinnyPlan {
 };
 bool skinny_plan(const GemmParams& p, bool a_bf16, SkinnyPlan* out);
 hipError_t launch_skinny(const GemmParams& p, const SkinnyPlan& pl, hipStream_t st);
+// Rounds of co-resident blocks the plan's grid takes (1: every block at once).
+int skinny_rounds(const GemmParams& p, const SkinnyPlan& pl);
 // Bytes of split-K workspace the launch of `p` would use (0: it does not split).
 size_t gemm_workspace_bytes(const GemmParams& p);
 // Launches the GEMM; splits K only if p.ws is non-null (and then needs

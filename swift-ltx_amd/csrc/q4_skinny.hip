@@ -42,6 +42,7 @@
 //    epilogue (gated SiLU / GELU-tanh pair, bias, GELU-tanh, residual add)
 //    runs on the fp32 sums.
 #include "q4_common.hpp"
+#include "q4_dequant.hpp"
 #include "q4_launch.hpp"
 
 namespace sltx {
@@ -51,12 +52,6 @@ namespace {
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// s_waitcnt immediates (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt
-// 6:4, lgkmcnt 11:8; a field at its maximum does not wait)
-__host__ __device__ constexpr int vmcnt_only(int n) {
-    return (n & 0xF) | (0x7 << 4) | (0xF << 8) | (((n >> 4) & 0x3) << 14);
-}
-
 // 16-byte pieces of one array's scale / bias slab (rows x groups fp16), and
 // the pieces reserved per slab in LDS (whole waves of 64).
 __host__ __device__ constexpr int slab_pieces(int rows, int groups) { return rows * groups / 8; }
@@ -64,45 +59,9 @@ __host__ __device__ constexpr int slab_alloc(int rows, int groups) {
     return (slab_pieces(rows, groups) + 63) / 64 * 64;
 }
 
-// x[k .. k+7] as four fp16 pairs (x0,x1) (x2,x3) (x4,x5) (x6,x7) -> the
-// pairs (x0,x2) (x1,x3) (x4,x6) (x5,x7) of the dequantized word's order.
-__device__ __forceinline__ u32x4 permute_x(u32x4 r) {
-    u32x4 a;
-    a[0] = __builtin_amdgcn_perm(r[1], r[0], 0x05040100u);
-    a[1] = __builtin_amdgcn_perm(r[1], r[0], 0x07060302u);
-    a[2] = __builtin_amdgcn_perm(r[3], r[2], 0x05040100u);
-    a[3] = __builtin_amdgcn_perm(r[3], r[2], 0x07060302u);
-    return a;
-}
-
-// One packed word -> 8 fp16 s*q+b in the order q0,q2,q1,q3,q4,q6,q5,q7.
-__device__ __forceinline__ u32x4 dequant_word(uint32_t w, f16x2 s2, f16x2 b2) {
-    const uint32_t lo = w & 0x0F0F0F0Fu;          // bytes q0 q2 q4 q6
-    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;   // bytes q1 q3 q5 q7
-    const float k512 = 512.0f;                    // 2^9: fp8 byte b -> b
-    f16x2 q[4];
-    q[0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, k512, false);   // q0, q2
-    q[1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, k512, false);   // q1, q3
-    q[2] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, k512, true);    // q4, q6
-    q[3] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, k512, true);    // q5, q7
-    u32x4 o;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] = as_u32(__builtin_elementwise_fma(q[e], s2, b2));
-    return o;
-}
-
 __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
                                                   __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
-}
-
-__device__ __forceinline__ void store_one(const GemmParams& p, size_t o, float v) {
-    if (p.y_dtype == kF32)
-        reinterpret_cast<float*>(p.y)[o] = v;
-    else if (p.y_dtype == kBF16)
-        reinterpret_cast<uint16_t*>(p.y)[o] = f2bf(v);
-    else
-        reinterpret_cast<uint16_t*>(p.y)[o] = f2h(v);
 }
 
 // W waves, MT tiles of 16 activation rows, STEPS 128-wide k-steps per wave,
@@ -303,10 +262,15 @@ size_t skinny_lds(const GemmParams& p, int rt, bool pair, bool xl) {
            (xl ? (size_t)p.M * (p.K / 8 + 1) * 16 : 0);
 }
 
+// Blocks per CU a configuration is compiled for: two when a wave fits in
+// 128 VGPRs.
+constexpr int skinny_occ(int w, int mt, int steps, int ns, int rt) {
+    return (w == 8 && skinny_vgprs(mt, steps, ns, rt) <= 120) ? 2 : 1;
+}
+
 template <int W, int MT, int STEPS, bool PAIR, int RT, bool XL>
 hipError_t launch_cfg(const GemmParams& p, hipStream_t st) {
-    // two blocks per CU when a wave fits in 128 VGPRs
-    constexpr int OCC = (W == 8 && skinny_vgprs(MT, STEPS, PAIR ? 2 : 1, RT) <= 120) ? 2 : 1;
+    constexpr int OCC = skinny_occ(W, MT, STEPS, PAIR ? 2 : 1, RT);
     const dim3 grid((unsigned)((p.N + 16 * RT - 1) / (16 * RT))), block(64 * W);
     const size_t lds = skinny_lds(p, RT, PAIR, XL);
     hipLaunchKernelGGL((q4_skinny_kernel<W, MT, STEPS, PAIR, RT, OCC, XL>), grid, block, lds, st, p);
@@ -378,6 +342,12 @@ bool skinny_plan(const GemmParams& p, bool a_bf16, SkinnyPlan* out) {
     if ((sb & 15) != 0) return false;
     *out = pl;
     return true;
+}
+
+int skinny_rounds(const GemmParams& p, const SkinnyPlan& pl) {
+    const long blocks = (p.N + 16 * pl.RT - 1) / (16 * pl.RT);
+    const long per_round = (long)kCUs * skinny_occ(pl.W, pl.MT, pl.STEPS, p.w1 ? 2 : 1, pl.RT);
+    return (int)((blocks + per_round - 1) / per_round);
 }
 
 hipError_t launch_skinny(const GemmParams& p, const SkinnyPlan& pl, hipStream_t st) {

@@ -1,6 +1,12 @@
 """GPU parity of the small-M route (q4_skinny.hip: M <= 32, K a multiple of
 1024 or of 2048) through the C ABI.
 
+The narrow route (q4_narrow.hip, tests/test_gpu_narrow.py) runs M <= 4 where
+it applies (K / 512 in {4, 6, 8, 10, 12, 16, 20}, M * K * 2 <= 78 KB), and
+M <= 8 where this route's grid would take more than one round; the shapes
+here keep this route's own configurations covered: M > 4 with a one-round
+grid, or K = 1024, or X too large for the narrow route's LDS.
+
 Same semantics as the GEMM (matmulQ4Fast / matmulQ4FastF32, Ops.swift:312-381;
 the SwiGLU and GeGLU pairs, LlamaModel.swift:275-277 and
 T5Encoder.swift:191-199): the weights are dequantized to fp16 as s*q+b in one
@@ -22,9 +28,9 @@ pytestmark = pytest.mark.gpu
 # N not a multiple of 16, every group size.
 SHAPES = [
     (2, 200, 1024, 64), (5, 64, 2048, 32), (16, 100, 3072, 64), (8, 48, 4096, 128),
-    (3, 80, 5120, 64), (7, 33, 6144, 64), (17, 96, 1024, 32), (32, 112, 2048, 64),
-    (24, 50, 3072, 128), (31, 64, 4096, 64), (2, 96, 8192, 64), (16, 40, 10240, 64),
-    (9, 24, 14336, 32), (1, 300, 3072, 64),
+    (5, 80, 5120, 64), (7, 33, 6144, 64), (17, 96, 1024, 32), (32, 112, 2048, 64),
+    (24, 50, 3072, 128), (31, 64, 4096, 64), (6, 96, 8192, 64), (16, 40, 10240, 64),
+    (9, 24, 14336, 32), (1, 300, 1024, 64), (4, 64, 10240, 64),
 ]
 
 
@@ -70,7 +76,7 @@ def test_skinny_dequant_bit_exact(pkg, dev, K, g):
         assert np.array_equal(yq.cpu().numpy(), codes[ks]), c
 
 
-@pytest.mark.parametrize("M,N,K", [(2, 8192, 3072), (8, 200, 3072), (32, 8192, 3072),
+@pytest.mark.parametrize("M,N,K", [(5, 8192, 3072), (8, 200, 3072), (32, 8192, 3072),
                                    (20, 64, 4096)])
 @pytest.mark.parametrize("gelu", [False, True])
 def test_skinny_gated_pair(pkg, dev, M, N, K, gelu):
@@ -88,7 +94,7 @@ def test_skinny_gated_pair(pkg, dev, M, N, K, gelu):
     assert_parity(y.cpu().numpy(), ref, TOL_GEMM_F16, f"{'geglu' if gelu else 'swiglu'} M={M}")
 
 
-@pytest.mark.parametrize("M", [2, 12, 29])
+@pytest.mark.parametrize("M", [6, 12, 29])
 def test_skinny_residual_and_bias_gelu(pkg, dev, M):
     """The single-set epilogues on the small-M route: residual add
     (linear + elemAdd, LlamaModel.swift:330-331) and bias + GELU-tanh with an
