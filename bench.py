@@ -99,6 +99,9 @@ def parse():
                     help="only: the token-selection leg (graphs), then TRACE_CALLS eager calls of "
                          "each sampling case, for rocprofv3 --kernel-trace; with "
                          "--summarize-trace: summarize such a trace per case and kernel")
+    ap.add_argument("--small-m", action="store_true",
+                    help="only: the small-M legs (graphs of rotated weights), for rocprofv3 "
+                         "--kernel-trace runs of the narrow and small-M kernels")
     ap.add_argument("--summarize-trace", metavar="DIR",
                     help="print a markdown summary of a rocprofv3 --kernel-trace output folder "
                          "(rocpd .db or kernel_trace.csv) of this script; no GPU needed")
@@ -210,6 +213,8 @@ def main():
     if args.summarize_trace:
         if args.token_select:
             print(summarize_token_select_trace(args.summarize_trace))
+        elif args.small_m:
+            print(summarize_small_m_trace(args.summarize_trace))
         else:
             print(summarize_trace(args.summarize_trace, args.copies))
         return
@@ -239,6 +244,9 @@ def main():
         return
     if args.ceilings:
         ceilings_run(pkg, torch, gen, dev)
+        return
+    if args.small_m:
+        print(json.dumps(small_m_legs(pkg, torch, gen, dev, torch.cuda.Stream())), flush=True)
         return
     if args.token_select:
         print(json.dumps(token_select_leg(pkg, torch, gen, dev)), flush=True)
@@ -829,14 +837,14 @@ def gemm_legs(pkg, torch, gen, dev, cap):
     return res
 
 
-SMALL_M = (2, 8, 32, 128)
+SMALL_M = (2, 4, 8, 32, 128)
 
 
 def small_m_legs(pkg, torch, gen, dev, cap, min_gb=2.0):
     """Small M (T5 encoder layers at S <= 128, T5Encoder.swift:140-205, and
     short prompts): the Llama gate/up + SiLU shape and the T5-XXL shapes
     (K = 4096: q/k/v/o [4096 x 4096], gelu FFN wi_0/wi_1 [10240 x 4096] in
-    one launch, wo [4096 x 10240]) at M in 2, 8, 32, 128, each over weight
+    one launch, wo [4096 x 10240]) at M in 2, 4, 8, 32, 128, each over weight
     copies rotated to >= min_gb GB.  GB/s = weight + activation bytes per
     launch / median time; bound: HBM (every weight byte read once per launch)."""
     shapes = (("llama_gate_up_silu", 8192, 3072, 2, "silu"),
@@ -1021,7 +1029,7 @@ def _trace_rows(folder):
 
 def _short(name):
     n = name[5:] if name.startswith("void ") else name
-    n = n.replace("sltx::", "")
+    n = n.replace("sltx::", "").replace("(anonymous namespace)::", "")
     i = n.find("(")
     if i > 0 and not n.startswith("at::"):
         n = n[:i]
@@ -1106,6 +1114,41 @@ def summarize_token_select_trace(folder):
             meds.append(float(np.median([(r[2] - r[1]) / 1e3 for r in ks])))
         out.append(f"| {case} | " + " | ".join(f"{m:.1f}" for m in meds) +
                    f" | {sum(meds):.1f} |")
+    return "\n".join(out)
+
+
+def summarize_small_m_trace(folder):
+    """Markdown table of a kernel trace of `bench.py --small-m`: the legs run
+    in SMALL_M order per shape, and each (shape, M) is one unbroken run of
+    this library's dispatches (torch kernels that make the next inputs
+    separate them; the one-call warm-up before each graph is dropped).  Per
+    run: the kernels, blocks x threads, dispatches and the median duration of
+    each kernel."""
+    import numpy as np
+    runs, cur = [], []
+    for r in _trace_rows(folder):
+        if "q4_" in r[0] and "_kernel" in r[0] and "at::" not in r[0]:
+            cur.append(r)
+        elif cur:
+            runs.append(cur)
+            cur = []
+    if cur:
+        runs.append(cur)
+    runs = [r for r in runs if len(r) >= MIN_REPLAYS]   # drop the one-call warm-ups
+    names = ["llama_gate_up_silu", "t5_attn_proj", "t5_ffn_wi_gelu", "t5_ffn_wo"]
+    want = len(names) * len(SMALL_M)
+    if len(runs) != want:
+        return f"expected {want} runs of q4 dispatches, found {len(runs)}"
+    out = ["| shape | M | kernel | blocks x threads | dispatches | median us |",
+           "|---|---|---|---|---|---|"]
+    for i, run in enumerate(runs):
+        shape, M = names[i // len(SMALL_M)], SMALL_M[i % len(SMALL_M)]
+        kinds = {}
+        for r in run:
+            kinds.setdefault((_short(r[0]), r[3], r[4]), []).append((r[2] - r[1]) / 1e3)
+        for (k, blocks, threads), d in kinds.items():
+            out.append(f"| {shape} | {M} | `{k}` | {blocks} x {threads} | {len(d)} | "
+                       f"{float(np.median(d)):.2f} |")
     return "\n".join(out)
 
 
