@@ -12,9 +12,10 @@
 //    the gated epilogues) and all K; its W waves split K into equal slices of
 //    128 * STEPS.  In wave w, lane l covers row l % 16 of each 16-row tile
 //    and, in each 128-wide k-step, the 32 k at offset 32 * (l / 16): one
-//    16-byte load of packed words, four lanes reading 64 contiguous bytes of
-//    a row.  Every load of a wave is issued before the first MFMA, in the
-//    order of use.
+//    16-byte load of packed words per step.  Two steps are loaded together
+//    as 8 rows x 128 contiguous bytes per wave-wide load and swapped into
+//    that layout with one DPP move per word.  Every load of a wave is issued
+//    before the first MFMA, in the order of use.
 //  * The block's scales and biases (one contiguous slab per array) are
 //    copied to LDS with direct 16-byte global -> LDS loads, issued first.
 //  * The wave's slice of X (all M rows, 16 per MFMA tile) stays in
@@ -136,17 +137,39 @@ __global__ __launch_bounds__(64 * W, OCC) void q4_skinny_kernel(GemmParams p) {
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- packed words, step by step ----
+    // Steps t, t+1 of a tile and set are loaded as 2 x 8 rows x 128 bytes
+    // (whole lines: load h, lane l reads row (l & 7) | 8h, piece
+    // 4 * bit3(l) + l / 16 of the 128-byte run) and swapped into the MFMA
+    // layout before use: a load of the layout itself is 16 rows x 64 bytes,
+    // every request half a line, and streams ~15% slower.  An odd last step
+    // keeps that layout.
     u32x4 wq[STEPS][RT][NS];
+    const int prow = lane & 7, ppiece = 4 * ((lane >> 3) & 1) + (lane >> 4);
 #pragma unroll
-    for (int t = 0; t < STEPS; ++t)
+    for (int t = 0; t < STEPS; t += 2) {
+        if (t + 1 < STEPS) {
 #pragma unroll
-        for (int i = 0; i < RT; ++i)
+            for (int i = 0; i < RT; ++i)
 #pragma unroll
-            for (int s = 0; s < NS; ++s) {
-                const int row = min(n0 + 16 * i + r16, p.N - 1);
-                const uint32_t* wr = (s ? p.w1 : p.w0) + (size_t)row * (K / 8) + kw0 / 8;
-                wq[t][i][s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + 16 * t));
-            }
+                for (int s = 0; s < NS; ++s)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const int row = min(n0 + 16 * i + (prow | (h << 3)), p.N - 1);
+                        const uint32_t* wr = (s ? p.w1 : p.w0) + (size_t)row * (K / 8) +
+                                             (wave * 128 * STEPS + 128 * t) / 8 + ppiece * 4;
+                        wq[t + h][i][s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr));
+                    }
+        } else {
+#pragma unroll
+            for (int i = 0; i < RT; ++i)
+#pragma unroll
+                for (int s = 0; s < NS; ++s) {
+                    const int row = min(n0 + 16 * i + r16, p.N - 1);
+                    const uint32_t* wr = (s ? p.w1 : p.w0) + (size_t)row * (K / 8) + kw0 / 8;
+                    wq[t][i][s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + 16 * t));
+                }
+        }
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     // The slabs are complete once at most the X and weight loads issued after
@@ -190,7 +213,24 @@ __global__ __launch_bounds__(64 * W, OCC) void q4_skinny_kernel(GemmParams p) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) acc[i][s][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < STEPS; ++t)
+    for (int t = 0; t < STEPS; ++t) {
+        if ((t & 1) == 0 && t + 1 < STEPS) {
+            // lane l of the pair's load h holds row (l & 7) | 8h, piece
+            // 4 * bit3(l) + l / 16: lanes whose bit 3 is h already hold their
+            // step-h data; the others take it from lane l ^ 8 of the other
+            // load (a row rotation by 8 inside each 16-lane row, written
+            // only to the banks of 4 lanes that need it)
+#pragma unroll
+            for (int i = 0; i < RT; ++i)
+#pragma unroll
+                for (int s = 0; s < NS; ++s)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const int r0 = (int)wq[t][i][s][c], r1 = (int)wq[t + 1][i][s][c];
+                        wq[t][i][s][c] = (uint32_t)__builtin_amdgcn_update_dpp(r0, r1, 0x128, 0xF, 0xC, false);
+                        wq[t + 1][i][s][c] = (uint32_t)__builtin_amdgcn_update_dpp(r1, r0, 0x128, 0xF, 0x3, false);
+                    }
+        }
 #pragma unroll
         for (int i = 0; i < RT; ++i)
 #pragma unroll
@@ -209,6 +249,7 @@ __global__ __launch_bounds__(64 * W, OCC) void q4_skinny_kernel(GemmParams p) {
                         acc[i][s][mt] = mfma16(xa[mt][t][r], b, acc[i][s][mt]);
                 }
             }
+    }
 
 #pragma unroll
     for (int i = 0; i < RT; ++i)
