@@ -88,6 +88,9 @@ def parse():
     ap.add_argument("--traffic", action="store_true",
                     help="only: 24 launches of the dominant kernel over 12 weight copies, then a "
                          "256 MiB torch copy (the calibration kernel), for rocprofv3 --pmc runs")
+    ap.add_argument("--traffic-m", default="1",
+                    help="with --traffic: activation rows of the gate/up launches, a comma list "
+                         "(1: the GEMV; 2 and 8 run the narrow and small-M kernels)")
     ap.add_argument("--gemm-pmc", action="store_true",
                     help="only: 10 launches each of the M=750 prefill gate/up (SiLU) and down "
                          "GEMMs, for rocprofv3 --pmc MFMA-utilisation runs")
@@ -102,6 +105,10 @@ def parse():
     ap.add_argument("--small-m", action="store_true",
                     help="only: the small-M legs (graphs of rotated weights), for rocprofv3 "
                          "--kernel-trace runs of the narrow and small-M kernels")
+    ap.add_argument("--summarize-pmc", metavar="DIR",
+                    help="print the mean of the counter per kernel (dispatch count, KiB) of a "
+                         "rocprofv3 --pmc output folder (rocpd .db or counter_collection.csv); "
+                         "no GPU needed")
     ap.add_argument("--summarize-trace", metavar="DIR",
                     help="print a markdown summary of a rocprofv3 --kernel-trace output folder "
                          "(rocpd .db or kernel_trace.csv) of this script; no GPU needed")
@@ -210,6 +217,9 @@ def _wsb(q):
 
 def main():
     args = parse()
+    if args.summarize_pmc:
+        print(summarize_pmc(args.summarize_pmc))
+        return
     if args.summarize_trace:
         if args.token_select:
             print(summarize_token_select_trace(args.summarize_trace))
@@ -237,7 +247,7 @@ def main():
     gen.manual_seed(0)
 
     if args.traffic:
-        traffic_run(pkg, torch, gen, dev)
+        traffic_run(pkg, torch, gen, dev, tuple(int(m) for m in args.traffic_m.split(",")))
         return
     if args.gemm_pmc:
         gemm_pmc_run(pkg, torch, gen, dev)
@@ -882,16 +892,18 @@ def small_m_legs(pkg, torch, gen, dev, cap, min_gb=2.0):
 
 # ------------------------------------------------------------ PMC modes ---
 
-def traffic_run(pkg, torch, gen, dev):
-    """Workload for the FETCH_SIZE / WRITE_SIZE passes: the dominant kernel
-    (fused gate/up GEMV) 24 times over 12 distinct weight copies, then one
-    256 MiB copy_ whose counters give the bytes-per-count calibration."""
+def traffic_run(pkg, torch, gen, dev, ms=(1,)):
+    """Workload for the FETCH_SIZE / WRITE_SIZE passes: the fused gate/up +
+    SiLU x up launch at each M of `ms` (M = 1: the dominant GEMV) 24 times
+    over 12 distinct weight copies, then one 256 MiB copy_ whose counters
+    give the bytes-per-count calibration."""
     sets = [[q4(pkg, torch, 8192, 3072, gen, dev) for _ in range(2)] for _ in range(12)]
-    x = torch.randn(1, 3072, generator=gen, device=dev).half()
-    y = torch.empty(1, 8192, device=dev, dtype=torch.float16)
-    for _ in range(2):
-        for gate, up in sets:
-            pkg.matmul_q4_silu_mul(x, gate, up, 1, 3072, 8192, out=y)
+    for M in ms:
+        x = torch.randn(M, 3072, generator=gen, device=dev).half()
+        y = torch.empty(M, 8192, device=dev, dtype=torch.float16)
+        for _ in range(2):
+            for gate, up in sets:
+                pkg.matmul_q4_silu_mul(x, gate, up, M, 3072, 8192, out=y)
     src = torch.empty(256 * 2 ** 20 // 4, device=dev, dtype=torch.float32).normal_()
     dst = torch.empty_like(src)
     dst.copy_(src)
@@ -1114,6 +1126,30 @@ def summarize_token_select_trace(folder):
             meds.append(float(np.median([(r[2] - r[1]) / 1e3 for r in ks])))
         out.append(f"| {case} | " + " | ".join(f"{m:.1f}" for m in meds) +
                    f" | {sum(meds):.1f} |")
+    return "\n".join(out)
+
+
+def summarize_pmc(folder):
+    """Per kernel of a rocprofv3 --pmc run: dispatches and the mean value of
+    each counter collected (one line per kernel and counter)."""
+    import csv
+    import glob
+    import sqlite3
+    vals = {}
+    for db in sorted(glob.glob(os.path.join(folder, "**", "*.db"), recursive=True)):
+        c = sqlite3.connect(db)
+        for name, ctr, v in c.execute("select kernel_name, counter_name, value "
+                                      "from counters_collection"):
+            vals.setdefault((name, ctr), []).append(float(v))
+    if not vals:
+        for f in sorted(glob.glob(os.path.join(folder, "**", "*counter_collection.csv"),
+                                  recursive=True)):
+            for r in csv.DictReader(open(f)):
+                vals.setdefault((r["Kernel_Name"], r["Counter_Name"]), []).append(
+                    float(r["Counter_Value"]))
+    out = []
+    for (name, ctr), v in vals.items():
+        out.append(f"{ctr} {len(v):5d} dispatches  mean {sum(v) / len(v):14.1f}  {_short(name)}")
     return "\n".join(out)
 
 
