@@ -275,14 +275,15 @@ int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w
     p.splits = 1;
     p.split_tiles = 0;
     // M <= 4: the narrow route (4x4x4 MFMA blocks, whole-line loads).  M <= 8:
-    // the narrow route too when the small-M route's grid would not be
-    // resident at once; measured on the Llama and T5 shapes, the small-M
-    // route is faster otherwise.
+    // the narrow route too when the small-M route's grid would leave over a
+    // quarter of its block slots idle (a last round mostly empty, as for the
+    // T5 GeGLU pair: 320 blocks in two rounds of 256); measured on the Llama,
+    // T5 and vocabulary-head shapes, the small-M route is faster otherwise.
     NarrowPlan np;
     SkinnyPlan sp;
     const bool narrow = narrow_plan(p, x_dtype == kBF16, &np);
     const bool skinny = skinny_plan(p, x_dtype == kBF16, &sp);
-    if (narrow && (p.M <= 4 || !skinny || skinny_rounds(p, sp) > 1))
+    if (narrow && (p.M <= 4 || !skinny || skinny_fill(p, sp) < 0.75))
         return finish(launch_narrow(p, np, st), fn);
     if (skinny) return finish(launch_skinny(p, sp, st), fn);
     const size_t need = gemm_workspace_bytes(p);

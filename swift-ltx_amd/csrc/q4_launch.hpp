@@ -207,8 +207,9 @@ struct SkinnyPlan {
 };
 bool skinny_plan(const GemmParams& p, bool a_bf16, SkinnyPlan* out);
 hipError_t launch_skinny(const GemmParams& p, const SkinnyPlan& pl, hipStream_t st);
-// Rounds of co-resident blocks the plan's grid takes (1: every block at once).
-int skinny_rounds(const GemmParams& p, const SkinnyPlan& pl);
+// Blocks of the plan's grid over the co-resident block slots of the rounds
+// it takes (1: every round full).
+double skinny_fill(const GemmParams& p, const SkinnyPlan& pl);
 // Bytes of split-K workspace the launch of `p` would use (0: it does not split).
 size_t gemm_workspace_bytes(const GemmParams& p);
 // Launches the GEMM; splits K only if p.ws is non-null (and then needs

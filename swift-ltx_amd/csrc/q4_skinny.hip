@@ -385,10 +385,11 @@ bool skinny_plan(const GemmParams& p, bool a_bf16, SkinnyPlan* out) {
     return true;
 }
 
-int skinny_rounds(const GemmParams& p, const SkinnyPlan& pl) {
+double skinny_fill(const GemmParams& p, const SkinnyPlan& pl) {
     const long blocks = (p.N + 16 * pl.RT - 1) / (16 * pl.RT);
     const long per_round = (long)kCUs * skinny_occ(pl.W, pl.MT, pl.STEPS, p.w1 ? 2 : 1, pl.RT);
-    return (int)((blocks + per_round - 1) / per_round);
+    const long rounds = (blocks + per_round - 1) / per_round;
+    return (double)blocks / (double)(rounds * per_round);
 }
 
 hipError_t launch_skinny(const GemmParams& p, const SkinnyPlan& pl, hipStream_t st) {

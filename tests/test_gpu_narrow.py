@@ -2,8 +2,9 @@
 512 with K / 512 in {4, 6, 8, 10, 12, 16, 20}) through the C ABI.
 
 The route takes every M <= 4 it covers, and M <= 8 when the small-M
-route's grid would need more than one round of blocks (the shapes below
-with N >= 8260 and M > 4 are chosen for that).  Same semantics as the GEMM
+route's grid would leave over a quarter of its block slots idle (the shapes
+below with N >= 8260 and M > 4 are chosen for that: 259 blocks in two rounds
+of 256).  Same semantics as the GEMM
 (matmulQ4Fast / matmulQ4FastF32, Ops.swift:312-381; the SwiGLU and GeGLU
 pairs, LlamaModel.swift:275-277 and T5Encoder.swift:191-199): weights
 dequantized to fp16 as s*q+b in one fp16 FMA, fp32 accumulation.  Checked

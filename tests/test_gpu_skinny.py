@@ -3,9 +3,9 @@
 
 The narrow route (q4_narrow.hip, tests/test_gpu_narrow.py) runs M <= 4 where
 it applies (K / 512 in {4, 6, 8, 10, 12, 16, 20}, M * K * 2 <= 78 KB), and
-M <= 8 where this route's grid would take more than one round; the shapes
-here keep this route's own configurations covered: M > 4 with a one-round
-grid, or K = 1024, or X too large for the narrow route's LDS.
+M <= 8 where this route's grid would leave over a quarter of its block slots
+idle; the shapes here keep this route's own configurations covered: M > 4
+with full rounds, or K = 1024, or X too large for the narrow route's LDS.
 
 Same semantics as the GEMM (matmulQ4Fast / matmulQ4FastF32, Ops.swift:312-381;
 the SwiGLU and GeGLU pairs, LlamaModel.swift:275-277 and
