@@ -274,16 +274,17 @@ int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w
     p.ws = nullptr;
     p.splits = 1;
     p.split_tiles = 0;
-    // M <= 4: the narrow route (4x4x4 MFMA blocks, whole-line loads).  M <= 8:
-    // the narrow route too when the small-M route's grid would leave over a
-    // quarter of its block slots idle (a last round mostly empty, as for the
-    // T5 GeGLU pair: 320 blocks in two rounds of 256); measured on the Llama,
-    // T5 and vocabulary-head shapes, the small-M route is faster otherwise.
+    // One weight set at M <= 4: the narrow route (4x4x4 MFMA blocks,
+    // whole-line loads), unless the small-M route runs two row tiles per
+    // block at two blocks per CU (tall matrices such as the vocabulary head).
+    // Measured on the Llama, T5 and vocabulary-head shapes at M = 2, 4, 8,
+    // that is the faster route in every case; gated pairs and M > 4 are
+    // faster on the small-M route.
     NarrowPlan np;
     SkinnyPlan sp;
     const bool narrow = narrow_plan(p, x_dtype == kBF16, &np);
     const bool skinny = skinny_plan(p, x_dtype == kBF16, &sp);
-    if (narrow && (p.M <= 4 || !skinny || skinny_fill(p, sp) < 0.75))
+    if (narrow && (!skinny || !(sp.RT == 2 && sp.OCC == 2)))
         return finish(launch_narrow(p, np, st), fn);
     if (skinny) return finish(launch_skinny(p, sp, st), fn);
     const size_t need = gemm_workspace_bytes(p);

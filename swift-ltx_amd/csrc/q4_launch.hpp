@@ -187,13 +187,12 @@ constexpr int kMaxDevices = 64;
 int sample_noalloc_scratch_init(int dev);
 // The address resolved for `dev`, or null before sample_noalloc_scratch_init.
 void* sample_noalloc_scratch(int dev);
-// Narrow-M route (q4_narrow.hip, M <= 8): a wave owns 4 rows of each weight
-// set and 1/S of K's 512-k runs on 4x4x4 MFMA blocks; RG row groups (S waves
-// each) per block, MB A blocks of 4 activation rows.  narrow_plan returns
-// false when the shape or epilogue is not covered (the small-M route is
-// tried next).
+// Narrow-M route (q4_narrow.hip, M <= 4, one weight set): a wave owns 4
+// weight rows and 1/S of K's 512-k runs on 4x4x4 MFMA blocks; RG row groups
+// (S waves each) per block.  narrow_plan returns false when the shape or
+// epilogue is not covered.
 struct NarrowPlan {
-    int S, RG, MB;
+    int S, RG;
 };
 bool narrow_plan(const GemmParams& p, bool a_bf16, NarrowPlan* out);
 hipError_t launch_narrow(const GemmParams& p, const NarrowPlan& pl, hipStream_t st);
@@ -203,13 +202,12 @@ hipError_t launch_narrow(const GemmParams& p, const NarrowPlan& pl, hipStream_t 
 // GEMM then runs).
 struct SkinnyPlan {
     int W, MT, STEPS, RT;
+    int OCC;   // blocks per CU the configuration is compiled for
     bool XL;   // X staged in LDS (one 16-row tile, M * K * 2 bytes that fit)
 };
 bool skinny_plan(const GemmParams& p, bool a_bf16, SkinnyPlan* out);
 hipError_t launch_skinny(const GemmParams& p, const SkinnyPlan& pl, hipStream_t st);
-// Blocks of the plan's grid over the co-resident block slots of the rounds
-// it takes (1: every round full).
-double skinny_fill(const GemmParams& p, const SkinnyPlan& pl);
+
 // Bytes of split-K workspace the launch of `p` would use (0: it does not split).
 size_t gemm_workspace_bytes(const GemmParams& p);
 // Launches the GEMM; splits K only if p.ws is non-null (and then needs

@@ -1,11 +1,12 @@
-// q4_narrow.hip -- 4-bit dequant matmul for M <= 8 activation rows (short
-// prompts, batched decode, the T5 encoder at a few tokens) on CDNA4's
-// 4x4x4 MFMA blocks, as a weight stream shaped like the GEMV.
+// q4_narrow.hip -- 4-bit dequant matmul for M <= 4 activation rows and one
+// weight set (short prompts, batched decode, the T5 encoder at a few
+// tokens) on CDNA4's 4x4x4 MFMA blocks, as a weight stream shaped like the
+// GEMV.
 //
 // Same product as q4_gemm.hip, Y[M,N] = X[M,K] . dequant(W)[N,K]^T with the
 // weights dequantized to fp16 (s * q + b, one rounding) and fp32 accumulation
-// (matmulQ4Fast, Ops.swift:312-381).  At M <= 8 each weight byte feeds at
-// most 8 multiply-adds: the launch is bound by the weight stream, and what
+// (matmulQ4Fast, Ops.swift:312-381).  At M <= 4 each weight byte feeds at
+// most 4 multiply-adds: the launch is bound by the weight stream, and what
 // decides its time is how the loads reach HBM and how little work is left
 // once the last of them lands.
 //  * v_mfma_f32_4x4x4_16b_f16 is 16 independent 4x4x4 products: lane
@@ -17,25 +18,23 @@
 //    run.  One 16-byte load per lane is then 4 rows x 256 contiguous bytes,
 //    whole 128-byte lines (a load of 16 rows x 64 bytes, the 16x16 MFMA's
 //    operand shape, streams ~15% slower: every request is half a line).
-//  * A wave owns 4 rows of each weight set (gate and up for the gated
-//    epilogues) and 1/S of the runs of K, with every load in flight before
-//    the first MFMA, in use order.  S (1, 2 or 4) is chosen so the launch
-//    has about 16 waves per CU: a wave's loads come back close together,
-//    behind those of the waves that started before it, so what is left
-//    after the last load lands is one wave's dequantization, and smaller
-//    waves leave less.  The 16 per-piece partials are summed across lanes
-//    (DPP row rotations, then two cross-row shuffles), and the S waves of a
-//    row group add theirs through LDS, in a fixed order.
+//  * A wave owns 4 weight rows and 1/S of the runs of K, with every load in
+//    flight before the first MFMA, in use order.  S (1, 2 or 4) is chosen
+//    so the launch has about 16 waves per CU: a wave's loads come back close
+//    together, behind those of the waves that started before it, so what is
+//    left after the last load lands is one wave's dequantization, and
+//    smaller waves leave less.  The 16 per-piece partials are summed across
+//    lanes (DPP row rotations, then two cross-row shuffles), and the S waves
+//    of a row group add theirs through LDS, in a fixed order.
 //  * X's M rows are copied once per block to LDS (direct 16-byte copies,
 //    1 KB per wave-wide copy).  Piece c of row m is stored at position
-//    c ^ (m & 3) of its 1 KB chunk, so a fragment read -- 4 pieces of 4 rows
-//    per 16 lanes -- hits 16 distinct bank groups.  A rows past M read row
+//    c ^ m of its 1 KB chunk, so a fragment read -- 4 pieces of 4 rows per
+//    16 lanes -- hits 16 distinct bank groups.  A rows past M read row
 //    M - 1: their outputs are never stored.
-//  * Each weight word is dequantized in registers (q4_dequant.hpp) into
-//    two B fragments of 4 k; with M <= 4 one A block serves them, with
-//    M <= 8 two.  Per word that is 2 (or 4) MFMAs of 8 cycles each, the same
-//    matrix time as one 16x16x32 MFMA.  The dequantization (~57 cycles of
-//    VALU per wave-word) is the compute bound.
+//  * Each weight word is dequantized in registers (q4_dequant.hpp) into two
+//    B fragments of 4 k: 2 MFMAs of ~8 cycles per word, the same matrix time
+//    as one 16x16x32 MFMA.  The dequantization (~57 cycles of VALU per
+//    wave-word) is the compute bound.
 //  * A lane's scale and bias for a run are 2-byte loads issued with that
 //    run's weights (its 32 k lie in one group: group sizes 32, 64, 128).
 //    Copying each wave's slabs to LDS first instead measured slower: the
@@ -77,16 +76,14 @@ __device__ __forceinline__ float sum_pieces(float v) {
     return v;
 }
 
-// RUNS 512-k runs of K split over S waves, PAIR: two weight sets and a
-// gated epilogue, MB: A blocks of 4 activation rows (M <= 4 * MB).  A block
-// is W = S * RG waves: RG row groups of 4 rows.
-template <int RUNS, int S, bool PAIR, int MB>
+// RUNS 512-k runs of K split over S waves.  A block is W = S * RG waves: RG
+// row groups of 4 rows.
+template <int RUNS, int S>
 __global__ __launch_bounds__(64 * kNarrowMaxWaves) void q4_narrow_kernel(GemmParams p) {
-    constexpr int NS = PAIR ? 2 : 1;
     constexpr int R = RUNS / S;   // runs per wave
     static_assert(RUNS % S == 0, "runs split evenly");
     extern __shared__ u32x4 xl[];   // X rows [M][RUNS chunks of 64 pieces]
-    __shared__ float red[kNarrowMaxWaves][NS * MB * 4][4];   // partials of waves ks > 0
+    __shared__ float red[kNarrowMaxWaves][4][4];   // partials of waves ks > 0
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
     const int n = lane & 3, pc = lane >> 2;
     const int rg = wave / S, ks = wave - rg * S;
@@ -96,168 +93,116 @@ __global__ __launch_bounds__(64 * kNarrowMaxWaves) void q4_narrow_kernel(GemmPar
     for (int c = wave; c < M * RUNS; c += W) {   // wave-uniform
         const int m = c / RUNS, j = c - m * RUNS;
         const char* src = reinterpret_cast<const char*>(p.a) + ((size_t)m * K + j * 512) * 2 +
-                          (lane ^ (m & 3)) * 16;
+                          (lane ^ m) * 16;
         __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)(xl + c * 64), 16, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- the wave's rows and runs: scale, bias and packed words per run and
-    // set, in use order ----
+    // ---- the wave's rows and runs: scale, bias and packed words per run, in
+    // use order ----
     const int row0 = (blockIdx.x * (W / S) + rg) * 4;
     const int row = min(row0 + n, p.N - 1);   // clamped rows are computed and dropped
     const int gshift = 5 + p.gshift;          // log2(group size)
     const int j0 = ks * R;
-    u32x4 wq[R][NS];
-    uint32_t sv[R][NS], bv[R][NS];
+    u32x4 wq[R];
+    uint32_t sv[R], bv[R];
 #pragma unroll
-    for (int jj = 0; jj < R; ++jj)
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            const int j = j0 + jj;
-            const size_t gi = (size_t)row * p.groups + ((j * 512 + pc * 32) >> gshift);
-            sv[jj][s] = (s ? p.s1 : p.s0)[gi];
-            bv[jj][s] = (s ? p.b1 : p.b0)[gi];
-            const uint32_t* wr = (s ? p.w1 : p.w0) + (size_t)row * (K / 8) + j * 64 + pc * 4;
-            wq[jj][s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr));
-            // keep the issue order: left free, the scheduler groups the loads
-            // by kind, and the first run's scales then arrive with the last
-            // run's weights
-            __builtin_amdgcn_sched_barrier(0);
-        }
+    for (int jj = 0; jj < R; ++jj) {
+        const int j = j0 + jj;
+        const size_t gi = (size_t)row * p.groups + ((j * 512 + pc * 32) >> gshift);
+        sv[jj] = p.s0[gi];
+        bv[jj] = p.b0[gi];
+        const uint32_t* wr = p.w0 + (size_t)row * (K / 8) + j * 64 + pc * 4;
+        wq[jj] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr));
+        // keep the issue order: left free, the scheduler groups the loads by
+        // kind, and the first run's scales then arrive with the last run's
+        // weights
+        __builtin_amdgcn_sched_barrier(0);
+    }
 
     // X is in LDS once at most the loads issued after the copies are
     // outstanding; the barrier (assembly with a memory clobber, so no LDS
     // read moves above it) then covers the other waves' copies.
-    __builtin_amdgcn_s_waitcnt(vmcnt_only(R * NS * 3));
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(R * 3));
     asm volatile("s_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
 
-    // A rows past M read row M - 1 (their outputs are dropped).  Written as
-    // a select, the second block's row made the compiler wait for every
-    // load before the first MFMA.
-    const int xm0 = min(n, M - 1);
-    const int xm1 = min(4 + n, M - 1);
-    const u32x4* xr0 = xl + xm0 * (RUNS * 64) + 4 * pc;
-    const u32x4* xr1 = xl + xm1 * (RUNS * 64) + 4 * pc;
-    const int sw0 = xm0 & 3, sw1 = xm1 & 3;
+    // A rows past M read row M - 1 (their outputs are dropped).
+    const int xm = min(n, M - 1);
+    const u32x4* xr = xl + xm * (RUNS * 64) + 4 * pc;
 
-    // two accumulator chains per (set, A block): the halves of each word
-    f32x4 acc[NS][MB][2];
-#pragma unroll
-    for (int s = 0; s < NS; ++s)
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) acc[s][mb][0] = acc[s][mb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // two accumulator chains: the halves of each word
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int jj = 0; jj < R; ++jj) {
         const int j = j0 + jj;
-        u32x4 xa[MB][4];
+        u32x4 xa[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xa[r] = permute_x(xr[j * 64 + (r ^ xm)]);
+        const f16x2 s2 = as_f16x2(sv[jj] | (sv[jj] << 16));
+        const f16x2 b2 = as_f16x2(bv[jj] | (bv[jj] << 16));
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            xa[0][r] = permute_x(xr0[j * 64 + (r ^ sw0)]);
-            if constexpr (MB == 2) xa[1][r] = permute_x(xr1[j * 64 + (r ^ sw1)]);
+            const u32x4 b = dequant_word(wq[jj][r], s2, b2);
+            acc0 = mfma4(xa[r][0], xa[r][1], b[0], b[1], acc0);
+            acc1 = mfma4(xa[r][2], xa[r][3], b[2], b[3], acc1);
         }
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            const f16x2 s2 = as_f16x2(sv[jj][s] | (sv[jj][s] << 16));
-            const f16x2 b2 = as_f16x2(bv[jj][s] | (bv[jj][s] << 16));
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const u32x4 b = dequant_word(wq[jj][s][r], s2, b2);
-#pragma unroll
-                for (int mb = 0; mb < MB; ++mb) {
-                    acc[s][mb][0] = mfma4(xa[mb][r][0], xa[mb][r][1], b[0], b[1], acc[s][mb][0]);
-                    acc[s][mb][1] = mfma4(xa[mb][r][2], xa[mb][r][3], b[2], b[3], acc[s][mb][1]);
-                }
-            }
-            // one (run, set) at a time, in load order: work of later runs
-            // scheduled early would wait for their loads
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        // one run at a time, in load order: work of later runs scheduled
+        // early would wait for their loads
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     // ---- sum the pieces; lanes 0..3 hold the wave's partials of rows
-    // row0 .. row0 + 3 ----
-    float v[NS][MB][4];
+    // row0 .. row0 + 3, activation row e in element e ----
+    float v[4];
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[s][mb][e] = sum_pieces(acc[s][mb][0][e] + acc[s][mb][1][e]);
+    for (int e = 0; e < 4; ++e) v[e] = sum_pieces(acc0[e] + acc1[e]);
     if constexpr (S > 1) {
         if (ks > 0 && pc == 0) {
 #pragma unroll
-            for (int s = 0; s < NS; ++s)
-#pragma unroll
-                for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) red[wave][(s * MB + mb) * 4 + e][n] = v[s][mb][e];
+            for (int e = 0; e < 4; ++e) red[wave][e][n] = v[e];
         }
         __syncthreads();   // every load has landed: its wait for them costs nothing
         if (ks > 0) return;
 #pragma unroll
         for (int k = 1; k < S; ++k)
 #pragma unroll
-            for (int s = 0; s < NS; ++s)
-#pragma unroll
-                for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) v[s][mb][e] += red[wave + k][(s * MB + mb) * 4 + e][n];
+            for (int e = 0; e < 4; ++e) v[e] += red[wave + k][e][n];
     }
     const int rn = row0 + n;
     if (pc != 0 || rn >= p.N) return;
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int m = 4 * mb + e;
-            if (m >= M) continue;
-            float out;
-            if constexpr (PAIR) {
-                out = glu_f32(p.epilogue == kEpiGeluMul, v[0][mb][e], v[NS - 1][mb][e]);
-            } else {
-                out = v[0][mb][e];
-                if (p.bias) out += p.bias[rn];
-                if (p.epilogue == kEpiGeluTanh) out = gelu_tanh_f32(out);
-            }
-            const size_t oi = (size_t)m * p.N + rn;
-            if (!PAIR && p.epilogue == kEpiResidual)
-                reinterpret_cast<uint16_t*>(p.y)[oi] = residual_add_f16(p.residual[oi], out);
-            else
-                store_one(p, oi, out);
-        }
-}
-
-template <int RUNS, int S, bool PAIR, int MB>
-hipError_t launch_cfg(const GemmParams& p, const NarrowPlan& pl, hipStream_t st) {
-    const long groups4 = (p.N + 3) / 4;   // row groups
-    const dim3 grid((unsigned)((groups4 + pl.RG - 1) / pl.RG)), block(64 * S * pl.RG);
-    hipLaunchKernelGGL((q4_narrow_kernel<RUNS, S, PAIR, MB>), grid, block, narrow_lds(p), st, p);
-    return hipGetLastError();
+    for (int m = 0; m < 4; ++m) {
+        if (m >= M) break;
+        float out = v[m];
+        if (p.bias) out += p.bias[rn];
+        if (p.epilogue == kEpiGeluTanh) out = gelu_tanh_f32(out);
+        const size_t oi = (size_t)m * p.N + rn;
+        if (p.epilogue == kEpiResidual)
+            reinterpret_cast<uint16_t*>(p.y)[oi] = residual_add_f16(p.residual[oi], out);
+        else
+            store_one(p, oi, out);
+    }
 }
 
 template <int RUNS, int S>
-hipError_t launch_split(const GemmParams& p, const NarrowPlan& pl, hipStream_t st) {
+hipError_t launch_cfg(const GemmParams& p, const NarrowPlan& pl, hipStream_t st) {
     if constexpr (RUNS % S != 0) {
         return hipErrorInvalidValue;
     } else {
-        if (p.w1 != nullptr) {
-            if constexpr (RUNS <= 10)   // the pair's weights in flight fit the registers
-                return pl.MB == 1 ? launch_cfg<RUNS, S, true, 1>(p, pl, st)
-                                  : launch_cfg<RUNS, S, true, 2>(p, pl, st);
-            return hipErrorInvalidValue;
-        }
-        return pl.MB == 1 ? launch_cfg<RUNS, S, false, 1>(p, pl, st)
-                          : launch_cfg<RUNS, S, false, 2>(p, pl, st);
+        const long groups4 = (p.N + 3) / 4;   // row groups
+        const dim3 grid((unsigned)((groups4 + pl.RG - 1) / pl.RG)), block(64 * S * pl.RG);
+        hipLaunchKernelGGL((q4_narrow_kernel<RUNS, S>), grid, block, narrow_lds(p), st, p);
+        return hipGetLastError();
     }
 }
 
 template <int RUNS>
 hipError_t launch_runs(const GemmParams& p, const NarrowPlan& pl, hipStream_t st) {
     switch (pl.S) {
-        case 1: return launch_split<RUNS, 1>(p, pl, st);
-        case 2: return launch_split<RUNS, 2>(p, pl, st);
-        case 4: return launch_split<RUNS, 4>(p, pl, st);
+        case 1: return launch_cfg<RUNS, 1>(p, pl, st);
+        case 2: return launch_cfg<RUNS, 2>(p, pl, st);
+        case 4: return launch_cfg<RUNS, 4>(p, pl, st);
     }
     return hipErrorInvalidValue;
 }
@@ -265,22 +210,19 @@ hipError_t launch_runs(const GemmParams& p, const NarrowPlan& pl, hipStream_t st
 }  // namespace
 
 bool narrow_plan(const GemmParams& p, bool a_bf16, NarrowPlan* out) {
-    if (a_bf16 || p.M < 1 || p.M > 8 || p.N < 1 || p.K <= 0 || p.K % 512 != 0) return false;
-    if (p.gshift < 0 || p.gshift > 2) return false;
-    const bool pair = p.w1 != nullptr;
-    if (pair && p.epilogue != kEpiSiluMul && p.epilogue != kEpiGeluMul) return false;
-    if (!pair && p.epilogue != kEpiNone && p.epilogue != kEpiGeluTanh &&
-        p.epilogue != kEpiResidual)
+    if (a_bf16 || p.w1 != nullptr || p.M < 1 || p.M > 4 || p.N < 1 || p.K <= 0 ||
+        p.K % 512 != 0)
         return false;
-    const int runs = p.K / 512;
-    switch (runs) {   // the instantiated run counts
+    if (p.gshift < 0 || p.gshift > 2) return false;
+    if (p.epilogue != kEpiNone && p.epilogue != kEpiGeluTanh && p.epilogue != kEpiResidual)
+        return false;
+    switch (p.K / 512) {   // the instantiated run counts
         case 4: case 6: case 8: case 10: case 12: case 16: case 20: break;
         default: return false;
     }
-    if (pair && runs > 10) return false;
     if (narrow_lds(p) > (size_t)kNarrowMaxLds) return false;
+    const int runs = p.K / 512;
     NarrowPlan pl;
-    pl.MB = p.M <= 4 ? 1 : 2;
     // split K until the launch has about 16 waves per CU
     const long groups4 = (p.N + 3) / 4;
     pl.S = 1;

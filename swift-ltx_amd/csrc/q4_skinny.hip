@@ -355,7 +355,7 @@ bool skinny_plan(const GemmParams& p, bool a_bf16, SkinnyPlan* out) {
         p.epilogue != kEpiResidual)
         return false;
     const int mt = p.M <= 16 ? 1 : 2;
-    SkinnyPlan pl{0, mt, 0, 1, false};
+    SkinnyPlan pl{0, mt, 0, 1, 1, false};
     // 8 waves of 1..6 steps (1..4 with 32 activation rows), else 16 waves of
     // 1..5 steps (1..4 for a gated pair; 16 activation rows)
     if (p.K % 1024 == 0 && p.K / 1024 <= (mt == 1 ? 6 : 4)) {
@@ -368,11 +368,20 @@ bool skinny_plan(const GemmParams& p, bool a_bf16, SkinnyPlan* out) {
     } else {
         return false;
     }
-    // Two row tiles per block (the X slice serves twice the weight rows) when
-    // that still leaves one block per CU, with 8 waves.
-    if (pl.W == 8 && p.M > 4 && (p.N + 31) / 32 >= kCUs &&
-        skinny_vgprs(mt, pl.STEPS, 2, 2) <= kSkinnyMaxVgprs)
+    // Two row tiles per block (the X slice serves twice the weight rows), with
+    // 8 waves and at least one block per CU: when the two-tile block still
+    // fits two per CU, or above 8 activation rows.  Measured: the vocabulary
+    // head at M = 2 takes 43.8 us with two tiles (two blocks per CU) against
+    // 53.5 us with one; the gate/up pair at M = 8 (two tiles: one block per
+    // CU) 10.6 against 10.1 us, at M = 16 11.2 against 12.4 us.
+    const int ns = pair ? 2 : 1;
+    // (launch_steps instantiates two tiles where a gated pair of them fits
+    // the register budget; every two-tile block that fits two per CU does)
+    if (pl.W == 8 && (p.N + 31) / 32 >= kCUs &&
+        (skinny_occ(8, mt, pl.STEPS, ns, 2) == 2 ||
+         (p.M > 8 && skinny_vgprs(mt, pl.STEPS, 2, 2) <= kSkinnyMaxVgprs)))
         pl.RT = 2;
+    pl.OCC = skinny_occ(pl.W, mt, pl.STEPS, ns, pl.RT);
     // X in LDS: one 16-row tile whose rows fit beside the slabs, so that a
     // block still gets its share of the CU's LDS
     pl.XL = mt == 1 && skinny_lds(p, pl.RT, pair, true) <= (size_t)(pl.RT == 2 ? 128 : 64) * 1024;
@@ -383,13 +392,6 @@ bool skinny_plan(const GemmParams& p, bool a_bf16, SkinnyPlan* out) {
     if ((sb & 15) != 0) return false;
     *out = pl;
     return true;
-}
-
-double skinny_fill(const GemmParams& p, const SkinnyPlan& pl) {
-    const long blocks = (p.N + 16 * pl.RT - 1) / (16 * pl.RT);
-    const long per_round = (long)kCUs * skinny_occ(pl.W, pl.MT, pl.STEPS, p.w1 ? 2 : 1, pl.RT);
-    const long rounds = (blocks + per_round - 1) / per_round;
-    return (double)blocks / (double)(rounds * per_round);
 }
 
 hipError_t launch_skinny(const GemmParams& p, const SkinnyPlan& pl, hipStream_t st) {

@@ -1,11 +1,12 @@
 """GPU parity of the small-M route (q4_skinny.hip: M <= 32, K a multiple of
 1024 or of 2048) through the C ABI.
 
-The narrow route (q4_narrow.hip, tests/test_gpu_narrow.py) runs M <= 4 where
-it applies (K / 512 in {4, 6, 8, 10, 12, 16, 20}, M * K * 2 <= 78 KB), and
-M <= 8 where this route's grid would leave over a quarter of its block slots
-idle; the shapes here keep this route's own configurations covered: M > 4
-with full rounds, or K = 1024, or X too large for the narrow route's LDS.
+The narrow route (q4_narrow.hip, tests/test_gpu_narrow.py) runs one weight
+set at M <= 4 where it applies (K / 512 in {4, 6, 8, 10, 12, 16, 20},
+M * K * 2 <= 78 KB), unless this route runs two row tiles per block at two
+blocks per CU (N >= 8161, K <= 3072).  The shapes here keep this route's own
+configurations covered: gated pairs, M > 4, that two-tile case at M <= 4,
+K = 1024, or X too large for the narrow route's LDS.
 
 Same semantics as the GEMM (matmulQ4Fast / matmulQ4FastF32, Ops.swift:312-381;
 the SwiGLU and GeGLU pairs, LlamaModel.swift:275-277 and
@@ -31,6 +32,7 @@ SHAPES = [
     (5, 80, 5120, 64), (7, 33, 6144, 64), (17, 96, 1024, 32), (32, 112, 2048, 64),
     (24, 50, 3072, 128), (31, 64, 4096, 64), (6, 96, 8192, 64), (16, 40, 10240, 64),
     (9, 24, 14336, 32), (1, 300, 1024, 64), (4, 64, 10240, 64),
+    (2, 8200, 3072, 64), (4, 8300, 2048, 32), (6, 8190, 3072, 128),
 ]
 
 
@@ -50,20 +52,20 @@ def test_skinny_shapes(pkg, dev, M, N, K, g):
     assert torch.equal(y32.half(), y16)
 
 
-@pytest.mark.parametrize("K,g", [(1024, 64), (2048, 32), (4096, 128), (3072, 64), (8192, 64)])
-def test_skinny_dequant_bit_exact(pkg, dev, K, g):
-    """x rows are unit vectors e_k (16 per call, over every k): each output is
+@pytest.mark.parametrize("K,g,M,N", [(1024, 64, 16, 48), (2048, 32, 16, 48), (4096, 128, 16, 48),
+                                     (3072, 64, 16, 48), (8192, 64, 16, 48), (3072, 64, 4, 8200)])
+def test_skinny_dequant_bit_exact(pkg, dev, K, g, M, N):
+    """x rows are unit vectors e_k (M per call, over every k): each output is
     one dequantized weight, exact in fp32, so every lane, step, wave and
     nibble position of the route is checked bit for bit against fp16(s*q+b),
-    and with s = 1, b = 0 against the unpacked codes."""
+    and with s = 1, b = 0 against the unpacked codes.  M = 4, N = 8200 is the
+    two-tile block at two blocks per CU with X in LDS."""
     import torch
-    N = 48
     _, [(w, s, b)] = o.make_inputs(1, N, K, g, seed=K + g)
     want = rounded_weights_f16(w, s, b, g).T.astype(np.float32)     # [K, N]
     codes = o.unpack_q4(w).T.astype(np.float32)
     tw, ts, tb = to_dev(w, dev), to_dev(s, dev), to_dev(b, dev)
     ones, zeros = to_dev(np.ones_like(s), dev), to_dev(np.zeros_like(b), dev)
-    M = 16
     for c in range(K // M):
         ks = np.arange(M) * (K // M) + c          # spread over waves and steps
         x = np.zeros((M, K), dtype=np.float16)
