@@ -90,7 +90,8 @@ def parse():
                          "256 MiB torch copy (the calibration kernel), for rocprofv3 --pmc runs")
     ap.add_argument("--traffic-m", default="1",
                     help="with --traffic: activation rows of the gate/up launches, a comma list "
-                         "(1: the GEMV; 2 and 8 run the narrow and small-M kernels)")
+                         "(1: the GEMV; 2 and 8: the small-M kernel; at 1 < M <= 4 also the "
+                         "down projection on the narrow kernel)")
     ap.add_argument("--gemm-pmc", action="store_true",
                     help="only: 10 launches each of the M=750 prefill gate/up (SiLU) and down "
                          "GEMMs, for rocprofv3 --pmc MFMA-utilisation runs")
@@ -895,15 +896,26 @@ def small_m_legs(pkg, torch, gen, dev, cap, min_gb=2.0):
 def traffic_run(pkg, torch, gen, dev, ms=(1,)):
     """Workload for the FETCH_SIZE / WRITE_SIZE passes: the fused gate/up +
     SiLU x up launch at each M of `ms` (M = 1: the dominant GEMV) 24 times
-    over 12 distinct weight copies, then one 256 MiB copy_ whose counters
-    give the bytes-per-count calibration."""
+    over 12 distinct weight copies -- and, at 1 < M <= 4, the down
+    projection (3072 x 8192, one weight set: the narrow route) 24 times over
+    12 copies -- then one 256 MiB copy_ whose counters give the
+    bytes-per-count calibration."""
     sets = [[q4(pkg, torch, 8192, 3072, gen, dev) for _ in range(2)] for _ in range(12)]
+    downs = None
     for M in ms:
         x = torch.randn(M, 3072, generator=gen, device=dev).half()
         y = torch.empty(M, 8192, device=dev, dtype=torch.float16)
         for _ in range(2):
             for gate, up in sets:
                 pkg.matmul_q4_silu_mul(x, gate, up, M, 3072, 8192, out=y)
+        if 1 < M <= 4:
+            if downs is None:
+                downs = [q4(pkg, torch, 3072, 8192, gen, dev) for _ in range(12)]
+            a = torch.randn(M, 8192, generator=gen, device=dev).half()
+            z = torch.empty(M, 3072, device=dev, dtype=torch.float16)
+            for _ in range(2):
+                for w in downs:
+                    pkg.linear(a, w, M, 8192, 3072, fast=True, out=z)
     src = torch.empty(256 * 2 ** 20 // 4, device=dev, dtype=torch.float32).normal_()
     dst = torch.empty_like(src)
     dst.copy_(src)
