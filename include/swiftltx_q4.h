@@ -392,6 +392,19 @@ int sltx_hbm_read(const void* src, uint64_t bytes, uint32_t* sink, void* stream)
  *   sltx_probe_sync_words(blocks) zeroed words (64-byte aligned); a wait
  *   that runs out of polls adds one to *faults and the kernel finishes. */
 int sltx_probe_empty(void* stream);
+/* Route query (no counterpart in the reference; for tests and tuning): the
+ * kernel family sltx_matmul_q4_fast[_f32], sltx_matmul_q4_ex, the gated pair
+ * entry points at M > 1 and sltx_matmul_q4_residual at M > 1 run for this
+ * shape (gated: a gate/up pair), with 16-byte aligned operands.  Nothing is
+ * launched and no device is needed.  Returns an sltx_route, or a negative
+ * sltx_status for invalid arguments. */
+typedef enum {
+    SLTX_ROUTE_GEMM = 0,     /* MFMA GEMM, split over K when its tiles would not fill the GPU */
+    SLTX_ROUTE_SMALL_M = 1,  /* small-M weight stream (M <= 32, 16x16x32 MFMA) */
+    SLTX_ROUTE_NARROW = 2    /* narrow weight stream (one weight set, M <= 4, 4x4x4 MFMA) */
+} sltx_route;
+int sltx_gemm_route(int32_t M, int32_t N, int32_t K, int32_t group_size, int32_t gated,
+                    int32_t x_dtype);
 int sltx_probe_mfma(const void* ab, int32_t blocks, int32_t iters, float* sink, uint64_t* clocks,
                     void* stream);
 int sltx_probe_sync_words(int32_t blocks);

@@ -68,6 +68,7 @@ EXPORTED = (
     "sltx_probe_mfma",
     "sltx_probe_sync_words",
     "sltx_probe_sync",
+    "sltx_gemm_route",
     "sltx_argmax",
     "sltx_sample_top_p",
     "sltx_sample_top_p_noalloc",
@@ -173,6 +174,8 @@ def lib():
         L.sltx_probe_empty.restype = ctypes.c_int
         L.sltx_probe_mfma.argtypes = [P, I32, I32, P, P, P]
         L.sltx_probe_mfma.restype = ctypes.c_int
+        L.sltx_gemm_route.argtypes = [I32, I32, I32, I32, I32, I32]
+        L.sltx_gemm_route.restype = ctypes.c_int
         L.sltx_probe_sync_words.argtypes = [I32]
         L.sltx_probe_sync_words.restype = ctypes.c_int
         L.sltx_probe_sync.argtypes = [I32, I32, I32, I32, P, P, P]
@@ -603,6 +606,19 @@ def probe_mfma(ab, blocks, iters, sink, clocks, stream=None):
     _need(clocks, "clocks", blocks * 2, (torch.int64,))
     check(lib().sltx_probe_mfma(_ptr(ab), blocks, iters, _ptr(sink), _ptr(clocks),
                                 _stream(stream)))
+
+
+ROUTES = {0: "gemm", 1: "small_m", 2: "narrow"}
+
+
+def gemm_route(M, N, K, group_size=64, gated=False, x_dtype=None):
+    """The kernel family a matmul of this shape runs (sltx_gemm_route):
+    "gemm", "small_m" or "narrow".  No device needed."""
+    code = SLTX_F16 if x_dtype is None else _dtype_code(x_dtype)
+    rc = lib().sltx_gemm_route(M, N, K, group_size, 1 if gated else 0, code)
+    if rc < 0:
+        check(rc)
+    return ROUTES[rc]
 
 
 def probe_sync_words(blocks):

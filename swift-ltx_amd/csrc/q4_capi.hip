@@ -249,6 +249,21 @@ int release_workspace(hipStream_t st) {
     return kOk;
 }
 
+// The route run_gemm takes for p (SLTX_ROUTE_*), and the plans it launches
+// with.  One weight set at M <= 4: the narrow route (4x4x4 MFMA blocks,
+// whole-line loads), unless the small-M route runs two row tiles per block
+// at two blocks per CU (tall matrices such as the vocabulary head).
+// Measured on the Llama, T5 and vocabulary-head shapes at M = 2, 4, 8, that
+// is the faster route in every case; gated pairs and M > 4 are faster on the
+// small-M route.
+int gemm_route(const GemmParams& p, bool a_bf16, NarrowPlan* np, SkinnyPlan* sp) {
+    const bool narrow = narrow_plan(p, a_bf16, np);
+    const bool skinny = skinny_plan(p, a_bf16, sp);
+    if (narrow && (!skinny || !(sp->RT == 2 && sp->OCC == 2))) return SLTX_ROUTE_NARROW;
+    if (skinny) return SLTX_ROUTE_SMALL_M;
+    return SLTX_ROUTE_GEMM;
+}
+
 int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w0,
              const sltx_q4_weight* w1, const float* bias, int epilogue, void* out, int y_dtype,
              int M, int K, int N, hipStream_t st, const void* residual = nullptr) {
@@ -274,19 +289,11 @@ int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w
     p.ws = nullptr;
     p.splits = 1;
     p.split_tiles = 0;
-    // One weight set at M <= 4: the narrow route (4x4x4 MFMA blocks,
-    // whole-line loads), unless the small-M route runs two row tiles per
-    // block at two blocks per CU (tall matrices such as the vocabulary head).
-    // Measured on the Llama, T5 and vocabulary-head shapes at M = 2, 4, 8,
-    // that is the faster route in every case; gated pairs and M > 4 are
-    // faster on the small-M route.
     NarrowPlan np;
     SkinnyPlan sp;
-    const bool narrow = narrow_plan(p, x_dtype == kBF16, &np);
-    const bool skinny = skinny_plan(p, x_dtype == kBF16, &sp);
-    if (narrow && (!skinny || !(sp.RT == 2 && sp.OCC == 2)))
-        return finish(launch_narrow(p, np, st), fn);
-    if (skinny) return finish(launch_skinny(p, sp, st), fn);
+    const int route = gemm_route(p, x_dtype == kBF16, &np, &sp);
+    if (route == SLTX_ROUTE_NARROW) return finish(launch_narrow(p, np, st), fn);
+    if (route == SLTX_ROUTE_SMALL_M) return finish(launch_skinny(p, sp, st), fn);
     const size_t need = gemm_workspace_bytes(p);
     if (need > 0) p.ws = stream_workspace(st, need);
     return finish(launch_gemm(p, x_dtype == kBF16, st), fn);
@@ -921,6 +928,36 @@ int sltx_probe_mfma(const void* ab, int32_t blocks, int32_t iters, float* sink, 
 }
 
 int sltx_probe_sync_words(int32_t blocks) { return blocks < 1 ? 0 : probe_sync_words(blocks); }
+
+int sltx_gemm_route(int32_t M, int32_t N, int32_t K, int32_t group_size, int32_t gated,
+                    int32_t x_dtype) {
+    const char* fn = "sltx_gemm_route";
+    if (M < 1 || N < 1 || K <= 0 || K % 32 != 0)
+        return fail(kErrInvalid, "%s: M, N must be >= 1 and K a positive multiple of 32", fn);
+    if (group_size <= 0 || K % group_size != 0 || log2_group(group_size) < 0)
+        return fail(kErrInvalid, "%s: group_size must be 32, 64 or 128 and divide K", fn);
+    if (x_dtype != kF16 && x_dtype != kBF16) return fail(kErrInvalid, "%s: bad x_dtype", fn);
+    // operands at 256-byte aligned stand-in addresses: the plans read only
+    // the shape and the pointers' alignment
+    const void* al = reinterpret_cast<const void*>(uintptr_t{256});
+    GemmParams p{};
+    p.a = al;
+    p.w0 = static_cast<const uint32_t*>(al);
+    p.s0 = p.b0 = static_cast<const uint16_t*>(al);
+    p.w1 = gated ? p.w0 : nullptr;
+    p.s1 = p.b1 = gated ? p.s0 : nullptr;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.groups = K / group_size;
+    p.gshift = log2_group(group_size);
+    p.y_dtype = kF16;
+    p.epilogue = gated ? kEpiSiluMul : kEpiNone;
+    p.splits = 1;
+    NarrowPlan np;
+    SkinnyPlan sp;
+    return gemm_route(p, x_dtype == kBF16, &np, &sp);
+}
 
 int sltx_probe_sync(int32_t mode, int32_t fence, int32_t blocks, int32_t rounds, uint32_t* sync,
                     int32_t* faults, void* stream) {

@@ -1,0 +1,72 @@
+"""Which kernel family a matmul runs, through sltx_gemm_route (no device
+needed): the rules run_gemm applies between the MFMA GEMM, the small-M
+weight stream and the narrow weight stream, on the Llama-3.2-3B, T5-XXL and
+vocabulary-head shapes they were measured on, and the routes the GPU parity
+tests of each small-M kernel rely on.
+"""
+import pytest
+
+import test_gpu_narrow
+import test_gpu_skinny
+
+LLAMA_PAIR = dict(N=8192, K=3072, gated=True)
+T5_WI_PAIR = dict(N=10240, K=4096, gated=True)
+
+
+@pytest.mark.parametrize("M", [2, 4, 8, 16, 32])
+def test_gated_pairs_stream_on_the_small_m_route(pkg, M):
+    assert pkg.gemm_route(M, **LLAMA_PAIR) == "small_m"
+    assert pkg.gemm_route(M, **T5_WI_PAIR) == "small_m"
+
+
+@pytest.mark.parametrize("N,K", [(5120, 3072), (3072, 3072), (3072, 8192), (4096, 4096),
+                                 (4096, 10240)])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_one_weight_set_at_m_le_4_is_narrow(pkg, N, K, M):
+    if K == 10240 and M > 3:   # X = M * K * 2 bytes over the route's 78 KB of LDS
+        assert pkg.gemm_route(M, N, K) == "small_m"
+    else:
+        assert pkg.gemm_route(M, N, K) == "narrow"
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
+def test_vocabulary_head_takes_two_row_tiles(pkg, M):
+    """128256 x 3072: the small-M route's two-tile block fits two per CU, and
+    is faster than the narrow route (44 vs 47 us at M = 2)."""
+    assert pkg.gemm_route(M, 128256, 3072) == "small_m"
+
+
+@pytest.mark.parametrize("N,K", [(5120, 3072), (3072, 8192), (4096, 4096), (8192, 3072)])
+def test_m_above_4_leaves_the_narrow_route(pkg, N, K):
+    for M in (5, 8, 16, 32):
+        # 17..32 activation rows take at most 4 steps of 1024 k per wave
+        want = "gemm" if M > 16 and K > 4096 else "small_m"
+        assert pkg.gemm_route(M, N, K) == want, (M, N, K)
+
+
+def test_large_m_and_unsupported_shapes_take_the_gemm(pkg):
+    import torch
+    assert pkg.gemm_route(750, **LLAMA_PAIR) == "gemm"
+    assert pkg.gemm_route(128, 8192, 3072) == "gemm"
+    assert pkg.gemm_route(33, 8192, 3072) == "gemm"
+    assert pkg.gemm_route(2, 3072, 8192, x_dtype=torch.bfloat16) == "gemm"
+    assert pkg.gemm_route(9, 24, 14336, group_size=32) == "gemm"   # past both step counts
+
+
+def test_invalid_arguments_raise(pkg):
+    for args in ((0, 64, 1024), (2, 0, 1024), (2, 64, 100)):
+        with pytest.raises(pkg.SltxError):
+            pkg.gemm_route(*args)
+    with pytest.raises(pkg.SltxError):
+        pkg.gemm_route(2, 64, 1024, group_size=16)
+
+
+def test_narrow_parity_shapes_run_the_narrow_route(pkg):
+    for M, N, K, g in test_gpu_narrow.SHAPES:
+        assert pkg.gemm_route(M, N, K, group_size=g) == "narrow", (M, N, K, g)
+
+
+def test_small_m_parity_shapes_run_the_small_m_route(pkg):
+    for M, N, K, g in test_gpu_skinny.SHAPES:
+        want = "gemm" if K == 14336 else "small_m"
+        assert pkg.gemm_route(M, N, K, group_size=g) == want, (M, N, K, g)
