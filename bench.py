@@ -800,50 +800,64 @@ def token_select_leg(pkg, torch, gen, dev, vocab=128256):
 
 # ---------------------------------------------------------------- GEMMs ---
 
-def gemm_legs(pkg, torch, gen, dev, cap):
+def gemm_legs(pkg, torch, gen, dev, cap, min_gb=2.0):
     """BASELINE configs 3 (M = 750 prefill gate/up + SiLU and down), 4b
-    (lm_head M = 750) and 5 (LTX DiT FFN, M = 6144 bf16): graphs of R launches
-    on one resident weight (compute-bound: each weight is re-read once per
-    tile row, not once per launch)."""
+    (lm_head M = 750) and 5 (LTX DiT FFN, M = 6144 bf16): graphs of launches
+    over weight copies rotated to >= min_gb GB (the measurement rule: one
+    resident weight would be served from the 256 MB MALL, as a prefill's
+    layers never are), then, for comparison, `resident`: the same launch
+    repeated on one weight."""
     res = {}
 
-    def leg(fn, flops, reps):
-        g = capture(torch, lambda: [fn() for _ in range(reps)], cap, warm=fn)
-        st = rate(replay_stats(torch, g.replay, reps), flops=flops)
+    def leg(fn_w, make_w, flops, reps, wbytes):
+        copies = max(2, math.ceil(min_gb * 1e9 / wbytes))
+        ws = [make_w() for _ in range(copies)]
+        g = capture(torch, lambda: [fn_w(w) for w in ws], cap, warm=lambda: fn_w(ws[0]))
+        st = rate(replay_stats(torch, g.replay, copies), flops=flops)
         del g
+        g = capture(torch, lambda: [fn_w(ws[0]) for _ in range(reps)], cap,
+                    warm=lambda: fn_w(ws[0]))
+        warm = rate(replay_stats(torch, g.replay, reps), flops=flops)
+        del g, ws
+        torch.cuda.empty_cache()
+        st["weight_copies"] = copies
+        st["resident"] = {k: warm[k] for k in ("median_us", "tflops", "frac_mfma")}
         return st
+
+    def wb(N, K, sets=1):   # packed weights, scales and biases of one copy
+        return sets * (N * K // 2 + 4 * N * K // 64)
 
     M = 750
     xa = torch.randn(M, 3072, generator=gen, device=dev).half()
-    gu = [q4(pkg, torch, 8192, 3072, gen, dev) for _ in range(2)]
     h = torch.empty(M, 8192, device=dev, dtype=torch.float16)
     res["prefill_gate_up_silu_m750"] = leg(
-        lambda: pkg.matmul_q4_silu_mul(xa, gu[0], gu[1], M, 3072, 8192, out=h),
-        2 * 2 * M * 8192 * 3072, 10)
-    dw = q4(pkg, torch, 3072, 8192, gen, dev)
+        lambda w: pkg.matmul_q4_silu_mul(xa, w[0], w[1], M, 3072, 8192, out=h),
+        lambda: [q4(pkg, torch, 8192, 3072, gen, dev) for _ in range(2)],
+        2 * 2 * M * 8192 * 3072, 10, wb(8192, 3072, 2))
     y = torch.empty(M, 3072, device=dev, dtype=torch.float16)
     res["prefill_down_m750"] = leg(
-        lambda: pkg.matmul_q4_fast(h, *_wsb(dw), M, 8192, 3072, G, out=y),
-        2 * M * 3072 * 8192, 10)
-    del gu, dw
-    lm = q4(pkg, torch, 128256, 3072, gen, dev)
+        lambda w: pkg.matmul_q4_fast(h, *_wsb(w), M, 8192, 3072, G, out=y),
+        lambda: q4(pkg, torch, 3072, 8192, gen, dev),
+        2 * M * 3072 * 8192, 10, wb(3072, 8192))
     yl = torch.empty(M, 128256, device=dev, dtype=torch.float16)
     res["lm_head_gemm_m750"] = leg(
-        lambda: pkg.matmul_q4_fast(xa, *_wsb(lm), M, 3072, 128256, G, out=yl),
-        2 * M * 128256 * 3072, 5)
-    del lm, yl
+        lambda w: pkg.matmul_q4_fast(xa, *_wsb(w), M, 3072, 128256, G, out=yl),
+        lambda: q4(pkg, torch, 128256, 3072, gen, dev),
+        2 * M * 128256 * 3072, 5, wb(128256, 3072))
+    del yl
     Md = 6144
     xd = torch.randn(Md, 2048, generator=gen, device=dev).bfloat16()
-    up = q4(pkg, torch, 8192, 2048, gen, dev)
-    down = q4(pkg, torch, 2048, 8192, gen, dev)
     hd = torch.empty(Md, 8192, device=dev, dtype=torch.bfloat16)
     yd = torch.empty(Md, 2048, device=dev, dtype=torch.float32)
     res["dit_ffn_up_gelu_m6144_bf16"] = leg(
-        lambda: pkg.matmul_q4_ex(xd, up, Md, 8192, out=hd, epilogue=pkg.SLTX_EPI_GELU_TANH),
-        2 * Md * 8192 * 2048, 5)
+        lambda w: pkg.matmul_q4_ex(xd, w, Md, 8192, out=hd, epilogue=pkg.SLTX_EPI_GELU_TANH),
+        lambda: q4(pkg, torch, 8192, 2048, gen, dev),
+        2 * Md * 8192 * 2048, 5, wb(8192, 2048))
     res["dit_ffn_down_m6144_bf16"] = leg(
-        lambda: pkg.matmul_q4_ex(hd, down, Md, 2048, out=yd), 2 * Md * 2048 * 8192, 5)
-    del xd, up, down, hd, yd
+        lambda w: pkg.matmul_q4_ex(hd, w, Md, 2048, out=yd),
+        lambda: q4(pkg, torch, 2048, 8192, gen, dev),
+        2 * Md * 2048 * 8192, 5, wb(2048, 8192))
+    del xd, hd, yd
     torch.cuda.empty_cache()
     return res
 
