@@ -867,12 +867,14 @@ SMALL_M = (2, 4, 8, 32, 128)
 
 def small_m_legs(pkg, torch, gen, dev, cap, min_gb=2.0):
     """Small M (T5 encoder layers at S <= 128, T5Encoder.swift:140-205, and
-    short prompts): the Llama gate/up + SiLU shape and the T5-XXL shapes
-    (K = 4096: q/k/v/o [4096 x 4096], gelu FFN wi_0/wi_1 [10240 x 4096] in
-    one launch, wo [4096 x 10240]) at M in 2, 4, 8, 32, 128, each over weight
-    copies rotated to >= min_gb GB.  GB/s = weight + activation bytes per
-    launch / median time; bound: HBM (every weight byte read once per launch)."""
+    short prompts): the Llama gate/up + SiLU and q|k|v shapes and the T5-XXL
+    shapes (K = 4096: q/k/v/o [4096 x 4096], gelu FFN wi_0/wi_1 [10240 x 4096]
+    in one launch, wo [4096 x 10240]) at M in 2, 4, 8, 32, 128, each over
+    weight copies rotated to >= min_gb GB, with the route each launch takes.
+    GB/s = weight + activation bytes per launch / median time; bound: HBM
+    (every weight byte read once per launch)."""
     shapes = (("llama_gate_up_silu", 8192, 3072, 2, "silu"),
+              ("llama_qkv", 5120, 3072, 1, None),
               ("t5_attn_proj", 4096, 4096, 1, None),
               ("t5_ffn_wi_gelu", 10240, 4096, 2, "gelu"),
               ("t5_ffn_wo", 4096, 10240, 1, None))
@@ -898,6 +900,7 @@ def small_m_legs(pkg, torch, gen, dev, cap, min_gb=2.0):
             st = rate(replay_stats(torch, g.replay, copies),
                       nbytes=gemv_bytes(N, K, nsets, M=M), flops=2 * M * N * K * nsets)
             del g
+            st["route"] = pkg.gemm_route(M, N, K, gated=nsets == 2)
             row[f"m{M}"] = st
         res[name] = row
         del ws
@@ -1197,7 +1200,7 @@ def summarize_small_m_trace(folder):
     if cur:
         runs.append(cur)
     runs = [r for r in runs if len(r) >= MIN_REPLAYS]   # drop the one-call warm-ups
-    names = ["llama_gate_up_silu", "t5_attn_proj", "t5_ffn_wi_gelu", "t5_ffn_wo"]
+    names = ["llama_gate_up_silu", "llama_qkv", "t5_attn_proj", "t5_ffn_wi_gelu", "t5_ffn_wo"]
     want = len(names) * len(SMALL_M)
     if len(runs) != want:
         return f"expected {want} runs of q4 dispatches, found {len(runs)}"

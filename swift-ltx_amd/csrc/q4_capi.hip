@@ -255,11 +255,21 @@ int release_workspace(hipStream_t st) {
 // at two blocks per CU (tall matrices such as the vocabulary head).
 // Measured on the Llama, T5 and vocabulary-head shapes at M = 2, 4, 8, that
 // is the faster route in every case; gated pairs and M > 4 are faster on the
-// small-M route.
+// small-M route, up to M = 16.
 int gemm_route(const GemmParams& p, bool a_bf16, NarrowPlan* np, SkinnyPlan* sp) {
     const bool narrow = narrow_plan(p, a_bf16, np);
     const bool skinny = skinny_plan(p, a_bf16, sp);
     if (narrow && (!skinny || !(sp->RT == 2 && sp->OCC == 2))) return SLTX_ROUTE_NARROW;
+    // 16 < M <= 32: the mid-M route for gated pairs, and for one weight set
+    // whose small-M grid would leave CUs idle (its blocks of 32 rows fewer
+    // than the CUs) at N >= 5120.  Measured at M = 20, 24, 32 (us per launch,
+    // weights rotated over >= 2 GB), mid-M against small-M: Llama gate/up
+    // pair 11.5-11.6 against 13.4-15.3, q|k|v (5120 x 3072) 9.5-9.7 against
+    // 11.8-14.9; o (3072 x 3072) 9.3-9.5 against 7.4-8.8 and a single
+    // 8192 x 3072 set 9.8-9.9 against 8.8-10.4 stay on the small-M route.
+    if (p.M > 16 && mid_plan(p, a_bf16) &&
+        (p.w1 != nullptr || !skinny || (p.N >= 5120 && (p.N + 31) / 32 < kCUs)))
+        return SLTX_ROUTE_MID;
     if (skinny) return SLTX_ROUTE_SMALL_M;
     return SLTX_ROUTE_GEMM;
 }
@@ -294,6 +304,7 @@ int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w
     const int route = gemm_route(p, x_dtype == kBF16, &np, &sp);
     if (route == SLTX_ROUTE_NARROW) return finish(launch_narrow(p, np, st), fn);
     if (route == SLTX_ROUTE_SMALL_M) return finish(launch_skinny(p, sp, st), fn);
+    if (route == SLTX_ROUTE_MID) return finish(launch_mid(p, st), fn);
     const size_t need = gemm_workspace_bytes(p);
     if (need > 0) p.ws = stream_workspace(st, need);
     return finish(launch_gemm(p, x_dtype == kBF16, st), fn);

@@ -46,6 +46,7 @@
 #include <type_traits>
 
 #include "q4_common.hpp"
+#include "q4_dequant.hpp"
 #include "q4_launch.hpp"
 
 namespace sltx {
@@ -56,37 +57,6 @@ constexpr int kThreads = 64 * NW;
 constexpr int NT = BN / 32 / NW;       // 32-row weight tiles (MFMA N-tiles) per wave
 constexpr int NSA = 4;     // A stages in LDS
 constexpr int GPMAX = 4;   // scale/bias groups per row per 128 k (group size 32)
-
-// LDS layout of a 64-wide k-tile: 128-byte rows of eight 16-byte columns.
-// Logical column c of row r sits at physical column c ^ (r & 7) ^ ((r >> 3) & 1).
-// A ds_read_b128 is served 16 lanes at a time by 64 4-byte banks (256 B): 16
-// consecutive rows reading one logical column hit 16 distinct (row parity,
-// column) slots, i.e. no bank conflicts.
-__device__ __forceinline__ int swz(int row, int col16) {
-    return row * 8 + (col16 ^ (row & 7) ^ ((row >> 3) & 1));
-}
-
-// One 32-bit word (8 nibbles, k order) -> 8 fp16 values s*q+b.  Nibbles are
-// spread to bytes and interleaved back into k order with v_perm_b32; then
-// v_cvt_scalef32_pk_f16_fp8 turns two bytes into two exact fp16 integers (an
-// fp8 e4m3 byte b < 16 is b * 2^-9, and the instruction's scale, of which only
-// the exponent counts, is 2^9) and one fp16 FMA q*s+b rounds once.
-__device__ __forceinline__ u32x4 dequant_word_f16(uint32_t w, f16x2 s2, f16x2 b2) {
-    const uint32_t lo = w & 0x0F0F0F0Fu;          // bytes q6 q4 q2 q0
-    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;   // bytes q7 q5 q3 q1
-    const uint32_t q03 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);   // bytes q3 q2 q1 q0
-    const uint32_t q47 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);   // bytes q7 q6 q5 q4
-    const float k512 = 512.0f;
-    f16x2 q[4];
-    q[0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(q03, k512, false);   // q0, q1
-    q[1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(q03, k512, true);    // q2, q3
-    q[2] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(q47, k512, false);   // q4, q5
-    q[3] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(q47, k512, true);    // q6, q7
-    u32x4 o;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] = as_u32(__builtin_elementwise_fma(q[e], s2, b2));   // v_pk_fma_f16
-    return o;
-}
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));

@@ -207,6 +207,12 @@ struct SkinnyPlan {
 };
 bool skinny_plan(const GemmParams& p, bool a_bf16, SkinnyPlan* out);
 hipError_t launch_skinny(const GemmParams& p, const SkinnyPlan& pl, hipStream_t st);
+// Mid-M route (q4_mid.hip, M <= 32, K % 256 == 0, fp16 X): 64 weight rows
+// per block over all K, 2 row tiles x 4 K-groups of waves, X and packed W
+// copied to LDS in whole lines through 4- and 8-stage rings.  mid_plan
+// returns false when the shape, epilogue or alignment is not covered.
+bool mid_plan(const GemmParams& p, bool a_bf16);
+hipError_t launch_mid(const GemmParams& p, hipStream_t st);
 
 // Bytes of split-K workspace the launch of `p` would use (0: it does not split).
 size_t gemm_workspace_bytes(const GemmParams& p);

@@ -1,0 +1,313 @@
+// q4_mid.hip -- 4-bit dequant matmul for 16 < M <= 32 activation rows
+// (T5 encoder layers at short sequence lengths, short prompts, batched
+// decode) on CDNA4 MFMA, as a weight stream.
+//
+// Same product as q4_gemm.hip, Y[M,N] = X[M,K] . dequant(W)[N,K]^T with fp32
+// accumulation (matmulQ4Fast, Ops.swift:312-381).  At these M a weight byte
+// feeds at most 32 multiply-adds, so the kernel should run at the weight
+// stream's rate; what it must not do is load X badly.  X is M x K fp16 (up to
+// 256 KB at K = 4096) and every block needs all of it: the small-M route's
+// per-wave X fragments (16 rows x 64 B per load, a K slice per wave) cost a
+// CU more load issue than its weights.  Here:
+//  * A block owns 64 weight rows -- 32 gate + 32 up rows of the same output
+//    columns for the gated epilogues, else 64 consecutive rows -- and all K,
+//    in NR rounds of 256 k.  It has 16 waves.  The 8 compute waves are
+//    2 row tiles x 4 K-groups: wave 2g + j computes row tile j over k-tile g
+//    of every round, as one 32x32x16 MFMA tile (all 32 activation rows; rows
+//    past M are copies of row M - 1, never stored).  Four copy waves copy the
+//    weights, four copy X and the scales and biases, all by direct
+//    global -> LDS copies in whole 128-byte lines.
+//  * Weights: the block's packed rows are copied at the start, in groups of
+//    four rounds (512 contiguous bytes of two rows per wave-wide copy, the
+//    GEMV's pattern: the DRAM pages of a row are read in long runs), so the
+//    whole weight stream is in flight at once, and a round's compute waits
+//    only for its group.  The 16-byte piece c of a row r lands at
+//    c ^ (r & 15) of the row's 512 bytes, so that the fragment reads of 16
+//    rows hit distinct banks.
+//  * X: each round's 32 rows x 256 k, a few rounds ahead in a ring of
+//    stages (the 16-byte column c of row r at c ^ (r & 7) ^ ((r >> 3) & 1)),
+//    and first the block's scales and biases (one slab per array).  One
+//    barrier per round hands a stage over.  Each copy role waits only for
+//    its own copies: s_waitcnt counts a wave's memory operations in issue
+//    order, so a wave that issued both streams would wait for weights issued
+//    before the X copy it needs.
+//  * Inside a k-tile the k order is permuted as in q4_gemm.hip: k-step s of
+//    lane half h is packed word 4h + s of the row, so a lane's B fragments
+//    over the k-tile are one 16-byte piece, dequantized in registers
+//    (v_perm_b32 byte pairing, v_cvt_scalef32_pk_f16_fp8, one v_pk_fma_f16
+//    per pair: s * q + b rounded once), and its A fragment is 16-byte column
+//    4h + s of the X row.
+//  * After the last round the four K-groups' accumulator tiles are summed in
+//    LDS in a fixed order and the epilogue (gated SiLU / GELU-tanh pair,
+//    bias, GELU-tanh, residual add) runs on the fp32 sums.
+#include "q4_common.hpp"
+#include "q4_dequant.hpp"
+#include "q4_launch.hpp"
+
+namespace sltx {
+
+namespace {
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+constexpr int NCW = 8;                     // compute waves
+constexpr int NLW = 4;                     // copy waves per stream (weights, X)
+constexpr int MTHREADS = 64 * (NCW + 2 * NLW);
+constexpr int CTHREADS = 64 * NCW;
+constexpr int LTHREADS = 64 * NLW;
+constexpr int KG = 4;                      // K-groups: k-tile g of each round
+constexpr int BM = 32;                     // activation rows (one MFMA tile)
+constexpr int RK = 64 * KG;                // k per round
+constexpr int XSLOTS = KG * BM * 8;        // 16-byte slots of an X stage
+constexpr int NXC = XSLOTS / LTHREADS;     // X copies per X-copy thread per round
+static_assert(NXC * LTHREADS == XSLOTS, "whole copies");
+constexpr int BROWS = 64;                  // weight rows per block
+constexpr int GSLOTS = BROWS * 32;         // 16-byte slots of a weight group (4 rounds)
+constexpr int NWG = GSLOTS / LTHREADS;     // weight copies per W-copy thread per group
+static_assert(NWG * LTHREADS == GSLOTS, "whole copies");
+constexpr size_t kMaxLds = 160 * 1024;
+// X ring stages: as many as fit beside the weights (12 rounds: 96 KB of them)
+__host__ __device__ constexpr int mid_nsx(int nr) { return nr <= 8 ? 5 : 3; }
+__host__ __device__ constexpr size_t mid_static_lds(int nr) {
+    return (size_t)(nr / 4) * GSLOTS * 16 + (size_t)mid_nsx(nr) * XSLOTS * 16 + LTHREADS * 4;
+}
+static_assert(mid_nsx(12) * XSLOTS * 4 >= NCW * 1024, "the K-group sums fit the ring");
+
+__device__ __forceinline__ f32x16 mfma32_f16(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// 16-byte pieces of one scale / bias slab (rows x groups fp16), and the
+// pieces reserved per slab in LDS (whole waves of 64).
+__host__ __device__ constexpr int mid_slab_pieces(int rows, int groups) { return rows * groups / 8; }
+__host__ __device__ constexpr int mid_slab_alloc(int rows, int groups) {
+    return (mid_slab_pieces(rows, groups) + 63) / 64 * 64;
+}
+
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <bool PAIR, int NR>
+__global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
+    constexpr int NSLAB = PAIR ? 4 : 2;         // s0, b0[, s1, b1]
+    constexpr int SROWS = PAIR ? 32 : 64;       // rows per slab
+    constexpr int NG = NR / 4;                  // weight groups
+    constexpr int NSX = mid_nsx(NR);
+    // At the start of round q an X-copy wave has issued X(q + 1 .. q + NSX - 2)
+    // after X(q).
+    constexpr int WAIT_X = (NSX - 2) * NXC;
+    static_assert(NR % 4 == 0 && NSX >= 3, "rounds");
+    __shared__ u32x4 wl[NG * GSLOTS];           // weights [group][row][32 pieces]
+    __shared__ u32x4 xs[NSX * XSLOTS];          // X ring; after the loop, the K-group sums
+    __shared__ uint32_t spare[LTHREADS];        // destination of the copies past the end
+    extern __shared__ u32x4 sb_lds[];           // [NSLAB][alloc] slabs
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n0 = blockIdx.x * (PAIR ? 32 : 64);
+    const int K = p.K, groups = p.groups;
+    const int alloc = mid_slab_alloc(SROWS, groups);
+    f32x16 acc;
+
+    if (wave >= NCW + NLW) {
+        // ---- X-copy waves: the slabs, then X round by round ----
+        const int lt = tid - CTHREADS - LTHREADS, lw = 64 * (wave - NCW - NLW);
+        const int pieces = mid_slab_pieces(SROWS, groups);
+        const int valid = min(SROWS, p.N - n0) * groups * 2;   // slab bytes inside the arrays
+        for (int a = 0; a < NSLAB; ++a) {
+            const uint16_t* arr = a == 0 ? p.s0 : a == 1 ? p.b0 : a == 2 ? p.s1 : p.b1;
+            const char* src = reinterpret_cast<const char*>(arr + (size_t)n0 * groups);
+            for (int c0 = lw; c0 < pieces; c0 += LTHREADS) {
+                int off = (c0 + lane) * 16;
+                if (off >= valid) off = 0;   // a spare copy of piece 0
+                __builtin_amdgcn_global_load_lds((const void*)(src + off),
+                                                 (lds_ptr_t)(sb_lds + a * alloc + c0), 16, 0, 0);
+            }
+        }
+        // X slot s of a stage: k-tile s / 256, row (s / 8) % 32, physical
+        // column s % 8, i.e. logical column (s % 8) ^ (row & 7) ^ ((row >> 3) & 1)
+        const uint16_t* A = reinterpret_cast<const uint16_t*>(p.a);
+        const uint16_t* x_src[NXC];
+#pragma unroll
+        for (int i = 0; i < NXC; ++i) {
+            const int s = lt + LTHREADS * i;
+            const int kt = s / (BM * 8), row = (s >> 3) & (BM - 1);
+            const int c16 = (s & 7) ^ (row & 7) ^ ((row >> 3) & 1);
+            x_src[i] = A + (size_t)min(row, p.M - 1) * K + kt * 64 + c16 * 8;
+        }
+        const char* spare_src = reinterpret_cast<const char*>(p.a) + lane * 4;
+        auto issue_x = [&](int q) {   // NXC vector-memory ops
+            if (q < NR) {
+                u32x4* st = xs + (q % NSX) * XSLOTS + lw;
+#pragma unroll
+                for (int i = 0; i < NXC; ++i)
+                    __builtin_amdgcn_global_load_lds((const void*)(x_src[i] + (size_t)q * RK),
+                                                     (lds_ptr_t)(st + LTHREADS * i), 16, 0, 0);
+            } else {
+#pragma unroll
+                for (int i = 0; i < NXC; ++i)
+                    __builtin_amdgcn_global_load_lds((const void*)spare_src, (lds_ptr_t)(spare + lw), 4, 0, 0);
+            }
+        };
+        for (int q = 0; q < NSX - 1; ++q) issue_x(q);
+        for (int q = 0; q < NR; ++q) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_only(WAIT_X));
+            lds_barrier();
+            issue_x(q + NSX - 1);   // into the stage round q - 1 read
+        }
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    } else if (wave >= NCW) {
+        // ---- W-copy waves: every group at once, then one wait per group ----
+        // Copy i of group G covers rows 2c, 2c + 1 (c = wave index + 4 i),
+        // lane l: row 2c + l / 32, the row's piece (l % 32) ^ (row & 15) of
+        // the group's 512 bytes, landing in slot l of the copy.
+        const int lw = wave - NCW;
+        const uint32_t* w_src[NWG];
+#pragma unroll
+        for (int i = 0; i < NWG; ++i) {
+            const int row = 2 * (lw + NLW * i) + (lane >> 5);
+            const uint32_t* W = (PAIR && row >= 32) ? p.w1 : p.w0;
+            int n = PAIR ? n0 + (row & 31) : n0 + row;
+            if (n >= p.N) n = 0;   // rows past N read row 0 (never stored)
+            w_src[i] = W + (size_t)n * (K / 8) + (((lane & 31) ^ (row & 15)) * 4);
+        }
+#pragma unroll
+        for (int G = 0; G < NG; ++G)
+#pragma unroll
+            for (int i = 0; i < NWG; ++i)
+                __builtin_amdgcn_global_load_lds((const void*)(w_src[i] + G * 128),
+                                                 (lds_ptr_t)(wl + G * GSLOTS + 64 * (lw + NLW * i)),
+                                                 16, 0, 0);
+        static_assert(NG <= 3, "group waits");
+        for (int q = 0; q < NR; ++q) {
+            if (q % 4 == 0) {   // group q / 4 landed: NG - 1 - q / 4 groups issued after it
+                const int later = NG - 1 - q / 4;
+                if (later == 0) __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+                else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_only(NWG));
+                else __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * NWG));
+            }
+            lds_barrier();
+        }
+    } else {
+        // ---- compute waves ----
+        const int j = wave & 1, g = wave >> 1;   // row tile, K-group
+        const int r = lane & 31, h = lane >> 5;  // MFMA row / column, k half
+        const int wrow = 32 * j + r;             // block row
+
+        // this lane's scale / bias: slab (2e, 2e + 1), row srow, group of k
+        // q * 256 + 64 g + 32 h
+        const uint16_t* sbl = reinterpret_cast<const uint16_t*>(sb_lds);
+        const int e = PAIR ? j : 0, srow = PAIR ? r : 32 * j + r;
+        const uint16_t* s_row = sbl + (size_t)(2 * e) * alloc * 8 + srow * groups;
+        const uint16_t* b_row = s_row + (size_t)alloc * 8;
+        const int glog2 = 5 + p.gshift;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+#pragma unroll
+        for (int q = 0; q < NR; ++q) {
+            lds_barrier();
+            const u32x4* xst = xs + (q % NSX) * XSLOTS + g * (BM * 8);
+            const u32x4 wpc = wl[(q / 4) * GSLOTS + wrow * 32 + ((8 * (q % 4) + 2 * g + h) ^ (wrow & 15))];
+            const int gi = (q * RK + 64 * g + 32 * h) >> glog2;
+            const uint32_t sv = s_row[gi], bv = b_row[gi];
+            const f16x2 s2 = as_f16x2(sv | (sv << 16));
+            const f16x2 b2 = as_f16x2(bv | (bv << 16));
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const u32x4 a = xst[swz(r, 4 * h + s)];
+                acc = mfma32_f16(a, dequant_word_f16(wpc[s], s2, b2), acc);
+            }
+        }
+    }
+
+    // ---- sum the K-groups' tiles (LDS, fixed order), epilogue ----
+    __syncthreads();   // every copy landed, every ring read done
+    float* red = reinterpret_cast<float*>(xs);   // wave w's tile at [w][v][lane]
+    if (wave < NCW) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) red[wave * 1024 + v * 64 + lane] = acc[v];
+    }
+    __syncthreads();
+
+    // D[m][c] of a 32x32 tile is element 4 (m / 8) + m % 4 of lane
+    // c + 32 ((m / 4) % 2)
+    constexpr int NCOLS = PAIR ? 32 : 64;
+    for (int o = tid; o < BM * NCOLS; o += MTHREADS) {
+        const int m = o / NCOLS, c = o % NCOLS;
+        const int n = n0 + c;
+        if (m >= p.M || n >= p.N) continue;
+        const int jj = PAIR ? 0 : c >> 5;
+        const int idx = (4 * (m >> 3) + (m & 3)) * 64 + (c & 31) + 32 * ((m >> 2) & 1);
+        float v0 = 0.0f, v1 = 0.0f;
+#pragma unroll
+        for (int gg = 0; gg < KG; ++gg) {
+            v0 += red[(2 * gg + jj) * 1024 + idx];
+            if constexpr (PAIR) v1 += red[(2 * gg + 1) * 1024 + idx];
+        }
+        float out;
+        if constexpr (PAIR) {
+            out = glu_f32(p.epilogue == kEpiGeluMul, v0, v1);
+        } else {
+            out = v0;
+            if (p.bias) out += p.bias[n];
+            if (p.epilogue == kEpiGeluTanh) out = gelu_tanh_f32(out);
+        }
+        const size_t oi = (size_t)m * p.N + n;
+        if (!PAIR && p.epilogue == kEpiResidual)
+            reinterpret_cast<uint16_t*>(p.y)[oi] = residual_add_f16(p.residual[oi], out);
+        else
+            store_one(p, oi, out);
+    }
+}
+
+size_t mid_lds(const GemmParams& p, bool pair) {
+    const int rows = pair ? 32 : 64;
+    return (size_t)(pair ? 4 : 2) * mid_slab_alloc(rows, p.groups) * 16;
+}
+
+template <bool PAIR>
+hipError_t launch_nr(const GemmParams& p, const dim3& grid, size_t lds, hipStream_t st) {
+    switch (p.K / RK) {
+        case 8: hipLaunchKernelGGL((q4_mid_kernel<PAIR, 8>), grid, dim3(MTHREADS), lds, st, p); break;
+        case 12: hipLaunchKernelGGL((q4_mid_kernel<PAIR, 12>), grid, dim3(MTHREADS), lds, st, p); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool mid_plan(const GemmParams& p, bool a_bf16) {
+    if (a_bf16 || p.M < 1 || p.M > BM || p.N < 1) return false;
+    // rounds of 256 k the kernel is built for (K = 2048, 3072: the block's
+    // packed weights fit LDS beside the X ring)
+    if (p.K != 8 * RK && p.K != 12 * RK) return false;
+    // whole 16-byte slab pieces per row group of 8 (the last block's slab
+    // stops at a piece boundary: no copy reads past the arrays)
+    if (p.gshift < 0 || p.gshift > 2 || p.groups % 8 != 0) return false;
+    const bool pair = p.w1 != nullptr;
+    if (pair && p.epilogue != kEpiSiluMul && p.epilogue != kEpiGeluMul) return false;
+    if (!pair && p.epilogue != kEpiNone && p.epilogue != kEpiGeluTanh &&
+        p.epilogue != kEpiResidual)
+        return false;
+    if (mid_static_lds(p.K / RK) + mid_lds(p, pair) > kMaxLds) return false;
+    // 16-byte loads and copies: X rows, W rows and the scale / bias slabs
+    uintptr_t al = reinterpret_cast<uintptr_t>(p.a) | reinterpret_cast<uintptr_t>(p.w0) |
+                   reinterpret_cast<uintptr_t>(p.s0) | reinterpret_cast<uintptr_t>(p.b0);
+    if (pair)
+        al |= reinterpret_cast<uintptr_t>(p.w1) | reinterpret_cast<uintptr_t>(p.s1) |
+              reinterpret_cast<uintptr_t>(p.b1);
+    return (al & 15) == 0;
+}
+
+hipError_t launch_mid(const GemmParams& p, hipStream_t st) {
+    const bool pair = p.w1 != nullptr;
+    const int rows = pair ? 32 : 64;
+    const dim3 grid((unsigned)((p.N + rows - 1) / rows));
+    const size_t lds = mid_lds(p, pair);
+    return pair ? launch_nr<true>(p, grid, lds, st) : launch_nr<false>(p, grid, lds, st);
+}
+
+}  // namespace sltx

@@ -78,12 +78,13 @@ def test_skinny_dequant_bit_exact(pkg, dev, K, g, M, N):
         assert np.array_equal(yq.cpu().numpy(), codes[ks]), c
 
 
-@pytest.mark.parametrize("M,N,K", [(5, 8192, 3072), (8, 200, 3072), (32, 8192, 3072),
+@pytest.mark.parametrize("M,N,K", [(5, 8192, 3072), (8, 200, 3072), (32, 4096, 4096),
                                    (20, 64, 4096)])
 @pytest.mark.parametrize("gelu", [False, True])
 def test_skinny_gated_pair(pkg, dev, M, N, K, gelu):
     import torch
     g = 64
+    assert pkg.gemm_route(M, N, K, gated=True) == "small_m"
     x, [(wg, sg, bg), (wu, su, bu)] = o.make_inputs(M, N, K, g, seed=M + N + K + gelu,
                                                     n_weights=2)
     gate = o.matmul_q4_f64(x, wg, sg, bg, g)

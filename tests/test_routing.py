@@ -1,11 +1,12 @@
 """Which kernel family a matmul runs, through sltx_gemm_route (no device
-needed): the rules run_gemm applies between the MFMA GEMM, the small-M
-weight stream and the narrow weight stream, on the Llama-3.2-3B, T5-XXL and
-vocabulary-head shapes they were measured on, and the routes the GPU parity
-tests of each small-M kernel rely on.
+needed): the rules run_gemm applies between the MFMA GEMM, the mid-M, small-M
+and narrow weight streams, on the Llama-3.2-3B, T5-XXL and vocabulary-head
+shapes they were measured on, and the routes the GPU parity tests of each
+small-M kernel rely on.
 """
 import pytest
 
+import test_gpu_mid
 import test_gpu_narrow
 import test_gpu_skinny
 
@@ -13,10 +14,26 @@ LLAMA_PAIR = dict(N=8192, K=3072, gated=True)
 T5_WI_PAIR = dict(N=10240, K=4096, gated=True)
 
 
-@pytest.mark.parametrize("M", [2, 4, 8, 16, 32])
+@pytest.mark.parametrize("M", [2, 4, 8, 16])
 def test_gated_pairs_stream_on_the_small_m_route(pkg, M):
     assert pkg.gemm_route(M, **LLAMA_PAIR) == "small_m"
     assert pkg.gemm_route(M, **T5_WI_PAIR) == "small_m"
+
+
+@pytest.mark.parametrize("M", [17, 20, 24, 32])
+def test_mid_m_route_above_16_rows(pkg, M):
+    """17..32 rows: gated pairs and tall-enough single sets whose small-M grid
+    leaves CUs idle take the mid-M route (Llama gate/up pair 11.6 against
+    15.3 us at M = 32, q|k|v 9.7 against 14.9); K = 4096 is not built there,
+    and o (3072 rows) and a single 8192-row set are faster on the small-M
+    route."""
+    assert pkg.gemm_route(M, **LLAMA_PAIR) == "mid"
+    assert pkg.gemm_route(M, 5120, 3072) == "mid"
+    assert pkg.gemm_route(M, **T5_WI_PAIR) == "small_m"
+    assert pkg.gemm_route(M, 3072, 3072) == "small_m"
+    assert pkg.gemm_route(M, 8192, 3072) == "small_m"
+    assert pkg.gemm_route(M, 4096, 4096) == "small_m"
+    assert pkg.gemm_route(M, 8192, 3072, group_size=32, gated=True) == "small_m"   # LDS
 
 
 @pytest.mark.parametrize("N,K", [(5120, 3072), (3072, 3072), (3072, 8192), (4096, 4096),
@@ -41,6 +58,8 @@ def test_m_above_4_leaves_the_narrow_route(pkg, N, K):
     for M in (5, 8, 16, 32):
         # 17..32 activation rows take at most 4 steps of 1024 k per wave
         want = "gemm" if M > 16 and K > 4096 else "small_m"
+        if M > 16 and (N, K) == (5120, 3072):
+            want = "mid"
         assert pkg.gemm_route(M, N, K) == want, (M, N, K)
 
 
@@ -70,3 +89,8 @@ def test_small_m_parity_shapes_run_the_small_m_route(pkg):
     for M, N, K, g in test_gpu_skinny.SHAPES:
         want = "gemm" if K == 14336 else "small_m"
         assert pkg.gemm_route(M, N, K, group_size=g) == want, (M, N, K, g)
+
+
+def test_mid_parity_shapes_run_the_mid_route(pkg):
+    for M, N, K, g in test_gpu_mid.SHAPES:
+        assert pkg.gemm_route(M, N, K, group_size=g) == "mid", (M, N, K, g)
