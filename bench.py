@@ -405,13 +405,17 @@ def main():
 
 def hbm_ceilings(pkg, torch, dev, cap, read_gib=4, copy_gib=1):
     """Measured HBM ceilings: a read-only stream of read_gib GiB
-    (sltx_hbm_read: 16-byte nontemporal loads over the whole GPU, XOR-reduced)
+    (sltx_hbm_read: 16-byte nontemporal loads over the whole GPU, XOR-reduced),
+    the same stream through direct global -> LDS copies (sltx_hbm_read_lds)
     and a device copy of copy_gib GiB (torch copy_, bytes read + written)."""
     src = torch.empty(read_gib * 2 ** 30 // 4, device=dev, dtype=torch.int32)
     src.random_()
     sink = torch.empty(pkg.lib().sltx_hbm_read_blocks(), device=dev, dtype=torch.int32)
     g = capture(torch, lambda: pkg.hbm_read(src, sink), cap)
     rd = rate(replay_stats(torch, g.replay, 1), nbytes=src.numel() * 4)
+    del g
+    g = capture(torch, lambda: pkg.hbm_read(src, sink, lds=True), cap)
+    rl = rate(replay_stats(torch, g.replay, 1), nbytes=src.numel() * 4)
     del g, src
     n = copy_gib * 2 ** 30 // 2
     a = torch.empty(n, device=dev, dtype=torch.float16).normal_()
@@ -422,6 +426,9 @@ def hbm_ceilings(pkg, torch, dev, cap, read_gib=4, copy_gib=1):
     torch.cuda.empty_cache()
     return {"read_gbs": rd["gbs"], "read_frac_of_peak": rd["frac_hbm"],
             "read_what": f"sltx_hbm_read of {read_gib} GiB, median of {rd['replays']} replays",
+            "read_lds_gbs": rl["gbs"],
+            "read_lds_what": f"sltx_hbm_read_lds (direct global -> LDS copies) of {read_gib} GiB, "
+                             f"median of {rl['replays']} replays",
             "copy_gbs": cp["gbs"],
             "copy_what": f"{copy_gib} GiB device copy (read + written), median of "
                          f"{cp['replays']} replays"}

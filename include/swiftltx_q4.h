@@ -373,6 +373,10 @@ int sltx_sample_top_p_state(const void* logits, int32_t dtype, int32_t n, float 
  * checked.  No counterpart in the reference. */
 int sltx_hbm_read_blocks(void);
 int sltx_hbm_read(const void* src, uint64_t bytes, uint32_t* sink, void* stream);
+/* The same read through direct global -> LDS copies (16 bytes a lane, each
+ * read back from LDS and XOR-ed): the rate at which a kernel can stream from
+ * HBM into LDS.  Same arguments and sink.  No counterpart in the reference. */
+int sltx_hbm_read_lds(const void* src, uint64_t bytes, uint32_t* sink, void* stream);
 
 /* Probes of what bounds the kernels (no counterpart in the reference):
  * - sltx_probe_empty: one launch of an empty one-wave kernel (the launch

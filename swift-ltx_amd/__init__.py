@@ -64,6 +64,7 @@ EXPORTED = (
     "sltx_decode_layer_faults",
     "sltx_hbm_read_blocks",
     "sltx_hbm_read",
+    "sltx_hbm_read_lds",
     "sltx_probe_empty",
     "sltx_probe_mfma",
     "sltx_probe_sync_words",
@@ -170,6 +171,8 @@ def lib():
         L.sltx_hbm_read_blocks.restype = ctypes.c_int
         L.sltx_hbm_read.argtypes = [P, ctypes.c_uint64, P, P]
         L.sltx_hbm_read.restype = ctypes.c_int
+        L.sltx_hbm_read_lds.argtypes = [P, ctypes.c_uint64, P, P]
+        L.sltx_hbm_read_lds.restype = ctypes.c_int
         L.sltx_probe_empty.argtypes = [P]
         L.sltx_probe_empty.restype = ctypes.c_int
         L.sltx_probe_mfma.argtypes = [P, I32, I32, P, P, P]
@@ -578,17 +581,18 @@ def decode_layer_faults(stream=None) -> int:
     return int(n.value)
 
 
-def hbm_read(src, sink=None, stream=None):
+def hbm_read(src, sink=None, stream=None, lds=False):
     """Streams the bytes of device tensor `src` (contiguous, size a multiple of
-    16) through the GPU's loads; returns the per-block XOR words (int32
-    device tensor of sltx_hbm_read_blocks() entries)."""
+    16) through the GPU's loads (lds: through direct global -> LDS copies,
+    sltx_hbm_read_lds); returns the per-block XOR words (int32 device tensor
+    of sltx_hbm_read_blocks() entries)."""
     torch = _torch()
     if sink is None:
         sink = torch.empty(lib().sltx_hbm_read_blocks(), dtype=torch.int32, device=src.device)
     _need(src, "src", src.numel())
     _need(sink, "sink", lib().sltx_hbm_read_blocks(), (torch.int32,))
-    check(lib().sltx_hbm_read(_ptr(src), src.numel() * src.element_size(), _ptr(sink),
-                              _stream(stream)))
+    fn = lib().sltx_hbm_read_lds if lds else lib().sltx_hbm_read
+    check(fn(_ptr(src), src.numel() * src.element_size(), _ptr(sink), _stream(stream)))
     return sink
 
 

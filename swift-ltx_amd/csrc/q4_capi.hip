@@ -905,16 +905,24 @@ int sltx_decode_layer_q4(const void* attn, const void* residual, const sltx_q4_w
 
 int sltx_hbm_read_blocks(void) { return hbm_read_blocks(); }
 
-int sltx_hbm_read(const void* src, uint64_t bytes, uint32_t* sink, void* stream) {
-    const char* fn = "sltx_hbm_read";
+static int hbm_read_common(const char* fn, const void* src, uint64_t bytes, uint32_t* sink,
+                           bool lds, void* stream) {
     if (bytes == 0) return kOk;
     if (!src || !sink) return fail(kErrInvalid, "%s: null pointer argument", fn);
     if (bytes % 16 != 0 || !aligned(src, 16) || !aligned(sink, 4))
         return fail(kErrInvalid, "%s: bytes must be a multiple of 16, src 16-byte aligned", fn);
     int rc = ensure_device();
     if (rc != kOk) return rc;
-    return finish(launch_hbm_read(src, (long)(bytes / 16), sink, static_cast<hipStream_t>(stream)),
+    return finish(launch_hbm_read(src, (long)(bytes / 16), sink, lds, static_cast<hipStream_t>(stream)),
                   fn);
+}
+
+int sltx_hbm_read(const void* src, uint64_t bytes, uint32_t* sink, void* stream) {
+    return hbm_read_common("sltx_hbm_read", src, bytes, sink, false, stream);
+}
+
+int sltx_hbm_read_lds(const void* src, uint64_t bytes, uint32_t* sink, void* stream) {
+    return hbm_read_common("sltx_hbm_read_lds", src, bytes, sink, true, stream);
 }
 
 int sltx_probe_empty(void* stream) {

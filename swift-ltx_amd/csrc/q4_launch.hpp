@@ -229,9 +229,10 @@ size_t gemm_partials_workspace_bytes(const GemmParams& p);
 hipError_t launch_gemm_residual_rms_norm(GemmParams p, bool a_bf16, const float* norm_w, float eps,
                                          uint16_t* res_out, uint16_t* norm_out, bool sum_rounded,
                                          hipStream_t st);
-// HBM read ceiling (q4_probe.hip): sink holds hbm_read_blocks() words.
+// HBM read ceiling (q4_probe.hip): sink holds hbm_read_blocks() words; lds:
+// the same stream through direct global -> LDS copies.
 int hbm_read_blocks();
-hipError_t launch_hbm_read(const void* src, long n16, uint32_t* sink, hipStream_t st);
+hipError_t launch_hbm_read(const void* src, long n16, uint32_t* sink, bool lds, hipStream_t st);
 // launch floor, register-only MFMA and grid hand-off probes (q4_probe.hip)
 hipError_t launch_probe_empty(hipStream_t st);
 hipError_t launch_probe_mfma(const void* ab, int blocks, int iters, float* sink,
