@@ -137,3 +137,32 @@ def test_mid_in_graph(pkg, dev):
         gr.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+def test_mid_declines_misaligned_scales(pkg, dev):
+    """The route copies scales and biases as 16-byte pieces; with them at a
+    2-byte offset (the C ABI accepts 2-byte alignment) the launch takes the
+    GEMM's generic path instead and gives the same products, against the
+    oracle.  A 2-byte-aligned x is rejected by the C ABI."""
+    import torch
+    M, N, K, g = 24, 5120, 3072, 64
+    assert pkg.gemm_route(M, N, K) == "mid"
+    x, [(w, s, b)] = o.make_inputs(M, N, K, g, seed=77)
+    tx, tw = to_dev(x, dev), to_dev(w, dev)
+    ts, tb = to_dev(s, dev), to_dev(b, dev)
+    views = []
+    for t in (ts, tb):
+        buf = torch.empty(t.numel() + 8, dtype=t.dtype, device=dev)
+        v = buf[1:1 + t.numel()].view(t.shape)   # 2 bytes past a 16-byte boundary
+        v.copy_(t)
+        assert v.data_ptr() % 16 == 2
+        views.append(v)
+    y_al = pkg.matmul_q4_fast_f32(tx, tw, ts, tb, M, K, N, g)
+    y_mis = pkg.matmul_q4_fast_f32(tx, tw, views[0], views[1], M, K, N, g)
+    torch.cuda.synchronize()
+    ref = o.matmul_q4_f64(x, w, s, b, g)
+    assert_parity(y_al.cpu().numpy(), ref, TOL_GEMM_F16, "aligned")
+    assert_parity(y_mis.cpu().numpy(), ref, TOL_GEMM_F16, "scales and biases at +2 bytes")
+    xbuf = torch.empty(M * K + 8, dtype=torch.float16, device=dev)
+    with pytest.raises(pkg.SltxError):
+        pkg.matmul_q4_fast_f32(xbuf[1:1 + M * K].view(M, K), tw, ts, tb, M, K, N, g)
