@@ -260,16 +260,12 @@ int gemm_route(const GemmParams& p, bool a_bf16, NarrowPlan* np, SkinnyPlan* sp)
     const bool narrow = narrow_plan(p, a_bf16, np);
     const bool skinny = skinny_plan(p, a_bf16, sp);
     if (narrow && (!skinny || !(sp->RT == 2 && sp->OCC == 2))) return SLTX_ROUTE_NARROW;
-    // 16 < M <= 32: the mid-M route for gated pairs, and for one weight set
-    // whose small-M grid would leave CUs idle (its blocks of 32 rows fewer
-    // than the CUs) at N >= 5120.  Measured at M = 20, 24, 32 (us per launch,
-    // weights rotated over >= 2 GB), mid-M against small-M: Llama gate/up
-    // pair 11.5-11.6 against 13.4-15.3, q|k|v (5120 x 3072) 9.5-9.7 against
-    // 11.8-14.9; o (3072 x 3072) 9.3-9.5 against 7.4-8.8 and a single
-    // 8192 x 3072 set 9.8-9.9 against 8.8-10.4 stay on the small-M route.
-    if (p.M > 16 && mid_plan(p, a_bf16) &&
-        (p.w1 != nullptr || !skinny || (p.N >= 5120 && (p.N + 31) / 32 < kCUs)))
-        return SLTX_ROUTE_MID;
+    // 16 < M <= 32: the mid-M route where it is built.  Measured at M = 20,
+    // 24, 32 (us per launch, weights rotated over >= 2 GB), mid-M against
+    // small-M: Llama gate/up pair 11.7-11.9 against 13.4-15.3, q|k|v
+    // (5120 x 3072) 6.6-6.7 against 11.8-14.9, o (3072 x 3072) 6.3-6.4
+    // against 7.4-8.8, a single 8192 x 3072 set 7.4-7.6 against 8.8-10.4.
+    if (p.M > 16 && mid_plan(p, a_bf16)) return SLTX_ROUTE_MID;
     if (skinny) return SLTX_ROUTE_SMALL_M;
     return SLTX_ROUTE_GEMM;
 }

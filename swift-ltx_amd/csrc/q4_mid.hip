@@ -9,16 +9,19 @@
 // 256 KB at K = 4096) and every block needs all of it: the small-M route's
 // per-wave X fragments (16 rows x 64 B per load, a K slice per wave) cost a
 // CU more load issue than its weights.  Here:
-//  * A block owns 64 weight rows -- 32 gate + 32 up rows of the same output
-//    columns for the gated epilogues, else 64 consecutive rows -- and all K,
-//    in NR rounds of 256 k.  It has 16 waves.  The 8 compute waves are
-//    2 row tiles x 4 K-groups: wave 2g + j computes row tile j over k-tile g
-//    of every round, as one 32x32x16 MFMA tile (all 32 activation rows; rows
+//  * A block owns all K for 32 + 32 rows (gate and up of the same output
+//    columns, for the gated epilogues) or 32 rows of one weight set.  It has
+//    16 waves.  The 8 compute waves are 2 row tiles x 4 K-groups (gated,
+//    rounds of 256 k: wave 2g + j computes row tile j over k-tile g of every
+//    round) or 1 row tile x 8 K-groups (one set, rounds of 512 k: wave g over
+//    k-tile g), each as one 32x32x16 MFMA tile (all 32 activation rows; rows
 //    past M are copies of row M - 1, never stored).  Four copy waves copy the
 //    weights, four copy X and the scales and biases, all by direct
-//    global -> LDS copies in whole 128-byte lines.
+//    global -> LDS copies in whole 128-byte lines.  One set in 32-row blocks
+//    was measured faster than in 64-row blocks (2 tiles x 4 K-groups) at every
+//    N tried: twice the blocks, half the weight bytes per block.
 //  * Weights: the block's packed rows are copied at the start, in groups of
-//    four rounds (512 contiguous bytes of two rows per wave-wide copy, the
+//    1024 k (512 contiguous bytes of two rows per wave-wide copy, the
 //    GEMV's pattern: the DRAM pages of a row are read in long runs), so the
 //    whole weight stream is in flight at once, and a round's compute waits
 //    only for its group.  The 16-byte piece c of a row r lands at
@@ -55,23 +58,31 @@ constexpr int NLW = 4;                     // copy waves per stream (weights, X)
 constexpr int MTHREADS = 64 * (NCW + 2 * NLW);
 constexpr int CTHREADS = 64 * NCW;
 constexpr int LTHREADS = 64 * NLW;
-constexpr int KG = 4;                      // K-groups: k-tile g of each round
 constexpr int BM = 32;                     // activation rows (one MFMA tile)
-constexpr int RK = 64 * KG;                // k per round
-constexpr int XSLOTS = KG * BM * 8;        // 16-byte slots of an X stage
-constexpr int NXC = XSLOTS / LTHREADS;     // X copies per X-copy thread per round
-static_assert(NXC * LTHREADS == XSLOTS, "whole copies");
-constexpr int BROWS = 64;                  // weight rows per block
-constexpr int GSLOTS = BROWS * 32;         // 16-byte slots of a weight group (4 rounds)
-constexpr int NWG = GSLOTS / LTHREADS;     // weight copies per W-copy thread per group
-static_assert(NWG * LTHREADS == GSLOTS, "whole copies");
 constexpr size_t kMaxLds = 160 * 1024;
-// X ring stages: as many as fit beside the weights (12 rounds: 96 KB of them)
-__host__ __device__ constexpr int mid_nsx(int nr) { return nr <= 8 ? 5 : 3; }
-__host__ __device__ constexpr size_t mid_static_lds(int nr) {
-    return (size_t)(nr / 4) * GSLOTS * 16 + (size_t)mid_nsx(nr) * XSLOTS * 16 + LTHREADS * 4;
-}
-static_assert(mid_nsx(12) * XSLOTS * 4 >= NCW * 1024, "the K-group sums fit the ring");
+// Two shapes of block.  Gated pairs: 32 gate + 32 up rows, 2 row tiles x 4
+// K-groups, rounds of 256 k.  KG8 (one weight set): 32 weight rows, 1 row
+// tile x 8 K-groups, rounds of 512 k.  Either way a weight group is 512 bytes
+// of every block row (4 or 2 rounds).
+template <bool KG8>
+struct MidShape {
+    static constexpr int KG = KG8 ? 8 : 4;            // K-groups: k-tile g of each round
+    static constexpr int RK = 64 * KG;                // k per round
+    static constexpr int BROWS = KG8 ? 32 : 64;       // weight rows per block
+    static constexpr int RPG = 1024 / RK;             // rounds per weight group (1024 k)
+    static constexpr int XSLOTS = KG * BM * 8;        // 16-byte slots of an X stage
+    static constexpr int NXC = XSLOTS / LTHREADS;     // X copies per X-copy thread per round
+    static constexpr int GSLOTS = BROWS * 32;         // 16-byte slots of a weight group
+    static constexpr int NWG = GSLOTS / LTHREADS;     // weight copies per W-copy thread per group
+    static_assert(NXC * LTHREADS == XSLOTS && NWG * LTHREADS == GSLOTS, "whole copies");
+    static_assert(RPG * RK == 1024 && 2 * KG * RPG == 32, "a group is 512 bytes of a row");
+    // X ring stages: as many as fit beside the weights (ng groups of them)
+    static constexpr int nsx(int ng) { return (KG8 || ng > 2) ? 3 : 5; }
+    static constexpr size_t static_lds(int ng) {
+        return (size_t)ng * GSLOTS * 16 + (size_t)nsx(ng) * XSLOTS * 16 + LTHREADS * 4;
+    }
+    static_assert(nsx(3) * XSLOTS * 4 >= NCW * 1024, "the K-group sums fit the ring");
+};
 
 __device__ __forceinline__ f32x16 mfma32_f16(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
@@ -89,16 +100,20 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-template <bool PAIR, int NR>
+template <bool PAIR, bool KG8, int NG>
 __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
+    using S = MidShape<KG8>;
+    static_assert(PAIR != KG8, "gated pairs: two row tiles; one set: the 32-row block");
+    constexpr int KG = S::KG, RK = S::RK, BROWS = S::BROWS, RPG = S::RPG;
+    constexpr int XSLOTS = S::XSLOTS, NXC = S::NXC, GSLOTS = S::GSLOTS, NWG = S::NWG;
+    constexpr int NR = NG * RPG;                // rounds
     constexpr int NSLAB = PAIR ? 4 : 2;         // s0, b0[, s1, b1]
-    constexpr int SROWS = PAIR ? 32 : 64;       // rows per slab
-    constexpr int NG = NR / 4;                  // weight groups
-    constexpr int NSX = mid_nsx(NR);
+    constexpr int SROWS = PAIR ? 32 : BROWS;    // rows per slab
+    constexpr int NSX = S::nsx(NG);
     // At the start of round q an X-copy wave has issued X(q + 1 .. q + NSX - 2)
     // after X(q).
     constexpr int WAIT_X = (NSX - 2) * NXC;
-    static_assert(NR % 4 == 0 && NSX >= 3, "rounds");
+    static_assert(NSX >= 3, "rounds");
     __shared__ u32x4 wl[NG * GSLOTS];           // weights [group][row][32 pieces]
     __shared__ u32x4 xs[NSX * XSLOTS];          // X ring; after the loop, the K-group sums
     __shared__ uint32_t spare[LTHREADS];        // destination of the copies past the end
@@ -106,7 +121,7 @@ __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n0 = blockIdx.x * (PAIR ? 32 : 64);
+    const int n0 = blockIdx.x * (PAIR ? 32 : BROWS);
     const int K = p.K, groups = p.groups;
     const int alloc = mid_slab_alloc(SROWS, groups);
     f32x16 acc;
@@ -182,8 +197,8 @@ __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
                                                  16, 0, 0);
         static_assert(NG <= 3, "group waits");
         for (int q = 0; q < NR; ++q) {
-            if (q % 4 == 0) {   // group q / 4 landed: NG - 1 - q / 4 groups issued after it
-                const int later = NG - 1 - q / 4;
+            if (q % RPG == 0) {   // group q / RPG landed: NG - 1 - q / RPG issued after it
+                const int later = NG - 1 - q / RPG;
                 if (later == 0) __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
                 else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_only(NWG));
                 else __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * NWG));
@@ -192,7 +207,8 @@ __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
         }
     } else {
         // ---- compute waves ----
-        const int j = wave & 1, g = wave >> 1;   // row tile, K-group
+        const int j = KG8 ? 0 : wave & 1;        // row tile
+        const int g = KG8 ? wave : wave >> 1;    // K-group
         const int r = lane & 31, h = lane >> 5;  // MFMA row / column, k half
         const int wrow = 32 * j + r;             // block row
 
@@ -209,7 +225,8 @@ __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
         for (int q = 0; q < NR; ++q) {
             lds_barrier();
             const u32x4* xst = xs + (q % NSX) * XSLOTS + g * (BM * 8);
-            const u32x4 wpc = wl[(q / 4) * GSLOTS + wrow * 32 + ((8 * (q % 4) + 2 * g + h) ^ (wrow & 15))];
+            const u32x4 wpc = wl[(q / RPG) * GSLOTS + wrow * 32 +
+                                 ((2 * KG * (q % RPG) + 2 * g + h) ^ (wrow & 15))];
             const int gi = (q * RK + 64 * g + 32 * h) >> glog2;
             const uint32_t sv = s_row[gi], bv = b_row[gi];
             const f16x2 s2 = as_f16x2(sv | (sv << 16));
@@ -233,18 +250,20 @@ __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
 
     // D[m][c] of a 32x32 tile is element 4 (m / 8) + m % 4 of lane
     // c + 32 ((m / 4) % 2)
-    constexpr int NCOLS = PAIR ? 32 : 64;
+    constexpr int NCOLS = PAIR ? 32 : BROWS;
     for (int o = tid; o < BM * NCOLS; o += MTHREADS) {
         const int m = o / NCOLS, c = o % NCOLS;
         const int n = n0 + c;
         if (m >= p.M || n >= p.N) continue;
-        const int jj = PAIR ? 0 : c >> 5;
+        const int jj = (PAIR || KG8) ? 0 : c >> 5;
         const int idx = (4 * (m >> 3) + (m & 3)) * 64 + (c & 31) + 32 * ((m >> 2) & 1);
+        // the tile of (K-group gg, row tile t) is wave 2 gg + t (KG8: wave gg)
+        auto wv = [&](int gg, int t) { return KG8 ? gg : 2 * gg + t; };
         float v0 = 0.0f, v1 = 0.0f;
 #pragma unroll
         for (int gg = 0; gg < KG; ++gg) {
-            v0 += red[(2 * gg + jj) * 1024 + idx];
-            if constexpr (PAIR) v1 += red[(2 * gg + 1) * 1024 + idx];
+            v0 += red[wv(gg, jj) * 1024 + idx];
+            if constexpr (PAIR) v1 += red[wv(gg, 1) * 1024 + idx];
         }
         float out;
         if constexpr (PAIR) {
@@ -262,16 +281,20 @@ __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
     }
 }
 
+// Dynamic LDS: the scale / bias slabs (32 rows each)
 size_t mid_lds(const GemmParams& p, bool pair) {
-    const int rows = pair ? 32 : 64;
-    return (size_t)(pair ? 4 : 2) * mid_slab_alloc(rows, p.groups) * 16;
+    return (size_t)(pair ? 4 : 2) * mid_slab_alloc(32, p.groups) * 16;
 }
 
-template <bool PAIR>
-hipError_t launch_nr(const GemmParams& p, const dim3& grid, size_t lds, hipStream_t st) {
-    switch (p.K / RK) {
-        case 8: hipLaunchKernelGGL((q4_mid_kernel<PAIR, 8>), grid, dim3(MTHREADS), lds, st, p); break;
-        case 12: hipLaunchKernelGGL((q4_mid_kernel<PAIR, 12>), grid, dim3(MTHREADS), lds, st, p); break;
+size_t mid_static_lds(int ng, bool pair) {
+    return pair ? MidShape<false>::static_lds(ng) : MidShape<true>::static_lds(ng);
+}
+
+template <bool PAIR, bool KG8>
+hipError_t launch_ng(const GemmParams& p, const dim3& grid, size_t lds, hipStream_t st) {
+    switch (p.K / 1024) {
+        case 2: hipLaunchKernelGGL((q4_mid_kernel<PAIR, KG8, 2>), grid, dim3(MTHREADS), lds, st, p); break;
+        case 3: hipLaunchKernelGGL((q4_mid_kernel<PAIR, KG8, 3>), grid, dim3(MTHREADS), lds, st, p); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -281,9 +304,9 @@ hipError_t launch_nr(const GemmParams& p, const dim3& grid, size_t lds, hipStrea
 
 bool mid_plan(const GemmParams& p, bool a_bf16) {
     if (a_bf16 || p.M < 1 || p.M > BM || p.N < 1) return false;
-    // rounds of 256 k the kernel is built for (K = 2048, 3072: the block's
-    // packed weights fit LDS beside the X ring)
-    if (p.K != 8 * RK && p.K != 12 * RK) return false;
+    // weight groups (512 bytes of each block row) the kernel is built for:
+    // K = 2048, 3072 (the block's packed weights fit LDS beside the X ring)
+    if (p.K != 2048 && p.K != 3072) return false;
     // whole 16-byte slab pieces per row group of 8 (the last block's slab
     // stops at a piece boundary: no copy reads past the arrays)
     if (p.gshift < 0 || p.gshift > 2 || p.groups % 8 != 0) return false;
@@ -292,7 +315,7 @@ bool mid_plan(const GemmParams& p, bool a_bf16) {
     if (!pair && p.epilogue != kEpiNone && p.epilogue != kEpiGeluTanh &&
         p.epilogue != kEpiResidual)
         return false;
-    if (mid_static_lds(p.K / RK) + mid_lds(p, pair) > kMaxLds) return false;
+    if (mid_static_lds(p.K / 1024, pair) + mid_lds(p, pair) > kMaxLds) return false;
     // 16-byte loads and copies: X rows, W rows and the scale / bias slabs
     uintptr_t al = reinterpret_cast<uintptr_t>(p.a) | reinterpret_cast<uintptr_t>(p.w0) |
                    reinterpret_cast<uintptr_t>(p.s0) | reinterpret_cast<uintptr_t>(p.b0);
@@ -304,10 +327,9 @@ bool mid_plan(const GemmParams& p, bool a_bf16) {
 
 hipError_t launch_mid(const GemmParams& p, hipStream_t st) {
     const bool pair = p.w1 != nullptr;
-    const int rows = pair ? 32 : 64;
-    const dim3 grid((unsigned)((p.N + rows - 1) / rows));
+    const dim3 grid((unsigned)((p.N + 31) / 32));   // 32 output columns per block
     const size_t lds = mid_lds(p, pair);
-    return pair ? launch_nr<true>(p, grid, lds, st) : launch_nr<false>(p, grid, lds, st);
+    return pair ? launch_ng<true, false>(p, grid, lds, st) : launch_ng<false, true>(p, grid, lds, st);
 }
 
 }  // namespace sltx

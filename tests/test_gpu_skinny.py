@@ -29,8 +29,8 @@ pytestmark = pytest.mark.gpu
 # N not a multiple of 16, every group size.
 SHAPES = [
     (2, 200, 1024, 64), (5, 64, 2048, 32), (16, 100, 3072, 64), (8, 48, 4096, 128),
-    (5, 80, 5120, 64), (7, 33, 6144, 64), (17, 96, 1024, 32), (32, 112, 2048, 64),
-    (24, 50, 3072, 128), (31, 64, 4096, 64), (6, 96, 8192, 64), (16, 40, 10240, 64),
+    (5, 80, 5120, 64), (7, 33, 6144, 64), (17, 96, 1024, 32), (32, 112, 1024, 64),
+    (24, 50, 4096, 128), (31, 64, 4096, 64), (6, 96, 8192, 64), (16, 40, 10240, 64),
     (9, 24, 14336, 32), (1, 300, 1024, 64), (4, 64, 10240, 64),
     (2, 8200, 3072, 64), (4, 8300, 2048, 32), (6, 8190, 3072, 128),
 ]
@@ -78,13 +78,18 @@ def test_skinny_dequant_bit_exact(pkg, dev, K, g, M, N):
         assert np.array_equal(yq.cpu().numpy(), codes[ks]), c
 
 
-@pytest.mark.parametrize("M,N,K", [(5, 8192, 3072), (8, 200, 3072), (32, 4096, 4096),
-                                   (20, 64, 4096)])
+# Gated pairs (M, N, K, g).  Above 16 rows at K = 2048 / 3072 only group size
+# 32 stays on this route (the mid-M route's LDS does not hold its slabs):
+# those cases keep the 2- and 3-step instantiations of 32 activation rows.
+PAIR_SHAPES = [(5, 8192, 3072, 64), (8, 200, 3072, 64), (32, 4096, 4096, 64),
+               (20, 64, 4096, 64), (24, 96, 2048, 32), (32, 64, 3072, 32)]
+
+
+@pytest.mark.parametrize("M,N,K,g", PAIR_SHAPES)
 @pytest.mark.parametrize("gelu", [False, True])
-def test_skinny_gated_pair(pkg, dev, M, N, K, gelu):
+def test_skinny_gated_pair(pkg, dev, M, N, K, g, gelu):
     import torch
-    g = 64
-    assert pkg.gemm_route(M, N, K, gated=True) == "small_m"
+    assert pkg.gemm_route(M, N, K, group_size=g, gated=True) == "small_m"
     x, [(wg, sg, bg), (wu, su, bu)] = o.make_inputs(M, N, K, g, seed=M + N + K + gelu,
                                                     n_weights=2)
     gate = o.matmul_q4_f64(x, wg, sg, bg, g)

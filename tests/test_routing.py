@@ -22,18 +22,18 @@ def test_gated_pairs_stream_on_the_small_m_route(pkg, M):
 
 @pytest.mark.parametrize("M", [17, 20, 24, 32])
 def test_mid_m_route_above_16_rows(pkg, M):
-    """17..32 rows: gated pairs and tall-enough single sets whose small-M grid
-    leaves CUs idle take the mid-M route (Llama gate/up pair 11.6 against
-    15.3 us at M = 32, q|k|v 9.7 against 14.9); K = 4096 is not built there,
-    and o (3072 rows) and a single 8192-row set are faster on the small-M
-    route."""
+    """17..32 rows at K = 2048 / 3072 take the mid-M route (Llama gate/up pair
+    11.9 against 15.3 us at M = 32, q|k|v 6.7 against 14.9, o 6.4 against 8.8,
+    a single 8192-row set 7.6 against 10.4).  K = 4096 is not built there, nor
+    a gated pair at group size 32 (its scales and biases overflow LDS)."""
     assert pkg.gemm_route(M, **LLAMA_PAIR) == "mid"
-    assert pkg.gemm_route(M, 5120, 3072) == "mid"
+    for N in (5120, 3072, 8192, 64, 33):
+        assert pkg.gemm_route(M, N, 3072) == "mid", N
+    assert pkg.gemm_route(M, 3072, 3072, group_size=32) == "mid"
     assert pkg.gemm_route(M, **T5_WI_PAIR) == "small_m"
-    assert pkg.gemm_route(M, 3072, 3072) == "small_m"
-    assert pkg.gemm_route(M, 8192, 3072) == "small_m"
     assert pkg.gemm_route(M, 4096, 4096) == "small_m"
     assert pkg.gemm_route(M, 8192, 3072, group_size=32, gated=True) == "small_m"   # LDS
+    assert pkg.gemm_route(M, 8192, 2048, group_size=32, gated=True) == "small_m"
 
 
 @pytest.mark.parametrize("N,K", [(5120, 3072), (3072, 3072), (3072, 8192), (4096, 4096),
@@ -58,7 +58,7 @@ def test_m_above_4_leaves_the_narrow_route(pkg, N, K):
     for M in (5, 8, 16, 32):
         # 17..32 activation rows take at most 4 steps of 1024 k per wave
         want = "gemm" if M > 16 and K > 4096 else "small_m"
-        if M > 16 and (N, K) == (5120, 3072):
+        if M > 16 and K in (2048, 3072):
             want = "mid"
         assert pkg.gemm_route(M, N, K) == want, (M, N, K)
 
@@ -89,6 +89,8 @@ def test_small_m_parity_shapes_run_the_small_m_route(pkg):
     for M, N, K, g in test_gpu_skinny.SHAPES:
         want = "gemm" if K == 14336 else "small_m"
         assert pkg.gemm_route(M, N, K, group_size=g) == want, (M, N, K, g)
+    for M, N, K, g in test_gpu_skinny.PAIR_SHAPES:
+        assert pkg.gemm_route(M, N, K, group_size=g, gated=True) == "small_m", (M, N, K, g)
 
 
 def test_mid_parity_shapes_run_the_mid_route(pkg):
