@@ -1,7 +1,7 @@
-"""GPU parity of the mid-M route (q4_mid.hip: 16 < M <= 32, K = 2048 or 3072,
-fp16 activations) through the C ABI: gated pairs (32 gate + 32 up rows per
-block, group sizes 64 and 128) and single weight sets (32 rows per block,
-every group size).
+"""GPU parity of the mid-M route (q4_mid.hip: 16 < M <= 32, and 8 < M <= 16
+for one weight set of 4096..16384 rows; K = 2048 or 3072, fp16 activations)
+through the C ABI: gated pairs (32 gate + 32 up rows per block, group sizes
+64 and 128) and single weight sets (32 rows per block, every group size).
 
 Same semantics as the GEMM (matmulQ4Fast / matmulQ4FastF32, Ops.swift:312-381;
 the SwiGLU and GeGLU pairs, LlamaModel.swift:275-277 and
@@ -26,7 +26,8 @@ pytestmark = pytest.mark.gpu
 SHAPES = [
     (17, 5120, 2048, 64), (32, 5150, 3072, 128), (24, 6000, 2048, 128), (20, 5184, 3072, 64),
     (31, 8160, 3072, 64), (29, 5130, 2048, 64), (32, 20, 3072, 32), (18, 100, 2048, 32),
-    (25, 3072, 3072, 64), (32, 8192, 3072, 32),
+    (25, 3072, 3072, 64), (32, 8192, 3072, 32), (12, 5120, 3072, 64), (9, 4100, 2048, 128),
+    (16, 16384, 2048, 32),
 ]
 
 

@@ -108,7 +108,7 @@ def test_skinny_residual_and_bias_gelu(pkg, dev, M):
     (linear + elemAdd, LlamaModel.swift:330-331) and bias + GELU-tanh with an
     fp16 activation (DiTLinear's q4 branch, DiTModel.swift:102-125)."""
     import torch
-    N, K, g = 160, 2048, 64
+    N, K, g = 160, 4096, 64
     x, [(w, s, b)] = o.make_inputs(M, N, K, g, seed=300 + M)
     rng = np.random.default_rng(M)
     res = rng.standard_normal((M, N)).astype(np.float16)

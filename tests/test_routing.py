@@ -36,6 +36,19 @@ def test_mid_m_route_above_16_rows(pkg, M):
     assert pkg.gemm_route(M, 8192, 2048, group_size=32, gated=True) == "small_m"
 
 
+@pytest.mark.parametrize("M", [9, 12, 16])
+def test_mid_m_route_for_one_set_above_8_rows(pkg, M):
+    """9..16 rows: one weight set of 4096..16384 rows takes the mid-M route
+    (q|k|v 6.5 against 8.5 us at M = 12); o (3072 rows), the vocabulary head
+    and gated pairs stay on the small-M route."""
+    assert pkg.gemm_route(M, 5120, 3072) == "mid"
+    assert pkg.gemm_route(M, 8192, 3072) == "mid"
+    assert pkg.gemm_route(M, 16384, 2048) == "mid"
+    assert pkg.gemm_route(M, 3072, 3072) == "small_m"
+    assert pkg.gemm_route(M, 128256, 3072) == "small_m"
+    assert pkg.gemm_route(M, **LLAMA_PAIR) == "small_m"
+
+
 @pytest.mark.parametrize("N,K", [(5120, 3072), (3072, 3072), (3072, 8192), (4096, 4096),
                                  (4096, 10240)])
 @pytest.mark.parametrize("M", [1, 2, 3, 4])
@@ -58,7 +71,7 @@ def test_m_above_4_leaves_the_narrow_route(pkg, N, K):
     for M in (5, 8, 16, 32):
         # 17..32 activation rows take at most 4 steps of 1024 k per wave
         want = "gemm" if M > 16 and K > 4096 else "small_m"
-        if M > 16 and K in (2048, 3072):
+        if K in (2048, 3072) and (M > 16 or (M > 8 and 4096 <= N <= 16384)):
             want = "mid"
         assert pkg.gemm_route(M, N, K) == want, (M, N, K)
 
