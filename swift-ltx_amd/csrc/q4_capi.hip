@@ -260,16 +260,22 @@ int gemm_route(const GemmParams& p, bool a_bf16, NarrowPlan* np, SkinnyPlan* sp)
     const bool narrow = narrow_plan(p, a_bf16, np);
     const bool skinny = skinny_plan(p, a_bf16, sp);
     if (narrow && (!skinny || !(sp->RT == 2 && sp->OCC == 2))) return SLTX_ROUTE_NARROW;
-    // 16 < M <= 32: the mid-M route where it is built; one weight set of
-    // 4096..16384 rows already above 8 rows.  Measured (us per launch,
-    // weights rotated over >= 2 GB), mid-M against small-M: at M = 20, 24,
-    // 32 the Llama gate/up pair 11.7-11.9 against 13.4-15.3, q|k|v
-    // (5120 x 3072) 6.6-6.7 against 11.8-14.9, o (3072 x 3072) 6.3-6.4
-    // against 7.4-8.8, a single 8192 x 3072 set 7.4-7.6 against 8.8-10.4; at
-    // M = 12, 16 q|k|v 6.5 against 8.5 / 9.5 and the 8192-row set 7.3
-    // against 7.3 / 7.7, while o (6.2 against 5.7 / 6.1) and the vocabulary
-    // head (M = 8: 87 against 62 us) stay on the small-M route.
-    const bool mid_rows = p.M > 16 || (p.M > 8 && p.w1 == nullptr && p.N >= 4096 && p.N <= 16384);
+    // The mid-M route: above 16 rows where it is built (at K > 3072 only
+    // where the small-M route cannot run or above 24 rows), and one weight
+    // set of 4096..16384 rows at K <= 3072 above 8 rows.  Measured (us per
+    // launch, weights rotated over >= 2 GB), mid-M against small-M / GEMM:
+    // - M = 20, 24, 32: Llama gate/up pair 11.7-11.9 against 13.4-15.3,
+    //   q|k|v (5120 x 3072) 6.6-6.7 against 11.8-14.9, o (3072 x 3072)
+    //   6.3-6.4 against 7.4-8.8, a single 8192 x 3072 set 7.4-7.6 against
+    //   8.8-10.4; Llama down (3072 x 8192) 15.4 against the GEMM's 22.8-23.0,
+    //   T5 wo (4096 x 10240) 14.4-14.9 against the GEMM's 26.9-28;
+    //   T5 q/k/v/o (4096 x 4096) 9.9 / 9.9 / 9.9 against 8.9 / 9.6 / 10.9;
+    // - M = 12, 16: q|k|v 6.5 against 8.5 / 9.5, the 8192-row set 7.3
+    //   against 7.3 / 7.7; o 6.2 against 5.7 / 6.1, T5 q/k/v/o 9.8 against
+    //   6.7 / 7.3, the vocabulary head (M = 8) 87 against 62 us.
+    const bool kshort = p.K <= 3072;
+    const bool mid_rows = (p.M > 16 && (kshort || !skinny || p.M > 24)) ||
+                          (p.M > 8 && kshort && p.w1 == nullptr && p.N >= 4096 && p.N <= 16384);
     if (mid_rows && mid_plan(p, a_bf16)) return SLTX_ROUTE_MID;
     if (skinny) return SLTX_ROUTE_SMALL_M;
     return SLTX_ROUTE_GEMM;

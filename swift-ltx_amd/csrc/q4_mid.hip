@@ -76,10 +76,10 @@ struct MidShape {
     static constexpr int NWG = GSLOTS / LTHREADS;     // weight copies per W-copy thread per group
     static_assert(NXC * LTHREADS == XSLOTS && NWG * LTHREADS == GSLOTS, "whole copies");
     static_assert(RPG * RK == 1024 && 2 * KG * RPG == 32, "a group is 512 bytes of a row");
-    // X ring stages: as many as fit beside the weights (ng groups of them)
-    static constexpr int nsx(int ng) { return (KG8 || ng > 2) ? 3 : 5; }
-    static constexpr size_t static_lds(int ng) {
-        return (size_t)ng * GSLOTS * 16 + (size_t)nsx(ng) * XSLOTS * 16 + LTHREADS * 4;
+    // X ring stages: as many as fit beside wsl weight-group slots
+    static constexpr int nsx(int wsl) { return (KG8 || wsl > 2) ? 3 : 5; }
+    static constexpr size_t static_lds(int wsl) {
+        return (size_t)wsl * GSLOTS * 16 + (size_t)nsx(wsl) * XSLOTS * 16 + LTHREADS * 4;
     }
     static_assert(nsx(3) * XSLOTS * 4 >= NCW * 1024, "the K-group sums fit the ring");
 };
@@ -100,7 +100,10 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-template <bool PAIR, bool KG8, int NG>
+// NG weight groups of 1024 k in WSL LDS slots: WSL = NG holds the whole K;
+// WSL < NG refills the slot of group G - 1 with group G + WSL - 1 once every
+// wave has finished group G - 1.
+template <bool PAIR, bool KG8, int NG, int WSL>
 __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
     using S = MidShape<KG8>;
     static_assert(PAIR != KG8, "gated pairs: two row tiles; one set: the 32-row block");
@@ -109,12 +112,13 @@ __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
     constexpr int NR = NG * RPG;                // rounds
     constexpr int NSLAB = PAIR ? 4 : 2;         // s0, b0[, s1, b1]
     constexpr int SROWS = PAIR ? 32 : BROWS;    // rows per slab
-    constexpr int NSX = S::nsx(NG);
+    constexpr int NSX = S::nsx(WSL);
+    static_assert(WSL >= 2 && WSL <= NG && WSL <= 3, "weight slots");
     // At the start of round q an X-copy wave has issued X(q + 1 .. q + NSX - 2)
     // after X(q).
     constexpr int WAIT_X = (NSX - 2) * NXC;
     static_assert(NSX >= 3, "rounds");
-    __shared__ u32x4 wl[NG * GSLOTS];           // weights [group][row][32 pieces]
+    __shared__ u32x4 wl[WSL * GSLOTS];          // weights [slot][row][32 pieces]
     __shared__ u32x4 xs[NSX * XSLOTS];          // X ring; after the loop, the K-group sums
     __shared__ uint32_t spare[LTHREADS];        // destination of the copies past the end
     extern __shared__ u32x4 sb_lds[];           // [NSLAB][alloc] slabs
@@ -188,22 +192,28 @@ __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
             if (n >= p.N) n = 0;   // rows past N read row 0 (never stored)
             w_src[i] = W + (size_t)n * (K / 8) + (((lane & 31) ^ (row & 15)) * 4);
         }
-#pragma unroll
-        for (int G = 0; G < NG; ++G)
+        auto issue_w = [&](int G) {   // NWG vector-memory ops: group G into slot G % WSL
+            u32x4* slot = wl + (G % WSL) * GSLOTS;
 #pragma unroll
             for (int i = 0; i < NWG; ++i)
-                __builtin_amdgcn_global_load_lds((const void*)(w_src[i] + G * 128),
-                                                 (lds_ptr_t)(wl + G * GSLOTS + 64 * (lw + NLW * i)),
-                                                 16, 0, 0);
-        static_assert(NG <= 3, "group waits");
+                __builtin_amdgcn_global_load_lds((const void*)(w_src[i] + (size_t)G * 128),
+                                                 (lds_ptr_t)(slot + 64 * (lw + NLW * i)), 16, 0, 0);
+        };
+        for (int G = 0; G < WSL; ++G) issue_w(G);
         for (int q = 0; q < NR; ++q) {
-            if (q % RPG == 0) {   // group q / RPG landed: NG - 1 - q / RPG issued after it
-                const int later = NG - 1 - q / RPG;
+            const int G = q / RPG;
+            if (q % RPG == 0) {
+                // group G landed.  Issued after it: groups 1 .. WSL - 1 at
+                // G = 0; later only group G + WSL - 2 (issued at the start of
+                // group G - 1), if it exists and is not G itself
+                const int later = G == 0 ? WSL - 1 : min(NG - 1 - G, WSL - 2);
                 if (later == 0) __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
                 else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_only(NWG));
                 else __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * NWG));
             }
             lds_barrier();
+            // every wave is past group G - 1: its slot takes group G + WSL - 1
+            if (q % RPG == 0 && G >= 1 && G + WSL - 1 < NG) issue_w(G + WSL - 1);
         }
     } else {
         // ---- compute waves ----
@@ -225,7 +235,7 @@ __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
         for (int q = 0; q < NR; ++q) {
             lds_barrier();
             const u32x4* xst = xs + (q % NSX) * XSLOTS + g * (BM * 8);
-            const u32x4 wpc = wl[(q / RPG) * GSLOTS + wrow * 32 +
+            const u32x4 wpc = wl[((q / RPG) % WSL) * GSLOTS + wrow * 32 +
                                  ((2 * KG * (q % RPG) + 2 * g + h) ^ (wrow & 15))];
             const int gi = (q * RK + 64 * g + 32 * h) >> glog2;
             const uint32_t sv = s_row[gi], bv = b_row[gi];
@@ -286,27 +296,62 @@ size_t mid_lds(const GemmParams& p, bool pair) {
     return (size_t)(pair ? 4 : 2) * mid_slab_alloc(32, p.groups) * 16;
 }
 
-size_t mid_static_lds(int ng, bool pair) {
-    return pair ? MidShape<false>::static_lds(ng) : MidShape<true>::static_lds(ng);
+size_t mid_static_lds(int wsl, bool pair) {
+    return pair ? MidShape<false>::static_lds(wsl) : MidShape<true>::static_lds(wsl);
 }
 
-template <bool PAIR, bool KG8>
-hipError_t launch_ng(const GemmParams& p, const dim3& grid, size_t lds, hipStream_t st) {
-    switch (p.K / 1024) {
-        case 2: hipLaunchKernelGGL((q4_mid_kernel<PAIR, KG8, 2>), grid, dim3(MTHREADS), lds, st, p); break;
-        case 3: hipLaunchKernelGGL((q4_mid_kernel<PAIR, KG8, 3>), grid, dim3(MTHREADS), lds, st, p); break;
-        default: return hipErrorInvalidValue;
+// Weight-group slots: the whole K (up to 3 groups) when it fits LDS beside
+// the X ring and the slabs, else 3 or 2 slots refilled as the groups are
+// used (one weight set only); 0: none fits.
+int mid_wsl(const GemmParams& p, bool pair) {
+    const int ng = p.K / 1024;
+    for (int wsl = ng < 3 ? ng : 3; wsl >= 2; --wsl) {
+        if (pair && wsl != ng) break;
+        if (mid_static_lds(wsl, pair) + mid_lds(p, pair) <= kMaxLds) return wsl;
     }
+    return 0;
+}
+
+template <bool PAIR, bool KG8, int NG, int WSL>
+hipError_t launch_cfg(const GemmParams& p, const dim3& grid, size_t lds, hipStream_t st) {
+    hipLaunchKernelGGL((q4_mid_kernel<PAIR, KG8, NG, WSL>), grid, dim3(MTHREADS), lds, st, p);
     return hipGetLastError();
+}
+
+// (groups, slots) built: gated pairs at K = 2048, 3072 (whole K); one set at
+// K = 2048, 3072, 4096, 8192, 10240.
+bool mid_built(bool pair, int ng, int wsl) {
+    if (pair) return (ng == 2 || ng == 3) && wsl == ng;
+    return ng == 2 ? wsl == 2 : (ng == 3 || ng == 4 || ng == 8 || ng == 10) && (wsl == 2 || wsl == 3);
+}
+
+hipError_t launch_sel(const GemmParams& p, bool pair, int wsl, const dim3& grid, size_t lds,
+                      hipStream_t st) {
+    const int ng = p.K / 1024;
+    if (pair) {
+        if (ng == 2) return launch_cfg<true, false, 2, 2>(p, grid, lds, st);
+        if (ng == 3) return launch_cfg<true, false, 3, 3>(p, grid, lds, st);
+        return hipErrorInvalidValue;
+    }
+    switch (ng * 4 + wsl) {
+        case 2 * 4 + 2: return launch_cfg<false, true, 2, 2>(p, grid, lds, st);
+        case 3 * 4 + 2: return launch_cfg<false, true, 3, 2>(p, grid, lds, st);
+        case 3 * 4 + 3: return launch_cfg<false, true, 3, 3>(p, grid, lds, st);
+        case 4 * 4 + 2: return launch_cfg<false, true, 4, 2>(p, grid, lds, st);
+        case 4 * 4 + 3: return launch_cfg<false, true, 4, 3>(p, grid, lds, st);
+        case 8 * 4 + 2: return launch_cfg<false, true, 8, 2>(p, grid, lds, st);
+        case 8 * 4 + 3: return launch_cfg<false, true, 8, 3>(p, grid, lds, st);
+        case 10 * 4 + 2: return launch_cfg<false, true, 10, 2>(p, grid, lds, st);
+        case 10 * 4 + 3: return launch_cfg<false, true, 10, 3>(p, grid, lds, st);
+    }
+    return hipErrorInvalidValue;
 }
 
 }  // namespace
 
 bool mid_plan(const GemmParams& p, bool a_bf16) {
     if (a_bf16 || p.M < 1 || p.M > BM || p.N < 1) return false;
-    // weight groups (512 bytes of each block row) the kernel is built for:
-    // K = 2048, 3072 (the block's packed weights fit LDS beside the X ring)
-    if (p.K != 2048 && p.K != 3072) return false;
+    if (p.K <= 0 || p.K % 1024 != 0) return false;
     // whole 16-byte slab pieces per row group of 8 (the last block's slab
     // stops at a piece boundary: no copy reads past the arrays)
     if (p.gshift < 0 || p.gshift > 2 || p.groups % 8 != 0) return false;
@@ -315,7 +360,8 @@ bool mid_plan(const GemmParams& p, bool a_bf16) {
     if (!pair && p.epilogue != kEpiNone && p.epilogue != kEpiGeluTanh &&
         p.epilogue != kEpiResidual)
         return false;
-    if (mid_static_lds(p.K / 1024, pair) + mid_lds(p, pair) > kMaxLds) return false;
+    const int wsl = mid_wsl(p, pair);
+    if (wsl == 0 || !mid_built(pair, p.K / 1024, wsl)) return false;
     // 16-byte loads and copies: X rows, W rows and the scale / bias slabs
     uintptr_t al = reinterpret_cast<uintptr_t>(p.a) | reinterpret_cast<uintptr_t>(p.w0) |
                    reinterpret_cast<uintptr_t>(p.s0) | reinterpret_cast<uintptr_t>(p.b0);
@@ -328,8 +374,7 @@ bool mid_plan(const GemmParams& p, bool a_bf16) {
 hipError_t launch_mid(const GemmParams& p, hipStream_t st) {
     const bool pair = p.w1 != nullptr;
     const dim3 grid((unsigned)((p.N + 31) / 32));   // 32 output columns per block
-    const size_t lds = mid_lds(p, pair);
-    return pair ? launch_ng<true, false>(p, grid, lds, st) : launch_ng<false, true>(p, grid, lds, st);
+    return launch_sel(p, pair, mid_wsl(p, pair), grid, mid_lds(p, pair), st);
 }
 
 }  // namespace sltx

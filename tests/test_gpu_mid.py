@@ -1,7 +1,9 @@
 """GPU parity of the mid-M route (q4_mid.hip: 16 < M <= 32, and 8 < M <= 16
-for one weight set of 4096..16384 rows; K = 2048 or 3072, fp16 activations)
-through the C ABI: gated pairs (32 gate + 32 up rows per block, group sizes
-64 and 128) and single weight sets (32 rows per block, every group size).
+for one weight set of 4096..16384 rows; fp16 activations) through the C ABI:
+gated pairs at K = 2048 / 3072 (32 gate + 32 up rows per block, group sizes
+64 and 128) and single weight sets at K = 2048, 3072, 4096, 8192, 10240 (32
+rows per block; the weight groups of 1024 k held whole or in a ring of 2-3
+LDS slots).
 
 Same semantics as the GEMM (matmulQ4Fast / matmulQ4FastF32, Ops.swift:312-381;
 the SwiGLU and GeGLU pairs, LlamaModel.swift:275-277 and
@@ -9,9 +11,9 @@ T5Encoder.swift:191-199): the weights are dequantized to fp16 as s*q+b in one
 fp16 FMA and multiplied with fp32 accumulation, so the outputs are checked
 against the fp64 oracle (tolerances of tests/helpers.py), against the
 fp16-rounded weights, and bit for bit through unit vectors.  The shapes cover
-both weight-group counts (K = 2048, 3072), the X ring's wrap-around and the
-spare copies past the end, a last block with fewer than 32 rows, grids from
-one block to 256, and every group size.
+every built weight-group count and slot ring, the X ring's wrap-around and
+the spare copies past the end, a last block with fewer than 32 rows, grids
+from one block to 256, and every group size.
 """
 import numpy as np
 import pytest
@@ -27,7 +29,8 @@ SHAPES = [
     (17, 5120, 2048, 64), (32, 5150, 3072, 128), (24, 6000, 2048, 128), (20, 5184, 3072, 64),
     (31, 8160, 3072, 64), (29, 5130, 2048, 64), (32, 20, 3072, 32), (18, 100, 2048, 32),
     (25, 3072, 3072, 64), (32, 8192, 3072, 32), (12, 5120, 3072, 64), (9, 4100, 2048, 128),
-    (16, 16384, 2048, 32),
+    (16, 16384, 2048, 32), (28, 4096, 4096, 64), (32, 3072, 8192, 64), (17, 4096, 10240, 128),
+    (26, 4096, 4096, 32), (24, 100, 8192, 128), (29, 90, 10240, 64), (31, 4096, 4096, 128),
 ]
 
 
@@ -48,7 +51,7 @@ def test_mid_shapes(pkg, dev, M, N, K, g):
     assert torch.equal(y32.half(), y16)
 
 
-@pytest.mark.parametrize("K,g,M,N", [(3072, 64, 32, 5120), (2048, 128, 24, 5150), (3072, 32, 17, 70)])
+@pytest.mark.parametrize("K,g,M,N", [(3072, 64, 32, 5120), (2048, 128, 24, 5150), (3072, 32, 17, 70), (8192, 64, 20, 96)])
 def test_mid_dequant_bit_exact(pkg, dev, K, g, M, N):
     """x rows are unit vectors e_k (M per call, over every k): each output is
     one dequantized weight, exact in fp32, so every lane, k-step, K-group,

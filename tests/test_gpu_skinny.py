@@ -30,7 +30,7 @@ pytestmark = pytest.mark.gpu
 SHAPES = [
     (2, 200, 1024, 64), (5, 64, 2048, 32), (16, 100, 3072, 64), (8, 48, 4096, 128),
     (5, 80, 5120, 64), (7, 33, 6144, 64), (17, 96, 1024, 32), (32, 112, 1024, 64),
-    (24, 50, 4096, 128), (31, 64, 4096, 64), (6, 96, 8192, 64), (16, 40, 10240, 64),
+    (24, 50, 4096, 128), (22, 64, 4096, 64), (6, 96, 8192, 64), (16, 40, 10240, 64),
     (9, 24, 14336, 32), (1, 300, 1024, 64), (4, 64, 10240, 64),
     (2, 8200, 3072, 64), (4, 8300, 2048, 32), (6, 8190, 3072, 128),
 ]
@@ -102,7 +102,7 @@ def test_skinny_gated_pair(pkg, dev, M, N, K, g, gelu):
     assert_parity(y.cpu().numpy(), ref, TOL_GEMM_F16, f"{'geglu' if gelu else 'swiglu'} M={M}")
 
 
-@pytest.mark.parametrize("M", [6, 12, 29])
+@pytest.mark.parametrize("M", [6, 12, 23])
 def test_skinny_residual_and_bias_gelu(pkg, dev, M):
     """The single-set epilogues on the small-M route: residual add
     (linear + elemAdd, LlamaModel.swift:330-331) and bias + GELU-tanh with an

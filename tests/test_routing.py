@@ -24,27 +24,34 @@ def test_gated_pairs_stream_on_the_small_m_route(pkg, M):
 def test_mid_m_route_above_16_rows(pkg, M):
     """17..32 rows at K = 2048 / 3072 take the mid-M route (Llama gate/up pair
     11.9 against 15.3 us at M = 32, q|k|v 6.7 against 14.9, o 6.4 against 8.8,
-    a single 8192-row set 7.6 against 10.4).  K = 4096 is not built there, nor
-    a gated pair at group size 32 (its scales and biases overflow LDS)."""
+    a single 8192-row set 7.6 against 10.4), and at K = 8192 / 10240, where
+    the small-M route does not run (Llama down 15.4 against the GEMM's 23.0,
+    T5 wo 14.9 against 26.9).  At K = 4096 one set takes it above 24 rows
+    (T5 q/k/v/o 9.9 against 10.9 at M = 32, 9.9 against 9.6 at M = 24); a
+    gated pair at K = 4096 or group size 32 is not built there."""
     assert pkg.gemm_route(M, **LLAMA_PAIR) == "mid"
     for N in (5120, 3072, 8192, 64, 33):
         assert pkg.gemm_route(M, N, 3072) == "mid", N
     assert pkg.gemm_route(M, 3072, 3072, group_size=32) == "mid"
+    assert pkg.gemm_route(M, 3072, 8192) == "mid"
+    assert pkg.gemm_route(M, 4096, 10240) == "mid"
     assert pkg.gemm_route(M, **T5_WI_PAIR) == "small_m"
-    assert pkg.gemm_route(M, 4096, 4096) == "small_m"
+    assert pkg.gemm_route(M, 4096, 4096) == ("mid" if M > 24 else "small_m")
     assert pkg.gemm_route(M, 8192, 3072, group_size=32, gated=True) == "small_m"   # LDS
     assert pkg.gemm_route(M, 8192, 2048, group_size=32, gated=True) == "small_m"
 
 
 @pytest.mark.parametrize("M", [9, 12, 16])
 def test_mid_m_route_for_one_set_above_8_rows(pkg, M):
-    """9..16 rows: one weight set of 4096..16384 rows takes the mid-M route
-    (q|k|v 6.5 against 8.5 us at M = 12); o (3072 rows), the vocabulary head
-    and gated pairs stay on the small-M route."""
+    """9..16 rows: one weight set of 4096..16384 rows at K <= 3072 takes the
+    mid-M route (q|k|v 6.5 against 8.5 us at M = 12); o (3072 rows), the
+    vocabulary head, T5 q/k/v/o (K = 4096) and gated pairs stay on the small-M
+    route."""
     assert pkg.gemm_route(M, 5120, 3072) == "mid"
     assert pkg.gemm_route(M, 8192, 3072) == "mid"
     assert pkg.gemm_route(M, 16384, 2048) == "mid"
     assert pkg.gemm_route(M, 3072, 3072) == "small_m"
+    assert pkg.gemm_route(M, 4096, 4096) == "small_m"
     assert pkg.gemm_route(M, 128256, 3072) == "small_m"
     assert pkg.gemm_route(M, **LLAMA_PAIR) == "small_m"
 
@@ -72,6 +79,8 @@ def test_m_above_4_leaves_the_narrow_route(pkg, N, K):
         # 17..32 activation rows take at most 4 steps of 1024 k per wave
         want = "gemm" if M > 16 and K > 4096 else "small_m"
         if K in (2048, 3072) and (M > 16 or (M > 8 and 4096 <= N <= 16384)):
+            want = "mid"
+        if M > 24 or (M > 16 and K > 4096):   # K = 4096 / 8192 above the small-M route
             want = "mid"
         assert pkg.gemm_route(M, N, K) == want, (M, N, K)
 
