@@ -270,6 +270,8 @@ int gemm_route(const GemmParams& p, bool a_bf16, NarrowPlan* np, SkinnyPlan* sp)
     //   8.8-10.4; Llama down (3072 x 8192) 15.4 against the GEMM's 22.8-23.0,
     //   T5 wo (4096 x 10240) 14.4-14.9 against the GEMM's 26.9-28;
     //   T5 q/k/v/o (4096 x 4096) 9.9 / 9.9 / 9.9 against 8.9 / 9.6 / 10.9;
+    //   the T5 GeGLU pair (2 x 10240 x 4096) 31.5 at M = 25-32 against 36.7
+    //   at M = 32;
     // - M = 12, 16: q|k|v 6.5 against 8.5 / 9.5, the 8192-row set 7.3
     //   against 7.3 / 7.7; o 6.2 against 5.7 / 6.1, T5 q/k/v/o 9.8 against
     //   6.7 / 7.3, the vocabulary head (M = 8) 87 against 62 us.

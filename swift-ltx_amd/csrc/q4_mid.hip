@@ -76,12 +76,13 @@ struct MidShape {
     static constexpr int NWG = GSLOTS / LTHREADS;     // weight copies per W-copy thread per group
     static_assert(NXC * LTHREADS == XSLOTS && NWG * LTHREADS == GSLOTS, "whole copies");
     static_assert(RPG * RK == 1024 && 2 * KG * RPG == 32, "a group is 512 bytes of a row");
-    // X ring stages: as many as fit beside wsl weight-group slots
-    static constexpr int nsx(int wsl) { return (KG8 || wsl > 2) ? 3 : 5; }
-    static constexpr size_t static_lds(int wsl) {
-        return (size_t)wsl * GSLOTS * 16 + (size_t)nsx(wsl) * XSLOTS * 16 + LTHREADS * 4;
+    // X ring stages: as many as fit beside wsl slots for ng weight groups
+    // (five only for a gated pair holding K = 2048 whole)
+    static constexpr int nsx(int ng, int wsl) { return (!KG8 && ng == 2 && wsl == 2) ? 5 : 3; }
+    static constexpr size_t static_lds(int ng, int wsl) {
+        return (size_t)wsl * GSLOTS * 16 + (size_t)nsx(ng, wsl) * XSLOTS * 16 + LTHREADS * 4;
     }
-    static_assert(nsx(3) * XSLOTS * 4 >= NCW * 1024, "the K-group sums fit the ring");
+    static_assert(nsx(3, 3) * XSLOTS * 4 >= NCW * 1024, "the K-group sums fit the ring");
 };
 
 __device__ __forceinline__ f32x16 mfma32_f16(u32x4 a, u32x4 b, f32x16 c) {
@@ -112,7 +113,7 @@ __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
     constexpr int NR = NG * RPG;                // rounds
     constexpr int NSLAB = PAIR ? 4 : 2;         // s0, b0[, s1, b1]
     constexpr int SROWS = PAIR ? 32 : BROWS;    // rows per slab
-    constexpr int NSX = S::nsx(WSL);
+    constexpr int NSX = S::nsx(NG, WSL);
     static_assert(WSL >= 2 && WSL <= NG && WSL <= 3, "weight slots");
     // At the start of round q an X-copy wave has issued X(q + 1 .. q + NSX - 2)
     // after X(q).
@@ -296,19 +297,25 @@ size_t mid_lds(const GemmParams& p, bool pair) {
     return (size_t)(pair ? 4 : 2) * mid_slab_alloc(32, p.groups) * 16;
 }
 
-size_t mid_static_lds(int wsl, bool pair) {
-    return pair ? MidShape<false>::static_lds(wsl) : MidShape<true>::static_lds(wsl);
+size_t mid_static_lds(int ng, int wsl, bool pair) {
+    return pair ? MidShape<false>::static_lds(ng, wsl) : MidShape<true>::static_lds(ng, wsl);
+}
+
+// (groups, slots) built: gated pairs at K = 2048, 3072 (whole K) and 4096
+// (two or three slots); one set at K = 2048, 3072, 4096, 8192, 10240.
+bool mid_built(bool pair, int ng, int wsl) {
+    if (pair) return ((ng == 2 || ng == 3) && wsl == ng) || (ng == 4 && (wsl == 2 || wsl == 3));
+    return ng == 2 ? wsl == 2 : (ng == 3 || ng == 4 || ng == 8 || ng == 10) && (wsl == 2 || wsl == 3);
 }
 
 // Weight-group slots: the whole K (up to 3 groups) when it fits LDS beside
 // the X ring and the slabs, else 3 or 2 slots refilled as the groups are
-// used (one weight set only); 0: none fits.
+// used; 0: no built configuration fits.
 int mid_wsl(const GemmParams& p, bool pair) {
     const int ng = p.K / 1024;
-    for (int wsl = ng < 3 ? ng : 3; wsl >= 2; --wsl) {
-        if (pair && wsl != ng) break;
-        if (mid_static_lds(wsl, pair) + mid_lds(p, pair) <= kMaxLds) return wsl;
-    }
+    for (int wsl = ng < 3 ? ng : 3; wsl >= 2; --wsl)
+        if (mid_built(pair, ng, wsl) && mid_static_lds(ng, wsl, pair) + mid_lds(p, pair) <= kMaxLds)
+            return wsl;
     return 0;
 }
 
@@ -318,19 +325,14 @@ hipError_t launch_cfg(const GemmParams& p, const dim3& grid, size_t lds, hipStre
     return hipGetLastError();
 }
 
-// (groups, slots) built: gated pairs at K = 2048, 3072 (whole K); one set at
-// K = 2048, 3072, 4096, 8192, 10240.
-bool mid_built(bool pair, int ng, int wsl) {
-    if (pair) return (ng == 2 || ng == 3) && wsl == ng;
-    return ng == 2 ? wsl == 2 : (ng == 3 || ng == 4 || ng == 8 || ng == 10) && (wsl == 2 || wsl == 3);
-}
-
 hipError_t launch_sel(const GemmParams& p, bool pair, int wsl, const dim3& grid, size_t lds,
                       hipStream_t st) {
     const int ng = p.K / 1024;
     if (pair) {
         if (ng == 2) return launch_cfg<true, false, 2, 2>(p, grid, lds, st);
         if (ng == 3) return launch_cfg<true, false, 3, 3>(p, grid, lds, st);
+        if (ng == 4 && wsl == 2) return launch_cfg<true, false, 4, 2>(p, grid, lds, st);
+        if (ng == 4 && wsl == 3) return launch_cfg<true, false, 4, 3>(p, grid, lds, st);
         return hipErrorInvalidValue;
     }
     switch (ng * 4 + wsl) {
@@ -360,8 +362,7 @@ bool mid_plan(const GemmParams& p, bool a_bf16) {
     if (!pair && p.epilogue != kEpiNone && p.epilogue != kEpiGeluTanh &&
         p.epilogue != kEpiResidual)
         return false;
-    const int wsl = mid_wsl(p, pair);
-    if (wsl == 0 || !mid_built(pair, p.K / 1024, wsl)) return false;
+    if (mid_wsl(p, pair) == 0) return false;
     // 16-byte loads and copies: X rows, W rows and the scale / bias slabs
     uintptr_t al = reinterpret_cast<uintptr_t>(p.a) | reinterpret_cast<uintptr_t>(p.w0) |
                    reinterpret_cast<uintptr_t>(p.s0) | reinterpret_cast<uintptr_t>(p.b0);

@@ -76,13 +76,13 @@ def test_mid_dequant_bit_exact(pkg, dev, K, g, M, N):
         assert np.array_equal(yq.cpu().numpy(), codes[ks]), c
 
 
-@pytest.mark.parametrize("M,N,K", [(32, 8192, 3072), (17, 200, 3072), (24, 10240, 2048),
-                                   (31, 40, 2048)])
+@pytest.mark.parametrize("M,N,K,g", [(32, 8192, 3072, 64), (17, 200, 3072, 64),
+                                     (24, 10240, 2048, 64), (31, 40, 2048, 128),
+                                     (32, 10240, 4096, 64), (27, 300, 4096, 128)])
 @pytest.mark.parametrize("gelu", [False, True])
-def test_mid_gated_pair(pkg, dev, M, N, K, gelu):
+def test_mid_gated_pair(pkg, dev, M, N, K, g, gelu):
     import torch
-    g = 64
-    assert pkg.gemm_route(M, N, K, gated=True) == "mid"
+    assert pkg.gemm_route(M, N, K, group_size=g, gated=True) == "mid"
     x, [(wg, sg, bg), (wu, su, bu)] = o.make_inputs(M, N, K, g, seed=M + N + K + gelu,
                                                     n_weights=2)
     gate = o.matmul_q4_f64(x, wg, sg, bg, g)
