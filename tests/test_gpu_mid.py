@@ -78,7 +78,8 @@ def test_mid_dequant_bit_exact(pkg, dev, K, g, M, N):
 
 @pytest.mark.parametrize("M,N,K,g", [(32, 8192, 3072, 64), (17, 200, 3072, 64),
                                      (24, 10240, 2048, 64), (31, 40, 2048, 128),
-                                     (32, 10240, 4096, 64), (27, 300, 4096, 128)])
+                                     (32, 10240, 4096, 64), (27, 300, 4096, 128),
+                                     (32, 8192, 2048, 32), (19, 72, 2048, 32)])
 @pytest.mark.parametrize("gelu", [False, True])
 def test_mid_gated_pair(pkg, dev, M, N, K, g, gelu):
     import torch

@@ -28,8 +28,8 @@ def test_mid_m_route_above_16_rows(pkg, M):
     the small-M route does not run (Llama down 15.4 against the GEMM's 23.0,
     T5 wo 14.9 against 26.9).  At K = 4096 it takes over above 24 rows (T5
     q/k/v/o 9.9 against 10.9 at M = 32, 9.9 against 9.6 at M = 24; the T5
-    GeGLU pair 31.5 against 36.7 at M = 32); a gated pair at group size 32 is
-    not built there."""
+    GeGLU pair 31.5 against 36.7 at M = 32); a gated pair at group size 32
+    fits the LDS at K = 2048 only."""
     assert pkg.gemm_route(M, **LLAMA_PAIR) == "mid"
     for N in (5120, 3072, 8192, 64, 33):
         assert pkg.gemm_route(M, N, 3072) == "mid", N
@@ -39,7 +39,7 @@ def test_mid_m_route_above_16_rows(pkg, M):
     assert pkg.gemm_route(M, **T5_WI_PAIR) == ("mid" if M > 24 else "small_m")
     assert pkg.gemm_route(M, 4096, 4096) == ("mid" if M > 24 else "small_m")
     assert pkg.gemm_route(M, 8192, 3072, group_size=32, gated=True) == "small_m"   # LDS
-    assert pkg.gemm_route(M, 8192, 2048, group_size=32, gated=True) == "small_m"
+    assert pkg.gemm_route(M, 8192, 2048, group_size=32, gated=True) == "mid"   # 160 KB
 
 
 @pytest.mark.parametrize("M", [9, 12, 16])
