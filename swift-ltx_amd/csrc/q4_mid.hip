@@ -303,13 +303,13 @@ size_t mid_static_lds(int ng, int wsl, bool pair) {
     return pair ? MidShape<false>::static_lds(ng, wsl) : MidShape<true>::static_lds(ng, wsl);
 }
 
-// (groups, slots) built: the whole K at K = 2048, 3072 (one set at K = 3072
-// also in two slots); two slots at K = 4096 (pairs, one set), 8192, 10240
-// (one set).  At K = 4096 three slots measured slower at M = 32: 32.8 us
-// against 31.6 on the T5 GeGLU pair, 9.90 against 9.61 on T5 q/k/v/o.
+// (groups, slots) built: gated pairs with the whole K at K = 2048, 3072 and
+// in two slots at K = 4096; one set in two slots at K = 2048 .. 10240.  Three
+// slots measured slower at M = 32: 32.8 us against 31.6 on the T5 GeGLU pair,
+// 9.90 against 9.61 on T5 q/k/v/o, 6.65 against 6.51 on Llama q|k|v.
 bool mid_built(bool pair, int ng, int wsl) {
-    if (ng == 2 || ng == 3) return wsl == ng || (!pair && ng == 3 && wsl == 2);
-    return wsl == 2 && (ng == 4 || (!pair && (ng == 8 || ng == 10)));
+    if (pair) return (ng == 2 || ng == 3) ? wsl == ng : ng == 4 && wsl == 2;
+    return wsl == 2 && (ng == 2 || ng == 3 || ng == 4 || ng == 8 || ng == 10);
 }
 
 // Weight-group slots: the whole K (up to 3 groups) when it fits LDS beside
@@ -341,7 +341,6 @@ hipError_t launch_sel(const GemmParams& p, bool pair, int wsl, const dim3& grid,
     switch (ng * 4 + wsl) {
         case 2 * 4 + 2: return launch_cfg<false, true, 2, 2>(p, grid, lds, st);
         case 3 * 4 + 2: return launch_cfg<false, true, 3, 2>(p, grid, lds, st);
-        case 3 * 4 + 3: return launch_cfg<false, true, 3, 3>(p, grid, lds, st);
         case 4 * 4 + 2: return launch_cfg<false, true, 4, 2>(p, grid, lds, st);
         case 8 * 4 + 2: return launch_cfg<false, true, 8, 2>(p, grid, lds, st);
         case 10 * 4 + 2: return launch_cfg<false, true, 10, 2>(p, grid, lds, st);
