@@ -20,10 +20,11 @@
 //    global -> LDS copies in whole 128-byte lines.  One set in 32-row blocks
 //    was measured faster than in 64-row blocks (2 tiles x 4 K-groups) at every
 //    N tried: twice the blocks, half the weight bytes per block.
-//  * Weights: the block's packed rows are copied at the start, in groups of
-//    1024 k (512 contiguous bytes of two rows per wave-wide copy, the
-//    GEMV's pattern: the DRAM pages of a row are read in long runs), so the
-//    whole weight stream is in flight at once, and a round's compute waits
+//  * Weights: the block's packed rows are copied in groups of 1024 k (512
+//    contiguous bytes of two rows per wave-wide copy, the GEMV's pattern:
+//    the DRAM pages of a row are read in long runs) into two LDS slots:
+//    groups 0 and 1 at the start, then the slot of group G - 1 takes group
+//    G + 1 once every wave is past group G - 1.  A round's compute waits
 //    only for its group.  The 16-byte piece c of a row r lands at
 //    c ^ (r & 15) of the row's 512 bytes, so that the fragment reads of 16
 //    rows hit distinct banks.
@@ -76,9 +77,9 @@ struct MidShape {
     static constexpr int NWG = GSLOTS / LTHREADS;     // weight copies per W-copy thread per group
     static_assert(NXC * LTHREADS == XSLOTS && NWG * LTHREADS == GSLOTS, "whole copies");
     static_assert(RPG * RK == 1024 && 2 * KG * RPG == 32, "a group is 512 bytes of a row");
-    // X ring stages: as many as fit beside wsl slots for ng weight groups
-    // (five only for a gated pair holding K = 2048 whole)
-    static constexpr int nsx(int ng, int wsl) { return (!KG8 && ng == 2 && wsl == 2) ? 5 : 3; }
+    // X ring stages: five for a gated pair (two weight slots), three for one
+    // set
+    static constexpr int nsx(int ng, int wsl) { return (!KG8 && wsl == 2) ? 5 : 3; }
     static constexpr size_t static_lds(int ng, int wsl) {
         return (size_t)wsl * GSLOTS * 16 + (size_t)nsx(ng, wsl) * XSLOTS * 16;
     }
@@ -303,12 +304,13 @@ size_t mid_static_lds(int ng, int wsl, bool pair) {
     return pair ? MidShape<false>::static_lds(ng, wsl) : MidShape<true>::static_lds(ng, wsl);
 }
 
-// (groups, slots) built: gated pairs with the whole K at K = 2048, 3072 and
-// in two slots at K = 4096; one set in two slots at K = 2048 .. 10240.  Three
-// slots measured slower at M = 32: 32.8 us against 31.6 on the T5 GeGLU pair,
-// 9.90 against 9.61 on T5 q/k/v/o, 6.65 against 6.51 on Llama q|k|v.
+// (groups, slots) built: two slots, gated pairs at K = 2048, 3072, 4096 (with
+// five X stages), one set at K = 2048 .. 10240.  At M = 32 three slots
+// measured slower: 32.8 us against 31.6 on the T5 GeGLU pair, 9.90 against
+// 9.61 on T5 q/k/v/o, 6.65 against 6.51 on Llama q|k|v; the Llama gate/up
+// pair with the whole K in three slots and three X stages 11.6 against 11.0.
 bool mid_built(bool pair, int ng, int wsl) {
-    if (pair) return (ng == 2 || ng == 3) ? wsl == ng : ng == 4 && wsl == 2;
+    if (pair) return (ng == 2 || ng == 3 || ng == 4) && wsl == 2;
     return wsl == 2 && (ng == 2 || ng == 3 || ng == 4 || ng == 8 || ng == 10);
 }
 
@@ -334,7 +336,7 @@ hipError_t launch_sel(const GemmParams& p, bool pair, int wsl, const dim3& grid,
     const int ng = p.K / 1024;
     if (pair) {
         if (ng == 2) return launch_cfg<true, false, 2, 2>(p, grid, lds, st);
-        if (ng == 3) return launch_cfg<true, false, 3, 3>(p, grid, lds, st);
+        if (ng == 3) return launch_cfg<true, false, 3, 2>(p, grid, lds, st);
         if (ng == 4 && wsl == 2) return launch_cfg<true, false, 4, 2>(p, grid, lds, st);
         return hipErrorInvalidValue;
     }
