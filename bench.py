@@ -28,11 +28,12 @@ roofline   = the dominant kernel (fused gate/up GEMV, 28.33 MB per launch):
              per launch.  `--summarize-trace` computes the same statistic from
              a kernel trace (the median over replays of the replay's mean
              kernel duration).  measured_ceiling: a read-only stream
-             (sltx_hbm_read) and a device copy, same replay method.
+             (csrc/bench/hbm_read.hip, in lib/libswiftltx_bench.so) and a
+             device copy, same replay method.
 extra      = the other BASELINE configs and the paths around the GEMV, each
              by the same replay method: config 1 (q_proj GEMV over >= 2 GB of
              rotated copies), config 4a (lm_head GEMV over 10 rotated copies,
-             2.2 GB), the fused-norm and single-launch decode layers, the
+             2.2 GB), the fused-norm decode layer, the
              decode token (greedy / sampled), the 750-token prefill, token
              selection, small M (2..128) and the M > 1 MFMA GEMMs (configs 3,
              4b, 5) against the 2.5 PFLOP/s dense fp16/bf16 peak.
@@ -95,10 +96,6 @@ def parse():
     ap.add_argument("--gemm-pmc", action="store_true",
                     help="only: 10 launches each of the M=750 prefill gate/up (SiLU) and down "
                          "GEMMs, for rocprofv3 --pmc MFMA-utilisation runs")
-    ap.add_argument("--ceilings", action="store_true",
-                    help="only: the probes of what bounds the kernels -- launch floor, "
-                         "register-only MFMA rate and clock, grid hand-off cost by block count, "
-                         "GEMV marginal rate, hipBLASLt dense fp16 at the M=750 shapes")
     ap.add_argument("--token-select", action="store_true",
                     help="only: the token-selection leg (graphs), then TRACE_CALLS eager calls of "
                          "each sampling case, for rocprofv3 --kernel-trace; with "
@@ -253,9 +250,6 @@ def main():
     if args.gemm_pmc:
         gemm_pmc_run(pkg, torch, gen, dev)
         return
-    if args.ceilings:
-        ceilings_run(pkg, torch, gen, dev)
-        return
     if args.small_m:
         print(json.dumps(small_m_legs(pkg, torch, gen, dev, torch.cuda.Stream())), flush=True)
         return
@@ -288,9 +282,9 @@ def main():
                       out=outs["down_proj"])
 
     # The library's per-device state is set up by a call that is not a step
-    # (a 16-byte read), so that no step runs outside the warm-up and the timed
+    # (sltx_init), so that no step runs outside the warm-up and the timed
     # region.  Steps 0..W-1 are the warm-up graph, W..W+K-1 the timed graph.
-    pkg.hbm_read(torch.zeros(4, device=dev, dtype=torch.int32))
+    pkg.check(pkg.lib().sltx_init())
     torch.cuda.synchronize()
 
     def graph_of(first, n):
@@ -343,8 +337,6 @@ def main():
     legs["config1_q_proj_gemv_m1"] = config1_leg(pkg, torch, gen, dev, cap)
     legs["lm_head_gemv_m1_cold"] = lm_head_cold_leg(pkg, torch, gen, dev, cap)
     legs["decode_layer_fused_norms"] = fused_layer_leg(pkg, torch, gen, dev, layers, cap)
-    legs["decode_layer_single_launch"] = single_launch_layer_leg(pkg, torch, gen, dev, layers,
-                                                                 cap)
     model = synthetic_llama(pkg, torch, gen, dev, layers)
     legs["decode_token_greedy"] = decode_token_leg(pkg, torch, gen, dev, model)
     legs["prefill_750"] = prefill_leg(pkg, torch, gen, dev, model)
@@ -403,18 +395,51 @@ def main():
 
 # ------------------------------------------------------------ ceilings ---
 
+_BENCH_LIB = None
+
+
+def bench_lib():
+    """lib/libswiftltx_bench.so: measurement kernels built beside the product
+    library (swift-ltx_amd/csrc/bench/) and loaded only here."""
+    global _BENCH_LIB
+    if _BENCH_LIB is None:
+        import ctypes
+        path = os.path.join(REPO, "swift-ltx_amd", "lib", "libswiftltx_bench.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is missing: run python swift-ltx_amd/build.py")
+        L = ctypes.CDLL(path)
+        L.sltx_bench_hbm_read_blocks.argtypes = []
+        L.sltx_bench_hbm_read_blocks.restype = ctypes.c_int
+        L.sltx_bench_hbm_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p,
+                                          ctypes.c_int32, ctypes.c_void_p]
+        L.sltx_bench_hbm_read.restype = ctypes.c_int
+        _BENCH_LIB = L
+    return _BENCH_LIB
+
+
+def hbm_read(torch, src, sink, lds=False):
+    """Streams the bytes of device tensor src (contiguous, a multiple of 16)
+    through the GPU's loads into registers (or, lds, through direct global ->
+    LDS copies); sink: int32 [bench_lib().sltx_bench_hbm_read_blocks()]."""
+    rc = bench_lib().sltx_bench_hbm_read(src.data_ptr(), src.numel() * src.element_size(),
+                                         sink.data_ptr(), 1 if lds else 0,
+                                         torch.cuda.current_stream().cuda_stream)
+    if rc != 0:
+        raise RuntimeError(f"sltx_bench_hbm_read failed: {rc}")
+
+
 def hbm_ceilings(pkg, torch, dev, cap, read_gib=4, copy_gib=1):
-    """Measured HBM ceilings: a read-only stream of read_gib GiB
-    (sltx_hbm_read: 16-byte nontemporal loads over the whole GPU, XOR-reduced),
-    the same stream through direct global -> LDS copies (sltx_hbm_read_lds)
-    and a device copy of copy_gib GiB (torch copy_, bytes read + written)."""
+    """Measured HBM ceilings: a read-only stream of read_gib GiB (16-byte
+    nontemporal loads over the whole GPU, XOR-reduced; csrc/bench/hbm_read.hip),
+    the same stream through direct global -> LDS copies, and a device copy of
+    copy_gib GiB (torch copy_, bytes read + written)."""
     src = torch.empty(read_gib * 2 ** 30 // 4, device=dev, dtype=torch.int32)
     src.random_()
-    sink = torch.empty(pkg.lib().sltx_hbm_read_blocks(), device=dev, dtype=torch.int32)
-    g = capture(torch, lambda: pkg.hbm_read(src, sink), cap)
+    sink = torch.empty(bench_lib().sltx_bench_hbm_read_blocks(), device=dev, dtype=torch.int32)
+    g = capture(torch, lambda: hbm_read(torch, src, sink), cap)
     rd = rate(replay_stats(torch, g.replay, 1), nbytes=src.numel() * 4)
     del g
-    g = capture(torch, lambda: pkg.hbm_read(src, sink, lds=True), cap)
+    g = capture(torch, lambda: hbm_read(torch, src, sink, lds=True), cap)
     rl = rate(replay_stats(torch, g.replay, 1), nbytes=src.numel() * 4)
     del g, src
     n = copy_gib * 2 ** 30 // 2
@@ -425,9 +450,9 @@ def hbm_ceilings(pkg, torch, dev, cap, read_gib=4, copy_gib=1):
     del g, a, b
     torch.cuda.empty_cache()
     return {"read_gbs": rd["gbs"], "read_frac_of_peak": rd["frac_hbm"],
-            "read_what": f"sltx_hbm_read of {read_gib} GiB, median of {rd['replays']} replays",
+            "read_what": f"register read of {read_gib} GiB, median of {rd['replays']} replays",
             "read_lds_gbs": rl["gbs"],
-            "read_lds_what": f"sltx_hbm_read_lds (direct global -> LDS copies) of {read_gib} GiB, "
+            "read_lds_what": f"direct global -> LDS copies of {read_gib} GiB, "
                              f"median of {rl['replays']} replays",
             "copy_gbs": cp["gbs"],
             "copy_what": f"{copy_gib} GiB device copy (read + written), median of "
@@ -503,39 +528,6 @@ def fused_layer_leg(pkg, torch, gen, dev, layers, cap):
     st.update({"launches_per_layer": 4,
                "note": "rms_norm, residual add + rms_norm and the final residual add run inside "
                        "the projections' kernels"})
-    return st
-
-
-def single_launch_layer_leg(pkg, torch, gen, dev, layers, cap):
-    """The same fused layer as one launch (sltx_decode_layer_q4): o_proj,
-    residual + rms_norm, gate/up + SiLU x up, down + residual, then the next
-    layer's rms_norm + q|k|v (layer i's o/gate/up/down with layer i+1's q|k|v:
-    the same weights per layer as the 4-launch form).  Rotated over the copies."""
-    K = 3072
-    n1 = (1.0 + 0.1 * torch.randn(K, generator=gen, device=dev)).float()
-    n2 = (1.0 + 0.1 * torch.randn(K, generator=gen, device=dev)).float()
-    h = (0.1 * torch.randn(1, K, generator=gen, device=dev)).half()
-    attn = (0.1 * torch.randn(1, K, generator=gen, device=dev)).half()
-    res = torch.empty(1, K, device=dev, dtype=torch.float16)
-    qkv = torch.empty(1, 5120, device=dev, dtype=torch.float16)
-    n = len(layers)
-
-    def call(i):
-        w, wn = layers[i].w, layers[(i + 1) % n].w
-        pkg.decode_layer(attn, h, w["o_proj"][0], n2, w["gate_up_proj"][0],
-                         w["gate_up_proj"][1], w["down_proj"][0], 1e-5, next_norm=n1,
-                         next_qkv=wn["qkv_proj"][0], residual_out=res, next_qkv_out=qkv,
-                         stream=cap)
-
-    g = capture(torch, lambda: [call(i) for i in range(n)], cap, warm=lambda: call(0))
-    nbytes = LAYER_BYTES + 2 * K * 4 + 5 * 2 * K
-    st = rate(replay_stats(torch, g.replay, n), nbytes=nbytes)
-    del g
-    faults = pkg.decode_layer_faults(cap)
-    st.update({"launches_per_layer": 1, "bounded_wait_faults": faults,
-               "note": "phases hand over through tagged words in device memory; slower than the "
-                       "4-launch form on this GPU (the hand-off under full HBM load costs more "
-                       "than a launch)"})
     return st
 
 
@@ -632,125 +624,7 @@ def prefill_leg(pkg, torch, gen, dev, mw, S=750):
     return st
 
 
-# ------------------------------------------------------------ ceilings ---
-
-def _event_us(torch, fn, reps=7):
-    """Median over reps of one eager call's event-timed duration (us)."""
-    import numpy as np
-    out = []
-    for _ in range(reps):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        fn()
-        e1.record()
-        torch.cuda.synchronize()
-        out.append(e0.elapsed_time(e1) * 1e3)
-    return float(np.median(out))
-
-
-def ceilings_run(pkg, torch, gen, dev):
-    """The probes behind the bounds the kernels are judged against; prints
-    one JSON object per probe (also read by rocprofv3 --kernel-trace runs)."""
-    import numpy as np
-    import torch.nn.functional as F
-
-    def emit(name, obj):
-        print(json.dumps({"probe": name, **obj}), flush=True)
-
-    # launch floor: a graph of 200 dependent empty launches
-    s = torch.cuda.Stream()
-    g = capture(torch, lambda: [pkg.probe_empty(stream=s) for _ in range(200)], s,
-                warm=lambda: pkg.probe_empty(stream=s))
-    with torch.cuda.stream(s):
-        st = replay_stats(torch, g.replay, 200)
-    emit("launch_floor", {"us_per_launch": st, "launches_per_graph": 200})
-    del g
-
-    # register-only MFMA rate and clock: 1 and 2 waves per SIMD
-    ab = torch.randn(256, 8, generator=gen, device=dev).half()
-    kcu = 256
-    for blocks in (kcu, 2 * kcu):
-        iters = 40000
-        sink = torch.empty(blocks * 256, device=dev)
-        clocks = torch.zeros(blocks, 2, dtype=torch.int64, device=dev)
-        pkg.probe_mfma(ab, blocks, 100, sink, clocks)
-        us = _event_us(torch, lambda: pkg.probe_mfma(ab, blocks, iters, sink, clocks), reps=5)
-        c = clocks.cpu().numpy().astype(np.float64)
-        mhz = np.median(c[:, 0] / np.maximum(c[:, 1], 1)) * 100.0
-        flops = blocks * 4 * iters * 4 * 2 * 32 * 32 * 16
-        emit("mfma_register_only", {"blocks": blocks, "waves_per_simd": blocks * 4 // (4 * kcu),
-                                    "iters": iters, "us": round(us, 1),
-                                    "tflops": round(flops / (us * 1e-6) / 1e12, 1),
-                                    "frac_of_2500": round(flops / (us * 1e-6) / 1e12 / 2500, 4),
-                                    "shader_clock_mhz": round(float(mhz), 1)})
-
-    # grid-wide hand-off inside one launch, by block count
-    faults = torch.zeros(1, dtype=torch.int32, device=dev)
-    R = 200
-    for mode, mname in ((0, "one counter"), (1, "per-XCD counters"), (2, "tagged words"),
-                        (3, "per-XCD counters + 16 data words a block")):
-        for fence in ((0, 1) if mode < 3 else (0,)):
-            rows = []
-            for blocks in (8, 32, 64, 128, 256, 512, 1024):
-                sync = torch.zeros(pkg.probe_sync_words(blocks), dtype=torch.int32, device=dev)
-
-                def one(rounds):
-                    sync.zero_()   # a fresh buffer every launch (both sides of the difference)
-                    pkg.probe_sync(mode, fence, blocks, rounds, sync, faults)
-
-                def run(rounds):
-                    return _event_us(torch, lambda: one(rounds), reps=5)
-                try:
-                    t0, t1 = run(0), run(R)
-                except pkg.SltxError as e:
-                    rows.append({"blocks": blocks, "error": str(e)})
-                    continue
-                rows.append({"blocks": blocks, "us_per_barrier": round((t1 - t0) / R, 3)})
-            emit("grid_handoff", {"mode": mname, "fence": bool(fence), "rounds": R,
-                                  "by_blocks": rows,
-                                  "faults": int(faults.item())})
-            faults.zero_()
-
-    # GEMV marginal rate: M = 1, K = 3072, cold weights (rotated over >= 2 GB)
-    pts = []
-    for N in (3072, 8192, 16384, 32768, 65536, 131072):
-        nb = gemv_bytes(N, 3072)
-        copies = max(2, min(800, -(-2 * 2 ** 30 // nb)))
-        ws = [q4(pkg, torch, N, 3072, gen, dev) for _ in range(copies)]
-        x = torch.randn(1, 3072, generator=gen, device=dev).half()
-        y = torch.empty(1, N, device=dev, dtype=torch.float16)
-        cap = torch.cuda.Stream()
-        gr = capture(torch, lambda: [pkg.matmul_q4(x, *_wsb(w), 1, 3072, N, G, out=y,
-                                                   stream=cap) for w in ws], cap)
-        with torch.cuda.stream(cap):
-            st = replay_stats(torch, gr.replay, copies)
-        pts.append((nb, st["median_us"]))
-        emit("gemv_size", {"N": N, "K": 3072, "bytes": nb, "copies": copies, "us": st})
-        del gr, ws
-        torch.cuda.empty_cache()
-    b = np.array([p[0] for p in pts], dtype=np.float64)
-    t = np.array([p[1] for p in pts], dtype=np.float64)
-    big = b >= gemv_bytes(16384, 3072)
-    slope, icpt = np.polyfit(b[big], t[big], 1)
-    emit("gemv_marginal", {"fit_over_bytes": [int(v) for v in b[big]],
-                           "marginal_gbs": round(1e-3 / slope, 1),
-                           "frac_of_8000": round(1e-3 / slope / HBM_PEAK_GBS, 4),
-                           "fixed_us": round(float(icpt), 2)})
-
-    # hipBLASLt through torch: dense fp16 at the M = 750 shapes and 4096^3
-    for name, M, K, N in (("gate_up_m750_dense", 750, 3072, 16384),
-                          ("down_m750_dense", 750, 8192, 3072),
-                          ("square_4096", 4096, 4096, 4096)):
-        xa = torch.randn(M, K, generator=gen, device=dev).half()
-        wb = torch.randn(N, K, generator=gen, device=dev).half()
-        out = torch.empty(M, N, device=dev, dtype=torch.float16)
-        cap = torch.cuda.Stream()
-        gr = capture(torch, lambda: [torch.matmul(xa, wb.t(), out=out) for _ in range(10)], cap)
-        with torch.cuda.stream(cap):
-            st = rate(replay_stats(torch, gr.replay, 10), flops=2 * M * N * K)
-        emit("hipblaslt_fp16", {"shape": name, "M": M, "K": K, "N": N, "us": st})
-        del gr
-
+# ------------------------------------------------------- token selection ---
 
 SAMPLE_CASES = ("sample_top_p", "sample_top_p_flat", "sample_top_p_two_levels",
                 "sample_top_p_near_flat", "sample_top_p_two_clusters")

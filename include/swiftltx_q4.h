@@ -247,54 +247,6 @@ int sltx_matmul_q4_residual_rms_norm(const void* x, const sltx_q4_weight* w, con
                                      int32_t sum_rounded, void* residual_out, void* norm_out,
                                      void* stream);
 
-/* One decode layer after attention, in a single launch: the four dependent
- * projections of transformerBlock that follow attention and the next layer's
- * input norm + q|k|v (LlamaModel.swift:324-331, then :288-292 of the next
- * layer), which the reference encodes as separate dispatches into one command
- * buffer (MetalContext.swift:109-134):
- *   o            = half(attn . Wo^T)
- *   h1           = half(residual + o)
- *   act          = half(silu(n . Wg^T) * (n . Wu^T)),  n = rms_norm(h1; post_norm)
- *                  with the sum of squares over the unrounded residual + o
- *                  (residualRmsNorm, Kernels.swift:238-290)
- *   residual_out = half(h1 + half(act . Wd^T))
- *   next_qkv_out = half(rms_norm(residual_out; next_norm) . Wqkv^T)  (if next_qkv)
- * The same values as sltx_matmul_q4, sltx_residual_rmsnorm_matmul_q4_silu_mul,
- * sltx_matmul_q4_residual and sltx_rmsnorm_matmul_q4 called in sequence, up
- * to the order of the sums of squares.  Pass next_qkv = NULL for the last
- * layer.  o_proj is [hidden, hidden] (K = hidden: the attention width must
- * equal hidden), gate/up [ffn, hidden], down [hidden, ffn], next_qkv
- * [next_qkv_rows, hidden]; one group_size for all.  Built for hidden 3072 /
- * ffn 8192 (Llama-3.2-3B) and 2048 / 8192 (Llama-3.2-1B) with up to 8192
- * q|k|v rows on a 256-CU MI355X; other shapes return SLTX_ERR_UNSUPPORTED
- * (use the per-projection entry points), as do group sizes whose scales
- * take more than 128 halves per row-iteration (group 32 at hidden 3072).
- * attn, residual, residual_out, post_norm and next_norm 16-byte aligned;
- * every weight's scales and biases 8-byte aligned.  The outputs may overlap attn or
- * residual (every block has read its inputs before any output is written)
- * but not each other.  One block per CU must be resident at once: the launch
- * is refused when the occupancy does not allow it, and work running
- * concurrently on other streams can delay blocks past the kernel's bounded
- * waits (then the results are wrong and sltx_decode_layer_faults reports it).
- * Uses a per-stream sync area (about 4 * (2 hidden + ffn) bytes, zeroed when
- * allocated, freed by sltx_release_workspace): under graph capture call it
- * once eagerly on that stream first.  Calls sharing a stream's sync area are
- * ordered by the stream; a graph replayed on another stream must not overlap
- * them.  No single reference entry point: it replaces the sequence named
- * above. */
-int sltx_decode_layer_q4(const void* attn, const void* residual, const sltx_q4_weight* o_proj,
-                         const float* post_norm, const sltx_q4_weight* gate,
-                         const sltx_q4_weight* up, const sltx_q4_weight* down,
-                         const float* next_norm, const sltx_q4_weight* next_qkv,
-                         int32_t next_qkv_rows, int32_t hidden, int32_t ffn, float eps,
-                         void* residual_out, void* next_qkv_out, void* stream);
-
-/* Waits of sltx_decode_layer_q4 calls on `stream` that gave up since the last
- * query (0 when every call's blocks were co-resident), read after the
- * stream's queued work and reset.  Not under capture.  No counterpart in the
- * reference. */
-int sltx_decode_layer_faults(void* stream, int32_t* faults);
-
 /* ---- Token selection after the lm_head (LlamaModel.swift:153,161) ----
  * Both read n logits (SLTX_F16 or SLTX_F32, device) and write one int32 token
  * id to device memory, so the next step's embedding gather can consume it
@@ -365,37 +317,6 @@ int sltx_sample_top_p_state(const void* logits, int32_t dtype, int32_t n, float 
                             float top_p, float repetition_penalty,
                             const sltx_sample_state* state, int32_t* out_index, void* stream);
 
-/* ---- Measurement ----
- * The HBM read ceiling the weight streams are judged against: reads `bytes`
- * (a multiple of 16) from src with 16-byte loads over the whole GPU and
- * writes, per block, the XOR of the 32-bit words it read to sink (which holds
- * sltx_hbm_read_blocks() words), so the reads cannot be elided and can be
- * checked.  No counterpart in the reference. */
-int sltx_hbm_read_blocks(void);
-int sltx_hbm_read(const void* src, uint64_t bytes, uint32_t* sink, void* stream);
-/* The same read through direct global -> LDS copies (16 bytes a lane, each
- * read back from LDS and XOR-ed): the rate at which a kernel can stream from
- * HBM into LDS.  Same arguments and sink.  No counterpart in the reference. */
-int sltx_hbm_read_lds(const void* src, uint64_t bytes, uint32_t* sink, void* stream);
-
-/* Probes of what bounds the kernels (no counterpart in the reference):
- * - sltx_probe_empty: one launch of an empty one-wave kernel (the launch
- *   floor, timed in a graph of many);
- * - sltx_probe_mfma: `blocks` blocks of 256 threads, each wave running
- *   `iters` x 4 independent v_mfma_f32_32x32x16_f16 on register operands
- *   taken from ab (256 x 16 bytes, 16-byte aligned); sink gets 256 floats a
- *   block (the sums, so nothing is elided), clocks 2 words a block: shader
- *   clock cycles and 100 MHz wall ticks of the loop;
- * - sltx_probe_sync: `rounds` grid-wide barriers among `blocks` one-wave
- *   blocks (at most what the device holds at once: SLTX_ERR_INVALID
- *   beyond), arrival by mode 0 one agent-scope counter, 1 per-XCD counters
- *   then one global counter, 2 tagged words polled by every block, 3 as 1
- *   after storing 16 data words a block (agent scope, completion awaited),
- *   which every block reads back after the wait; `fence`
- *   adds agent-scope release / acquire fences around each.  sync holds
- *   sltx_probe_sync_words(blocks) zeroed words (64-byte aligned); a wait
- *   that runs out of polls adds one to *faults and the kernel finishes. */
-int sltx_probe_empty(void* stream);
 /* Route query (no counterpart in the reference; for tests and tuning): the
  * kernel family sltx_matmul_q4_fast[_f32], sltx_matmul_q4_ex, the gated pair
  * entry points at M > 1 and sltx_matmul_q4_residual at M > 1 run for this
@@ -406,15 +327,10 @@ typedef enum {
     SLTX_ROUTE_GEMM = 0,     /* MFMA GEMM, split over K when its tiles would not fill the GPU */
     SLTX_ROUTE_SMALL_M = 1,  /* small-M weight stream (M <= 32, 16x16x32 MFMA) */
     SLTX_ROUTE_NARROW = 2,   /* narrow weight stream (one weight set, M <= 4, 4x4x4 MFMA) */
-    SLTX_ROUTE_MID = 3       /* pipelined weight stream (16 < M <= 32, X and W through LDS, 32x32x16 MFMA) */
+    SLTX_ROUTE_MID = 3       /* pipelined weight stream (8 < M <= 32, X and W through LDS, 32x32x16 MFMA) */
 } sltx_route;
 int sltx_gemm_route(int32_t M, int32_t N, int32_t K, int32_t group_size, int32_t gated,
                     int32_t x_dtype);
-int sltx_probe_mfma(const void* ab, int32_t blocks, int32_t iters, float* sink, uint64_t* clocks,
-                    void* stream);
-int sltx_probe_sync_words(int32_t blocks);
-int sltx_probe_sync(int32_t mode, int32_t fence, int32_t blocks, int32_t rounds, uint32_t* sync,
-                    int32_t* faults, void* stream);
 
 /* ---- safetensors weights (SafeTensorsFile, SafeTensors.swift:41-118) ----
  * Reads the files swift-ltx's loader reads (ModelWeights.swift:40-154) into

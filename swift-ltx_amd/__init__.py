@@ -60,15 +60,6 @@ EXPORTED = (
     "sltx_residual_rmsnorm_matmul_q4_silu_mul",
     "sltx_matmul_q4_residual",
     "sltx_matmul_q4_residual_rms_norm",
-    "sltx_decode_layer_q4",
-    "sltx_decode_layer_faults",
-    "sltx_hbm_read_blocks",
-    "sltx_hbm_read",
-    "sltx_hbm_read_lds",
-    "sltx_probe_empty",
-    "sltx_probe_mfma",
-    "sltx_probe_sync_words",
-    "sltx_probe_sync",
     "sltx_gemm_route",
     "sltx_argmax",
     "sltx_sample_top_p",
@@ -163,26 +154,8 @@ def lib():
         L.sltx_residual_rmsnorm_matmul_q4_silu_mul.argtypes = [P, P, P, F, P, W, W, P, I32, P]
         L.sltx_matmul_q4_residual.argtypes = [P, W, P, P, I32, I32, P]
         L.sltx_matmul_q4_residual_rms_norm.argtypes = [P, W, P, P, F, I32, I32, I32, P, P, P]
-        L.sltx_decode_layer_q4.argtypes = [P, P, W, P, W, W, W, P, W, I32, I32, I32, F, P, P, P]
-        L.sltx_decode_layer_q4.restype = ctypes.c_int
-        L.sltx_decode_layer_faults.argtypes = [P, P]
-        L.sltx_decode_layer_faults.restype = ctypes.c_int
-        L.sltx_hbm_read_blocks.argtypes = []
-        L.sltx_hbm_read_blocks.restype = ctypes.c_int
-        L.sltx_hbm_read.argtypes = [P, ctypes.c_uint64, P, P]
-        L.sltx_hbm_read.restype = ctypes.c_int
-        L.sltx_hbm_read_lds.argtypes = [P, ctypes.c_uint64, P, P]
-        L.sltx_hbm_read_lds.restype = ctypes.c_int
-        L.sltx_probe_empty.argtypes = [P]
-        L.sltx_probe_empty.restype = ctypes.c_int
-        L.sltx_probe_mfma.argtypes = [P, I32, I32, P, P, P]
-        L.sltx_probe_mfma.restype = ctypes.c_int
         L.sltx_gemm_route.argtypes = [I32, I32, I32, I32, I32, I32]
         L.sltx_gemm_route.restype = ctypes.c_int
-        L.sltx_probe_sync_words.argtypes = [I32]
-        L.sltx_probe_sync_words.restype = ctypes.c_int
-        L.sltx_probe_sync.argtypes = [I32, I32, I32, I32, P, P, P]
-        L.sltx_probe_sync.restype = ctypes.c_int
         L.sltx_argmax.argtypes = [P, I32, I32, P, P]
         L.sltx_sample_top_p.argtypes = [P, I32, I32, F, F, F, P, I32, F, P, P]
         L.sltx_sample_top_p_noalloc.argtypes = [P, I32, I32, F, F, F, P, I32, F, P, P]
@@ -537,81 +510,6 @@ def matmul_q4_residual_rms_norm(x, w: Q4Weight, residual, norm_weight, eps, M, N
     return residual_out, norm_out
 
 
-def decode_layer(attn, residual, o_proj: Q4Weight, post_norm, gate: Q4Weight, up: Q4Weight,
-                 down: Q4Weight, eps, next_norm=None, next_qkv: Q4Weight | None = None,
-                 residual_out=None, next_qkv_out=None, stream=None):
-    """One decode layer after attention in a single launch (sltx_decode_layer_q4):
-    o_proj, residual + rms_norm, gate/up + SiLU x up, down + residual, and with
-    next_qkv the next layer's rms_norm + q|k|v (LlamaModel.swift:324-331,
-    :288-292) -> (residual_out [1, hidden], next_qkv_out [1, rows] or None)."""
-    torch = _torch()
-    H, F = int(gate.K), int(gate.N)
-    residual_out = _new((1, H), torch.float16, residual) if residual_out is None else residual_out
-    nq = 0
-    if next_qkv is not None:
-        nq = next_qkv.N
-        next_qkv_out = _new((1, nq), torch.float16, residual) if next_qkv_out is None else next_qkv_out
-    if _shape_ok(H, gate.group_size) and _shape_ok(F, down.group_size):
-        for t, n in ((attn, "attn"), (residual, "residual"), (residual_out, "residual_out")):
-            _need(t, n, H, _f16())
-        _need(post_norm, "post_norm", H, (torch.float32,))
-        _need_w(o_proj, H, what="o_proj")
-        _need_w(gate, F, what="gate")
-        _need_w(up, F, what="up")
-        _need_w(down, H, what="down")
-        if next_qkv is not None:
-            _need(next_norm, "next_norm", H, (torch.float32,))
-            _need_w(next_qkv, nq, what="next_qkv")
-            _need(next_qkv_out, "next_qkv_out", nq, _f16())
-    co, cg, cu, cd = o_proj.c(), gate.c(), up.c(), down.c()
-    cq = next_qkv.c() if next_qkv is not None else None
-    check(lib().sltx_decode_layer_q4(
-        _ptr(attn), _ptr(residual), ctypes.byref(co), _ptr(post_norm), ctypes.byref(cg),
-        ctypes.byref(cu), ctypes.byref(cd), _ptr(next_norm) if cq else None,
-        ctypes.byref(cq) if cq else None, nq, H, F, eps, _ptr(residual_out),
-        _ptr(next_qkv_out) if cq else None, _stream(stream)))
-    return residual_out, (next_qkv_out if cq else None)
-
-
-def decode_layer_faults(stream=None) -> int:
-    """Bounded waits of decode_layer calls on `stream` that gave up since the
-    last query (0 when all blocks were co-resident); waits for the stream."""
-    n = ctypes.c_int32(0)
-    check(lib().sltx_decode_layer_faults(_stream(stream), ctypes.byref(n)))
-    return int(n.value)
-
-
-def hbm_read(src, sink=None, stream=None, lds=False):
-    """Streams the bytes of device tensor `src` (contiguous, size a multiple of
-    16) through the GPU's loads (lds: through direct global -> LDS copies,
-    sltx_hbm_read_lds); returns the per-block XOR words (int32 device tensor
-    of sltx_hbm_read_blocks() entries)."""
-    torch = _torch()
-    if sink is None:
-        sink = torch.empty(lib().sltx_hbm_read_blocks(), dtype=torch.int32, device=src.device)
-    _need(src, "src", src.numel())
-    _need(sink, "sink", lib().sltx_hbm_read_blocks(), (torch.int32,))
-    fn = lib().sltx_hbm_read_lds if lds else lib().sltx_hbm_read
-    check(fn(_ptr(src), src.numel() * src.element_size(), _ptr(sink), _stream(stream)))
-    return sink
-
-
-def probe_empty(stream=None):
-    """One launch of an empty kernel (sltx_probe_empty)."""
-    check(lib().sltx_probe_empty(_stream(stream)))
-
-
-def probe_mfma(ab, blocks, iters, sink, clocks, stream=None):
-    """Register-only MFMA loop (sltx_probe_mfma): ab fp16 [256, 8], sink
-    float32 [blocks * 256], clocks int64 [blocks, 2]."""
-    torch = _torch()
-    _need(ab, "ab", 256 * 8, (torch.float16,))
-    _need(sink, "sink", blocks * 256, (torch.float32,))
-    _need(clocks, "clocks", blocks * 2, (torch.int64,))
-    check(lib().sltx_probe_mfma(_ptr(ab), blocks, iters, _ptr(sink), _ptr(clocks),
-                                _stream(stream)))
-
-
 ROUTES = {0: "gemm", 1: "small_m", 2: "narrow", 3: "mid"}
 
 
@@ -623,20 +521,6 @@ def gemm_route(M, N, K, group_size=64, gated=False, x_dtype=None):
     if rc < 0:
         check(rc)
     return ROUTES[rc]
-
-
-def probe_sync_words(blocks):
-    return int(lib().sltx_probe_sync_words(blocks))
-
-
-def probe_sync(mode, fence, blocks, rounds, sync, faults, stream=None):
-    """rounds grid barriers among `blocks` one-wave blocks (sltx_probe_sync);
-    sync: zeroed int32 [probe_sync_words(blocks)], faults: int32 [1]."""
-    torch = _torch()
-    _need(sync, "sync", probe_sync_words(blocks), (torch.int32,))
-    _need(faults, "faults", 1, (torch.int32,))
-    check(lib().sltx_probe_sync(mode, fence, blocks, rounds, _ptr(sync), _ptr(faults),
-                                _stream(stream)))
 
 
 def matmul_q4_geglu(x, gate: Q4Weight, up: Q4Weight, M, K, N, out=None, stream=None):

@@ -1,9 +1,12 @@
-"""Build the gfx950 shared library libswiftltx_q4.so in-tree with hipcc.
+"""Build the gfx950 shared libraries in-tree with hipcc.
 
     python swift-ltx_amd/build.py            # rebuild every object
     python swift-ltx_amd/build.py --if-stale # only when a source is newer
 
-Objects go to swift-ltx_amd/_build/, the library to swift-ltx_amd/lib/.
+csrc/*.hip -> lib/libswiftltx_q4.so, the drop-in library (include/swiftltx_q4.h).
+csrc/bench/*.hip -> lib/libswiftltx_bench.so, measurement kernels that only
+bench.py loads (the HBM read ceiling); not part of the C ABI.
+Objects go to swift-ltx_amd/_build/, the libraries to swift-ltx_amd/lib/.
 Every HIP file is compiled for gfx950 only, with packed-fp32 instruction
 selection disabled (hipcc's host pass warns that it does not know the
 feature; that warning is expected).
@@ -22,6 +25,7 @@ CSRC = os.path.join(PKG, "csrc")
 OBJ_DIR = os.path.join(PKG, "_build")
 LIB_DIR = os.path.join(PKG, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libswiftltx_q4.so")
+BENCH_LIB_PATH = os.path.join(LIB_DIR, "libswiftltx_bench.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 DEVICE_FLAGS = [
@@ -38,20 +42,26 @@ def sources() -> list[str]:
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
 
 
+def bench_sources() -> list[str]:
+    return sorted(glob.glob(os.path.join(CSRC, "bench", "*.hip")))
+
+
 def headers() -> list[str]:
     return (sorted(glob.glob(os.path.join(CSRC, "*.hpp")))
             + sorted(glob.glob(os.path.join(REPO, "include", "*.h"))))
 
 
 def is_stale() -> bool:
-    if not os.path.exists(LIB_PATH):
+    if not os.path.exists(LIB_PATH) or not os.path.exists(BENCH_LIB_PATH):
         return True
-    t = os.path.getmtime(LIB_PATH)
-    return any(os.path.getmtime(f) > t for f in sources() + headers() + [__file__])
+    t = min(os.path.getmtime(LIB_PATH), os.path.getmtime(BENCH_LIB_PATH))
+    return any(os.path.getmtime(f) > t
+               for f in sources() + bench_sources() + headers() + [__file__])
 
 
 def _compile(src: str) -> str:
-    obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
+    sub = "bench_" if os.path.basename(os.path.dirname(src)) == "bench" else ""
+    obj = os.path.join(OBJ_DIR, sub + os.path.basename(src) + ".o")
     cmd = [HIPCC, *DEVICE_FLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
@@ -63,20 +73,27 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(force: bool = True, jobs: int = 8) -> str:
-    """Compile every csrc/*.hip for gfx950 and link LIB_PATH; returns its path."""
-    if not force and not is_stale():
-        return LIB_PATH
-    os.makedirs(OBJ_DIR, exist_ok=True)
-    os.makedirs(LIB_DIR, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        objs = list(ex.map(_compile, sources()))
-    tmp = LIB_PATH + ".tmp%d" % os.getpid()
+def _link(objs: list[str], path: str) -> None:
+    tmp = path + ".tmp%d" % os.getpid()
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stderr)
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, path)
+
+
+def build(force: bool = True, jobs: int = 8) -> str:
+    """Compile every csrc/*.hip (and csrc/bench/*.hip) for gfx950, link
+    LIB_PATH and BENCH_LIB_PATH; returns LIB_PATH."""
+    if not force and not is_stale():
+        return LIB_PATH
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    os.makedirs(LIB_DIR, exist_ok=True)
+    main, bench = sources(), bench_sources()
+    with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        objs = list(ex.map(_compile, main + bench))
+    _link(objs[:len(main)], LIB_PATH)
+    _link(objs[len(main):], BENCH_LIB_PATH)
     return LIB_PATH
 
 

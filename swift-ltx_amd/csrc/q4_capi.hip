@@ -188,38 +188,6 @@ float* stream_workspace(hipStream_t st, size_t need) {
     return static_cast<float*>(ptr);
 }
 
-// Per-stream sync area of the single-launch decode layer (epoch, fault
-// counter, exchanged vectors).  Kept apart from the workspace, whose other
-// users would overwrite the tagged words, and zeroed when allocated: a tag is
-// never 0 and the epoch starts at 0.  Same growth and retirement rules.
-std::map<std::pair<int, hipStream_t>, StreamWs> g_sync;
-
-uint32_t* stream_sync_area(hipStream_t st, size_t need) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    auto& e = g_sync[{dev, st}];
-    if (e.bytes >= need) return static_cast<uint32_t*>(e.ptr);
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
-        return nullptr;
-    void* ptr = nullptr;
-    const size_t bytes = std::max(need, 2 * e.bytes);
-    if (hipMalloc(&ptr, bytes) != hipSuccess) {
-        (void)hipGetLastError();
-        return nullptr;
-    }
-    if (hipMemsetAsync(ptr, 0, bytes, st) != hipSuccess) {
-        (void)hipGetLastError();
-        (void)hipFree(ptr);
-        return nullptr;
-    }
-    if (e.ptr) e.retired.push_back(e.ptr);
-    e.ptr = ptr;
-    e.bytes = bytes;
-    return static_cast<uint32_t*>(ptr);
-}
-
 int release_workspace(hipStream_t st) {
     int dev = 0;
     hipError_t err = hipGetDevice(&dev);
@@ -228,18 +196,13 @@ int release_workspace(hipStream_t st) {
     {
         std::lock_guard<std::mutex> lk(g_ws_mu);
         auto it = g_ws.find({dev, st});
-        auto is = g_sync.find({dev, st});
-        if (it == g_ws.end() && is == g_sync.end()) return kOk;
+        if (it == g_ws.end()) return kOk;
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
             return fail(kErrInvalid, "sltx_release_workspace: the stream is being captured");
-        for (auto* m : {&g_ws, &g_sync}) {
-            auto f = m->find({dev, st});
-            if (f == m->end()) continue;
-            bufs.insert(bufs.end(), f->second.retired.begin(), f->second.retired.end());
-            bufs.push_back(f->second.ptr);
-            m->erase(f);
-        }
+        bufs = it->second.retired;
+        bufs.push_back(it->second.ptr);
+        g_ws.erase(it);
     }
     // the stream's queued work may still use the buffers
     err = hipStreamSynchronize(st);
@@ -821,142 +784,6 @@ int sltx_matmul_q4_residual_rms_norm(const void* x, const sltx_q4_weight* w, con
                   fn);
 }
 
-int sltx_decode_layer_q4(const void* attn, const void* residual, const sltx_q4_weight* o_proj,
-                         const float* post_norm, const sltx_q4_weight* gate,
-                         const sltx_q4_weight* up, const sltx_q4_weight* down,
-                         const float* next_norm, const sltx_q4_weight* next_qkv,
-                         int32_t next_qkv_rows, int32_t hidden, int32_t ffn, float eps,
-                         void* residual_out, void* next_qkv_out, void* stream) {
-    const char* fn = "sltx_decode_layer_q4";
-    if (!o_proj || !gate || !up || !down) return fail(kErrInvalid, "%s: null weight descriptor", fn);
-    if (hidden <= 0 || ffn <= 0) return fail(kErrInvalid, "%s: hidden and ffn must be positive", fn);
-    if (o_proj->K != hidden || gate->K != hidden || up->K != hidden || down->K != ffn)
-        return fail(kErrInvalid,
-                    "%s: o_proj, gate and up need K = hidden (%d), down K = ffn (%d)", fn, hidden, ffn);
-    const int g = o_proj->group_size;
-    if (gate->group_size != g || up->group_size != g || down->group_size != g ||
-        (next_qkv && next_qkv->group_size != g))
-        return fail(kErrUnsupported, "%s: every weight must have the same group_size", fn);
-    int rc;
-    if ((rc = check_weight(fn, attn, o_proj->weight, o_proj->scales, o_proj->biases, residual_out, 1,
-                           hidden, hidden, g)) != kOk ||
-        (rc = check_weight(fn, attn, gate->weight, gate->scales, gate->biases, residual_out, 1, hidden,
-                           ffn, g)) != kOk ||
-        (rc = check_weight(fn, attn, up->weight, up->scales, up->biases, residual_out, 1, hidden, ffn,
-                           g)) != kOk ||
-        (rc = check_weight(fn, attn, down->weight, down->scales, down->biases, residual_out, 1, ffn,
-                           hidden, g)) != kOk)
-        return rc;
-    if (next_qkv) {
-        if (next_qkv->K != hidden) return fail(kErrInvalid, "%s: next_qkv K must be hidden", fn);
-        if (next_qkv_rows <= 0) return fail(kErrInvalid, "%s: next_qkv_rows must be positive", fn);
-        if (!next_norm || !next_qkv_out) return fail(kErrInvalid, "%s: null pointer argument", fn);
-        if ((rc = check_weight(fn, attn, next_qkv->weight, next_qkv->scales, next_qkv->biases,
-                               next_qkv_out, 1, hidden, next_qkv_rows, g)) != kOk)
-            return rc;
-        if (!aligned(next_norm, 16) || !aligned(next_qkv_out, 2))
-            return fail(kErrInvalid, "%s: misaligned next_norm or next_qkv_out", fn);
-        if (overlap(next_qkv_out, (size_t)next_qkv_rows * 2, residual_out, (size_t)hidden * 2))
-            return fail(kErrInvalid, "%s: next_qkv_out overlaps residual_out", fn);
-    }
-    for (const sltx_q4_weight* w : {o_proj, gate, up, down, next_qkv})
-        if (w && (!aligned(w->scales, 8) || !aligned(w->biases, 8)))
-            return fail(kErrInvalid, "%s: scales and biases must be 8-byte aligned", fn);
-    if (!residual || !post_norm) return fail(kErrInvalid, "%s: null pointer argument", fn);
-    if (!aligned(residual, 16) || !aligned(post_norm, 16) || !aligned(residual_out, 16))
-        return fail(kErrInvalid, "%s: residual, post_norm and residual_out must be 16-byte aligned",
-                    fn);
-    if ((rc = ensure_device()) != kOk) return rc;
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    int dev = 0, cus = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
-    DecodeLayerParams p = {};
-    p.attn = static_cast<const uint16_t*>(attn);
-    p.h = static_cast<const uint16_t*>(residual);
-    p.wo = o_proj->weight; p.so = o_proj->scales; p.bo = o_proj->biases;
-    p.post_norm = post_norm;
-    p.wg = gate->weight; p.sg = gate->scales; p.bg = gate->biases;
-    p.wu = up->weight; p.su = up->scales; p.bu = up->biases;
-    p.wd = down->weight; p.sd = down->scales; p.bd = down->biases;
-    p.next_norm = next_qkv ? next_norm : nullptr;
-    p.wq = next_qkv ? next_qkv->weight : nullptr;
-    p.sq = next_qkv ? next_qkv->scales : nullptr;
-    p.bq = next_qkv ? next_qkv->biases : nullptr;
-    p.h_out = static_cast<uint16_t*>(residual_out);
-    p.qkv_out = static_cast<uint16_t*>(next_qkv_out);
-    p.eps = eps;
-    p.H = hidden;
-    p.F = ffn;
-    p.nq = next_qkv ? next_qkv_rows : 0;
-    p.groups_h = hidden / g;
-    p.groups_f = ffn / g;
-    p.gshift = log2_group(g);
-    p.spin_limit = kDecodeSpinLimit;
-    if (!decode_layer_supported(p, cus))
-        return fail(kErrUnsupported,
-                    "%s: no kernel built for hidden %d, ffn %d, %d q|k|v rows on %d CUs (use the "
-                    "per-projection entry points)", fn, hidden, ffn, p.nq, cus);
-    if (!decode_layer_resident(p, cus, cus))
-        return fail(kErrUnsupported, "%s: %d blocks cannot all be resident on %d CUs", fn, cus, cus);
-    uint32_t* sync = stream_sync_area(st, decode_layer_sync_bytes(hidden, ffn));
-    if (!sync)
-        return fail(kErrInvalid,
-                    "%s: no sync area on this stream (it is being captured: call it once eagerly "
-                    "on the same stream first)", fn);
-    p.sync = sync;
-    p.xo = sync + 64;
-    p.xa = p.xo + hidden;
-    p.xd = p.xa + ffn;
-    return finish(launch_decode_layer(p, cus, st), fn);
-}
-
-int sltx_hbm_read_blocks(void) { return hbm_read_blocks(); }
-
-static int hbm_read_common(const char* fn, const void* src, uint64_t bytes, uint32_t* sink,
-                           bool lds, void* stream) {
-    if (bytes == 0) return kOk;
-    if (!src || !sink) return fail(kErrInvalid, "%s: null pointer argument", fn);
-    if (bytes % 16 != 0 || !aligned(src, 16) || !aligned(sink, 4))
-        return fail(kErrInvalid, "%s: bytes must be a multiple of 16, src 16-byte aligned", fn);
-    int rc = ensure_device();
-    if (rc != kOk) return rc;
-    return finish(launch_hbm_read(src, (long)(bytes / 16), sink, lds, static_cast<hipStream_t>(stream)),
-                  fn);
-}
-
-int sltx_hbm_read(const void* src, uint64_t bytes, uint32_t* sink, void* stream) {
-    return hbm_read_common("sltx_hbm_read", src, bytes, sink, false, stream);
-}
-
-int sltx_hbm_read_lds(const void* src, uint64_t bytes, uint32_t* sink, void* stream) {
-    return hbm_read_common("sltx_hbm_read_lds", src, bytes, sink, true, stream);
-}
-
-int sltx_probe_empty(void* stream) {
-    int rc = ensure_device();
-    if (rc != kOk) return rc;
-    return finish(launch_probe_empty(static_cast<hipStream_t>(stream)), "sltx_probe_empty");
-}
-
-int sltx_probe_mfma(const void* ab, int32_t blocks, int32_t iters, float* sink, uint64_t* clocks,
-                    void* stream) {
-    const char* fn = "sltx_probe_mfma";
-    if (!ab || !sink || !clocks) return fail(kErrInvalid, "%s: null pointer argument", fn);
-    if (blocks < 1 || blocks > 65536 || iters < 0)
-        return fail(kErrInvalid, "%s: blocks must be in [1, 65536], iters >= 0", fn);
-    if (!aligned(ab, 16) || !aligned(sink, 4) || !aligned(clocks, 8))
-        return fail(kErrInvalid, "%s: misaligned pointer", fn);
-    int rc = ensure_device();
-    if (rc != kOk) return rc;
-    return finish(launch_probe_mfma(ab, blocks, iters, sink,
-                                    reinterpret_cast<unsigned long long*>(clocks),
-                                    static_cast<hipStream_t>(stream)), fn);
-}
-
-int sltx_probe_sync_words(int32_t blocks) { return blocks < 1 ? 0 : probe_sync_words(blocks); }
-
 int sltx_gemm_route(int32_t M, int32_t N, int32_t K, int32_t group_size, int32_t gated,
                     int32_t x_dtype) {
     const char* fn = "sltx_gemm_route";
@@ -985,52 +812,6 @@ int sltx_gemm_route(int32_t M, int32_t N, int32_t K, int32_t group_size, int32_t
     NarrowPlan np;
     SkinnyPlan sp;
     return gemm_route(p, x_dtype == kBF16, &np, &sp);
-}
-
-int sltx_probe_sync(int32_t mode, int32_t fence, int32_t blocks, int32_t rounds, uint32_t* sync,
-                    int32_t* faults, void* stream) {
-    const char* fn = "sltx_probe_sync";
-    if (!sync || !faults) return fail(kErrInvalid, "%s: null pointer argument", fn);
-    if (mode < 0 || mode > 3 || rounds < 0 || blocks < 1)
-        return fail(kErrInvalid, "%s: mode must be 0 to 3, rounds >= 0, blocks >= 1", fn);
-    if (!aligned(sync, 64) || !aligned(faults, 4))
-        return fail(kErrInvalid, "%s: sync must be 64-byte aligned", fn);
-    int rc = ensure_device();
-    if (rc != kOk) return rc;
-    const int cap = probe_sync_max_blocks();
-    if (blocks > cap)
-        return fail(kErrInvalid, "%s: %d blocks exceed the %d this device holds at once", fn,
-                    blocks, cap);
-    return finish(launch_probe_sync(mode, fence, blocks, rounds, sync, faults,
-                                    static_cast<hipStream_t>(stream)), fn);
-}
-
-int sltx_decode_layer_faults(void* stream, int32_t* faults) {
-    const char* fn = "sltx_decode_layer_faults";
-    if (!faults) return fail(kErrInvalid, "%s: null pointer argument", fn);
-    *faults = 0;
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
-    void* ptr = nullptr;
-    {
-        std::lock_guard<std::mutex> lk(g_ws_mu);
-        auto it = g_sync.find({dev, st});
-        if (it == g_sync.end()) return kOk;
-        ptr = it->second.ptr;
-    }
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
-        return fail(kErrInvalid, "%s: the stream is being captured", fn);
-    uint32_t v = 0;
-    uint32_t* counter = static_cast<uint32_t*>(ptr) + 1;
-    if ((e = hipStreamSynchronize(st)) != hipSuccess ||
-        (e = hipMemcpy(&v, counter, 4, hipMemcpyDeviceToHost)) != hipSuccess ||
-        (e = hipMemsetAsync(counter, 0, 4, st)) != hipSuccess || (e = hipStreamSynchronize(st)) != hipSuccess)
-        return hip_fail(e, fn);
-    *faults = (int32_t)(v > 0x7fffffffu ? 0x7fffffffu : v);
-    return kOk;
 }
 
 }  // extern "C"

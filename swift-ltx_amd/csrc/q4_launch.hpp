@@ -131,46 +131,6 @@ struct SampleParams {
     uint2* cand;            // [n] (probability bits, id)
 };
 
-// One decode layer after attention in a single launch (q4_decode.hip): o,
-// residual + rms_norm, gate/up + SiLU, down + residual, and (wq non-null) the
-// next layer's rms_norm + q|k|v.  Weights as GemvParams; sync and the three
-// exchange vectors live in a zeroed per-stream area of
-// decode_layer_sync_bytes(H, F) bytes.
-struct DecodeLayerParams {
-    const uint16_t* attn;        // [H] o_proj input
-    const uint16_t* h;           // [H] residual stream in
-    const uint32_t* wo;          // [H, H/8]
-    const uint16_t *so, *bo;
-    const float* post_norm;      // [H]
-    const uint32_t *wg, *wu;     // [F, H/8]
-    const uint16_t *sg, *bg, *su, *bu;
-    const uint32_t* wd;          // [H, F/8]
-    const uint16_t *sd, *bd;
-    const float* next_norm;      // [H] (with wq)
-    const uint32_t* wq;          // [nq, H/8] or null (last layer)
-    const uint16_t *sq, *bq;
-    uint16_t* h_out;             // [H] residual stream out
-    uint16_t* qkv_out;           // [nq]
-    uint32_t* sync;              // [0] epoch, [1] timed-out waits
-    uint32_t *xo, *xa, *xd;      // exchanged vectors, [H], [F], [H] tagged words
-    float eps;
-    int H, F, nq;
-    int groups_h, groups_f;      // H / g, F / g
-    int gshift;                  // log2(g / 32)
-    int spin_limit;              // polls before a wait gives up
-};
-
-// Polls a wait of the single-launch decode layer makes before it gives up
-// (about 0.1 s; a grid that is not all resident, e.g. beside another
-// kernel, is the only way to reach it).
-constexpr int kDecodeSpinLimit = 1 << 16;
-size_t decode_layer_sync_bytes(int H, int F);
-// 1 if a kernel is built for these shapes on a grid of G blocks.
-int decode_layer_supported(const DecodeLayerParams& p, int G);
-// 1 if G blocks of that kernel can all be resident on `cus` CUs.
-int decode_layer_resident(const DecodeLayerParams& p, int G, int cus);
-hipError_t launch_decode_layer(const DecodeLayerParams& p, int G, hipStream_t st);
-
 hipError_t launch_gemv(const GemvParams& p, bool swiglu, hipStream_t st);
 hipError_t launch_embedding_q4(const EmbedParams& p, int n, hipStream_t st);
 size_t sample_workspace_bytes(int n);
@@ -229,18 +189,6 @@ size_t gemm_partials_workspace_bytes(const GemmParams& p);
 hipError_t launch_gemm_residual_rms_norm(GemmParams p, bool a_bf16, const float* norm_w, float eps,
                                          uint16_t* res_out, uint16_t* norm_out, bool sum_rounded,
                                          hipStream_t st);
-// HBM read ceiling (q4_probe.hip): sink holds hbm_read_blocks() words; lds:
-// the same stream through direct global -> LDS copies.
-int hbm_read_blocks();
-hipError_t launch_hbm_read(const void* src, long n16, uint32_t* sink, bool lds, hipStream_t st);
-// launch floor, register-only MFMA and grid hand-off probes (q4_probe.hip)
-hipError_t launch_probe_empty(hipStream_t st);
-hipError_t launch_probe_mfma(const void* ab, int blocks, int iters, float* sink,
-                             unsigned long long* clocks, hipStream_t st);
-int probe_sync_words(int blocks);
-int probe_sync_max_blocks();
-hipError_t launch_probe_sync(int mode, int fence, int blocks, int rounds, uint32_t* sync,
-                             int* faults, hipStream_t st);
 hipError_t launch_silu_mul(const uint16_t* a, const uint16_t* b, uint16_t* out, long count,
                            hipStream_t st);
 // Row-wise RMS norm, optionally of a + b (then the rounded sum goes to res_out).

@@ -83,7 +83,7 @@ struct MidShape {
     static constexpr size_t static_lds(int ng, int wsl) {
         return (size_t)wsl * GSLOTS * 16 + (size_t)nsx(ng, wsl) * XSLOTS * 16;
     }
-    static_assert(nsx(3, 3) * XSLOTS * 4 >= NCW * 1024, "the K-group sums fit the ring");
+    static_assert(nsx(3, 2) * XSLOTS * 4 >= NCW * 1024, "the K-group sums fit the ring");
 };
 
 __device__ __forceinline__ f32x16 mfma32_f16(u32x4 a, u32x4 b, f32x16 c) {
@@ -102,9 +102,9 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// NG weight groups of 1024 k in WSL LDS slots: WSL = NG holds the whole K;
-// WSL < NG refills the slot of group G - 1 with group G + WSL - 1 once every
-// wave has finished group G - 1.
+// NG weight groups of 1024 k in WSL = 2 LDS slots (the only count built):
+// the slot of group G - 1 is refilled with group G + 1 once every wave has
+// finished group G - 1.
 template <bool PAIR, bool KG8, int NG, int WSL>
 __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
     using S = MidShape<KG8>;
@@ -115,7 +115,7 @@ __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
     constexpr int NSLAB = PAIR ? 4 : 2;         // s0, b0[, s1, b1]
     constexpr int SROWS = PAIR ? 32 : BROWS;    // rows per slab
     constexpr int NSX = S::nsx(NG, WSL);
-    static_assert(WSL >= 2 && WSL <= NG && WSL <= 3, "weight slots");
+    static_assert(WSL == 2 && WSL <= NG, "weight slots");
     // At the start of round q an X-copy wave has issued X(q + 1 .. q + NSX - 2)
     // after X(q).
     constexpr int WAIT_X = (NSX - 2) * NXC;
@@ -314,14 +314,12 @@ bool mid_built(bool pair, int ng, int wsl) {
     return wsl == 2 && (ng == 2 || ng == 3 || ng == 4 || ng == 8 || ng == 10);
 }
 
-// Weight-group slots: the whole K (up to 3 groups) when it fits LDS beside
-// the X ring and the slabs, else 2 slots refilled as the groups are used;
-// 0: no built configuration fits.
+// Weight-group slots: 2, refilled as the groups are used, when that build
+// exists for K and fits LDS beside the X ring and the slabs; 0 otherwise.
 int mid_wsl(const GemmParams& p, bool pair) {
     const int ng = p.K / 1024;
-    for (int wsl = ng < 3 ? ng : 3; wsl >= 2; --wsl)
-        if (mid_built(pair, ng, wsl) && mid_static_lds(ng, wsl, pair) + mid_lds(p, pair) <= kMaxLds)
-            return wsl;
+    if (mid_built(pair, ng, 2) && mid_static_lds(ng, 2, pair) + mid_lds(p, pair) <= kMaxLds)
+        return 2;
     return 0;
 }
 
@@ -337,7 +335,7 @@ hipError_t launch_sel(const GemmParams& p, bool pair, int wsl, const dim3& grid,
     if (pair) {
         if (ng == 2) return launch_cfg<true, false, 2, 2>(p, grid, lds, st);
         if (ng == 3) return launch_cfg<true, false, 3, 2>(p, grid, lds, st);
-        if (ng == 4 && wsl == 2) return launch_cfg<true, false, 4, 2>(p, grid, lds, st);
+        if (ng == 4) return launch_cfg<true, false, 4, 2>(p, grid, lds, st);
         return hipErrorInvalidValue;
     }
     switch (ng * 4 + wsl) {

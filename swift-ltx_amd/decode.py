@@ -13,14 +13,6 @@ Mirrors LlamaModel.generate / forward / transformerBlock
   final rmsNorm + lm_head linear               sltx_rmsnorm_matmul_q4
   argmax / sample                              sltx_argmax / sltx_sample_top_p
 
-With single_launch_layers=True each layer after its attention is one launch
-of sltx_decode_layer_q4 (o, residual + RMSNorm, gate/up + SiLU, down +
-residual, and the next layer's RMSNorm + q|k|v); layer 0's RMSNorm + q|k|v
-stays its own launch.  It issues a quarter of the launches (useful where the
-host pays for each launch) but is slower inside a HIP graph on an MI355X:
-its three grid-wide exchanges cost more than the launch boundaries they
-replace.
-
 The chosen token id stays in device memory and is the next step's input, so a
 step can be captured once as a HIP graph and replayed per token: greedy
 (temperature 0, argmax as the reference uses), or sampled with a SamplerState,
@@ -37,7 +29,7 @@ from __future__ import annotations
 
 import random
 
-from . import (Q4Weight, argmax, decode_layer, embedding_q4, linear, matmul_q4_residual,
+from . import (Q4Weight, argmax, embedding_q4, linear, matmul_q4_residual,
                rmsnorm_matmul_q4, residual_rmsnorm_matmul_q4_silu_mul, sample, sample_with_state)
 
 
@@ -56,10 +48,9 @@ class DecodeStep:
     layers[i].{qkv_proj, o_proj, gate_proj, up_proj, down_proj,
     input_norm_weight, post_norm_weight}) and a config with hidden_size,
     intermediate_size, num_attention_heads, num_key_value_heads, head_dim,
-    vocab_size, rms_norm_eps.  single_launch_layers: see the module docstring
-    (the attention width must equal hidden_size)."""
+    vocab_size, rms_norm_eps."""
 
-    def __init__(self, weights, attention=None, stream=None, single_launch_layers=False):
+    def __init__(self, weights, attention=None, stream=None):
         import torch
         c = weights.config
         self.w = weights
@@ -75,9 +66,6 @@ class DecodeStep:
                 if not isinstance(getattr(lw, name), Q4Weight):
                     raise ValueError(f"layer {i}: {name} is not a 4-bit weight")
         self.attention = attention or q_rows_attention(self.q_dim)
-        self.single_launch = bool(single_launch_layers)
-        if self.single_launch and self.q_dim != self.hidden:
-            raise ValueError("single_launch_layers needs heads * head_dim == hidden_size")
         dev = weights.embed_tokens.weight.device
         f16 = torch.float16
         self.token = torch.zeros(1, dtype=torch.int32, device=dev)       # input / chosen token
@@ -106,26 +94,9 @@ class DecodeStep:
         """Embedding of self.token through the lm_head into self.logits."""
         c, w, s = self.c, self.w, self.stream
         embedding_q4(w.embed_tokens, c.vocab_size, self.token, out=self.h, stream=s)
-        if self.single_launch:
-            self._layers_single_launch()
-        else:
-            self._layers()
+        self._layers()
         rmsnorm_matmul_q4(self.h, w.norm_weight, c.rms_norm_eps, w.lm_head, c.vocab_size,
                           out=self.logits, stream=s)
-
-    def _layers_single_launch(self):
-        c, w, s = self.c, self.w, self.stream
-        eps, layers = c.rms_norm_eps, w.layers
-        rmsnorm_matmul_q4(self.h, layers[0].input_norm_weight, eps, layers[0].qkv_proj,
-                          self.qkv_rows, out=self.qkv, stream=s)
-        for i, lw in enumerate(layers):
-            attn = self.attention(i, self.qkv)
-            nxt = layers[i + 1] if i + 1 < len(layers) else None
-            # in place: the kernel reads attn and h before it writes h and qkv
-            decode_layer(attn, self.h, lw.o_proj, lw.post_norm_weight, lw.gate_proj, lw.up_proj,
-                         lw.down_proj, eps, next_norm=nxt.input_norm_weight if nxt else None,
-                         next_qkv=nxt.qkv_proj if nxt else None, residual_out=self.h,
-                         next_qkv_out=self.qkv if nxt else None, stream=s)
 
     def _layers(self):
         c, w, s = self.c, self.w, self.stream

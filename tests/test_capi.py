@@ -357,31 +357,3 @@ def test_matmul_residual_rms_norm_validation(pkg):
     assert call(no=X) == -1 and "overlaps x" in pkg.last_error()
     wg = _w(pkg, g=48)
     assert call(wp=ctypes.byref(wg)) == -2
-
-
-def test_decode_layer_validation(pkg):
-    """sltx_decode_layer_q4 argument checks that run before any HIP call."""
-    L = pkg.lib()
-    A = ALIGNED
-    H, F = 3072, 8192
-    wo, wg, wu, wd = _wq(pkg, K=H), _wq(pkg, K=H), _wq(pkg, K=H), _wq(pkg, K=F)
-    wq = _wq(pkg, K=H)
-    B = ctypes.byref
-
-    def call(attn=A, res=A, o=wo, pn=A, g=wg, u=wu, d=wd, nn=A, q=wq, nq=5120, h=H, f=F, ro=2 * A,
-             qo=3 * A):
-        return L.sltx_decode_layer_q4(attn, res, B(o) if o else None, pn, B(g) if g else None,
-                                      B(u) if u else None, B(d) if d else None, nn,
-                                      B(q) if q else None, nq, h, f, 1e-5, ro, qo, None)
-    assert call(o=None) == -1 and "null weight" in pkg.last_error()
-    assert call(h=0) == -1 and "positive" in pkg.last_error()
-    assert call(d=_wq(pkg, K=H)) == -1 and "ffn" in pkg.last_error()
-    assert call(g=_wq(pkg, K=F)) == -1 and "hidden" in pkg.last_error()
-    assert call(u=_wq(pkg, K=H, g=128)) == -2 and "group_size" in pkg.last_error()
-    assert call(nq=0) == -1 and "next_qkv_rows" in pkg.last_error()
-    assert call(nn=None) == -1 and "null" in pkg.last_error()
-    assert call(qo=2 * A + 64) == -1 and "overlaps residual_out" in pkg.last_error()
-    assert call(ro=2 * A + 2) == -1 and "16-byte" in pkg.last_error()
-    assert call(res=None) == -1 and "null" in pkg.last_error()
-    assert call(attn=A + 2) == -1 and "x must be 16-byte aligned" in pkg.last_error()
-    assert L.sltx_decode_layer_faults(None, None) == -1

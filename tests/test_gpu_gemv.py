@@ -217,20 +217,23 @@ def test_silu_mul_standalone(pkg, dev):
 
 
 @pytest.mark.parametrize("lds", [False, True])
-def test_hbm_read_probe_reads_every_word(pkg, dev, lds):
-    """The read-ceiling probes (sltx_hbm_read, and sltx_hbm_read_lds through
-    direct global -> LDS copies) touch every 32-bit word once: the XOR of
-    their per-block words equals the XOR of the buffer, for sizes that are not
-    multiples of the grid's step, with one or several steps per block (odd
-    and even counts); a wrong size is rejected."""
+def test_bench_hbm_read_reads_every_word(dev, lds):
+    """bench.py's read ceiling (csrc/bench/hbm_read.hip, into registers, and
+    through direct global -> LDS copies) touches every 32-bit word once: the
+    XOR of its per-block words equals the XOR of the buffer, for sizes that
+    are not multiples of the grid's step, with one or several steps per block
+    (odd and even counts); a size that is not a multiple of 16 is rejected."""
     import torch
+    import bench
+    sink = torch.empty(bench.bench_lib().sltx_bench_hbm_read_blocks(), dtype=torch.int32,
+                       device=dev)
     for nbytes in (16, 4096 * 16 + 48, 1024 * 4096 * 16 * 3 + 16384 * 3 + 16 * 5,
                    64 * 2 ** 20 + 16 * 7):
         src = torch.randint(-2**31, 2**31 - 1, (nbytes // 4,), device=dev, dtype=torch.int64).to(torch.int32)
-        sink = pkg.hbm_read(src, lds=lds)
+        bench.hbm_read(torch, src, sink, lds=lds)
         torch.cuda.synchronize()
         want = np.bitwise_xor.reduce(src.cpu().numpy().view(np.uint32))
         got = np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32))
         assert got == want, nbytes
-    with pytest.raises(pkg.SltxError):
-        pkg.hbm_read(torch.zeros(5, dtype=torch.int16, device=dev), lds=lds)
+    with pytest.raises(RuntimeError):
+        bench.hbm_read(torch, torch.zeros(5, dtype=torch.int16, device=dev), sink, lds=lds)

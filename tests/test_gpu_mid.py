@@ -2,8 +2,8 @@
 for one weight set of 4096..16384 rows; fp16 activations) through the C ABI:
 gated pairs at K = 2048 / 3072 (32 gate + 32 up rows per block, group sizes
 64 and 128) and single weight sets at K = 2048, 3072, 4096, 8192, 10240 (32
-rows per block; the weight groups of 1024 k held whole or in a ring of 2-3
-LDS slots).
+rows per block; the weight groups of 1024 k in two LDS slots, refilled as
+the groups are used).
 
 Same semantics as the GEMM (matmulQ4Fast / matmulQ4FastF32, Ops.swift:312-381;
 the SwiGLU and GeGLU pairs, LlamaModel.swift:275-277 and
@@ -11,7 +11,7 @@ T5Encoder.swift:191-199): the weights are dequantized to fp16 as s*q+b in one
 fp16 FMA and multiplied with fp32 accumulation, so the outputs are checked
 against the fp64 oracle (tolerances of tests/helpers.py), against the
 fp16-rounded weights, and bit for bit through unit vectors.  The shapes cover
-every built weight-group count and slot ring, the X ring's wrap-around and
+every built weight-group count, the X ring's wrap-around and
 the spare copies past the end, a last block with fewer than 32 rows, grids
 from one block to 256, and every group size.
 """
@@ -31,6 +31,7 @@ SHAPES = [
     (25, 3072, 3072, 64), (32, 8192, 3072, 32), (12, 5120, 3072, 64), (9, 4100, 2048, 128),
     (16, 16384, 2048, 32), (28, 4096, 4096, 64), (32, 3072, 8192, 64), (17, 4096, 10240, 128),
     (26, 4096, 4096, 32), (24, 100, 8192, 128), (29, 90, 10240, 64), (31, 4096, 4096, 128),
+    (17, 64, 2048, 32),
 ]
 
 
