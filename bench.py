@@ -18,7 +18,10 @@ value      = algorithmic bytes of exactly K steps / GPU time of those K
              a decode loop would), bracketed by torch.cuda.synchronize() and
              timed by events recorded around the replay on its stream (the
              host wall clock around it, which adds one replay's launch and
-             synchronize latency, is in timing.host_wall_gbs).
+             synchronize latency, is in timing.host_wall_gbs).  Before the
+             warm-up every layer copy is read once by a plain read kernel
+             (not a step), so that the timed steps read weights the GPU has
+             read before, as decode tokens after the first do.
 stats      = the same layer over >= 50 replays (and >= 200 ms) of a graph of
              one rotation over the copies, an event after each replay:
              median and quartiles of the time per step.
@@ -37,6 +40,9 @@ extra      = the other BASELINE configs and the paths around the GEMV, each
              decode token (greedy / sampled), the 750-token prefill, token
              selection, small M (2..128) and the M > 1 MFMA GEMMs (configs 3,
              4b, 5) against the 2.5 PFLOP/s dense fp16/bf16 peak.
+configs    = the last key of the line: every BASELINE config as us and
+             fraction of its roofline (a log that keeps only the line's tail
+             still holds them).
 cpu_baseline = C restatements of the same dequant matmul (Swift, the
              reference's host language, is not installed): single-thread
              scalar and all-cores 8-wide SIMD, median of 5 runs per config.
@@ -297,6 +303,13 @@ def main():
     g_warm = graph_of(0, args.warmup) if args.warmup > 0 else None
     g_timed = graph_of(args.warmup, args.steps)
     uploaded = upload_graph(g_timed, cap)
+    # Every weight copy is read once (a read kernel, not a step) before the
+    # warm-up: the timed steps then read weights the GPU has read before, as
+    # every decode token after the first does.  Measured without it, the
+    # timed replay (the first read of those copies since their
+    # initialization wrote them) took 21.0 us/step against 18.0 for a replay
+    # of the same graph right after it; with it, 18.8.
+    prime_weights(torch, dev, layers)
     torch.cuda.synchronize()
     if g_warm is not None:
         g_warm.replay()
@@ -390,7 +403,38 @@ def main():
         "cpu_baseline": cpu,
         "extra": legs,
     }
+    line["configs"] = config_summary(value, args.steps, wall, layer_st, dom_us, legs)
     print(json.dumps(line))
+
+
+def config_summary(value, steps, wall, layer_st, dom_us, legs):
+    """Every BASELINE config in a few numbers, for the end of the JSON line
+    (whose tail is what a log keeps): us and fraction of the HBM (GEMV) or
+    dense MFMA (GEMM) peak."""
+    def hbm(st):
+        return {"us": st["median_us"], "frac_hbm": st["frac_hbm"]} if st else None
+
+    def mfma(st):
+        return {"us": st["median_us"], "frac_mfma": st["frac_mfma"]} if st else None
+
+    gemm = legs.get("gemm", {})
+    return {
+        "c1_q_proj_gemv": hbm(legs.get("config1_q_proj_gemv_m1")),
+        "c2_decode_layer": {"value_us_per_step": round(1e6 * wall / steps, 3),
+                            "value_frac_hbm": round(value / HBM_PEAK_GBS, 4),
+                            "stats_us": layer_st["median_us"],
+                            "stats_frac_hbm": layer_st["frac_hbm"],
+                            "gate_up_us": dom_us,
+                            "gate_up_frac_hbm": round(DOMINANT_BYTES / (dom_us * 1e-6)
+                                                      / 1e9 / HBM_PEAK_GBS, 4),
+                            "fused_norms_us": legs["decode_layer_fused_norms"]["median_us"]},
+        "c3_prefill_gate_up_silu_m750": mfma(gemm.get("prefill_gate_up_silu_m750")),
+        "c3_prefill_down_m750": mfma(gemm.get("prefill_down_m750")),
+        "c4a_lm_head_gemv_cold": hbm(legs.get("lm_head_gemv_m1_cold")),
+        "c4b_lm_head_gemm_m750": mfma(gemm.get("lm_head_gemm_m750")),
+        "c5_dit_up_gelu_m6144": mfma(gemm.get("dit_ffn_up_gelu_m6144_bf16")),
+        "c5_dit_down_m6144": mfma(gemm.get("dit_ffn_down_m6144_bf16")),
+    }
 
 
 # ------------------------------------------------------------ ceilings ---
@@ -426,6 +470,17 @@ def hbm_read(torch, src, sink, lds=False):
                                          torch.cuda.current_stream().cuda_stream)
     if rc != 0:
         raise RuntimeError(f"sltx_bench_hbm_read failed: {rc}")
+
+
+def prime_weights(torch, dev, layers):
+    """One read of every layer copy's packed weights, scales and biases with
+    the bench library's read kernel (csrc/bench/hbm_read.hip)."""
+    sink = torch.empty(bench_lib().sltx_bench_hbm_read_blocks(), device=dev, dtype=torch.int32)
+    for lay in layers:
+        for ws in lay.w.values():
+            for w in ws:
+                for t in (w.weight, w.scales, w.biases):
+                    hbm_read(torch, t, sink)
 
 
 def hbm_ceilings(pkg, torch, dev, cap, read_gib=4, copy_gib=1):
