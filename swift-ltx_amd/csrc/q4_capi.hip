@@ -219,7 +219,8 @@ int release_workspace(hipStream_t st) {
 // Measured on the Llama, T5 and vocabulary-head shapes at M = 2, 4, 8, that
 // is the faster route in every case; gated pairs and M > 4 are faster on the
 // small-M route, up to M = 16.
-int gemm_route(const GemmParams& p, bool a_bf16, NarrowPlan* np, SkinnyPlan* sp) {
+int gemm_route(const GemmParams& p, bool a_bf16, NarrowPlan* np, SkinnyPlan* sp, WidePlan* wp) {
+    if (p.M > 32) return wide_plan(p, a_bf16, wp) ? SLTX_ROUTE_WIDE : SLTX_ROUTE_GEMM;
     const bool narrow = narrow_plan(p, a_bf16, np);
     const bool skinny = skinny_plan(p, a_bf16, sp);
     if (narrow && (!skinny || !(sp->RT == 2 && sp->OCC == 2))) return SLTX_ROUTE_NARROW;
@@ -273,10 +274,21 @@ int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w
     p.split_tiles = 0;
     NarrowPlan np;
     SkinnyPlan sp;
-    const int route = gemm_route(p, x_dtype == kBF16, &np, &sp);
+    WidePlan wp;
+    const int route = gemm_route(p, x_dtype == kBF16, &np, &sp, &wp);
     if (route == SLTX_ROUTE_NARROW) return finish(launch_narrow(p, np, st), fn);
     if (route == SLTX_ROUTE_SMALL_M) return finish(launch_skinny(p, sp, st), fn);
     if (route == SLTX_ROUTE_MID) return finish(launch_mid(p, st), fn);
+    if (route == SLTX_ROUTE_WIDE) {
+        if (wp.splits > 1 && !(p.ws = stream_workspace(st, wp.ws_bytes))) {
+            // no workspace (the stream is being captured): the same product
+            // through the GEMM
+            const size_t need = gemm_workspace_bytes(p);
+            if (need > 0) p.ws = stream_workspace(st, need);
+            return finish(launch_gemm(p, x_dtype == kBF16, st), fn);
+        }
+        return finish(launch_wide(p, wp, st), fn);
+    }
     const size_t need = gemm_workspace_bytes(p);
     if (need > 0) p.ws = stream_workspace(st, need);
     return finish(launch_gemm(p, x_dtype == kBF16, st), fn);
@@ -811,7 +823,8 @@ int sltx_gemm_route(int32_t M, int32_t N, int32_t K, int32_t group_size, int32_t
     p.splits = 1;
     NarrowPlan np;
     SkinnyPlan sp;
-    return gemm_route(p, x_dtype == kBF16, &np, &sp);
+    WidePlan wp;
+    return gemm_route(p, x_dtype == kBF16, &np, &sp, &wp);
 }
 
 }  // extern "C"

@@ -47,6 +47,7 @@
 
 #include "q4_common.hpp"
 #include "q4_dequant.hpp"
+#include "q4_epilogue.hpp"
 #include "q4_launch.hpp"
 
 namespace sltx {
@@ -95,97 +96,6 @@ __device__ __forceinline__ f32x16 mfma32(const u32x4 a, const u32x4 b, f32x16 c)
     else
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                       __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-}
-
-__device__ __forceinline__ void store_out(const GemmParams& p, size_t o, float v) {
-    if (p.y_dtype == kF32)
-        reinterpret_cast<float*>(p.y)[o] = v;
-    else if (p.y_dtype == kBF16)
-        reinterpret_cast<uint16_t*>(p.y)[o] = f2bf(v);
-    else
-        reinterpret_cast<uint16_t*>(p.y)[o] = f2h(v);
-}
-
-// Whether rows of y (and of the residual) can take 16-byte vector stores.
-__device__ __forceinline__ bool out_vec_ok(const GemmParams& p) {
-    return (p.N & 7) == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0 &&
-           (p.epilogue != kEpiResidual || (reinterpret_cast<uintptr_t>(p.residual) & 15) == 0);
-}
-
-// Eight consecutive outputs row[n0 .. n0+7] (columns past N dropped): one
-// 16-byte store (two for fp32) when `vec` (N % 8 == 0, 16-byte aligned y),
-// else one store per element.
-__device__ __forceinline__ void store_out8(const GemmParams& p, size_t row, int n0,
-                                           const float* v, bool vec) {
-    if (vec && n0 + 8 <= p.N) {
-        if (p.y_dtype == kF32) {
-            f32x4* d = reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.y) + row + n0);
-            d[0] = f32x4{v[0], v[1], v[2], v[3]};
-            d[1] = f32x4{v[4], v[5], v[6], v[7]};
-        } else {
-            u32x4 o;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t lo = p.y_dtype == kBF16 ? f2bf(v[2 * e]) : f2h(v[2 * e]);
-                const uint32_t hi = p.y_dtype == kBF16 ? f2bf(v[2 * e + 1]) : f2h(v[2 * e + 1]);
-                o[e] = lo | (hi << 16);
-            }
-            *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(p.y) + row + n0) = o;
-        }
-        return;
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-        if (n0 + e < p.N) store_out(p, row + n0 + e, v[e]);
-}
-
-// Non-SiLU epilogue (bias, GELU-tanh, residual add) on eight consecutive
-// outputs, then stored as store_out8 does.
-__device__ __forceinline__ void epi_store8(const GemmParams& p, size_t row, int n0, float* v,
-                                           bool vec) {
-    if (p.bias) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] += p.bias[n0 + e < p.N ? n0 + e : 0];
-    }
-    if (p.epilogue == kEpiGeluTanh) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = gelu_tanh_f32(v[e]);
-    }
-    if (p.epilogue == kEpiResidual) {
-        if (vec && n0 + 8 <= p.N) {
-            const u32x4 r = *reinterpret_cast<const u32x4*>(p.residual + row + n0);
-            u32x4 o;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t lo = residual_add_f16((uint16_t)(r[e] & 0xFFFFu), v[2 * e]);
-                const uint32_t hi = residual_add_f16((uint16_t)(r[e] >> 16), v[2 * e + 1]);
-                o[e] = lo | (hi << 16);
-            }
-            *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(p.y) + row + n0) = o;
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                if (n0 + e < p.N)
-                    reinterpret_cast<uint16_t*>(p.y)[row + n0 + e] =
-                        residual_add_f16(p.residual[row + n0 + e], v[e]);
-        }
-        return;
-    }
-    store_out8(p, row, n0, v, vec);
-}
-
-// Eight raw fp32 partial sums into a workspace row (16-byte aligned rows when
-// N % 4 == 0).
-__device__ __forceinline__ void store_f32x8(float* wsr, int n0, int N, const float* v) {
-    if ((N & 3) == 0 && n0 + 8 <= N) {
-        f32x4* d = reinterpret_cast<f32x4*>(wsr + n0);
-        d[0] = f32x4{v[0], v[1], v[2], v[3]};
-        d[1] = f32x4{v[4], v[5], v[6], v[7]};
-        return;
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-        if (n0 + e < N) wsr[n0 + e] = v[e];
 }
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
@@ -901,6 +811,17 @@ static void launch_dtype(const GemmParams& p, bool a_bf16, bool silu, long grid,
     }
 }
 
+hipError_t launch_splitk_reduce(const GemmParams& p, hipStream_t st) {
+    const bool silu = p.epilogue == kEpiSiluMul || p.epilogue == kEpiGeluMul;
+    const size_t total = (size_t)p.M * ((p.N + 7) / 8);
+    const long rgrid = (long)((total + 255) / 256);
+    if (silu)
+        hipLaunchKernelGGL(q4_splitk_reduce_kernel<true>, dim3(rgrid), dim3(256), 0, st, p);
+    else
+        hipLaunchKernelGGL(q4_splitk_reduce_kernel<false>, dim3(rgrid), dim3(256), 0, st, p);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm(GemmParams p, bool a_bf16, hipStream_t st) {
     const bool silu = p.epilogue == kEpiSiluMul || p.epilogue == kEpiGeluMul;
     GemmPlan plan = plan_gemm(p, p.ws != nullptr);
@@ -916,12 +837,7 @@ hipError_t launch_gemm(GemmParams p, bool a_bf16, hipStream_t st) {
     if (grid > 0x7fffffffL) return hipErrorInvalidValue;
     if (p.splits > 1) {
         launch_dtype<true>(p, a_bf16, silu, grid, plan.wm, st);
-        const size_t total = (size_t)p.M * ((p.N + 7) / 8);
-        const long rgrid = (long)((total + 255) / 256);
-        if (silu)
-            hipLaunchKernelGGL(q4_splitk_reduce_kernel<true>, dim3(rgrid), dim3(256), 0, st, p);
-        else
-            hipLaunchKernelGGL(q4_splitk_reduce_kernel<false>, dim3(rgrid), dim3(256), 0, st, p);
+        (void)launch_splitk_reduce(p, st);
     } else {
         launch_dtype<false>(p, a_bf16, silu, grid, plan.wm, st);
     }

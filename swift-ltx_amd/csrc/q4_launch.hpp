@@ -174,6 +174,27 @@ hipError_t launch_skinny(const GemmParams& p, const SkinnyPlan& pl, hipStream_t 
 bool mid_plan(const GemmParams& p, bool a_bf16);
 hipError_t launch_mid(const GemmParams& p, hipStream_t st);
 
+// Wide-M route (q4_wide.hip, 32 < M <= 256, fp16 X): 64 weight rows (or a
+// 32-row gate/up pair) per block over all of its K range, up to 128
+// activation rows per block (more rows take more blocks), the 8 waves
+// splitting K; optionally split over K across blocks (fp32 partials in the
+// workspace, then the split-K reduce pass).  wide_plan returns false when the
+// shape, epilogue or alignment is not covered.
+struct WidePlan {
+    int tm;          // 32-row MFMA tiles per block (2..4)
+    int mblocks;     // blocks along M
+    int mrows;       // activation rows per M-block
+    int nblocks;     // blocks along N
+    int splits;      // K splits across blocks
+    int kblk;        // k per split (a multiple of 128)
+    size_t ws_bytes; // fp32 partials when splits > 1
+};
+bool wide_plan(const GemmParams& p, bool a_bf16, WidePlan* out);
+// p.ws must hold pl.ws_bytes when pl.splits > 1.
+hipError_t launch_wide(GemmParams p, const WidePlan& pl, hipStream_t st);
+// The split-K reduce pass: y = epilogue(sum of p.splits fp32 partials in p.ws).
+hipError_t launch_splitk_reduce(const GemmParams& p, hipStream_t st);
+
 // Bytes of split-K workspace the launch of `p` would use (0: it does not split).
 size_t gemm_workspace_bytes(const GemmParams& p);
 // Launches the GEMM; splits K only if p.ws is non-null (and then needs

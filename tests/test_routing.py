@@ -89,10 +89,32 @@ def test_m_above_4_leaves_the_narrow_route(pkg, N, K):
 def test_large_m_and_unsupported_shapes_take_the_gemm(pkg):
     import torch
     assert pkg.gemm_route(750, **LLAMA_PAIR) == "gemm"
-    assert pkg.gemm_route(128, 8192, 3072) == "gemm"
-    assert pkg.gemm_route(33, 8192, 3072) == "gemm"
+    assert pkg.gemm_route(257, 8192, 3072) == "gemm"
+    assert pkg.gemm_route(128, 8192, 3072, x_dtype=torch.bfloat16) == "gemm"
     assert pkg.gemm_route(2, 3072, 8192, x_dtype=torch.bfloat16) == "gemm"
     assert pkg.gemm_route(9, 24, 14336, group_size=32) == "gemm"   # past both step counts
+    assert pkg.gemm_route(100, 64, 192) == "gemm"                  # K not a multiple of 128
+
+
+@pytest.mark.parametrize("M", [33, 64, 100, 128, 200, 256])
+def test_wide_m_routing(pkg, M):
+    """33..256 rows (T5Encoder.swift:72-78, short prompts): the wide-M route
+    when its grid (64 weight rows per block, at most 128 activation rows per
+    block, K split until the grid fills the GPU) is one round of 256 blocks,
+    or two at M <= 64; else the GEMM (measured: a second round repeats the
+    whole per-block time)."""
+    one = lambda N, K, gated=False: pkg.gemm_route(M, N, K, gated=gated)
+    pair = lambda d: pkg.gemm_route(M, d["N"], d["K"], gated=True)
+    # one round at every M: Llama q|k|v, o, down; T5 q/k/v/o
+    assert one(5120, 3072) == "wide"
+    assert one(3072, 3072) == "wide"
+    assert one(3072, 8192) == "wide"
+    assert one(4096, 4096) == "wide"
+    # Llama gate/up pair: 256 blocks per 128-row block of M
+    assert pair(LLAMA_PAIR) == ("wide" if M <= 128 else "gemm")
+    # T5 GeGLU pair: 320 blocks; T5 wo: 64 blocks x 4 K splits per 128-row block
+    assert pair(T5_WI_PAIR) == ("wide" if M <= 64 else "gemm")
+    assert one(4096, 10240) == ("wide" if M <= 128 else "gemm")
 
 
 def test_invalid_arguments_raise(pkg):
