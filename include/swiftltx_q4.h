@@ -144,13 +144,17 @@ int sltx_linear(const void* x, const sltx_q4_weight* w, void* out, int32_t M, in
 int sltx_matmul_q4_silu_mul(const void* x, const sltx_q4_weight* gate, const sltx_q4_weight* up,
                             void* out, int32_t M, int32_t K, int32_t N, void* stream);
 
-/* Extended GEMM: x_dtype in {SLTX_F16, SLTX_BF16}; out_dtype in {SLTX_F16,
- * SLTX_BF16, SLTX_F32}; bias (fp32 [N]) optional (NULL = none); epilogue
- * SLTX_EPI_NONE or SLTX_EPI_GELU_TANH.  out = epi(x . dequant(W)^T + bias).
- * Covers DiTLinear.applyF32in's quantized branch (DiTModel.swift:102-125:
- * matmulQ4FastF32 then addBiasF32F32, Ops.swift:1780-1791) and the GELU-tanh
- * that follows it in the DiT feed-forward (DiTModel.swift:953,
- * Kernels.swift:1774-1783), with bf16 activations accepted directly. */
+/* Extended GEMM: x_dtype in {SLTX_F16, SLTX_BF16, SLTX_F32}; out_dtype in
+ * {SLTX_F16, SLTX_BF16, SLTX_F32}; bias (fp32 [N]) optional (NULL = none);
+ * epilogue SLTX_EPI_NONE or SLTX_EPI_GELU_TANH.  out = epi(x . dequant(W)^T +
+ * bias).  Covers DiTLinear.applyF32in's quantized branch
+ * (DiTModel.swift:102-125: castF32toF16, matmulQ4FastF32, then addBiasF32F32,
+ * Ops.swift:1780-1791) and the GELU-tanh that follows it in the DiT
+ * feed-forward (DiTModel.swift:953, Kernels.swift:1774-1783).  fp32 x is
+ * cast as the reference's cast_f32_to_f16 does, half(clamp(x, -65504,
+ * 65504)) (Kernels.swift:816-822), inside the GEMM as it stages x (no
+ * separate cast pass; x is then read as 4-byte values, 16-byte aligned); it
+ * always runs the MFMA GEMM.  bf16 x is multiplied as bf16. */
 int sltx_matmul_q4_ex(const void* x, int32_t x_dtype, const sltx_q4_weight* w, const float* bias,
                       int32_t epilogue, void* out, int32_t out_dtype, int32_t M, int32_t N,
                       void* stream);

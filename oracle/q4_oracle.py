@@ -71,6 +71,16 @@ def matmul_q4_f64(x: np.ndarray, w: np.ndarray, scales: np.ndarray, biases: np.n
     return np.asarray(x, dtype=np.float64) @ dequant_f64(w, scales, biases, group).T
 
 
+def cast_f32_to_f16_ref(x: np.ndarray) -> np.ndarray:
+    """cast_f32_to_f16 (Kernels.swift:816-822): half(clamp(x, -65504, 65504)),
+    the fp32 -> fp16 cast DiTLinear.applyF32in runs before matmulQ4FastF32
+    (DiTModel.swift:104-110).  Metal's clamp is fmin(fmax(x, lo), hi), and
+    fmax / fmin return the other operand when one is NaN, so NaN becomes
+    -65504; the cast rounds to nearest even."""
+    x = np.asarray(x, dtype=np.float32)
+    return np.fmin(np.fmax(x, np.float32(-65504.0)), np.float32(65504.0)).astype(np.float16)
+
+
 def silu_mul_f64(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     """silu(a)*b in fp64 (Kernels.swift:90-98 computes it in fp32)."""
     a = np.asarray(a, dtype=np.float64)

@@ -389,13 +389,15 @@ def matmul_q4_silu_mul(x, gate: Q4Weight, up: Q4Weight, M, K, N, out=None, strea
 
 def matmul_q4_ex(x, w: Q4Weight, M, N, out_dtype=None, bias=None, epilogue=SLTX_EPI_NONE,
                  out=None, stream=None):
-    """epi(x . dequant(W)^T + bias) with x fp16/bf16 and out fp16/bf16/fp32
-    (DiTLinear.applyF32in q4 branch, DiTModel.swift:102-125, + GELU-tanh)."""
+    """epi(x . dequant(W)^T + bias) with x fp16/bf16/fp32 and out
+    fp16/bf16/fp32 (DiTLinear.applyF32in q4 branch, DiTModel.swift:102-125,
+    + GELU-tanh); fp32 x is cast to fp16 with the +-65504 clamp of
+    cast_f32_to_f16 (Kernels.swift:816-822) inside the GEMM."""
     torch = _torch()
     if out is None:
         out = _new((M, N), out_dtype or torch.float32, x)
     if M > 0 and N > 0 and _shape_ok(w.K, w.group_size):
-        _need(x, "x", M * w.K, (torch.float16, torch.bfloat16))
+        _need(x, "x", M * w.K, (torch.float16, torch.bfloat16, torch.float32))
         _need_w(w, N)
         _need(out, "out", M * N, (torch.float16, torch.bfloat16, torch.float32))
         if bias is not None:

@@ -220,6 +220,7 @@ int release_workspace(hipStream_t st) {
 // is the faster route in every case; gated pairs and M > 4 are faster on the
 // small-M route, up to M = 16.
 int gemm_route(const GemmParams& p, bool a_bf16, NarrowPlan* np, SkinnyPlan* sp, WidePlan* wp) {
+    if (p.a_f32) return SLTX_ROUTE_GEMM;   // the only kernel that casts fp32 activations
     if (p.M > 32) return wide_plan(p, a_bf16, wp) ? SLTX_ROUTE_WIDE : SLTX_ROUTE_GEMM;
     const bool narrow = narrow_plan(p, a_bf16, np);
     const bool skinny = skinny_plan(p, a_bf16, sp);
@@ -250,7 +251,7 @@ int gemm_route(const GemmParams& p, bool a_bf16, NarrowPlan* np, SkinnyPlan* sp,
 int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w0,
              const sltx_q4_weight* w1, const float* bias, int epilogue, void* out, int y_dtype,
              int M, int K, int N, hipStream_t st, const void* residual = nullptr) {
-    GemmParams p;
+    GemmParams p{};
     p.a = x;
     p.w0 = w0.weight;
     p.s0 = w0.scales;
@@ -272,6 +273,7 @@ int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w
     p.ws = nullptr;
     p.splits = 1;
     p.split_tiles = 0;
+    p.a_f32 = x_dtype == kF32 ? 1 : 0;
     NarrowPlan np;
     SkinnyPlan sp;
     WidePlan wp;
@@ -442,8 +444,9 @@ int sltx_matmul_q4_ex(const void* x, int32_t x_dtype, const sltx_q4_weight* w, c
                       void* stream) {
     const char* fn = "sltx_matmul_q4_ex";
     if (!w) return fail(kErrInvalid, "%s: null weight descriptor", fn);
-    if (x_dtype != kF16 && x_dtype != kBF16)
-        return fail(kErrInvalid, "%s: x_dtype %d must be SLTX_F16 or SLTX_BF16", fn, x_dtype);
+    if (x_dtype != kF16 && x_dtype != kBF16 && x_dtype != kF32)
+        return fail(kErrInvalid, "%s: x_dtype %d must be SLTX_F16, SLTX_BF16 or SLTX_F32", fn,
+                    x_dtype);
     if (out_dtype != kF16 && out_dtype != kBF16 && out_dtype != kF32)
         return fail(kErrInvalid, "%s: out_dtype %d invalid", fn, out_dtype);
     if (epilogue != kEpiNone && epilogue != kEpiGeluTanh)
@@ -453,7 +456,7 @@ int sltx_matmul_q4_ex(const void* x, int32_t x_dtype, const sltx_q4_weight* w, c
     if (!aligned(out, out_dtype == kF32 ? 4 : 2)) return fail(kErrInvalid, "%s: misaligned out", fn);
     if (bias && !aligned(bias, 4)) return fail(kErrInvalid, "%s: misaligned bias", fn);
     if (M == 0 || N == 0) return kOk;
-    if ((rc = check_out_alias(fn, x, (size_t)M * w->K * 2, out,
+    if ((rc = check_out_alias(fn, x, (size_t)M * w->K * (x_dtype == kF32 ? 4 : 2), out,
                               (size_t)M * N * (out_dtype == kF32 ? 4 : 2))) != kOk)
         return rc;
     if ((rc = ensure_device()) != kOk) return rc;
@@ -764,7 +767,7 @@ int sltx_matmul_q4_residual_rms_norm(const void* x, const sltx_q4_weight* w, con
         return fail(kErrInvalid, "%s: an output overlaps x", fn);
     if ((rc = ensure_device()) != kOk) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    GemmParams p;
+    GemmParams p{};
     p.a = x;
     p.w0 = w->weight;
     p.s0 = w->scales;
@@ -803,7 +806,8 @@ int sltx_gemm_route(int32_t M, int32_t N, int32_t K, int32_t group_size, int32_t
         return fail(kErrInvalid, "%s: M, N must be >= 1 and K a positive multiple of 32", fn);
     if (group_size <= 0 || K % group_size != 0 || log2_group(group_size) < 0)
         return fail(kErrInvalid, "%s: group_size must be 32, 64 or 128 and divide K", fn);
-    if (x_dtype != kF16 && x_dtype != kBF16) return fail(kErrInvalid, "%s: bad x_dtype", fn);
+    if (x_dtype != kF16 && x_dtype != kBF16 && x_dtype != kF32)
+        return fail(kErrInvalid, "%s: bad x_dtype", fn);
     // operands at 256-byte aligned stand-in addresses: the plans read only
     // the shape and the pointers' alignment
     const void* al = reinterpret_cast<const void*>(uintptr_t{256});
@@ -821,6 +825,7 @@ int sltx_gemm_route(int32_t M, int32_t N, int32_t K, int32_t group_size, int32_t
     p.y_dtype = kF16;
     p.epilogue = gated ? kEpiSiluMul : kEpiNone;
     p.splits = 1;
+    p.a_f32 = x_dtype == kF32 ? 1 : 0;
     NarrowPlan np;
     SkinnyPlan sp;
     WidePlan wp;

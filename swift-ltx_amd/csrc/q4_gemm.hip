@@ -123,8 +123,15 @@ struct SB {
 // copy with a fixed count per k-tile and exact wait counts.  GEN = true: any
 // supported shape (K % 32 == 0, group 32/64/128): scale/bias staged through
 // registers, clamped tails, zero-filled A past K, full waits.
-template <int WM, bool BF16, bool SILU, bool GEN, bool SPLIT>
+// A32: fp32 activations (the generic path only), each cast to fp16 as
+// half(clamp(x, -65504, 65504)) -- cast_f32_to_f16, Kernels.swift:816-822,
+// which DiTLinear.applyF32in runs before matmulQ4FastF32
+// (DiTModel.swift:104-110) -- while it is staged: a k-tile's A is loaded into
+// registers three k-tiles ahead, then cast and written to its LDS stage at
+// the end of the k-tile that loaded it.
+template <int WM, bool BF16, bool SILU, bool GEN, bool SPLIT, bool A32 = false>
 __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
+    static_assert(!A32 || (GEN && !BF16 && !SILU), "fp32 activations: the generic fp16 path");
     constexpr int BM = 64 * WM;
     constexpr int TM = BM / 32;                // MFMA tiles along M per wave
     constexpr int A_STAGE = BM * BK / 8;       // 16-byte slots per A stage
@@ -283,15 +290,46 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
     // load_a / zero_a_tail / fetch_w take the tile index t with its value mod
     // 4 as a compile-time constant TP; load_wp / store_sb take the super-stage
     // with its parity.
-    auto load_a = [&](auto tp, int t) {   // NA vector-memory ops (tiles past the end re-read the last)
+    // A32: this thread's eight fp32 values of each of its NA slots.
+    f32x4 a32[A32 ? NA : 1][2];
+    const float* const A32src = reinterpret_cast<const float*>(p.a);
+    auto load_a = [&](auto tp, int t) {   // NA (A32: 2 NA) vector-memory ops (tiles past the end re-read the last)
         const int k0 = min(t, nk - 1) * BK;
         u32x4* stage = a_stage(tp);
 #pragma unroll
         for (int i = 0; i < NA; ++i) {
             int off = k0;
             if (GEN && k0 + a_col8[i] >= Kl) off = Kl - 8 - a_col8[i];
-            __builtin_amdgcn_global_load_lds((const void*)(a_src[i] + off),
-                                             (lds_ptr_t)(stage + (wn + NW * i) * 64), 16, 0, 0);
+            if constexpr (A32) {
+                // the slot's fp16 offset in A is also its fp32 element offset
+                const f32x4* src = reinterpret_cast<const f32x4*>(
+                    A32src + (a_src[i] - reinterpret_cast<const uint16_t*>(p.a)) + off);
+                a32[i][0] = src[0];
+                a32[i][1] = src[1];
+            } else {
+                __builtin_amdgcn_global_load_lds((const void*)(a_src[i] + off),
+                                                 (lds_ptr_t)(stage + (wn + NW * i) * 64), 16, 0, 0);
+            }
+        }
+    };
+    // A32: tile t's slots from the registers load_a filled, cast with the
+    // clamp, into stage tp (zeros past K).
+    auto store_a32 = [&](auto tp, int t) {
+        if constexpr (A32) {
+            const int k0 = t * BK;
+            u32x4* stage = a_stage(tp);
+#pragma unroll
+            for (int i = 0; i < NA; ++i) {
+                u32x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float lo = a32[i][e >> 1][2 * (e & 1)], hi = a32[i][e >> 1][2 * (e & 1) + 1];
+                    o[e] = (uint32_t)f2h(fminf(fmaxf(lo, -65504.0f), 65504.0f)) |
+                           ((uint32_t)f2h(fminf(fmaxf(hi, -65504.0f), 65504.0f)) << 16);
+                }
+                if (k0 + a_col8[i] >= Kl) o = u32x4{0u, 0u, 0u, 0u};
+                stage[(wn + NW * i) * 64 + lane] = o;
+            }
         }
     };
     auto zero_a_tail = [&](auto tp, int t) {   // GEN: after the copy of tile t landed
@@ -404,7 +442,23 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
     // during it (the wait at the end of k-tile 0 covers them).  Generic path:
     // scale/bias of super-stage 0 to LDS, super-stage 1's stay in registers
     // and are written at the end of k-tile 0.
-    if constexpr (GEN) {
+    if constexpr (A32) {
+        // one tile of A registers: tiles 0, 1, 2 one after another
+        load_wp(I0{}, 0);
+        load_wp(I1{}, 1);
+        load_sb(0);
+        load_a(I0{}, 0);
+        SLTX_WAIT_VMCNT(0);
+        store_sb(I0{});
+        store_a32(I0{}, 0);
+        load_sb(1);
+        load_a(I1{}, 1);
+        SLTX_WAIT_VMCNT(0);
+        store_a32(I1{}, 1);
+        load_a(I2{}, 2);
+        SLTX_WAIT_VMCNT(0);
+        store_a32(I2{}, 2);
+    } else if constexpr (GEN) {
         load_a(I0{}, 0);
         load_a(I1{}, 1);
         load_a(I2{}, 2);
@@ -511,7 +565,12 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
         // vmcnt retires in issue order.  Even kt issued only A tile kt+3;
         // odd kt issued A tile kt+3 and super-stage (kt+3)/2 after A tile
         // kt+2 (issued at kt-1, which issued nothing else).
-        if constexpr (GEN) {
+        if constexpr (A32) {
+            // tile kt+3 (loaded at the start of this k-tile) into its stage,
+            // which k-tile kt-1 read before the last barrier
+            SLTX_WAIT_VMCNT(0);
+            store_a32(N3{}, kt + NSA - 1);
+        } else if constexpr (GEN) {
             SLTX_WAIT_VMCNT(0);
             zero_a_tail(std::integral_constant<int, (TP + 2) & 3>{}, kt + 2);
         } else if constexpr (ODD) {
@@ -747,7 +806,9 @@ static GemmPlan plan_gemm(const GemmParams& p, bool allow_split, bool partials =
     const size_t nw = silu ? 2 * (size_t)p.N : (size_t)p.N;
     GemmPlan best = {2, 0, tiles_n, 1, nk, 0};
     double best_us = 1e30;
-    for (int wm = 2; wm <= 3; ++wm) {
+    // fp32 activations hold a k-tile of A in registers: the 192-row tile
+    // would spill, so they take the 128-row tile only
+    for (int wm = 2; wm <= (p.a_f32 ? 2 : 3); ++wm) {
         const int bm = 64 * wm;
         const long tiles_m = (p.M + bm - 1) / bm;
         const long tiles = tiles_m * tiles_n;
@@ -782,6 +843,13 @@ size_t gemm_partials_workspace_bytes(const GemmParams& p) { return plan_gemm(p, 
 
 template <int WM, bool BF16, bool SPLIT>
 static void launch_wm(const GemmParams& p, bool silu, long grid, hipStream_t st) {
+    if constexpr (WM == 2) {
+        if (p.a_f32) {
+            hipLaunchKernelGGL((q4_gemm_kernel<2, false, false, true, SPLIT, true>), dim3(grid),
+                               dim3(kThreads), 0, st, p);
+            return;
+        }
+    }
     // The fixed-count kernel needs whole 128-k super-stages and group size 64
     // (scales and biases move as dword pairs of groups, so their arrays must
     // also be 4-byte aligned; 2-byte aligned ones take the generic kernel,

@@ -57,6 +57,7 @@ struct GemmParams {
     int splits;             // filled by launch_gemm
     int split_tiles;        // k-tiles per split (even), filled by launch_gemm
     uint32_t nib_mask;      // 0x0F0F0F0F, set by the launchers (a run-time value: see q4_gemm.hip)
+    int a_f32;              // a is fp32, cast to fp16 with the +-65504 clamp as it is staged (GEMM only)
 };
 
 // 4-bit embedding gather (q4_embed.hip).

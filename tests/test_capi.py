@@ -111,7 +111,7 @@ def test_silu_mul_fused_validation(pkg):
 
 
 @pytest.mark.parametrize("args,frag", [
-    (dict(x_dtype=2), "x_dtype"),
+    (dict(x_dtype=3), "x_dtype"),
     (dict(out_dtype=7), "out_dtype"),
     (dict(epilogue=1), "epilogue"),
     (dict(bias=ALIGNED + 2), "misaligned bias"),

@@ -256,6 +256,26 @@ def test_bf16_rounding(oracle):
 # leaves it bit-identical (eps = 0), b = 0 reduces the residual form to the
 # plain one, and the residual equals numpy's own fp16 addition.
 
+def test_cast_f32_to_f16_clamp_known_values(oracle):
+    """cast_f32_to_f16 (Kernels.swift:816-822) on values whose fp16 results
+    are fixed by hand: the clamp holds the finite range at the largest fp16,
+    65504 (without it 65520 and beyond round to infinity), NaN takes the
+    lower bound (Metal's fmax returns the non-NaN operand), and inside the
+    range the cast is round-to-nearest-even: 1 + 2^-11 is a tie that stays
+    at 1, 1 + 3 * 2^-11 rounds up to 1 + 2^-9, 2^-24 is the smallest fp16
+    subnormal and 2^-26 rounds to zero."""
+    x = np.array([1e6, -1e6, 65520.0, -65520.0, 65519.0, 70000.0, np.inf, -np.inf, np.nan,
+                  1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, 2.0 ** -24, 2.0 ** -26, -2.5, 0.0],
+                 dtype=np.float32)
+    want = [65504.0, -65504.0, 65504.0, -65504.0, 65504.0, 65504.0, 65504.0, -65504.0, -65504.0,
+            1.0, 1.0 + 2.0 ** -9, 2.0 ** -24, 0.0, -2.5, 0.0]
+    got = oracle.cast_f32_to_f16_ref(x)
+    assert got.dtype == np.float16
+    assert got.astype(np.float64).tolist() == want
+    # without the clamp the same inputs overflow: the clamp is what keeps them finite
+    assert np.isinf(np.float32(65520.0).astype(np.float16))
+
+
 def test_rms_norm_constant_vector():
     from oracle import q4_oracle as o
     w = np.array([0.5, 1.25, -2.0, 3.0] * 16, dtype=np.float32)
