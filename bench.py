@@ -38,7 +38,7 @@ extra      = the other BASELINE configs and the paths around the GEMV, each
              rotated copies), config 4a (lm_head GEMV over 10 rotated copies,
              2.2 GB), the fused-norm decode layer, the
              decode token (greedy / sampled), the 750-token prefill, token
-             selection, small M (2..128) and the M > 1 MFMA GEMMs (configs 3,
+             selection, small M (2..256) and the M > 1 MFMA GEMMs (configs 3,
              4b, 5) against the 2.5 PFLOP/s dense fp16/bf16 peak.
 configs    = the last key of the line: every BASELINE config as us and
              fraction of its roofline (a log that keeps only the line's tail
@@ -418,6 +418,12 @@ def config_summary(value, steps, wall, layer_st, dom_us, legs):
         return {"us": st["median_us"], "frac_mfma": st["frac_mfma"]} if st else None
 
     gemm = legs.get("gemm", {})
+
+    def small(name, M):
+        st = legs.get("small_m", {}).get(name, {}).get(f"m{M}")
+        return {"us": st["median_us"], "frac_hbm": st["frac_hbm"], "frac_mfma": st["frac_mfma"],
+                "route": st["route"]} if st else None
+
     return {
         "c1_q_proj_gemv": hbm(legs.get("config1_q_proj_gemv_m1")),
         "c2_decode_layer": {"value_us_per_step": round(1e6 * wall / steps, 3),
@@ -434,6 +440,9 @@ def config_summary(value, steps, wall, layer_st, dom_us, legs):
         "c4b_lm_head_gemm_m750": mfma(gemm.get("lm_head_gemm_m750")),
         "c5_dit_up_gelu_m6144": mfma(gemm.get("dit_ffn_up_gelu_m6144_bf16")),
         "c5_dit_down_m6144": mfma(gemm.get("dit_ffn_down_m6144_bf16")),
+        "c5_dit_up_m6144_f32in": mfma(gemm.get("dit_ffn_up_gelu_m6144_f32in")),
+        "m128_llama_gate_up_silu": small("llama_gate_up_silu", 128),
+        "m128_t5_ffn_wo": small("t5_ffn_wo", 128),
     }
 
 
@@ -738,7 +747,8 @@ def token_select_leg(pkg, torch, gen, dev, vocab=128256):
 
 def gemm_legs(pkg, torch, gen, dev, cap, min_gb=2.0):
     """BASELINE configs 3 (M = 750 prefill gate/up + SiLU and down), 4b
-    (lm_head M = 750) and 5 (LTX DiT FFN, M = 6144 bf16): graphs of launches
+    (lm_head M = 750) and 5 (LTX DiT FFN, M = 6144 bf16, and the up projection
+    with fp32 activations): graphs of launches
     over weight copies rotated to >= min_gb GB (the measurement rule: one
     resident weight would be served from the 256 MB MALL, as a prefill's
     layers never are), then, for comparison, `resident`: the same launch
@@ -793,19 +803,26 @@ def gemm_legs(pkg, torch, gen, dev, cap, min_gb=2.0):
         lambda w: pkg.matmul_q4_ex(hd, w, Md, 2048, out=yd),
         lambda: q4(pkg, torch, 2048, 8192, gen, dev),
         2 * Md * 2048 * 8192, 5, wb(2048, 8192))
-    del xd, hd, yd
+    # DiTLinear.applyF32in with fp32 activations (DiTModel.swift:102-125):
+    # the cast with the +-65504 clamp runs inside the GEMM's A staging
+    xf = torch.randn(Md, 2048, generator=gen, device=dev)
+    res["dit_ffn_up_gelu_m6144_f32in"] = leg(
+        lambda w: pkg.matmul_q4_ex(xf, w, Md, 8192, out=hd, epilogue=pkg.SLTX_EPI_GELU_TANH),
+        lambda: q4(pkg, torch, 8192, 2048, gen, dev),
+        2 * Md * 8192 * 2048, 5, wb(8192, 2048))
+    del xd, hd, yd, xf
     torch.cuda.empty_cache()
     return res
 
 
-SMALL_M = (2, 4, 8, 32, 128)
+SMALL_M = (2, 4, 8, 32, 64, 128, 256)
 
 
 def small_m_legs(pkg, torch, gen, dev, cap, min_gb=2.0):
-    """Small M (T5 encoder layers at S <= 128, T5Encoder.swift:140-205, and
+    """Small M (T5 encoder layers at S <= 256, T5Encoder.swift:140-205, and
     short prompts): the Llama gate/up + SiLU and q|k|v shapes and the T5-XXL
     shapes (K = 4096: q/k/v/o [4096 x 4096], gelu FFN wi_0/wi_1 [10240 x 4096]
-    in one launch, wo [4096 x 10240]) at M in 2, 4, 8, 32, 128, each over
+    in one launch, wo [4096 x 10240]) at M in SMALL_M, each over
     weight copies rotated to >= min_gb GB, with the route each launch takes.
     GB/s = weight + activation bytes per launch / median time; bound: HBM
     (every weight byte read once per launch)."""

@@ -18,7 +18,8 @@
  *     fill the GPU (split-K, e.g. M=750 x N=3072) and for every
  *     sltx_matmul_q4_residual_rms_norm, the block partials of
  *     sltx_argmax, and the probabilities and candidate list of
- *     sltx_sample_top_p[_state].  There is one per (device, stream),
+ *     sltx_sample_top_p[_state]; and a second one per stream for the fp16
+ *     copy of fp32 activations (sltx_matmul_q4_ex).  There is one per (device, stream),
  *     grown on first need to at least twice its old size; a replaced buffer
  *     is not freed (a graph captured earlier may still use it): every buffer
  *     lives until sltx_release_workspace(stream) or the process exits.  A
@@ -152,9 +153,12 @@ int sltx_matmul_q4_silu_mul(const void* x, const sltx_q4_weight* gate, const slt
  * Ops.swift:1780-1791) and the GELU-tanh that follows it in the DiT
  * feed-forward (DiTModel.swift:953, Kernels.swift:1774-1783).  fp32 x is
  * cast as the reference's cast_f32_to_f16 does, half(clamp(x, -65504,
- * 65504)) (Kernels.swift:816-822), inside the GEMM as it stages x (no
- * separate cast pass; x is then read as 4-byte values, 16-byte aligned); it
- * always runs the MFMA GEMM.  bf16 x is multiplied as bf16. */
+ * 65504)) (Kernels.swift:816-822): for N <= 512 inside the MFMA GEMM as it
+ * stages x; for wider outputs once, into a second per-stream buffer of M*K*2
+ * bytes (allocated like the workspace), after which the fp16 routes run --
+ * the same results as passing that cast as fp16 x.  A stream being captured
+ * whose buffer is missing or too small uses the in-GEMM cast.  bf16 x is
+ * multiplied as bf16. */
 int sltx_matmul_q4_ex(const void* x, int32_t x_dtype, const sltx_q4_weight* w, const float* bias,
                       int32_t epilogue, void* out, int32_t out_dtype, int32_t M, int32_t N,
                       void* stream);

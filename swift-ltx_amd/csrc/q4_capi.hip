@@ -5,6 +5,7 @@
 #include <cstdarg>
 #include <map>
 #include <mutex>
+#include <tuple>
 #include <utility>
 #include <vector>
 #include <string>
@@ -158,6 +159,9 @@ int run_gemv(const char* fn, const void* x, const sltx_q4_weight& w0, const sltx
 // current size.  A stream that is being captured into a graph never
 // allocates: if its workspace is missing or too small the GEMM runs unsplit
 // and sampling returns an error.
+// A stream has two such buffers: slot 0 for the kernels' scratch, slot 1 for
+// the fp16 copy of fp32 activations that sltx_matmul_q4_ex casts before a
+// GEMM whose scratch is in slot 0.
 // sltx_release_workspace frees one stream's buffers (current and retired).
 struct StreamWs {
     void* ptr = nullptr;
@@ -165,13 +169,13 @@ struct StreamWs {
     std::vector<void*> retired;
 };
 std::mutex g_ws_mu;
-std::map<std::pair<int, hipStream_t>, StreamWs> g_ws;
+std::map<std::tuple<int, hipStream_t, int>, StreamWs> g_ws;
 
-float* stream_workspace(hipStream_t st, size_t need) {
+float* stream_workspace(hipStream_t st, size_t need, int slot = 0) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    auto& e = g_ws[{dev, st}];
+    auto& e = g_ws[{dev, st, slot}];
     if (e.bytes >= need) return static_cast<float*>(e.ptr);
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
@@ -195,14 +199,17 @@ int release_workspace(hipStream_t st) {
     std::vector<void*> bufs;
     {
         std::lock_guard<std::mutex> lk(g_ws_mu);
-        auto it = g_ws.find({dev, st});
-        if (it == g_ws.end()) return kOk;
+        auto i0 = g_ws.find({dev, st, 0}), i1 = g_ws.find({dev, st, 1});
+        if (i0 == g_ws.end() && i1 == g_ws.end()) return kOk;
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
             return fail(kErrInvalid, "sltx_release_workspace: the stream is being captured");
-        bufs = it->second.retired;
-        bufs.push_back(it->second.ptr);
-        g_ws.erase(it);
+        for (auto it : {i0, i1}) {
+            if (it == g_ws.end()) continue;
+            bufs.insert(bufs.end(), it->second.retired.begin(), it->second.retired.end());
+            bufs.push_back(it->second.ptr);
+            g_ws.erase(it);
+        }
     }
     // the stream's queued work may still use the buffers
     err = hipStreamSynchronize(st);
@@ -460,8 +467,25 @@ int sltx_matmul_q4_ex(const void* x, int32_t x_dtype, const sltx_q4_weight* w, c
                               (size_t)M * N * (out_dtype == kF32 ? 4 : 2))) != kOk)
         return rc;
     if ((rc = ensure_device()) != kOk) return rc;
-    return run_gemm(fn, x, x_dtype, *w, nullptr, bias, epilogue, out, out_dtype, M, w->K, N,
-                    static_cast<hipStream_t>(stream));
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (x_dtype == kF32 && N > 2 * 256) {
+        // Wide outputs: the fused cast (the GEMM's fp32 staging) would be
+        // repeated by every one of the GEMM's column blocks, so x is cast once
+        // into the stream's second buffer and the fp16 routes run.  Measured
+        // at the DiT up shape (M = 6144, N = 8192, K = 2048): 343 us fused
+        // against 220 us for bf16 x.  Without that buffer (a stream being
+        // captured that never ran this shape eagerly) the fused cast runs.
+        const size_t xb = (size_t)M * w->K * 2;
+        void* x16 = stream_workspace(st, xb, 1);
+        if (x16) {
+            hipError_t e = launch_cast_f32_f16(static_cast<const float*>(x), static_cast<uint16_t*>(x16),
+                                               (long)M * w->K, st);
+            if (e != hipSuccess) return finish(e, fn);
+            return run_gemm(fn, x16, kF16, *w, nullptr, bias, epilogue, out, out_dtype, M, w->K, N,
+                            st);
+        }
+    }
+    return run_gemm(fn, x, x_dtype, *w, nullptr, bias, epilogue, out, out_dtype, M, w->K, N, st);
 }
 
 int sltx_matmul_q4_geglu(const void* x, const sltx_q4_weight* gate, const sltx_q4_weight* up,
@@ -825,7 +849,8 @@ int sltx_gemm_route(int32_t M, int32_t N, int32_t K, int32_t group_size, int32_t
     p.y_dtype = kF16;
     p.epilogue = gated ? kEpiSiluMul : kEpiNone;
     p.splits = 1;
-    p.a_f32 = x_dtype == kF32 ? 1 : 0;
+    // fp32 x: wide outputs are cast once and take the fp16 routes
+    p.a_f32 = x_dtype == kF32 && N <= 2 * 256 ? 1 : 0;
     NarrowPlan np;
     SkinnyPlan sp;
     WidePlan wp;

@@ -213,6 +213,8 @@ hipError_t launch_gemm_residual_rms_norm(GemmParams p, bool a_bf16, const float*
                                          hipStream_t st);
 hipError_t launch_silu_mul(const uint16_t* a, const uint16_t* b, uint16_t* out, long count,
                            hipStream_t st);
+// out = half(clamp(x, -65504, 65504)), count % 8 == 0, 16-byte aligned.
+hipError_t launch_cast_f32_f16(const float* x, uint16_t* out, long count, hipStream_t st);
 // Row-wise RMS norm, optionally of a + b (then the rounded sum goes to res_out).
 hipError_t launch_rms_norm(const uint16_t* a, const uint16_t* b, const float* w, float eps,
                            uint16_t* res_out, uint16_t* out, int rows, int dim, hipStream_t st);
