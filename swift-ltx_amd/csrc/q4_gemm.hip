@@ -656,8 +656,11 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
 
 // Split-K reduction: out[m, n] = epilogue(sum over splits of the partials),
 // summed in split order (deterministic).  SILU reduces gate and up
-// separately before silu(gate) * up.
-template <bool SILU>
+// separately before silu(gate) * up.  S > 0 is the split count, known at
+// compile time: every split's loads are issued before the first add, so the
+// pass pays one memory latency instead of one per split (the adds keep the
+// split order, so the sums are the same bit for bit).  S == 0: any count.
+template <bool SILU, int S>
 __global__ __launch_bounds__(256) void q4_splitk_reduce_kernel(GemmParams p) {
     // each thread: 8 consecutive outputs of one row
     const int nb8 = (p.N + 7) / 8;
@@ -672,6 +675,32 @@ __global__ __launch_bounds__(256) void q4_splitk_reduce_kernel(GemmParams p) {
     float a[8], u[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) a[e] = u[e] = 0.0f;
+    if constexpr (S > 0) {
+        f32x4 q[S][2], r[SILU ? S : 1][2];
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const f32x4* g = reinterpret_cast<const f32x4*>(src + s * stride + n0);
+            q[s][0] = g[0];
+            q[s][1] = g[1];
+            if (SILU) {
+                const f32x4* h = reinterpret_cast<const f32x4*>(src + s * stride + p.N + n0);
+                r[s][0] = h[0];
+                r[s][1] = h[1];
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                a[e] += q[s][0][e];
+                a[4 + e] += q[s][1][e];
+                if (SILU) {
+                    u[e] += r[s][0][e];
+                    u[4 + e] += r[s][1][e];
+                }
+            }
+        }
+    } else {
     for (int s = 0; s < p.splits; ++s, src += stride) {
         if (vin) {
             const f32x4* q = reinterpret_cast<const f32x4*>(src + n0);
@@ -700,6 +729,7 @@ __global__ __launch_bounds__(256) void q4_splitk_reduce_kernel(GemmParams p) {
             }
         }
     }
+    }
     const bool vec = out_vec_ok(p);
     if (SILU) {
         const bool gelu = p.epilogue == kEpiGeluMul;
@@ -722,8 +752,10 @@ __global__ __launch_bounds__(256) void q4_splitk_reduce_kernel(GemmParams p) {
 // The partial sums follow q4_splitk_reduce_kernel and the row sum of squares
 // follows rms_norm_vec_kernel (thread t: pieces t, t + 256, ... of 8 values;
 // wave trees, then the four waves in order), so the results equal the unfused
-// GEMM + reduce + norm sequence bit for bit.
-template <int VPT>
+// GEMM + reduce + norm sequence bit for bit.  S > 0 is the split count,
+// known at compile time: a piece's loads of every split are issued before its
+// first add (same order of adds).
+template <int VPT, int S>
 __global__ __launch_bounds__(256) void q4_splitk_residual_rms_norm_kernel(
     GemmParams p, const float* w, float eps, uint16_t* res_out, uint16_t* out, int sum_rounded) {
     __shared__ float red[4];
@@ -741,13 +773,30 @@ __global__ __launch_bounds__(256) void q4_splitk_residual_rms_norm_kernel(
 #pragma unroll
         for (int e = 0; e < 8; ++e) a[e] = 0.0f;
         const float* q = p.ws + m * p.N + (size_t)v * 8;
-        for (int s = 0; s < p.splits; ++s, q += stride) {
-            const f32x4 q0 = reinterpret_cast<const f32x4*>(q)[0];
-            const f32x4 q1 = reinterpret_cast<const f32x4*>(q)[1];
+        if constexpr (S > 0) {
+            f32x4 qs[S][2];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                a[e] += q0[e];
-                a[4 + e] += q1[e];
+            for (int s = 0; s < S; ++s) {
+                qs[s][0] = reinterpret_cast<const f32x4*>(q + s * stride)[0];
+                qs[s][1] = reinterpret_cast<const f32x4*>(q + s * stride)[1];
+            }
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    a[e] += qs[s][0][e];
+                    a[4 + e] += qs[s][1][e];
+                }
+            }
+        } else {
+            for (int s = 0; s < p.splits; ++s, q += stride) {
+                const f32x4 q0 = reinterpret_cast<const f32x4*>(q)[0];
+                const f32x4 q1 = reinterpret_cast<const f32x4*>(q)[1];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    a[e] += q0[e];
+                    a[4 + e] += q1[e];
+                }
             }
         }
         const f16x8 h = R[v];
@@ -879,14 +928,30 @@ static void launch_dtype(const GemmParams& p, bool a_bf16, bool silu, long grid,
     }
 }
 
+template <bool SILU>
+void launch_reduce_s(const GemmParams& p, dim3 g, hipStream_t st) {
+    // the loads-first form needs whole 16-byte rows (N % 8 == 0)
+    const int s = (p.N & 7) == 0 ? p.splits : 0;
+    switch (s) {
+    case 2: hipLaunchKernelGGL((q4_splitk_reduce_kernel<SILU, 2>), g, dim3(256), 0, st, p); break;
+    case 3: hipLaunchKernelGGL((q4_splitk_reduce_kernel<SILU, 3>), g, dim3(256), 0, st, p); break;
+    case 4: hipLaunchKernelGGL((q4_splitk_reduce_kernel<SILU, 4>), g, dim3(256), 0, st, p); break;
+    case 5: hipLaunchKernelGGL((q4_splitk_reduce_kernel<SILU, 5>), g, dim3(256), 0, st, p); break;
+    case 6: hipLaunchKernelGGL((q4_splitk_reduce_kernel<SILU, 6>), g, dim3(256), 0, st, p); break;
+    case 7: hipLaunchKernelGGL((q4_splitk_reduce_kernel<SILU, 7>), g, dim3(256), 0, st, p); break;
+    case 8: hipLaunchKernelGGL((q4_splitk_reduce_kernel<SILU, 8>), g, dim3(256), 0, st, p); break;
+    default: hipLaunchKernelGGL((q4_splitk_reduce_kernel<SILU, 0>), g, dim3(256), 0, st, p); break;
+    }
+}
+
 hipError_t launch_splitk_reduce(const GemmParams& p, hipStream_t st) {
     const bool silu = p.epilogue == kEpiSiluMul || p.epilogue == kEpiGeluMul;
     const size_t total = (size_t)p.M * ((p.N + 7) / 8);
-    const long rgrid = (long)((total + 255) / 256);
+    const dim3 rgrid((unsigned)((total + 255) / 256));
     if (silu)
-        hipLaunchKernelGGL(q4_splitk_reduce_kernel<true>, dim3(rgrid), dim3(256), 0, st, p);
+        launch_reduce_s<true>(p, rgrid, st);
     else
-        hipLaunchKernelGGL(q4_splitk_reduce_kernel<false>, dim3(rgrid), dim3(256), 0, st, p);
+        launch_reduce_s<false>(p, rgrid, st);
     return hipGetLastError();
 }
 
@@ -912,6 +977,19 @@ hipError_t launch_gemm(GemmParams p, bool a_bf16, hipStream_t st) {
     return hipGetLastError();
 }
 
+template <int VPT>
+void launch_rrn_s(const GemmParams& p, const float* norm_w, float eps, uint16_t* res_out,
+                  uint16_t* norm_out, int sr, hipStream_t st) {
+    const dim3 g(p.M), t(256);
+    switch (p.splits) {
+    case 1: hipLaunchKernelGGL((q4_splitk_residual_rms_norm_kernel<VPT, 1>), g, t, 0, st, p, norm_w, eps, res_out, norm_out, sr); break;
+    case 2: hipLaunchKernelGGL((q4_splitk_residual_rms_norm_kernel<VPT, 2>), g, t, 0, st, p, norm_w, eps, res_out, norm_out, sr); break;
+    case 3: hipLaunchKernelGGL((q4_splitk_residual_rms_norm_kernel<VPT, 3>), g, t, 0, st, p, norm_w, eps, res_out, norm_out, sr); break;
+    case 4: hipLaunchKernelGGL((q4_splitk_residual_rms_norm_kernel<VPT, 4>), g, t, 0, st, p, norm_w, eps, res_out, norm_out, sr); break;
+    default: hipLaunchKernelGGL((q4_splitk_residual_rms_norm_kernel<VPT, 0>), g, t, 0, st, p, norm_w, eps, res_out, norm_out, sr); break;
+    }
+}
+
 // GEMM into fp32 partials (one or more K splits; p.ws holds
 // gemm_partials_workspace_bytes(p)), then the fused reduce + residual +
 // RMSNorm pass.  Requires N % 8 == 0, N <= 16384 and 16-byte aligned rows.
@@ -932,16 +1010,15 @@ hipError_t launch_gemm_residual_rms_norm(GemmParams p, bool a_bf16, const float*
     if (grid > 0x7fffffffL) return hipErrorInvalidValue;
     launch_dtype<true>(p, a_bf16, false, grid, plan.wm, st);
     const int vpt = (p.N / 8 + 255) / 256;
-    const dim3 g(p.M), t(256);
     const int sr = sum_rounded ? 1 : 0;
     if (vpt == 1)
-        hipLaunchKernelGGL(q4_splitk_residual_rms_norm_kernel<1>, g, t, 0, st, p, norm_w, eps, res_out, norm_out, sr);
+        launch_rrn_s<1>(p, norm_w, eps, res_out, norm_out, sr, st);
     else if (vpt == 2)
-        hipLaunchKernelGGL(q4_splitk_residual_rms_norm_kernel<2>, g, t, 0, st, p, norm_w, eps, res_out, norm_out, sr);
+        launch_rrn_s<2>(p, norm_w, eps, res_out, norm_out, sr, st);
     else if (vpt <= 4)
-        hipLaunchKernelGGL(q4_splitk_residual_rms_norm_kernel<4>, g, t, 0, st, p, norm_w, eps, res_out, norm_out, sr);
+        launch_rrn_s<4>(p, norm_w, eps, res_out, norm_out, sr, st);
     else
-        hipLaunchKernelGGL(q4_splitk_residual_rms_norm_kernel<8>, g, t, 0, st, p, norm_w, eps, res_out, norm_out, sr);
+        launch_rrn_s<8>(p, norm_w, eps, res_out, norm_out, sr, st);
     return hipGetLastError();
 }
 

@@ -19,12 +19,13 @@
 //  * A round's X (BM rows x 256 bytes) and packed W (64 rows x 64 bytes) are
 //    copied global -> LDS directly (global_load_lds, 16-byte X pieces, W as
 //    dwords so that the 32 rows a wave reads land in distinct banks) into a
-//    4-stage ring, three rounds ahead.  Every thread issues the same number of
-//    copies per round, so one exact s_waitcnt vmcnt and one LDS-only barrier
-//    per round hand a stage over.  Each stage is its own array, and the loop
-//    is unrolled by 4 so that stage indices are compile-time: the compiler
-//    then knows that reads of one stage do not alias copies in flight into
-//    another.
+//    ring of 3 (TM = 4) or 4 stages, issued a ring's depth ahead.  Every
+//    thread issues the same number of copies per round (rounds past the last
+//    re-read it), so one exact s_waitcnt vmcnt and one LDS-only barrier per
+//    round hand a stage over.  Each stage is its own array, and the loop is
+//    unrolled by the ring depth so that stage indices are compile-time: the
+//    compiler then knows that reads of one stage do not alias copies in
+//    flight into another.
 //  * The block's scales and biases (64 rows x its K range's groups, at most
 //    64 groups) are read once into an LDS slab as scale | bias << 16 words.
 //  * After the last round the 8 waves' tiles are summed in LDS in a fixed
@@ -33,6 +34,7 @@
 //    K split across blocks the sums go to the fp32 workspace instead and the
 //    split-K reduce pass (q4_gemm.hip) applies the epilogue.
 #include <type_traits>
+#include <utility>
 
 #include "q4_common.hpp"
 #include "q4_dequant.hpp"
@@ -54,9 +56,27 @@ constexpr int WRD = RK / 8;         // packed words of a weight row per round (1
 constexpr int WDW = WBN * WRD;      // dwords of a W stage (1024)
 constexpr int NWC = WDW / WT;       // W dword copies per thread per round (2)
 constexpr int SLAB_G = 64;          // scale / bias groups a block holds
-constexpr int NSX = 4;              // ring stages
+// Ring stages by tile height (a stage is BM x 256 bytes of X + 4 KB of W).
+// Measured over the Llama and T5 shapes at M = 33..256: at TM = 4 three
+// stages run 0.1-0.5 us faster than four; at TM = 2 six or seven stages
+// (which the LDS would hold) run 0.5-1.7 us slower than four, three about
+// even.  The loop is not waiting on copy latency (every extra stage only
+// lengthens the prologue, which waits for the slab loads issued behind the
+// first rounds' copies).
+template <int TM>
+constexpr int wide_nsx() { return TM == 4 ? 3 : 4; }
 
 #define WIDE_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+
+// f(integral_constant<int, i>) for i = 0 .. N - 1, unrolled
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_seq(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_seq(f, std::make_integer_sequence<int, N>{});
+}
 
 struct WideArgs {
     int mrows;    // activation rows of this launch's M-blocks (the last may hold fewer)
@@ -107,19 +127,25 @@ __global__ __launch_bounds__(WT, 1) void q4_wide_kernel(GemmParams p, WideArgs w
     constexpr int NXC = XS / WT;        // X copies per thread per round
     static_assert(NXC * WT == XS && NWC * WT == WDW, "whole copies");
     constexpr int CPR = NXC + NWC;      // vector-memory ops per thread per round
+    constexpr int NSX = wide_nsx<TM>(); // ring stages
+    static_assert(NSX == 3 || NSX == 4, "ring depth");
     static_assert(XS * 16 >= 2 * 8 * 1024, "two waves' 32-row tiles fit one X stage");
+    // One array per stage (stage indices are compile-time, so the compiler
+    // sees that reads of one stage do not alias copies into another).  The
+    // fourth X array exists at NSX = 3 too: the K-groups' sums are staged in
+    // all four.
     __shared__ u32x4 xs0[XS], xs1[XS], xs2[XS], xs3[XS];
-    __shared__ uint32_t ws0[WDW], ws1[WDW], ws2[WDW], ws3[WDW];
+    __shared__ uint32_t ws0[WDW], ws1[WDW], ws2[WDW], ws3[NSX > 3 ? WDW : 1];
     __shared__ uint32_t slab[SLAB_G * WBN];
     auto xstage = [&](auto sc) -> u32x4* {
-        constexpr int S = decltype(sc)::value & 3;
+        constexpr int S = decltype(sc)::value % NSX;
         if constexpr (S == 0) return xs0;
         else if constexpr (S == 1) return xs1;
         else if constexpr (S == 2) return xs2;
         else return xs3;
     };
     auto wstage = [&](auto sc) -> uint32_t* {
-        constexpr int S = decltype(sc)::value & 3;
+        constexpr int S = decltype(sc)::value % NSX;
         if constexpr (S == 0) return ws0;
         else if constexpr (S == 1) return ws1;
         else if constexpr (S == 2) return ws2;
@@ -197,13 +223,8 @@ __global__ __launch_bounds__(WT, 1) void q4_wide_kernel(GemmParams p, WideArgs w
                                              (lds_ptr_t)(wd + (tid & ~63) + WT * i), 4, 0, 0);
     };
 
-    using I0 = std::integral_constant<int, 0>;
-    using I1 = std::integral_constant<int, 1>;
-    using I2 = std::integral_constant<int, 2>;
-    using I3 = std::integral_constant<int, 3>;
-    issue(I0{}, 0);
-    issue(I1{}, 1);
-    issue(I2{}, 2);
+    // rounds 0 .. NSX - 2 into their stages
+    static_for<NSX - 1>([&](auto sc) { issue(sc, decltype(sc)::value); });
 
     // ---- scale / bias slab: the block's rows over its K range ----
     // Every load is issued before the first is used (one memory latency for
@@ -240,7 +261,7 @@ __global__ __launch_bounds__(WT, 1) void q4_wide_kernel(GemmParams p, WideArgs w
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    // Round q's operands from stage q % 4: reads() issues the LDS reads (A
+    // Round q's operands from stage q % NSX: reads() issues the LDS reads (A
     // fragments, packed words, scale|bias words), settle() waits for them
     // (one lgkmcnt(0) that every value passes through) and dequantizes the B
     // fragments.
@@ -278,24 +299,24 @@ __global__ __launch_bounds__(WT, 1) void q4_wide_kernel(GemmParams p, WideArgs w
             b[j] = dequant_word_f16(wn[j], s2, b2);
         }
     };
-    // Every wave's copies of the round three after the last one issued have
-    // landed: this thread's were issued before two later rounds' (which may
-    // still be in flight), then the barrier.
+    // Every wave's copies of the next round to read have landed: this
+    // thread's were issued before NSX - 2 later rounds' (which may still be
+    // in flight), then the barrier.
     auto ready = [&]() {
         __builtin_amdgcn_s_waitcnt(vmcnt_only((NSX - 2) * CPR));
         WIDE_LDS_BARRIER();
     };
     // Round q (operands in a, b): round q + 1's stage is waited for, the
-    // stage round q read is refilled with round q + 4, round q + 1's LDS
+    // stage round q read is refilled with round q + NSX, round q + 1's LDS
     // reads are issued, then round q's MFMAs run while they return, and
     // round q + 1's B fragments are dequantized behind the MFMAs.
     auto round = [&](auto sc, int q) {
-        constexpr int S = decltype(sc)::value & 3;
+        constexpr int S = decltype(sc)::value % NSX;
         const bool more = q + 1 < nr;
         if (more) {
             ready();
             issue(std::integral_constant<int, S>{}, q + NSX);
-            reads(std::integral_constant<int, (S + 1) & 3>{}, q + 1);
+            reads(std::integral_constant<int, (S + 1) % NSX>{}, q + 1);
         }
 #pragma unroll
         for (int i = 0; i < TM; ++i)
@@ -305,19 +326,15 @@ __global__ __launch_bounds__(WT, 1) void q4_wide_kernel(GemmParams p, WideArgs w
     };
 
     ready();
-    reads(I0{}, 0);
+    reads(std::integral_constant<int, 0>{}, 0);
     settle();
-    issue(I3{}, 3);
+    issue(std::integral_constant<int, NSX - 1>{}, NSX - 1);
     int q = 0;
-    for (; q + 3 < nr; q += 4) {
-        round(I0{}, q);
-        round(I1{}, q + 1);
-        round(I2{}, q + 2);
-        round(I3{}, q + 3);
-    }
-    if (q < nr) round(I0{}, q);
-    if (q + 1 < nr) round(I1{}, q + 1);
-    if (q + 2 < nr) round(I2{}, q + 2);
+    for (; q + NSX - 1 < nr; q += NSX)
+        static_for<NSX>([&](auto sc) { round(sc, q + decltype(sc)::value); });
+    static_for<NSX - 1>([&](auto sc) {
+        if (q + decltype(sc)::value < nr) round(sc, q + decltype(sc)::value);
+    });
 
     // ---- the K-groups' sums, one 32-row tile at a time ----
     // Wave w's two tiles go to X stage w / 2 at float (w % 2) * 2048, as
