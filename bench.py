@@ -804,7 +804,8 @@ def gemm_legs(pkg, torch, gen, dev, cap, min_gb=2.0):
         lambda: q4(pkg, torch, 2048, 8192, gen, dev),
         2 * Md * 2048 * 8192, 5, wb(2048, 8192))
     # DiTLinear.applyF32in with fp32 activations (DiTModel.swift:102-125):
-    # the cast with the +-65504 clamp runs inside the GEMM's A staging
+    # the cast with the +-65504 clamp, one pass into a per-stream buffer at
+    # this output width, then the fp16 GEMM
     xf = torch.randn(Md, 2048, generator=gen, device=dev)
     res["dit_ffn_up_gelu_m6144_f32in"] = leg(
         lambda w: pkg.matmul_q4_ex(xf, w, Md, 8192, out=hd, epilogue=pkg.SLTX_EPI_GELU_TANH),
