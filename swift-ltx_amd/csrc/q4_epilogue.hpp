@@ -144,6 +144,16 @@ __device__ __forceinline__ void epi_storev(const GemmParams& p, size_t row, int 
     }
     if (p.epilogue == kEpiResidual) {
         // fp16 output only: the projection rounded, added to the residual, rounded
+        if (NV == 4 && (p.N & 3) == 0 && n0 + 4 <= p.N &&
+            ((reinterpret_cast<uintptr_t>(p.y) | reinterpret_cast<uintptr_t>(p.residual)) & 7) == 0) {
+            const uint2 r = *reinterpret_cast<const uint2*>(p.residual + row + n0);
+            const uint32_t o0 = residual_add_f16((uint16_t)(r.x & 0xFFFFu), v[0]) |
+                                ((uint32_t)residual_add_f16((uint16_t)(r.x >> 16), v[1]) << 16);
+            const uint32_t o1 = residual_add_f16((uint16_t)(r.y & 0xFFFFu), v[2]) |
+                                ((uint32_t)residual_add_f16((uint16_t)(r.y >> 16), v[3]) << 16);
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.y) + row + n0) = make_uint2(o0, o1);
+            return;
+        }
 #pragma unroll
         for (int e = 0; e < NV; ++e)
             if (n0 + e < p.N)

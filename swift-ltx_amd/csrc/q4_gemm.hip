@@ -129,9 +129,17 @@ struct SB {
 // (DiTModel.swift:104-110) -- while it is staged: a k-tile's A is loaded into
 // registers three k-tiles ahead, then cast and written to its LDS stage at
 // the end of the k-tile that loaded it.
-template <int WM, bool BF16, bool SILU, bool GEN, bool SPLIT, bool A32 = false>
+// PERSIST: the fast path over more output tiles than one round of blocks.
+// Each block walks a fixed list of tiles (see the tile selection below);
+// the copy ring runs on across tile boundaries -- the last three k-tiles of
+// a tile issue the next tile's first A tiles and packed-W / scale-bias
+// super-stages -- and the register epilogue of one tile runs while those
+// copies are in flight, so neither the next tile's first memory latency nor
+// its stores stall the MFMA stream for long.
+template <int WM, bool BF16, bool SILU, bool GEN, bool SPLIT, bool A32 = false, bool PERSIST = false>
 __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
     static_assert(!A32 || (GEN && !BF16 && !SILU), "fp32 activations: the generic fp16 path");
+    static_assert(!PERSIST || (!GEN && !SPLIT && !A32), "persistent tiles: the fast unsplit path");
     constexpr int BM = 64 * WM;
     constexpr int TM = BM / 32;                // MFMA tiles along M per wave
     constexpr int A_STAGE = BM * BK / 8;       // 16-byte slots per A stage
@@ -169,26 +177,43 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
     };
 
     // ---- tile selection (XCD-aware) ----
+    // The 8 XCDs receive workgroups round-robin (block b on XCD b % 8).  One
+    // tile per block: consecutive logical tiles (M fastest) go to one XCD.
+    // PERSIST (grid a multiple of 8): XCD x owns logical tiles [x T8,
+    // min((x + 1) T8, T)), T8 = ceil(T / 8), and its i-th block takes tiles
+    // x T8 + i, + G / 8, + 2 G / 8, ... (G = grid): the blocks of one XCD
+    // work on neighbouring tiles, which share weight columns, at any time.
     const int ntiles = p.tiles_m * p.tiles_n;
     int logical = blockIdx.x;
-    if ((gridDim.x & 7) == 0) {
-        const int per_xcd = gridDim.x >> 3;
-        logical = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    int pstride = 0, pend = 0;
+    if constexpr (PERSIST) {
+        const int per_x = (ntiles + 7) >> 3;
+        logical = (blockIdx.x & 7) * per_x + (blockIdx.x >> 3);
+        pend = min(((int)(blockIdx.x & 7) + 1) * per_x, ntiles);
+        pstride = gridDim.x >> 3;
+        if (logical >= pend) return;
+    } else {
+        if ((gridDim.x & 7) == 0) {
+            const int per_xcd = gridDim.x >> 3;
+            logical = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+        }
+        if (logical >= ntiles * (SPLIT ? p.splits : 1)) return;
     }
-    if (logical >= ntiles * (SPLIT ? p.splits : 1)) return;
     const int split = SPLIT ? logical / ntiles : 0;
     const int tile = SPLIT ? logical % ntiles : logical;
-    const int tile_m = tile % p.tiles_m;
-    const int tile_n = tile / p.tiles_m;
     // K range of this block: k-tiles [kb, kb + nk); Kl = its extent in k.
     const int nk_all = (p.K + BK - 1) / BK;
     const int kb = SPLIT ? split * p.split_tiles : 0;
     const int nk = SPLIT ? min(p.split_tiles, nk_all - kb) : nk_all;
     const int Kl = min(p.K - kb * BK, nk * BK);
     const int nss = (nk + 1) / 2;   // super-stages (pairs of k-tiles)
-    const int m0 = tile_m * BM;
     // SILU: a tile covers 128 output columns, as 128 gate rows + 128 up rows.
-    const int n0 = tile_n * (SILU ? BN / 2 : BN);
+    // m0 / n0: the tile the copies are reading (PERSIST: the next one from
+    // its first prefetch on); em0 / en0: the tile the accumulators hold.
+    int m0 = (tile % p.tiles_m) * BM;
+    int n0 = (tile / p.tiles_m) * (SILU ? BN / 2 : BN);
+    int em0 = m0, en0 = n0;
+    bool has_next = PERSIST && logical + pstride < pend;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wn = tid >> 6;
@@ -196,14 +221,16 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
     const int GP = 4 >> p.gshift;   // scale/bias groups per 128 k (g = 32, 64, 128)
 
     // Virtual W row -> matrix row (and which matrix, for SILU).  Wave wn owns
-    // virtual rows 64wn..64wn+63 as two 32-row MFMA tiles; with SILU tile 0 is
-    // gate and tile 1 up for the same 32 output columns.  Rows past N are
-    // clamped to row 0: computed, never stored.
+    // virtual rows 32wn..32wn+31 (one 32-row MFMA tile); with SILU its rows
+    // 0-15 are the gate rows and 16-31 the up rows of the same 16 output
+    // columns, n0 + 16wn .. +15, so that both halves of each output land in
+    // one lane (see the epilogue).  Rows past N are clamped to row 0:
+    // computed, never stored.
     auto wrow = [&](int v, const uint32_t*& W, const uint16_t*& S, const uint16_t*& B) {
         int n;
         if (SILU) {
-            const int tn = (v >> 5) & 1;
-            n = n0 + (v >> 6) * 32 + (v & 31);
+            const int tn = (v >> 4) & 1;
+            n = n0 + (v >> 5) * 16 + (v & 15);
             W = tn ? p.w1 : p.w0;
             S = tn ? p.s1 : p.s0;
             B = tn ? p.b1 : p.b0;
@@ -224,15 +251,18 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
     const uint16_t* A = reinterpret_cast<const uint16_t*>(p.a);
     const uint16_t* a_src[NA];
     int a_col8[NA];
+    auto set_a_src = [&]() {
 #pragma unroll
-    for (int i = 0; i < NA; ++i) {
-        const int slot = (wn + NW * i) * 64 + lane;
-        const int row = slot >> 3;
-        const int c16 = (slot & 7) ^ (row & 7) ^ ((row >> 3) & 1);
-        const int m = m0 + row;
-        a_col8[i] = c16 * 8;
-        a_src[i] = A + (size_t)(m < p.M ? m : p.M - 1) * p.K + kb * BK + c16 * 8;
-    }
+        for (int i = 0; i < NA; ++i) {
+            const int slot = (wn + NW * i) * 64 + lane;
+            const int row = slot >> 3;
+            const int c16 = (slot & 7) ^ (row & 7) ^ ((row >> 3) & 1);
+            const int m = m0 + row;
+            a_col8[i] = c16 * 8;
+            a_src[i] = A + (size_t)(m < p.M ? m : p.M - 1) * p.K + kb * BK + c16 * 8;
+        }
+    };
+    set_a_src();
 
     // ---- packed W: direct global -> LDS, two k-tiles (64 B per row) ----
     // Four lanes cover a row's 64 bytes, so each wave-wide copy reads 16 rows
@@ -240,17 +270,20 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
     // logical piece ^ ((row >> 2) & 3) (conflict-free reads below).
     const uint32_t* wp_src[NWP];
     int wp_piece[NWP];
+    auto set_wp_src = [&]() {
 #pragma unroll
-    for (int i = 0; i < NWP; ++i) {
-        const int slot = (wn + NW * i) * 64 + lane;
-        const int row = slot >> 2;
-        const int piece = (slot & 3) ^ ((row >> 2) & 3);
-        const uint32_t* W;
-        const uint16_t *S, *B;
-        const int n = wrow(row, W, S, B);
-        wp_piece[i] = piece;
-        wp_src[i] = W + (size_t)n * (p.K / 8) + kb * (BK / 8) + piece * 4;
-    }
+        for (int i = 0; i < NWP; ++i) {
+            const int slot = (wn + NW * i) * 64 + lane;
+            const int row = slot >> 2;
+            const int piece = (slot & 3) ^ ((row >> 2) & 3);
+            const uint32_t* W;
+            const uint16_t *S, *B;
+            const int n = wrow(row, W, S, B);
+            wp_piece[i] = piece;
+            wp_src[i] = W + (size_t)n * (p.K / 8) + kb * (BK / 8) + piece * 4;
+        }
+    };
+    set_wp_src();
 
     // ---- scale / bias ----
     const int g_base = (2 * kb) >> p.gshift;
@@ -260,14 +293,17 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
     // aligned: groups and g_base are even when K % 128 == 0 and splits cover
     // whole super-stages).
     const uint32_t* sbd_src[NSB];
+    auto set_sbd_src = [&]() {
 #pragma unroll
-    for (int i = 0; i < NSB; ++i) {
-        const int slot = (wn + NW * i) * 64 + lane;
-        const uint32_t* W;
-        const uint16_t *S, *B;
-        const int n = wrow(slot >> 1, W, S, B);
-        sbd_src[i] = reinterpret_cast<const uint32_t*>((slot & 1 ? B : S) + (size_t)n * p.groups + g_base);
-    }
+        for (int i = 0; i < NSB; ++i) {
+            const int slot = (wn + NW * i) * 64 + lane;
+            const uint32_t* W;
+            const uint16_t *S, *B;
+            const int n = wrow(slot >> 1, W, S, B);
+            sbd_src[i] = reinterpret_cast<const uint32_t*>((slot & 1 ? B : S) + (size_t)n * p.groups + g_base);
+        }
+    };
+    set_sbd_src();
     // Generic path: pair v = tid + 256 u is (row v / GP, group v % GP).
     // Consecutive threads read consecutive groups of a row.  Values land in
     // registers and are written to LDS one k-tile later; pairs past the tile
@@ -423,6 +459,13 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
         for (int i = 0; i < TM; ++i) dst[i] = sa[swz(i * 32 + lrow, c16)];
     };
 
+    // TRANS: the packed-weight fragment is the MFMA's A operand, so the
+    // accumulators hold D^T (weight rows along the lane's 16 values) -- the
+    // layout the register epilogue stores from.  Otherwise (the LDS-staged
+    // epilogue) the activation fragment is A, as measured 1.3% faster on the
+    // bf16 DiT down loop (the dequantized fragment is then read as the B
+    // operand).
+    constexpr bool TRANS = PERSIST || SILU;
     f32x16 acc[TM][NT];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -502,12 +545,28 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
         constexpr bool ODD = TP & 1;
         using N1 = std::integral_constant<int, (TP + 1) & 3>;
         using N3 = std::integral_constant<int, (TP + 3) & 3>;
-        load_a(N3{}, kt + NSA - 1);
+        int ta = kt + NSA - 1, tw = (kt + 3) >> 1;   // A tile and super-stage to copy
+        if constexpr (PERSIST) {
+            if (has_next) {
+                // from k-tile nk - 3 on, the copies read the next tile
+                if (kt == nk - (NSA - 1)) {
+                    const int nt = logical + pstride;
+                    m0 = (nt % p.tiles_m) * BM;
+                    n0 = (nt / p.tiles_m) * (SILU ? BN / 2 : BN);
+                    set_a_src();
+                    set_wp_src();
+                    set_sbd_src();
+                }
+                if (ta >= nk) ta -= nk;
+                if (tw >= nss) tw -= nss;
+            }
+        }
+        load_a(N3{}, ta);
         if constexpr (ODD) {
             // super-stage (kt+3)/2: parity ((TP+3) >> 1) & 1
-            load_wp(std::integral_constant<int, ((TP + 3) >> 1) & 1>{}, (kt + 3) >> 1);
-            if constexpr (GEN) load_sb((kt + 3) >> 1);
-            else load_sb_dma(std::integral_constant<int, ((TP + 3) >> 1) & 1>{}, (kt + 3) >> 1);
+            load_wp(std::integral_constant<int, ((TP + 3) >> 1) & 1>{}, tw);
+            if constexpr (GEN) load_sb(tw);
+            else load_sb_dma(std::integral_constant<int, ((TP + 3) >> 1) & 1>{}, tw);
         }
         const u32x4* sa = a_stage(tp);
         const u32x4* sa_n = a_stage(N1{});
@@ -532,7 +591,9 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < NT; ++j) acc[i][j] = mfma32<BF16>(af[b][i], bq[b][j], acc[i][j]);
+                for (int j = 0; j < NT; ++j)
+                    acc[i][j] = TRANS ? mfma32<BF16>(bq[b][j], af[b][i], acc[i][j])
+                                      : mfma32<BF16>(af[b][i], bq[b][j], acc[i][j]);
             if (ks + 1 < BK / 16) {
                 read_a(sa, ks + 1, af[b ^ 1]);
                 dequant(wk_c, sb_c, ks + 1, bq[b ^ 1]);
@@ -584,72 +645,160 @@ __global__ __launch_bounds__(kThreads, 1) void q4_gemm_kernel(GemmParams p) {
         sb_c = sb_n;
     };
 
-    int kt = 0;
-    for (; kt + 3 < nk; kt += 4) {
-        step(I0{}, kt);
-        step(I1{}, kt + 1);
-        step(I2{}, kt + 2);
-        step(I3{}, kt + 3);
-    }
-    if (kt < nk) step(I0{}, kt);
-    if (kt + 1 < nk) step(I1{}, kt + 1);
-    if (kt + 2 < nk) step(I2{}, kt + 2);
-
-    // ---- epilogue ----
-    // Each 32-row accumulator tile is staged through LDS (the A stages, idle
-    // once the last copy into them has landed) as two fp32 [32][128] buffers:
-    // with SILU gate (0) and up (1) of the block's 128 output columns,
-    // otherwise output columns 0-127 (0) and 128-255 (1).  All 512 threads
-    // then apply the epilogue to 8 consecutive columns each (thread t: row
-    // t / 16, columns 8 (t % 16)) and store them as 16-byte vectors.
+    // ---- epilogue, from registers (TRANS) ----
+    // The MFMAs compute D^T = W_tile . A_tile^T, so lane l holds, for activation row em0 + 32 i + l % 32,
+    // the wave's weight rows 8 g + 4 h + r (r = 0..3, h = l / 32) in
+    // acc[i][0][4 g + r]: four consecutive output columns per g.  One
+    // v_permlane32_swap per value gives each lane eight consecutive columns
+    // (groups g and g + 1 of lanes l and l + 32): lane l < 32 columns 0-7 of
+    // the pair, lane l + 32 columns 8-15, stored as one 16-byte vector.  With
+    // SILU, g = 0, 1 are gate rows and g + 2 the up rows of the same columns,
+    // so silu(gate) * up is formed before the swap.  No LDS and no barrier:
+    // a persistent block goes on to the next tile's k-tiles (copied during
+    // the last three of this one) while the stores drain.
     static_assert(NT == 1, "one 32-row MFMA tile of W rows per wave");
-    static_assert(32 * 128 * 4 <= A_STAGE * 16, "a 32 x 128 fp32 tile fits one A stage");
-    SLTX_WAIT_VMCNT(0);
-    SLTX_LDS_BARRIER();
-    float* const eb0 = reinterpret_cast<float*>(lds_a0);
-    float* const eb1 = reinterpret_cast<float*>(lds_a1);
-    float* const wdst = (SILU ? (wn & 1) : (wn >> 2)) ? eb1 : eb0;
-    const int wcol = (SILU ? (wn >> 1) : (wn & 3)) * 32 + lrow;
-    const int er = tid >> 4, ec = (tid & 15) * 8;
-    const bool vec = out_vec_ok(p);
+    auto swap8 = [&](const float (&lo)[4], const float (&hi)[4], float (&o)[8]) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+        for (int r = 0; r < 4; ++r) {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, lo[r]),
+                                                             __builtin_bit_cast(uint32_t, hi[r]),
+                                                             false, false);
+            o[r] = __builtin_bit_cast(float, (uint32_t)sw[0]);
+            o[4 + r] = __builtin_bit_cast(float, (uint32_t)sw[1]);
+        }
+    };
+    auto group = [&](const f32x16& t, int g, float (&o)[4]) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) wdst[(8 * (v >> 2) + 4 * h + (v & 3)) * 128 + wcol] = acc[i][0][v];
-        SLTX_LDS_BARRIER();
-        const int m = m0 + i * 32 + er;
-        if (m < p.M) {
-            float x0[8], x1[8];
-            const f32x4* r0 = reinterpret_cast<const f32x4*>(eb0 + er * 128 + ec);
-            const f32x4* r1 = reinterpret_cast<const f32x4*>(eb1 + er * 128 + ec);
-            const f32x4 a0 = r0[0], a1 = r0[1], b0 = r1[0], b1 = r1[1];
+        for (int r = 0; r < 4; ++r) o[r] = t[4 * g + r];
+    };
+    auto epilogue = [&]() {
+        const bool vec = out_vec_ok(p);
+        const int cw = en0 + (SILU ? 16 : 32) * wn + 8 * h;   // this lane's first column
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                x0[e] = a0[e];
-                x0[4 + e] = a1[e];
-                x1[e] = b0[e];
-                x1[4 + e] = b1[e];
-            }
+        for (int i = 0; i < TM; ++i) {
+            const int m = em0 + i * 32 + lrow;   // lanes l and l + 32 share a row
+            float x[8];
             if constexpr (SPLIT) {
                 // raw fp32 partial sums; the reduce kernel applies the epilogue
                 const size_t nw = SILU ? 2 * (size_t)p.N : (size_t)p.N;
-                float* wsr = p.ws + ((size_t)split * p.M + m) * nw;
-                store_f32x8(wsr, n0 + ec, p.N, x0);
-                if constexpr (SILU)
-                    store_f32x8(wsr + p.N, n0 + ec, p.N, x1);   // up partials follow gate's
-                else
-                    store_f32x8(wsr, n0 + 128 + ec, p.N, x1);
+                float* wsr = p.ws + ((size_t)split * p.M + (m < p.M ? m : 0)) * nw;
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    float lo[4], hi[4];
+                    group(acc[i][0], 2 * q, lo);
+                    group(acc[i][0], 2 * q + 1, hi);
+                    swap8(lo, hi, x);
+                    // SILU: q = 1 is up, whose partials follow gate's
+                    if (m < p.M) store_f32x8(SILU && q ? wsr + p.N : wsr, cw + (SILU ? 0 : 16 * q), p.N, x);
+                }
             } else if constexpr (SILU) {
                 const bool gelu = p.epilogue == kEpiGeluMul;
+                float lo[4], hi[4];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) x0[e] = glu_f32(gelu, x0[e], x1[e]);
-                store_out8(p, (size_t)m * p.N, n0 + ec, x0, vec);
+                for (int r = 0; r < 4; ++r) {
+                    lo[r] = glu_f32(gelu, acc[i][0][r], acc[i][0][8 + r]);
+                    hi[r] = glu_f32(gelu, acc[i][0][4 + r], acc[i][0][12 + r]);
+                }
+                swap8(lo, hi, x);
+                if (m < p.M) store_out8(p, (size_t)m * p.N, cw, x, vec);
             } else {
-                epi_store8(p, (size_t)m * p.N, n0 + ec, x0, vec);
-                epi_store8(p, (size_t)m * p.N, n0 + 128 + ec, x1, vec);
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    float lo[4], hi[4];
+                    group(acc[i][0], 2 * q, lo);
+                    group(acc[i][0], 2 * q + 1, hi);
+                    swap8(lo, hi, x);
+                    if (m < p.M) epi_store8(p, (size_t)m * p.N, cw + 16 * q, x, vec);
+                }
             }
         }
+    };
+
+    // One launch of a single round, one weight set (no SiLU pair): each
+    // 32-row accumulator tile (D, activation rows along the lane's 16 values,
+    // row 8 (v / 4) + 4 h + v % 4, column l % 32) is staged through LDS (the
+    // A stages, idle once the last copy into them has landed) as two fp32
+    // [32][128] buffers, output columns 0-127 and 128-255, so that all 512
+    // threads store whole 256-byte row segments: 16-byte pieces at 8 (t % 16)
+    // of row t / 16.  Measured against the register epilogue at DiT down
+    // (M = 6144, 25 MB of output at once): 2 us faster; the register stores
+    // put 32 rows in each store instruction.
+    auto staged_epilogue = [&]() {
+        static_assert(32 * 128 * 4 <= A_STAGE * 16, "a 32 x 128 fp32 tile fits one A stage");
+        SLTX_WAIT_VMCNT(0);
         SLTX_LDS_BARRIER();
+        float* const eb0 = reinterpret_cast<float*>(lds_a0);
+        float* const eb1 = reinterpret_cast<float*>(lds_a1);
+        float* const wdst = (wn >> 2) ? eb1 : eb0;
+        const int wcol = (wn & 3) * 32 + lrow;
+        const int er = tid >> 4, ec = (tid & 15) * 8;
+        const bool vec = out_vec_ok(p);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) wdst[(8 * (v >> 2) + 4 * h + (v & 3)) * 128 + wcol] = acc[i][0][v];
+            SLTX_LDS_BARRIER();
+            const int m = em0 + i * 32 + er;
+            if (m < p.M) {
+                float x0[8], x1[8];
+                const f32x4* r0 = reinterpret_cast<const f32x4*>(eb0 + er * 128 + ec);
+                const f32x4* r1 = reinterpret_cast<const f32x4*>(eb1 + er * 128 + ec);
+                const f32x4 a0 = r0[0], a1 = r0[1], b0 = r1[0], b1 = r1[1];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    x0[e] = a0[e];
+                    x0[4 + e] = a1[e];
+                    x1[e] = b0[e];
+                    x1[4 + e] = b1[e];
+                }
+                if constexpr (SPLIT) {
+                    // raw fp32 partial sums; the reduce kernel applies the epilogue
+                    float* wsr = p.ws + ((size_t)split * p.M + m) * (size_t)p.N;
+                    store_f32x8(wsr, en0 + ec, p.N, x0);
+                    store_f32x8(wsr, en0 + 128 + ec, p.N, x1);
+                } else {
+                    epi_store8(p, (size_t)m * p.N, en0 + ec, x0, vec);
+                    epi_store8(p, (size_t)m * p.N, en0 + 128 + ec, x1, vec);
+                }
+            }
+            SLTX_LDS_BARRIER();
+        }
+    };
+
+    for (;;) {
+        int kt = 0;
+        for (; kt + 3 < nk; kt += 4) {
+            step(I0{}, kt);
+            step(I1{}, kt + 1);
+            step(I2{}, kt + 2);
+            step(I3{}, kt + 3);
+        }
+        if constexpr (!PERSIST) {   // PERSIST: nk % 4 == 0
+            if (kt < nk) step(I0{}, kt);
+            if (kt + 1 < nk) step(I1{}, kt + 1);
+            if (kt + 2 < nk) step(I2{}, kt + 2);
+        }
+        if constexpr (PERSIST || SILU) {
+            // the block's last copies (clamped re-reads of the last k-tile)
+            // land before it ends and its LDS is released; the stores need
+            // no wait
+            if (!has_next) SLTX_WAIT_VMCNT(0);
+            epilogue();
+        } else {
+            static_assert(!TRANS, "the staged epilogue reads D, not D^T");
+            staged_epilogue();
+        }
+        if (!has_next) break;
+        // the next tile: its copies are in flight, its first k-step's operands
+        // were formed during the last k-step
+        logical += pstride;
+        em0 = m0;
+        en0 = n0;
+        has_next = logical + pstride < pend;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][0][v] = 0.0f;
     }
 }
 
@@ -906,6 +1055,20 @@ static void launch_wm(const GemmParams& p, bool silu, long grid, hipStream_t st)
     const uintptr_t sb_addr = reinterpret_cast<uintptr_t>(p.s0) | reinterpret_cast<uintptr_t>(p.b0) |
                               reinterpret_cast<uintptr_t>(p.s1) | reinterpret_cast<uintptr_t>(p.b1);
     const bool gen = p.K % (2 * BK) != 0 || p.gshift != 1 || (sb_addr & 3) != 0;
+    // More tiles than one block per CU: one persistent block per CU walks
+    // them (the ring's stage parity restarts with each tile: K % 256 == 0).
+    if constexpr (!SPLIT) {
+        if (!gen && p.K % (4 * BK) == 0 && (long)p.tiles_m * p.tiles_n > kCUs) {
+            const dim3 pg(kCUs);
+            if (silu)
+                hipLaunchKernelGGL((q4_gemm_kernel<WM, BF16, true, false, false, false, true>), pg,
+                                   dim3(kThreads), 0, st, p);
+            else
+                hipLaunchKernelGGL((q4_gemm_kernel<WM, BF16, false, false, false, false, true>), pg,
+                                   dim3(kThreads), 0, st, p);
+            return;
+        }
+    }
     if (silu && gen)
         hipLaunchKernelGGL((q4_gemm_kernel<WM, BF16, true, true, SPLIT>), dim3(grid), dim3(kThreads), 0, st, p);
     else if (silu)
