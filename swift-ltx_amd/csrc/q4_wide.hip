@@ -17,12 +17,11 @@
 //    block (v_mfma_f32_32x32x16_f16), each packed word is dequantized once
 //    per block and feeds TM MFMAs, and each A fragment feeds two.
 //  * A round's X (BM rows x 256 bytes) and packed W (64 rows x 64 bytes) are
-//    copied global -> LDS directly (global_load_lds, 16-byte X pieces, W as
-//    dwords so that the 32 rows a wave reads land in distinct banks) into a
-//    ring of 3 (TM = 4) or 4 stages, issued a ring's depth ahead.  Every
-//    thread issues the same number of copies per round (rounds past the last
-//    re-read it), so one exact s_waitcnt vmcnt and one LDS-only barrier per
-//    round hand a stage over.  Each stage is its own array, and the loop is
+//    copied global -> LDS directly (global_load_lds, 16-byte pieces; W by the
+//    first four waves, one piece per lane) into a ring of 3 (TM = 4) or 4
+//    stages, issued a ring's depth ahead.  Each wave issues the same number
+//    of copies every round (rounds past the last re-read it), so one exact
+//    s_waitcnt vmcnt and one LDS-only barrier per round hand a stage over.  Each stage is its own array, and the loop is
 //    unrolled by the ring depth so that stage indices are compile-time: the
 //    compiler then knows that reads of one stage do not alias copies in
 //    flight into another.
@@ -54,7 +53,8 @@ constexpr int RK = NWV * 16;        // k per round: one 16-k MFMA step per wave
 constexpr int XCH = RK * 2 / 16;    // 16-byte pieces of an X row per round (16)
 constexpr int WRD = RK / 8;         // packed words of a weight row per round (16)
 constexpr int WDW = WBN * WRD;      // dwords of a W stage (1024)
-constexpr int NWC = WDW / WT;       // W dword copies per thread per round (2)
+constexpr int WPC = WDW / 4;        // 16-byte W pieces per round (256)
+constexpr int WCW = WPC / 64;       // waves that copy them, one piece per lane (4)
 constexpr int SLAB_G = 64;          // scale / bias groups a block holds
 // Ring stages by tile height (a stage is BM x 256 bytes of X + 4 KB of W).
 // Measured over the Llama and T5 shapes at M = 33..256: at TM = 4 three
@@ -112,9 +112,14 @@ __device__ __forceinline__ f32x16 mfma32_f16(u32x4 a, u32x4 b, f32x16 c) {
 // X piece (row, c) of a stage sits at row * XCH + (c ^ (row & 15)): the 16
 // rows a quarter-wave reads at one logical piece hit 16 distinct pieces.
 __device__ __forceinline__ int xpos(int row, int c) { return row * XCH + (c ^ (row & 15)); }
-// W word (row, w) of a stage sits at row * WRD + (w ^ ((row >> 1) & 15)): the
-// 32 rows a half-wave reads at one logical word hit 32 distinct banks.
-__device__ __forceinline__ int wpos(int row, int w) { return row * WRD + (w ^ ((row >> 1) & 15)); }
+// W word (row, w) of a stage: the row's four 16-byte pieces, piece p at
+// position p ^ ((row >> 2) & 3).  The 32 rows a half-wave reads at one
+// logical word meet at most two to a bank.  (Copied as single words, which
+// allow a conflict-free layout, the copies took 16 instead of 4 wave-wide
+// copy instructions per round, and the route up to 0.7 us more per launch.)
+__device__ __forceinline__ int wpos(int row, int w) {
+    return row * WRD + ((((w >> 2) ^ (row >> 2)) & 3) << 2) + (w & 3);
+}
 // Slab entry (group gi, row) at gi * 64 + (row ^ (gi & 63)): conflict-free
 // both for the fill (consecutive groups of a row) and for the reads (the
 // rows of one group).
@@ -125,8 +130,10 @@ __global__ __launch_bounds__(WT, 1) void q4_wide_kernel(GemmParams p, WideArgs w
     constexpr int BM = 32 * TM;
     constexpr int XS = BM * XCH;        // 16-byte pieces of an X stage
     constexpr int NXC = XS / WT;        // X copies per thread per round
-    static_assert(NXC * WT == XS && NWC * WT == WDW, "whole copies");
-    constexpr int CPR = NXC + NWC;      // vector-memory ops per thread per round
+    static_assert(NXC * WT == XS && WCW * 64 == WPC && WCW <= NWV, "whole copies");
+    // vector-memory ops per thread per round: NXC, plus one W piece in the
+    // first WCW waves
+    constexpr int CPR_W = NXC + 1, CPR_X = NXC;
     constexpr int NSX = wide_nsx<TM>(); // ring stages
     static_assert(NSX == 3 || NSX == 4, "ring depth");
     static_assert(XS * 16 >= 2 * 8 * 1024, "two waves' 32-row tiles fit one X stage");
@@ -194,22 +201,22 @@ __global__ __launch_bounds__(WT, 1) void q4_wide_kernel(GemmParams p, WideArgs w
         const int m = min(m0 + row, p.M - 1);
         x_src[i] = A + (size_t)m * K + kb + c * 8;
     }
-    // W copy i of thread t fills dword d = t + WT i: row d / WRD, physical
-    // word d % WRD = logical word ^ ((row >> 1) & 15).
-    const uint32_t* w_src[NWC];
-#pragma unroll
-    for (int i = 0; i < NWC; ++i) {
-        const int d = tid + WT * i;
-        const int row = d / WRD;
-        const int w = (d % WRD) ^ ((row >> 1) & 15);
+    // W: thread t < WPC fills piece t of the stage: row t / 4, physical piece
+    // t % 4 = logical piece ^ ((row >> 2) & 3).
+    const bool w_copier = wave < WCW;
+    const uint32_t* w_src;
+    {
+        const int t = w_copier ? tid : 0;
+        const int row = t >> 2;
+        const int lp = (t & 3) ^ ((row >> 2) & 3);
         const uint32_t* W;
         const uint16_t *S, *B;
         const int n = wrow(row, W, S, B);
-        w_src[i] = W + (size_t)n * (K / 8) + kb / 8 + w;
+        w_src = W + (size_t)n * (K / 8) + kb / 8 + lp * 4;
     }
     // Round q (clamped to the last round: copies past the end re-read it into
     // a stage no later round reads).
-    auto issue = [&](auto sc, int q) {   // CPR vector-memory ops
+    auto issue = [&](auto sc, int q) {   // CPR_W or CPR_X vector-memory ops
         const int qc = min(q, nr - 1);
         u32x4* xd = xstage(sc);
         uint32_t* wd = wstage(sc);
@@ -217,10 +224,9 @@ __global__ __launch_bounds__(WT, 1) void q4_wide_kernel(GemmParams p, WideArgs w
         for (int i = 0; i < NXC; ++i)
             __builtin_amdgcn_global_load_lds((const void*)(x_src[i] + (size_t)qc * RK),
                                              (lds_ptr_t)(xd + (tid & ~63) + WT * i), 16, 0, 0);
-#pragma unroll
-        for (int i = 0; i < NWC; ++i)
-            __builtin_amdgcn_global_load_lds((const void*)(w_src[i] + (size_t)qc * WRD),
-                                             (lds_ptr_t)(wd + (tid & ~63) + WT * i), 4, 0, 0);
+        if (w_copier)
+            __builtin_amdgcn_global_load_lds((const void*)(w_src + (size_t)qc * WRD),
+                                             (lds_ptr_t)(wd + 4 * (tid & ~63)), 16, 0, 0);
     };
 
     // rounds 0 .. NSX - 2 into their stages
@@ -301,9 +307,14 @@ __global__ __launch_bounds__(WT, 1) void q4_wide_kernel(GemmParams p, WideArgs w
     };
     // Every wave's copies of the next round to read have landed: this
     // thread's were issued before NSX - 2 later rounds' (which may still be
-    // in flight), then the barrier.
+    // in flight), then the barrier.  (A separate W ring eight rounds deep,
+    // its first eight rounds issued with the prologue, measured 0.3-1 us
+    // slower on every shape: the prologue then waits for all of them.)
     auto ready = [&]() {
-        __builtin_amdgcn_s_waitcnt(vmcnt_only((NSX - 2) * CPR));
+        if (w_copier)
+            __builtin_amdgcn_s_waitcnt(vmcnt_only((NSX - 2) * CPR_W));
+        else
+            __builtin_amdgcn_s_waitcnt(vmcnt_only((NSX - 2) * CPR_X));
         WIDE_LDS_BARRIER();
     };
     // Round q (operands in a, b): round q + 1's stage is waited for, the
