@@ -32,15 +32,21 @@
 //  * LDS rows are 128 bytes with an XOR swizzle of the 16-byte columns (swz):
 //    the A fragment reads (16 consecutive rows, one logical column) and the
 //    copies are free of bank conflicts.
-//  * SILU pairs gate and up rows of the same output columns in waves 2c and
-//    2c+1; the up tile is handed to the gate wave through LDS at the end.
-//  * One barrier per k-tile.  Everything the next tile's first k-step needs
+//  * SILU: a wave's 32 weight rows are the 16 gate and the 16 up rows of the
+//    same 16 output columns, so silu(gate) * up is formed in the lane that
+//    holds both (register epilogue below).
+//  * One barrier per k-tile.  Everything the next k-tile's first k-step needs
 //    (its A fragments, its packed words and scale/bias) is already visible
 //    before that barrier, so it is read during the last k-step of the current
-//    tile and the MFMA stream does not drain at tile boundaries.
+//    k-tile and the MFMA stream does not drain at k-tile boundaries.
 //  * Tile order is XCD-aware: the 8 XCDs receive workgroups round-robin, so
 //    consecutive logical tiles (M fastest) are mapped to one XCD and the
 //    M-blocks sharing a weight column block share that XCD's L2.
+//  * More tiles than CUs (the lm_head and DiT up shapes): one persistent
+//    block per CU walks a tile list, the copy ring running on across tiles.
+//  * Outputs are stored from registers (SiLU pairs, persistent launches) or
+//    staged through LDS into whole row segments (single-round launches of one
+//    weight set); see the epilogue.
 //  * Shapes with too few output tiles to fill 256 CUs split K; partial sums
 //    go to an fp32 workspace and a second kernel adds them in split order.
 #include <type_traits>
