@@ -18,7 +18,9 @@
  *     fill the GPU (split-K, e.g. M=750 x N=3072) and for every
  *     sltx_matmul_q4_residual_rms_norm, the block partials of
  *     sltx_argmax, and the probabilities and candidate list of
- *     sltx_sample_top_p[_state]; and a second one per stream for the fp16
+ *     sltx_sample_top_p[_state], after 16 KB of split-K arrival counters
+ *     (zeroed when the buffer is allocated, left at zero by every launch);
+ *     and a second one per stream for the fp16
  *     copy of fp32 activations (sltx_matmul_q4_ex).  There is one per (device, stream),
  *     grown on first need to at least twice its old size; a replaced buffer
  *     is not freed (a graph captured earlier may still use it): every buffer

@@ -161,7 +161,10 @@ int run_gemv(const char* fn, const void* x, const sltx_q4_weight& w0, const sltx
 // and sampling returns an error.
 // A stream has two such buffers: slot 0 for the kernels' scratch, slot 1 for
 // the fp16 copy of fp32 activations that sltx_matmul_q4_ex casts before a
-// GEMM whose scratch is in slot 0.
+// GEMM whose scratch is in slot 0.  Slot 0 starts with the split-K arrival
+// counters (kTicketBytes, zeroed on the stream when the buffer is allocated;
+// each launch that uses them leaves them zero); `tickets` receives their
+// address and the scratch follows them.
 // sltx_release_workspace frees one stream's buffers (current and retired).
 struct StreamWs {
     void* ptr = nullptr;
@@ -171,25 +174,35 @@ struct StreamWs {
 std::mutex g_ws_mu;
 std::map<std::tuple<int, hipStream_t, int>, StreamWs> g_ws;
 
-float* stream_workspace(hipStream_t st, size_t need, int slot = 0) {
+float* stream_workspace(hipStream_t st, size_t need, int slot = 0, unsigned** tickets = nullptr) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    const size_t head = slot == 0 ? kTicketBytes : 0;
+    need += head;
     std::lock_guard<std::mutex> lk(g_ws_mu);
     auto& e = g_ws[{dev, st, slot}];
-    if (e.bytes >= need) return static_cast<float*>(e.ptr);
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
-        return nullptr;
-    void* ptr = nullptr;
-    const size_t bytes = std::max(need + need / 4, 2 * e.bytes);
-    if (hipMalloc(&ptr, bytes) != hipSuccess) {
-        (void)hipGetLastError();
-        return nullptr;
+    if (e.bytes < need) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+            return nullptr;
+        void* ptr = nullptr;
+        const size_t bytes = std::max(need + need / 4, 2 * e.bytes);
+        if (hipMalloc(&ptr, bytes) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        // not capturing: an ordinary memset ahead of the stream's later work
+        if (head && hipMemsetAsync(ptr, 0, head, st) != hipSuccess) {
+            (void)hipGetLastError();
+            (void)hipFree(ptr);
+            return nullptr;
+        }
+        if (e.ptr) e.retired.push_back(e.ptr);
+        e.ptr = ptr;
+        e.bytes = bytes;
     }
-    if (e.ptr) e.retired.push_back(e.ptr);
-    e.ptr = ptr;
-    e.bytes = bytes;
-    return static_cast<float*>(ptr);
+    if (tickets) *tickets = head ? static_cast<unsigned*>(e.ptr) : nullptr;
+    return reinterpret_cast<float*>(static_cast<char*>(e.ptr) + head);
 }
 
 int release_workspace(hipStream_t st) {
@@ -289,7 +302,7 @@ int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w
     if (route == SLTX_ROUTE_SMALL_M) return finish(launch_skinny(p, sp, st), fn);
     if (route == SLTX_ROUTE_MID) return finish(launch_mid(p, st), fn);
     if (route == SLTX_ROUTE_WIDE) {
-        if (wp.splits > 1 && !(p.ws = stream_workspace(st, wp.ws_bytes))) {
+        if (wp.splits > 1 && !(p.ws = stream_workspace(st, wp.ws_bytes, 0, &p.tickets))) {
             // no workspace (the stream is being captured): the same product
             // through the GEMM
             const size_t need = gemm_workspace_bytes(p);

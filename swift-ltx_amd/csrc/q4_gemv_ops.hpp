@@ -1,7 +1,6 @@
-// q4_gemv_ops.hpp -- the GEMV's per-lane building blocks, shared by the
-// stand-alone GEMV (q4_gemv.hip) and the single-launch decode layer
-// (q4_decode.hip): x preparation into dot order, the dequantizing dot over
-// one 32-nibble chunk, and the DPP / permlane row reductions.
+// q4_gemv_ops.hpp -- the GEMV's per-lane building blocks (q4_gemv.hip): x
+// preparation into dot order, the dequantizing dot over one 32-nibble chunk,
+// and the DPP / permlane row reductions.
 #pragma once
 
 #include "q4_common.hpp"

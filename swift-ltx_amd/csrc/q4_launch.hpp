@@ -54,6 +54,9 @@ struct GemmParams {
     int epilogue;           // Epilogue
     const uint16_t* residual;   // [M, N] fp16, epilogue kEpiResidual
     float* ws;              // split-K partials [splits][M][N or 2N] (null: no split)
+    // Split-K arrival counters, one per output tile (kTickets of them), zero
+    // between launches (the last block of a tile resets its own); null: none.
+    unsigned* tickets;
     int splits;             // filled by launch_gemm
     int split_tiles;        // k-tiles per split (even), filled by launch_gemm
     uint32_t nib_mask;      // 0x0F0F0F0F, set by the launchers (a run-time value: see q4_gemm.hip)
@@ -132,6 +135,11 @@ struct SampleParams {
     uint2* cand;            // [n] (probability bits, id)
 };
 
+// Arrival counters at the start of each per-stream workspace (zeroed when the
+// buffer is allocated; every launch leaves them zero).
+constexpr int kTickets = 4096;
+constexpr size_t kTicketBytes = kTickets * sizeof(unsigned);
+
 hipError_t launch_gemv(const GemvParams& p, bool swiglu, hipStream_t st);
 hipError_t launch_embedding_q4(const EmbedParams& p, int n, hipStream_t st);
 size_t sample_workspace_bytes(int n);
@@ -191,7 +199,9 @@ struct WidePlan {
     size_t ws_bytes; // fp32 partials when splits > 1
 };
 bool wide_plan(const GemmParams& p, bool a_bf16, WidePlan* out);
-// p.ws must hold pl.ws_bytes when pl.splits > 1.
+// p.ws must hold pl.ws_bytes and p.tickets be set when pl.splits > 1: the
+// last block of each output tile to finish adds the splits' partial sums
+// (no reduce pass).
 hipError_t launch_wide(GemmParams p, const WidePlan& pl, hipStream_t st);
 // The split-K reduce pass: y = epilogue(sum of p.splits fp32 partials in p.ws).
 hipError_t launch_splitk_reduce(const GemmParams& p, hipStream_t st);

@@ -29,9 +29,11 @@
 //    64 groups) are read once into an LDS slab as scale | bias << 16 words.
 //  * After the last round the 8 waves' tiles are summed in LDS in a fixed
 //    order (one 32-row tile at a time) and the epilogue (gated SiLU /
-//    GELU-tanh, bias, GELU-tanh, residual add) runs on the fp32 sums; with a
-//    K split across blocks the sums go to the fp32 workspace instead and the
-//    split-K reduce pass (q4_gemm.hip) applies the epilogue.
+//    GELU-tanh, bias, GELU-tanh, residual add) runs on the fp32 sums.  With a
+//    K split across blocks each block stores its sums to the fp32 workspace
+//    and counts its arrival on its output tile's counter; the last block to
+//    arrive adds the splits in split order and runs the epilogue (no reduce
+//    pass).
 #include <type_traits>
 #include <utility>
 
@@ -124,6 +126,120 @@ __device__ __forceinline__ int wpos(int row, int w) {
 // both for the fill (consecutive groups of a row) and for the reads (the
 // rows of one group).
 __device__ __forceinline__ int spos(int gi, int row) { return gi * WBN + (row ^ (gi & 63)); }
+
+// Split-K partial sums move through the workspace with accesses that are
+// coherent across the XCDs' L2s: buffer loads and stores with the sc1 cache
+// policy, the one the compiler gives agent-scope atomic loads and stores.
+// The stores have completed (vmcnt) before a block counts its arrival, and
+// the last block loads after reading the count, so no L2-wide write-back or
+// invalidate is needed (agent-scope fences, which do both, made the fix-up
+// slower than the separate reduce pass).
+constexpr int kSc1 = 16;   // cache-policy operand: sc1
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(const float* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, 0x7fffffff, 0x00020000);
+}
+
+// NV consecutive partial sums into row[n .. n+NV-1] (element offset `row`
+// in the workspace), columns past N dropped.
+template <int NV>
+__device__ __forceinline__ void store_f32v_sc1(__amdgpu_buffer_rsrc_t rs, size_t row, int n, int N,
+                                               const float* v) {
+    if ((N % NV) == 0 && n + NV <= N) {
+        const int o = (int)((row + n) * sizeof(float));
+        if constexpr (NV == 4) {
+            const u32x4 d = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                             __float_as_uint(v[3])};
+            __builtin_amdgcn_raw_buffer_store_b128(d, rs, o, 0, kSc1);
+        } else {
+            typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+            const u32x2 d = {__float_as_uint(v[0]), __float_as_uint(v[1])};
+            __builtin_amdgcn_raw_buffer_store_b64(d, rs, o, 0, kSc1);
+        }
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < NV; ++e)
+        if (n + e < N)
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[e]), rs,
+                                                  (int)((row + n + e) * sizeof(float)), 0, kSc1);
+}
+
+// NV consecutive partial sums row[n .. n+NV-1], loaded whatever n (columns
+// past N read an earlier column, to be discarded): no load sits behind a
+// branch.
+template <int NV>
+__device__ __forceinline__ void load_f32v_sc1(__amdgpu_buffer_rsrc_t rs, size_t row, int n, int N,
+                                              float* v) {
+    if ((N % NV) == 0) {
+        const int o = (int)((row + min(n, N - NV)) * sizeof(float));
+        if constexpr (NV == 4) {
+            const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, kSc1);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = __uint_as_float(q[e]);
+        } else {
+            const auto q = __builtin_amdgcn_raw_buffer_load_b64(rs, o, 0, kSc1);
+            v[0] = __uint_as_float(q[0]);
+            v[1] = __uint_as_float(q[1]);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < NV; ++e)
+            v[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                rs, (int)((row + min(n + e, N - 1)) * sizeof(float)), 0, kSc1));
+    }
+}
+
+// The last block of an output tile: the S splits' partial sums of the rows
+// and columns this thread summed (32 i + ml, n .. n + NV - 1) -- its own
+// split's from registers (own0 / own1), the others' loaded, every load
+// issued before the first add -- added in split order from zero as the
+// split-K reduce pass adds them, then the epilogue.
+template <int S, int TM, bool PAIR, int NV>
+__device__ __forceinline__ void wide_fixup(const GemmParams& p, int m0, int mrows, int ml, int n,
+                                           int split, const float (&own0)[TM][NV],
+                                           const float (&own1)[TM][NV]) {
+    const size_t nw = PAIR ? 2 * (size_t)p.N : (size_t)p.N;
+    const __amdgpu_buffer_rsrc_t rs = ws_rsrc(p.ws);
+    // slot o holds split o + (o >= split)
+    float g[TM][S - 1][NV], u[PAIR ? TM : 1][PAIR ? S - 1 : 1][NV];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int m = min(m0 + 32 * i + ml, p.M - 1);
+#pragma unroll
+        for (int o = 0; o < S - 1; ++o) {
+            const int j = o + (o >= split ? 1 : 0);
+            const size_t r = ((size_t)j * p.M + m) * nw;
+            load_f32v_sc1<NV>(rs, r, n, p.N, g[i][o]);
+            if constexpr (PAIR) load_f32v_sc1<NV>(rs, r + p.N, n, p.N, u[i][o]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int brow = 32 * i + ml;
+        const int m = m0 + brow;
+        if (brow >= mrows || m >= p.M) continue;
+        float a[NV], b[NV];
+#pragma unroll
+        for (int e = 0; e < NV; ++e) a[e] = b[e] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < S; ++j)
+#pragma unroll
+            for (int e = 0; e < NV; ++e) {
+                const int lo = j > 0 ? j - 1 : 0, hi = j < S - 1 ? j : S - 2;
+                a[e] += j == split ? own0[i][e] : (j < split ? g[i][hi][e] : g[i][lo][e]);
+                if constexpr (PAIR)
+                    b[e] += j == split ? own1[i][e] : (j < split ? u[i][hi][e] : u[i][lo][e]);
+            }
+        if constexpr (PAIR) {
+            const bool gelu = p.epilogue == kEpiGeluMul;
+#pragma unroll
+            for (int e = 0; e < NV; ++e) a[e] = glu_f32(gelu, a[e], b[e]);
+            store_outv<NV>(p, (size_t)m * p.N, n, a);
+        } else {
+            epi_storev<NV>(p, (size_t)m * p.N, n, a);
+        }
+    }
+}
 
 template <int TM, bool PAIR, bool SPLIT>
 __global__ __launch_bounds__(WT, 1) void q4_wide_kernel(GemmParams p, WideArgs wa) {
@@ -368,6 +484,12 @@ __global__ __launch_bounds__(WT, 1) void q4_wide_kernel(GemmParams p, WideArgs w
     const int j0 = PAIR ? 0 : cq >> 3;
     const int c0 = PAIR ? 2 * cq : 4 * (cq & 7);
     const int n = n0 + 32 * j0 + c0;
+    // this split's sums, kept for the fix-up should this block be the last
+    float own0[TM][NV], own1[TM][NV];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int e = 0; e < NV; ++e) own0[i][e] = own1[i][e] = 0.0f;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         if (i > 0) WIDE_LDS_BARRIER();
@@ -399,9 +521,15 @@ __global__ __launch_bounds__(WT, 1) void q4_wide_kernel(GemmParams p, WideArgs w
                 }
             }
             if constexpr (SPLIT) {
-                float* wsr = p.ws + ((size_t)split * p.M + m) * nw;
-                store_f32v<NV>(wsr, n, p.N, x0);
-                if constexpr (PAIR) store_f32v<NV>(wsr + p.N, n, p.N, x1);
+                const __amdgpu_buffer_rsrc_t rs = ws_rsrc(p.ws);
+                const size_t r = ((size_t)split * p.M + m) * nw;
+                store_f32v_sc1<NV>(rs, r, n, p.N, x0);
+                if constexpr (PAIR) store_f32v_sc1<NV>(rs, r + p.N, n, p.N, x1);
+#pragma unroll
+                for (int e = 0; e < NV; ++e) {
+                    own0[i][e] = x0[e];
+                    own1[i][e] = x1[e];
+                }
             } else if constexpr (PAIR) {
                 const bool gelu = p.epilogue == kEpiGeluMul;
 #pragma unroll
@@ -411,6 +539,29 @@ __global__ __launch_bounds__(WT, 1) void q4_wide_kernel(GemmParams p, WideArgs w
                 epi_storev<NV>(p, (size_t)m * p.N, n, x0);
             }
         }
+    }
+    if constexpr (SPLIT) {
+        // Arrival on the tile's counter: every thread's sc1 partial stores
+        // have completed (vmcnt) before the barrier, and thread 0 adds 1 after
+        // it (an agent-scope atomic); the block that reads S - 1 loads the
+        // partials (sc1) after its second barrier, and resets the counter
+        // for the next launch.
+        __shared__ int last_block;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0) {
+            unsigned* t = p.tickets + blockIdx.y * gridDim.x + blockIdx.x;
+            const unsigned prev = __hip_atomic_fetch_add(t, 1u, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+            const int last = prev + 1 == gridDim.z;
+            if (last) __hip_atomic_store(t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last_block = last;
+        }
+        __syncthreads();
+        if (!last_block) return;
+        if (gridDim.z == 2) wide_fixup<2, TM, PAIR, NV>(p, m0, wa.mrows, ml, n, split, own0, own1);
+        else if (gridDim.z == 4) wide_fixup<4, TM, PAIR, NV>(p, m0, wa.mrows, ml, n, split, own0, own1);
+        else wide_fixup<8, TM, PAIR, NV>(p, m0, wa.mrows, ml, n, split, own0, own1);
     }
 }
 
@@ -449,8 +600,8 @@ bool wide_plan(const GemmParams& p, bool a_bf16, WidePlan* out) {
     const int g = 32 << p.gshift;
     const int rounds = p.K / RK;
     const long blocks = (long)pl.nblocks * pl.mblocks;
-    int s = 1;
-    while (rounds % (2 * s) == 0 &&
+    int s = 1;   // 1, 2, 4 or 8 (the fix-up's instantiations)
+    while (s < 8 && rounds % (2 * s) == 0 &&
            ((long)p.K / s / g > SLAB_G || (blocks * s < 160 && rounds / (2 * s) >= 4)))
         s *= 2;
     if ((long)p.K / s / g > SLAB_G) return false;
@@ -472,7 +623,8 @@ bool wide_plan(const GemmParams& p, bool a_bf16, WidePlan* out) {
 
 hipError_t launch_wide(GemmParams p, const WidePlan& pl, hipStream_t st) {
     const bool pair = p.w1 != nullptr;
-    if (pl.splits > 1 && !p.ws) return hipErrorInvalidValue;
+    if (pl.splits > 1 && (!p.ws || !p.tickets || pl.nblocks * pl.mblocks > kTickets))
+        return hipErrorInvalidValue;
     p.splits = pl.splits;
     const WideArgs wa = {pl.mrows, pl.kblk};
     const dim3 grid((unsigned)pl.nblocks, (unsigned)pl.mblocks, (unsigned)pl.splits);
@@ -487,8 +639,7 @@ hipError_t launch_wide(GemmParams p, const WidePlan& pl, hipStream_t st) {
         else if (pl.tm == 3) e = launch_tm<3, false>(p, wa, grid, split, st);
         else e = launch_tm<4, false>(p, wa, grid, split, st);
     }
-    if (e != hipSuccess || !split) return e;
-    return launch_splitk_reduce(p, st);
+    return e;
 }
 
 }  // namespace sltx

@@ -1,8 +1,9 @@
 """GPU parity of the wide-M route (q4_wide.hip: 32 < M <= 256, fp16
 activations) through the C ABI: single weight sets and gated pairs, one
 block along M (33..128 rows, 2-4 MFMA row tiles) and two (129..256 rows),
-unsplit and split over K across blocks (the fp32 partials then go through
-the split-K reduce pass), every group size, the single-set epilogues.
+unsplit and split over K across blocks (the last block of each output tile
+adds the splits' fp32 partial sums; tests/test_gpu_wide_splits.py covers
+that hand-over), every group size, the single-set epilogues.
 
 Same semantics as the GEMM (matmulQ4Fast / matmulQ4FastF32, Ops.swift:312-381;
 the SwiGLU and GeGLU pairs, LlamaModel.swift:275-277 and
