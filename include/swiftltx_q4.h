@@ -29,7 +29,9 @@
  *     workspace is missing or too small,
  *     that GEMM runs unsplit (same results, lower throughput).  Capture after
  *     one eager call on the same stream to get the split kernel into a graph
- *     (with torch, pass that stream to torch.cuda.graph(..., stream=s)).
+ *     (with torch, pass that stream to torch.cuda.graph(..., stream=s)).  A
+ *     captured graph keeps using its stream's workspace: replay it on that
+ *     stream, or keep that stream's other work from overlapping the replay.
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = the default stream) and
  *     nothing synchronises: results are visible to later work on that stream.
  *     This mirrors the reference's batched mode (MetalContext.swift:109-134).
