@@ -143,8 +143,15 @@ class DecodeStep:
         return g
 
     def replay(self):
-        """One captured step."""
+        """One captured step, replayed on the capture stream (its kernels use
+        that stream's workspace): after the work queued so far on the caller's
+        current stream, and before that stream's later work."""
         if self.graph is None:
             raise RuntimeError("capture() first")
-        self.graph.replay()
+        import torch
+        cur = torch.cuda.current_stream()
+        self.stream.wait_stream(cur)
+        with torch.cuda.stream(self.stream):
+            self.graph.replay()
+        cur.wait_stream(self.stream)
         return self.token
