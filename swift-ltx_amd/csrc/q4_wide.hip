@@ -463,19 +463,21 @@ __global__ __launch_bounds__(WT, 1) void q4_wide_kernel(GemmParams p, WideArgs w
         if (q + decltype(sc)::value < nr) round(sc, q + decltype(sc)::value);
     });
 
-    // ---- the K-groups' sums, one 32-row tile at a time ----
-    // Wave w's two tiles go to X stage w / 2 at float (w % 2) * 2048, as
-    // [tile][element v][lane].  D[m][col] of a 32 x 32 tile is element
+    // ---- the K-groups' sums, G 32-row tiles at a time ----
+    // Wave w's two tiles of row tile i go to X stage w / 2 at float
+    // (i % G) * 4096 + (w % 2) * 2048, as [tile][element v][lane]: G = 2 where
+    // a stage holds two waves' tiles twice (TM = 4), which halves the
+    // barriers, else 1.  D[m][col] of a 32 x 32 tile is element
     // 4 (m / 8) + m % 4 of lane col + 32 ((m / 4) % 2).  Every thread then
     // sums 4 columns (one set) or 2 gate and 2 up columns (pair) of one row
     // over the 8 waves, in wave order.
+    constexpr int G = XS * 16 >= 2 * 2 * 8 * 1024 ? 2 : 1;
     __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
     WIDE_LDS_BARRIER();
-    auto buf = [&](int w) -> float* {
+    auto buf = [&](int w, int d) -> float* {
         u32x4* st = (w >> 1) == 0 ? xs0 : (w >> 1) == 1 ? xs1 : (w >> 1) == 2 ? xs2 : xs3;
-        return reinterpret_cast<float*>(st) + (w & 1) * 2048;
+        return reinterpret_cast<float*>(st) + d * 4096 + (w & 1) * 2048;
     };
-    float* const mine = buf(wave);
     constexpr int NV = PAIR ? 2 : 4;     // columns a thread sums
     const size_t nw = PAIR ? 2 * (size_t)p.N : (size_t)p.N;
     const int ml = tid >> 4, cq = tid & 15;
@@ -491,22 +493,29 @@ __global__ __launch_bounds__(WT, 1) void q4_wide_kernel(GemmParams p, WideArgs w
 #pragma unroll
         for (int e = 0; e < NV; ++e) own0[i][e] = own1[i][e] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-        if (i > 0) WIDE_LDS_BARRIER();
+    for (int i0 = 0; i0 < TM; i0 += G) {
+        if (i0 > 0) WIDE_LDS_BARRIER();
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int d = 0; d < G && i0 + d < TM; ++d) {
+            float* const mine = buf(wave, d);
 #pragma unroll
-            for (int e = 0; e < 16; ++e) mine[j * 1024 + e * 64 + lane] = acc[i][j][e];
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) mine[j * 1024 + e * 64 + lane] = acc[i0 + d][j][e];
+        }
         WIDE_LDS_BARRIER();
-        const int brow = 32 * i + ml;
-        const int m = m0 + brow;
-        if (brow < wa.mrows && m < p.M) {
+#pragma unroll
+        for (int d = 0; d < G && i0 + d < TM; ++d) {
+            const int i = i0 + d;
+            const int brow = 32 * i + ml;
+            const int m = m0 + brow;
+            if (brow >= wa.mrows || m >= p.M) continue;
             float x0[NV], x1[NV];
 #pragma unroll
             for (int e = 0; e < NV; ++e) x0[e] = x1[e] = 0.0f;
 #pragma unroll
             for (int w = 0; w < NWV; ++w) {
-                const float* bw = buf(w) + v * 64 + l0 + c0;
+                const float* bw = buf(w, d) + v * 64 + l0 + c0;
                 if constexpr (PAIR) {
                     const float2 g = *reinterpret_cast<const float2*>(bw);
                     const float2 u = *reinterpret_cast<const float2*>(bw + 1024);
