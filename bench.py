@@ -4,7 +4,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W]
     python bench.py --summarize-trace DIR     (a rocprofv3 output folder of this script)
 
-Workload: one Llama-3.2-3B decode layer's projections at
+Workload (benchmark config 2): one Llama-3.2-3B decode layer's projections at
 M = 1 with MLX 4-bit group-64 weights -- q/o [3072x3072], k/v [1024x3072],
 gate+up [8192x3072] fused with SiLU x up, down [3072x8192].  A step is one
 layer: 4 launches (q/k/v rows concatenated at load time into one [5120x3072]
@@ -33,14 +33,14 @@ roofline   = the dominant kernel (fused gate/up GEMV, 28.33 MB per launch):
              kernel duration).  measured_ceiling: a read-only stream
              (csrc/bench/hbm_read.hip, in lib/libswiftltx_bench.so) and a
              device copy, same replay method.
-extra      = the other BASELINE configs and the paths around the GEMV, each
+extra      = the other benchmark configs and the paths around the GEMV, each
              by the same replay method: config 1 (q_proj GEMV over >= 2 GB of
              rotated copies), config 4a (lm_head GEMV over 10 rotated copies,
              2.2 GB), the fused-norm decode layer, the
              decode token (greedy / sampled), the 750-token prefill, token
              selection, small M (2..256) and the M > 1 MFMA GEMMs (configs 3,
              4b, 5) against the 2.5 PFLOP/s dense fp16/bf16 peak.
-configs    = the last key of the line: every BASELINE config as us and
+configs    = the last key of the line: every benchmark config as us and
              fraction of its roofline (a log that keeps only the line's tail
              still holds them).
 cpu_baseline = C restatements of the same dequant matmul (Swift, the
@@ -314,7 +314,7 @@ def main():
     if g_warm is not None:
         g_warm.replay()
     # Exactly K steps, one replay, bracketed by synchronizes.  The time is
-    # the GPU's (events on the replaying stream, as BASELINE's rules time
+    # the GPU's (events on the replaying stream, as the benchmark's rules time
     # kernels); the host wall clock around it, which adds the launch and
     # synchronize latency of one replay (~75 us), is reported beside it.
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -374,7 +374,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "u4xf16->f32",
-        "data": "synthetic (BASELINE distributions: x~N(0,1) fp16, codes uniform 0..15, "
+        "data": "synthetic (the benchmark's distributions: x~N(0,1) fp16, codes uniform 0..15, "
                 "scales |N(0,0.02)| fp16, biases -8*scale)",
         "config": {"workload": "Llama-3.2-3B decode layer projections, M=1, MLX 4-bit g64 "
                                "(q,k,v rows concatenated at load, o, gate+up fused SiLU*up, "
@@ -408,7 +408,7 @@ def main():
 
 
 def config_summary(value, steps, wall, layer_st, dom_us, legs):
-    """Every BASELINE config in a few numbers, for the end of the JSON line
+    """Every benchmark config in a few numbers, for the end of the JSON line
     (whose tail is what a log keeps): us and fraction of the HBM (GEMV) or
     dense MFMA (GEMM) peak."""
     def hbm(st):
@@ -526,7 +526,7 @@ def hbm_ceilings(pkg, torch, dev, cap, read_gib=4, copy_gib=1):
 # --------------------------------------------------------- config legs ---
 
 def config1_leg(pkg, torch, gen, dev, cap, copies=400):
-    """one q_proj GEMV [3072 x 3072], M = 1, rotated over
+    """Benchmark config 1: one q_proj GEMV [3072 x 3072], M = 1, rotated over
     `copies` weight copies (400 x 5.31 MB = 2.12 GB)."""
     ws = [q4(pkg, torch, 3072, 3072, gen, dev) for _ in range(copies)]
     xx = torch.randn(1, 3072, generator=gen, device=dev).half()
@@ -542,7 +542,7 @@ def config1_leg(pkg, torch, gen, dev, cap, copies=400):
 
 
 def lm_head_cold_leg(pkg, torch, gen, dev, cap, copies=10):
-    """BASELINE config 4a: the tied lm_head GEMV [128256 x 3072], M = 1,
+    """Benchmark config 4a: the tied lm_head GEMV [128256 x 3072], M = 1,
     rotated over `copies` weight copies (10 x 222.6 MB = 2.23 GB, beyond the
     256 MB MALL)."""
     V = 128256
@@ -746,7 +746,7 @@ def token_select_leg(pkg, torch, gen, dev, vocab=128256):
 # ---------------------------------------------------------------- GEMMs ---
 
 def gemm_legs(pkg, torch, gen, dev, cap, min_gb=2.0):
-    """BASELINE configs 3 (M = 750 prefill gate/up + SiLU and down), 4b
+    """Benchmark configs 3 (M = 750 prefill gate/up + SiLU and down), 4b
     (lm_head M = 750) and 5 (LTX DiT FFN, M = 6144 bf16, and the up projection
     with fp32 activations): graphs of launches
     over weight copies rotated to >= min_gb GB (the measurement rule: one
@@ -932,7 +932,7 @@ def traffic_from_profiles():
 # --------------------------------------------------------- CPU baseline ---
 
 def cpu_baseline(runs=5):
-    """BASELINE's CPU plan: the same dequant matmul (w = s*q + b, group 64,
+    """The reference's CPU plan: the same dequant matmul (w = s*q + b, group 64,
     fp32 accumulate, fp16 out; gate/up with SiLU x up) as C restatements in
     oracle/q4_cpu_baseline.c -- a substitute for Swift, which is not
     installed: single-thread scalar (matmulCPU's loop order,
@@ -983,7 +983,7 @@ def cpu_baseline(runs=5):
         out[cname] = res
     c2 = out["config2_decode_layer_m1"]["simd"]
     return {"value": c2["gbs"], "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"BASELINE config 2 decode layer (7 projections + silu_mul, "
+            "sample": f"benchmark config 2 decode layer (7 projections + silu_mul, "
                       f"{out['config2_decode_layer_m1']['bytes']} algorithmic bytes), 8-wide "
                       f"SIMD C on {threads} threads, median of {runs} runs",
             "substitute": "C restatement of the Swift scalar / SIMD8<Float> CPU plan (no Swift "

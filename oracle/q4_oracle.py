@@ -284,7 +284,7 @@ def bf16_bits_to_f32(h: np.ndarray) -> np.ndarray:
 
 def make_inputs(M: int, N: int, K: int, group: int = 64, seed: int = 0, x_dtype: str = "f16",
                 n_weights: int = 1):
-    """Synthetic inputs with the distributions BASELINE states:
+    """Synthetic inputs with the benchmark's input distributions:
     x ~ N(0,1) (fp16, or bf16 bits when x_dtype == 'bf16'); codes uniform 0..15;
     scales ~ |N(0, 0.02)| fp16; biases = -8*scales (exact in fp16).
     Draw order from one default_rng(seed): x, then per weight set (codes, scales).

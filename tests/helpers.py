@@ -1,7 +1,7 @@
 """Shared helpers for the GPU parity tests.
 
 Tolerances (fp64 oracle = reference semantics w = s*q + b, exact):
-  GATE        BASELINE's parity bar: max|y - ref| / max|ref| <= 1e-2.
+  GATE        the parity bar: max|y - ref| / max|ref| <= 1e-2.
   elementwise |y - ref| <= rtol*|ref| + atol_rms*rms(ref), per path:
     GEMV, fp16 out      rtol 6e-4 (fp16 store, half ulp = 4.9e-4), atol 1e-4*rms
     GEMM, fp16 weights  rtol 1e-3, atol 3e-3*rms  (weights rounded to fp16 before
@@ -72,7 +72,7 @@ def rounded_weights_bf16(w, s, b, g):
 
 
 def gpu_inputs(M, N, K, g, seed, dev, x_dtype="f16", n_weights=1):
-    """Large synthetic inputs generated on the device (BASELINE distributions):
+    """Large synthetic inputs generated on the device (the benchmark's input distributions):
     x ~ N(0,1); codes uniform (random 32-bit words); scales |N(0,0.02)|;
     biases -8*scales.  Returns torch tensors (x, [(w, s, b)])."""
     import torch

@@ -4,7 +4,7 @@ same pipeline run in numpy from the oracle's functions
 (LlamaModel.swift:213-236, 284-331; attention replaced on both sides by the
 q rows, as DecodeStep's stand-in does):
 
-* each step's logits within the BASELINE gate (max|d|/max|ref| <= 1e-2) of the
+* each step's logits within the parity gate (max|d|/max|ref| <= 1e-2) of the
   numpy pipeline fed the same token, and the same argmax wherever the
   reference's top two logits are further apart than that;
 * graph replays reproduce the eager token sequence exactly.

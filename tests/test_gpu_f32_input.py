@@ -9,7 +9,7 @@ would each repeat the cast).
 Checked (1) bit for bit against the same call fed the oracle's cast of x as
 fp16 where the cast runs once (and to fp32 rounding where it runs inside the
 GEMM, whose plan may split K differently), at the LTX
-DiT feed-forward shapes (M = 6144, hidden 2048, ffn 8192)
+DiT feed-forward shapes (benchmark config 5: M = 6144, hidden 2048, ffn 8192)
 with inputs beyond +-65504 and infinities, and (2) against the fp64 oracle
 of that cast followed by the dequant matmul, on rows with and without
 clamped values, at config 5 and at small and ragged shapes (group sizes 32 /

@@ -167,7 +167,7 @@ def test_gemm_ex_dtypes_bias_gelu(pkg, dev, out, xdt, epi):
     assert o.max_rel_err(y, ref) <= 1e-2
 
 
-# ---- BASELINE configs at full size (sampled rows against the oracle) ----
+# ---- benchmark configs at full size (sampled rows against the oracle) ----
 
 def _sample_check(y, x, w, s, b, g, rows_m, tol, what, x_dtype="f16"):
     xs = host(x)[rows_m]
@@ -176,7 +176,7 @@ def _sample_check(y, x, w, s, b, g, rows_m, tol, what, x_dtype="f16"):
 
 
 def test_prefill_gate_up_swiglu_m750(pkg, dev):
-    """X [750, 3072] x gate/up [8192 x 3072], fused SiLU x up."""
+    """Benchmark config 3: X [750, 3072] x gate/up [8192 x 3072], fused SiLU x up."""
     import torch
     M, N, K, g = 750, 8192, 3072, 64
     x, [(wg, sg, bg), (wu, su, bu)] = gpu_inputs(M, N, K, g, seed=3, dev=dev, n_weights=2)
@@ -191,7 +191,7 @@ def test_prefill_gate_up_swiglu_m750(pkg, dev):
 
 
 def test_prefill_down_m750(pkg, dev):
-    """X [750, 8192] x down [3072 x 8192], fp16 out."""
+    """Benchmark config 3: X [750, 8192] x down [3072 x 8192], fp16 out."""
     import torch
     M, N, K, g = 750, 3072, 8192, 64
     x, [(w, s, b)] = gpu_inputs(M, N, K, g, seed=4, dev=dev)
@@ -203,7 +203,7 @@ def test_prefill_down_m750(pkg, dev):
 
 
 def test_lm_head_m750(pkg, dev):
-    """BASELINE config 4b: X [750, 3072] x lm_head [128256 x 3072]."""
+    """Benchmark config 4b: X [750, 3072] x lm_head [128256 x 3072]."""
     import torch
     M, N, K, g = 750, 128256, 3072, 64
     x, [(w, s, b)] = gpu_inputs(M, N, K, g, seed=5, dev=dev)
@@ -217,7 +217,7 @@ def test_lm_head_m750(pkg, dev):
 
 
 def test_dit_ffn_m6144_bf16(pkg, dev):
-    """bf16 X [6144, 2048] x up [8192 x 2048] -> GELU-tanh ->
+    """Benchmark config 5: bf16 X [6144, 2048] x up [8192 x 2048] -> GELU-tanh ->
     down [2048 x 8192], fp32 out (DiTModel.swift:930-956 dataflow)."""
     import torch
     M, K1, N1, g = 6144, 2048, 8192, 64

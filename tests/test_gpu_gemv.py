@@ -62,7 +62,7 @@ def test_gemv_shapes(pkg, dev, N, K, g):
 @pytest.mark.parametrize("K,g", [(256, 64), (3072, 64), (160, 32), (512, 128)])
 def test_gemv_nibbles_and_dequant_bit_exact(pkg, dev, K, g):
     """One-hot x picks column k: with s=1, b=0 the output is the unpacked code
-    q[n,k] exactly; with BASELINE scales/biases it is fp16(s*q+b) exactly."""
+    q[n,k] exactly; with the benchmark's scales/biases it is fp16(s*q+b) exactly."""
     import torch
     N = 64
     rng = np.random.default_rng(K)
@@ -123,7 +123,7 @@ def test_swiglu_gemv_shapes(pkg, dev, N, K):
     assert_parity(y.cpu().numpy(), ref, TOL_GEMV, f"swiglu N={N} K={K}")
 
 
-# BASELINE configs at full size: q/o, k/v, down, lm_head.  The oracle checks a
+# benchmark configs at full size: q/o, k/v, down, lm_head.  The oracle checks a
 # sample of rows; size-independent properties cover the rest.
 FULL = [("q_proj", 3072, 3072), ("k_proj", 1024, 3072), ("down_proj", 3072, 8192),
         ("lm_head", 128256, 3072)]
@@ -160,7 +160,7 @@ def test_gemv_full_size(pkg, dev, name, N, K):
 
 
 def test_gemv_full_size_swiglu(pkg, dev):
-    """gate/up [8192 x 3072] fused with SiLU x up."""
+    """gate/up [8192 x 3072] fused with SiLU x up (benchmark config 2)."""
     import torch
     N, K, g = 8192, 3072, 64
     x, [(wg, sg, bg), (wu, su, bu)] = gpu_inputs(1, N, K, g, seed=11, dev=dev, n_weights=2)

@@ -58,7 +58,7 @@ def test_persistent_gated_pair(pkg, dev, M, N, K, gelu):
     rows = np.array([0, 63, 64, 191, 192, M // 3, M - 1])
     xs = host(x)[rows].astype(np.float64)
     glu = (lambda a, b: o.gelu_tanh_f64(a) * b) if gelu else o.silu_mul_f64
-    # the BASELINE bar against the fp64 oracle ...
+    # the parity bar against the fp64 oracle ...
     ref = glu(o.matmul_q4_f64(xs, host(wg), host(sg), host(bg), g),
               o.matmul_q4_f64(xs, host(wu), host(su), host(bu), g))
     got = y.cpu().numpy()[rows].astype(np.float64)

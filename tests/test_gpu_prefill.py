@@ -4,7 +4,7 @@ against the same pipeline run in numpy from the oracle's functions
 (LlamaModel.swift:168-203, 230-282; attention replaced on both sides by the q
 rows, so every row depends on its own token only):
 
-* the last token's logits within the BASELINE gate (max|d|/max|ref| <= 1e-2)
+* the last token's logits within the parity gate (max|d|/max|ref| <= 1e-2)
   of the numpy pipeline, at prompt lengths that take the MFMA GEMM (M > 1,
   split-K included) and the GEMV (M = 1, for q|k|v and gate/up; the fused o
   and down calls run the GEMM at every M);

@@ -188,7 +188,7 @@ def test_cpu_baseline_matches_f64(oracle):
 
 
 def test_baseline_distribution(oracle):
-    """BASELINE's synthetic inputs: |y| has std ~5 at K=3072, bias == -8*scale exactly."""
+    """The benchmark's synthetic inputs: |y| has std ~5 at K=3072, bias == -8*scale exactly."""
     x, [(w, s, b)] = oracle.make_inputs(64, 256, 3072, 64, seed=0)
     assert np.array_equal(b.astype(np.float32), -8.0 * s.astype(np.float32))
     std = oracle.matmul_q4_f64(x, w, s, b, 64).std()
