@@ -632,7 +632,10 @@ bool wide_plan(const GemmParams& p, bool a_bf16, WidePlan* out) {
 
 hipError_t launch_wide(GemmParams p, const WidePlan& pl, hipStream_t st) {
     const bool pair = p.w1 != nullptr;
-    if (pl.splits > 1 && (!p.ws || !p.tickets || pl.nblocks * pl.mblocks > kTickets))
+    // split launches: a counter per output tile, and partial-sum offsets that
+    // fit the 32-bit byte offsets of the workspace's buffer accesses
+    if (pl.splits > 1 && (!p.ws || !p.tickets || pl.nblocks * pl.mblocks > kTickets ||
+                          pl.ws_bytes > 0x7fffffffu))
         return hipErrorInvalidValue;
     p.splits = pl.splits;
     const WideArgs wa = {pl.mrows, pl.kblk};

@@ -93,15 +93,16 @@ def test_wide_split_parity(pkg, dev, M, N, K, g, epi, splits):
 
 def test_wide_splits_back_to_back(pkg, dev):
     """Split launches of three shapes with different tile counts and split
-    counts, interleaved on one stream with no synchronization between them:
-    each launch must leave every counter at zero for the next."""
+    counts, interleaved on one stream with no synchronization between them
+    (120 launches): each launch must leave every counter at zero for the
+    next, and each must equal the first bit for bit."""
     import torch
     shapes = [CASES[0], CASES[1], CASES[2]]
     inputs = [_inputs(dev, *c[:5], seed=7 + i)[1] for i, c in enumerate(shapes)]
     st = torch.cuda.Stream()
     with torch.cuda.stream(st):
         first = [_run(pkg, a, *c[:5], stream=st) for a, c in zip(inputs, shapes)]
-        outs = [[_run(pkg, a, *c[:5], stream=st) for a, c in zip(inputs, shapes)] for _ in range(8)]
+        outs = [[_run(pkg, a, *c[:5], stream=st) for a, c in zip(inputs, shapes)] for _ in range(40)]
     st.synchronize()
     for rnd in outs:
         for r, f in zip(rnd, first):
