@@ -214,8 +214,13 @@ __global__ __launch_bounds__((64 * gemv_max_waves<CPL, SWIGLU, MULTI>())) void q
         ss = row_reduce<64>(ss);
         if ((threadIdx.x & 63) == 0) lds.red[threadIdx.x >> 6] = ss;
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        float ssum = 0.0f;
-        for (int w = 0; w < (NTH >> 6); ++w) ssum += lds.red[w];
+        // the block sum of the wave partials: lane l of each 16-lane row reads
+        // the partial of wave l % 16 (zero past the last wave), one LDS read
+        // per lane and a fixed DPP tree, instead of a serial loop of
+        // dependent LDS reads
+        const int nwv = NTH >> 6, wl = threadIdx.x & 15;
+        const float part = lds.red[wl < nwv ? wl : nwv - 1];
+        const float ssum = row_reduce<16>(wl < nwv ? part : 0.0f);
         const float rms = rsqrtf(ssum / (float)p.K + p.eps);
 #pragma unroll
         for (int u = 0; u < XPU; ++u) {
