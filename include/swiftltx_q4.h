@@ -27,7 +27,8 @@
  *     lives until sltx_release_workspace(stream) or the process exits.  A
  *     stream being captured into a HIP graph never allocates: if its
  *     workspace is missing or too small,
- *     that GEMM runs unsplit (same results, lower throughput).  Capture after
+ *     that GEMM runs unsplit (the same product, its fp32 sums in another
+ *     order; lower throughput).  Capture after
  *     one eager call on the same stream to get the split kernel into a graph
  *     (with torch, pass that stream to torch.cuda.graph(..., stream=s)).  A
  *     captured graph keeps using its stream's workspace: replay it on that
