@@ -166,7 +166,9 @@ __device__ __forceinline__ void store_f32v_sc1(__amdgpu_buffer_rsrc_t rs, size_t
 
 // NV consecutive partial sums row[n .. n+NV-1], loaded whatever n (columns
 // past N read an earlier column, to be discarded): no load sits behind a
-// branch.
+// branch.  n is a multiple of NV, so with N % NV == 0 a group lies wholly
+// before N or wholly past it, and clamping a group past N moves none of the
+// columns that are kept.
 template <int NV>
 __device__ __forceinline__ void load_f32v_sc1(__amdgpu_buffer_rsrc_t rs, size_t row, int n, int N,
                                               float* v) {
