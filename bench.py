@@ -896,8 +896,9 @@ def traffic_run(pkg, torch, gen, dev, ms=(1,)):
 
 def gemm_pmc_run(pkg, torch, gen, dev):
     """Workload for the MFMA-utilisation passes: the M=750 prefill GEMMs
-    (gate/up with SiLU x up, and down) 10 times each, after one warm-up
-    launch each."""
+    (gate/up with SiLU x up, and down), then the wide-M route at M = 128 (the
+    Llama gate/up pair, and T5 wo 4096 x 10240, which splits K), 11
+    launches each (the first is the warm-up)."""
     M, K, F = 750, 3072, 8192
     x = torch.randn(M, K, generator=gen, device=dev).half()
     a = torch.randn(M, F, generator=gen, device=dev).half()
@@ -910,6 +911,16 @@ def gemm_pmc_run(pkg, torch, gen, dev):
         pkg.matmul_q4_silu_mul(x, gate, up, M, K, F, out=y)
     for _ in range(11):
         pkg.linear(a, down, M, F, K, fast=True, out=z)
+    m, kt5, nt5 = 128, 10240, 4096
+    x128 = x[:m].contiguous()
+    wo = q4(pkg, torch, nt5, kt5, gen, dev)
+    xt5 = torch.randn(m, kt5, generator=gen, device=dev).half()
+    y128 = torch.empty(m, F, device=dev, dtype=torch.float16)
+    zt5 = torch.empty(m, nt5, device=dev, dtype=torch.float16)
+    for _ in range(11):
+        pkg.matmul_q4_silu_mul(x128, gate, up, m, K, F, out=y128)
+    for _ in range(11):
+        pkg.linear(xt5, wo, m, kt5, nt5, fast=True, out=zt5)
     torch.cuda.synchronize()
     print("gemm pmc run done", flush=True)
 
