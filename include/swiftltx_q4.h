@@ -15,7 +15,8 @@
  *     frees or keeps them.  Outputs are written, never read.
  *   - Memory: the only device memory the library allocates is a per-stream
  *     workspace: fp32 partial sums for GEMMs with too few output tiles to
- *     fill the GPU (split-K, e.g. M=750 x N=3072) and for every
+ *     fill the GPU (split-K, e.g. M=750 x N=3072, and at 8 < M <= 256 the
+ *     mid- and wide-M K splits, e.g. M=32 x 4096 x 10240) and for every
  *     sltx_matmul_q4_residual_rms_norm, the block partials of
  *     sltx_argmax, and the probabilities and candidate list of
  *     sltx_sample_top_p[_state], after 16 KB of split-K arrival counters

@@ -260,9 +260,16 @@ int gemm_route(const GemmParams& p, bool a_bf16, NarrowPlan* np, SkinnyPlan* sp,
     // - M = 12, 16: q|k|v 6.5 against 8.5 / 9.5, the 8192-row set 7.3
     //   against 7.3 / 7.7; o 6.2 against 5.7 / 6.1, T5 q/k/v/o 9.8 against
     //   6.7 / 7.3, the vocabulary head (M = 8) 87 against 62 us.
+    // One weight set that the mid-M route splits over K in two halves
+    // (mid_splits: N <= 4096, K = 4096, 8192 or 10240) takes it above 8 rows
+    // at K = 10240, 12 at K = 8192 and 16 at K = 4096.  Measured against the
+    // small-M route at M = 9 / 12 / 16 / 20 / 24: T5 wo 10.9-11.2 against
+    // 12.6 / 14.3 / 16.0 us, Llama down 11.4-11.5 against 9.9 / 11.2 / 12.6,
+    // T5 q/k/v/o 7.9-8.1 against 6.2 / 6.9 / 7.3 / 8.9 / 9.6.
     const bool kshort = p.K <= 3072;
     const bool mid_rows = (p.M > 16 && (kshort || !skinny || p.M > 24)) ||
-                          (p.M > 8 && kshort && p.w1 == nullptr && p.N >= 4096 && p.N <= 16384);
+                          (p.M > 8 && kshort && p.w1 == nullptr && p.N >= 4096 && p.N <= 16384) ||
+                          (mid_splits(p) == 2 && p.M > (p.K >= 10240 ? 8 : p.K >= 8192 ? 12 : 16));
     if (mid_rows && mid_plan(p, a_bf16)) return SLTX_ROUTE_MID;
     if (skinny) return SLTX_ROUTE_SMALL_M;
     return SLTX_ROUTE_GEMM;
@@ -300,7 +307,14 @@ int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w
     const int route = gemm_route(p, x_dtype == kBF16, &np, &sp, &wp);
     if (route == SLTX_ROUTE_NARROW) return finish(launch_narrow(p, np, st), fn);
     if (route == SLTX_ROUTE_SMALL_M) return finish(launch_skinny(p, sp, st), fn);
-    if (route == SLTX_ROUTE_MID) return finish(launch_mid(p, st), fn);
+    if (route == SLTX_ROUTE_MID) {
+        // two K halves where the blocks are few, when the stream's workspace
+        // exists (not first allocated under capture); else the whole K
+        int splits = mid_splits(p);
+        if (splits > 1 && !(p.ws = stream_workspace(st, mid_ws_bytes(p, splits), 0, &p.tickets)))
+            splits = 1;
+        return finish(launch_mid(p, splits, st), fn);
+    }
     if (route == SLTX_ROUTE_WIDE) {
         if (wp.splits > 1 && !(p.ws = stream_workspace(st, wp.ws_bytes, 0, &p.tickets))) {
             // no workspace (the stream is being captured): the same product

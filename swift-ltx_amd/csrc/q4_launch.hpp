@@ -176,18 +176,23 @@ struct SkinnyPlan {
 };
 bool skinny_plan(const GemmParams& p, bool a_bf16, SkinnyPlan* out);
 hipError_t launch_skinny(const GemmParams& p, const SkinnyPlan& pl, hipStream_t st);
-// Mid-M route (q4_mid.hip, M <= 32, K % 256 == 0, fp16 X): 64 weight rows
-// per block over all K, 2 row tiles x 4 K-groups of waves, X and packed W
-// copied to LDS in whole lines through 4- and 8-stage rings.  mid_plan
-// returns false when the shape, epilogue or alignment is not covered.
+// Mid-M route (q4_mid.hip, M <= 32, K % 1024 == 0, fp16 X): 32 output
+// columns per block (one set, or a gate/up pair) over all K or, for one set
+// over few blocks, half of it (mid_splits); 8 compute waves over K-groups
+// and 8 copy waves feeding LDS in whole lines.  mid_plan returns false when
+// the shape, epilogue or alignment is not covered.  With 2 splits p.ws must
+// hold mid_ws_bytes and p.tickets be set: the last of a tile's two blocks
+// adds the halves.
 bool mid_plan(const GemmParams& p, bool a_bf16);
-hipError_t launch_mid(const GemmParams& p, hipStream_t st);
+int mid_splits(const GemmParams& p);
+size_t mid_ws_bytes(const GemmParams& p, int splits);
+hipError_t launch_mid(const GemmParams& p, int splits, hipStream_t st);
 
 // Wide-M route (q4_wide.hip, 32 < M <= 256, fp16 X): 64 weight rows (or a
 // 32-row gate/up pair) per block over all of its K range, up to 128
 // activation rows per block (more rows take more blocks), the 8 waves
 // splitting K; optionally split over K across blocks (fp32 partials in the
-// workspace, then the split-K reduce pass).  wide_plan returns false when the
+// workspace; the last block of each output tile adds them).  wide_plan returns false when the
 // shape, epilogue or alignment is not covered.
 struct WidePlan {
     int tm;          // 32-row MFMA tiles per block (2..4)

@@ -44,9 +44,14 @@
 //  * After the last round the four K-groups' accumulator tiles are summed in
 //    LDS in a fixed order and the epilogue (gated SiLU / GELU-tanh pair,
 //    bias, GELU-tanh, residual add) runs on the fp32 sums.
+//  * One weight set over few blocks (N <= 4096: 128 blocks for 256 CUs) may
+//    split K in two halves across blocks (SPLIT): each block stores its
+//    half's sums to the workspace and the last of the two adds them, in
+//    split order, and runs the epilogue (q4_split.hpp).
 #include "q4_common.hpp"
 #include "q4_dequant.hpp"
 #include "q4_launch.hpp"
+#include "q4_split.hpp"
 
 namespace sltx {
 
@@ -104,11 +109,13 @@ __device__ __forceinline__ void lds_barrier() {
 
 // NG weight groups of 1024 k in WSL = 2 LDS slots (the only count built):
 // the slot of group G - 1 is refilled with group G + 1 once every wave has
-// finished group G - 1.
-template <bool PAIR, bool KG8, int NG, int WSL>
+// finished group G - 1.  SPLIT: block (x, y) covers groups y NG .. y NG +
+// NG - 1 of K = 2 NG groups.
+template <bool PAIR, bool KG8, int NG, int WSL, bool SPLIT>
 __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
     using S = MidShape<KG8>;
     static_assert(PAIR != KG8, "gated pairs: two row tiles; one set: the 32-row block");
+    static_assert(!SPLIT || KG8, "K splits: one weight set");
     constexpr int KG = S::KG, RK = S::RK, BROWS = S::BROWS, RPG = S::RPG;
     constexpr int XSLOTS = S::XSLOTS, NXC = S::NXC, GSLOTS = S::GSLOTS, NWG = S::NWG;
     constexpr int NR = NG * RPG;                // rounds
@@ -128,20 +135,26 @@ __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n0 = blockIdx.x * (PAIR ? 32 : BROWS);
     const int K = p.K, groups = p.groups;
-    const int alloc = mid_slab_alloc(SROWS, groups);
+    const int split = SPLIT ? (int)blockIdx.y : 0;
+    const int kb = split * NG * 1024;           // this block's first k
+    // scale groups of this block's K range: gblk from gbase
+    const int gblk = SPLIT ? groups / 2 : groups, gbase = split * gblk;
+    const int alloc = mid_slab_alloc(SROWS, gblk);
     f32x16 acc;
 
     if (wave >= NCW + NLW) {
         // ---- X-copy waves: the slabs, then X round by round ----
         const int lt = tid - CTHREADS - LTHREADS, lw = 64 * (wave - NCW - NLW);
-        const int pieces = mid_slab_pieces(SROWS, groups);
-        const int valid = min(SROWS, p.N - n0) * groups * 2;   // slab bytes inside the arrays
+        const int pieces = mid_slab_pieces(SROWS, gblk);
+        const int valid = min(SROWS, p.N - n0) * gblk * 2;   // slab bytes inside the arrays
         for (int a = 0; a < NSLAB; ++a) {
             const uint16_t* arr = a == 0 ? p.s0 : a == 1 ? p.b0 : a == 2 ? p.s1 : p.b1;
             const char* src = reinterpret_cast<const char*>(arr + (size_t)n0 * groups);
             for (int c0 = lw; c0 < pieces; c0 += LTHREADS) {
                 int off = (c0 + lane) * 16;
                 if (off >= valid) off = 0;   // a spare copy of piece 0
+                // SPLIT: the slab's row r is groups gbase .. of row n0 + r
+                if (SPLIT) off = (off / (gblk * 2)) * (groups * 2) + gbase * 2 + off % (gblk * 2);
                 __builtin_amdgcn_global_load_lds((const void*)(src + off),
                                                  (lds_ptr_t)(sb_lds + a * alloc + c0), 16, 0, 0);
             }
@@ -155,7 +168,7 @@ __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
             const int s = lt + LTHREADS * i;
             const int kt = s / (BM * 8), row = (s >> 3) & (BM - 1);
             const int c16 = (s & 7) ^ (row & 7) ^ ((row >> 3) & 1);
-            x_src[i] = A + (size_t)min(row, p.M - 1) * K + kt * 64 + c16 * 8;
+            x_src[i] = A + (size_t)min(row, p.M - 1) * K + kb + kt * 64 + c16 * 8;
         }
         const char* spare_src = reinterpret_cast<const char*>(p.a) + lane * 4;
         auto issue_x = [&](int q) {   // NXC vector-memory ops
@@ -194,7 +207,7 @@ __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
             const uint32_t* W = (PAIR && row >= 32) ? p.w1 : p.w0;
             int n = PAIR ? n0 + (row & 31) : n0 + row;
             if (n >= p.N) n = 0;   // rows past N read row 0 (never stored)
-            w_src[i] = W + (size_t)n * (K / 8) + (((lane & 31) ^ (row & 15)) * 4);
+            w_src[i] = W + (size_t)n * (K / 8) + kb / 8 + (((lane & 31) ^ (row & 15)) * 4);
         }
         auto issue_w = [&](int G) {   // NWG vector-memory ops: group G into slot G % WSL
             u32x4* slot = wl + (G % WSL) * GSLOTS;
@@ -230,7 +243,7 @@ __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
         // q * 256 + 64 g + 32 h
         const uint16_t* sbl = reinterpret_cast<const uint16_t*>(sb_lds);
         const int e = PAIR ? j : 0, srow = PAIR ? r : 32 * j + r;
-        const uint16_t* s_row = sbl + (size_t)(2 * e) * alloc * 8 + srow * groups;
+        const uint16_t* s_row = sbl + (size_t)(2 * e) * alloc * 8 + srow * gblk;
         const uint16_t* b_row = s_row + (size_t)alloc * 8;
         const int glog2 = 5 + p.gshift;
 #pragma unroll
@@ -241,7 +254,7 @@ __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
             const u32x4* xst = xs + (q % NSX) * XSLOTS + g * (BM * 8);
             const u32x4 wpc = wl[((q / RPG) % WSL) * GSLOTS + wrow * 32 +
                                  ((2 * KG * (q % RPG) + 2 * g + h) ^ (wrow & 15))];
-            const int gi = (q * RK + 64 * g + 32 * h) >> glog2;
+            const int gi = (q * RK + 64 * g + 32 * h) >> glog2;   // of the block's groups
             const uint32_t sv = s_row[gi], bv = b_row[gi];
             const f16x2 s2 = as_f16x2(sv | (sv << 16));
             const f16x2 b2 = as_f16x2(bv | (bv << 16));
@@ -265,10 +278,12 @@ __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
     // D[m][c] of a 32x32 tile is element 4 (m / 8) + m % 4 of lane
     // c + 32 ((m / 4) % 2)
     constexpr int NCOLS = PAIR ? 32 : BROWS;
+    static_assert(!SPLIT || BM * NCOLS == MTHREADS, "a split block: one output per thread");
     for (int o = tid; o < BM * NCOLS; o += MTHREADS) {
         const int m = o / NCOLS, c = o % NCOLS;
         const int n = n0 + c;
-        if (m >= p.M || n >= p.N) continue;
+        const bool valid = m < p.M && n < p.N;
+        if (!SPLIT && !valid) continue;
         const int jj = (PAIR || KG8) ? 0 : c >> 5;
         const int idx = (4 * (m >> 3) + (m & 3)) * 64 + (c & 31) + 32 * ((m >> 2) & 1);
         // the tile of (K-group gg, row tile t) is wave 2 gg + t (KG8: wave gg)
@@ -278,6 +293,20 @@ __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
         for (int gg = 0; gg < KG; ++gg) {
             v0 += red[wv(gg, jj) * 1024 + idx];
             if constexpr (PAIR) v1 += red[wv(gg, 1) * 1024 + idx];
+        }
+        if constexpr (SPLIT) {
+            // this half's sum to the workspace; the block that arrives second
+            // loads the other half's and adds the two in split order
+            const __amdgpu_buffer_rsrc_t rs = ws_rsrc(p.ws);
+            if (valid) store_f32v_sc1<1>(rs, ((size_t)split * p.M + m) * p.N, n, p.N, &v0);
+            if (!split_arrive_last(p.tickets + blockIdx.x, 2)) return;
+            if (!valid) return;
+            float other;
+            load_f32v_sc1<1>(rs, ((size_t)(1 - split) * p.M + m) * p.N, n, p.N, &other);
+            float sum = 0.0f;
+            sum += split == 0 ? v0 : other;
+            sum += split == 0 ? other : v0;
+            v0 = sum;
         }
         float out;
         if constexpr (PAIR) {
@@ -295,9 +324,10 @@ __global__ __launch_bounds__(MTHREADS, 1) void q4_mid_kernel(GemmParams p) {
     }
 }
 
-// Dynamic LDS: the scale / bias slabs (32 rows each)
-size_t mid_lds(const GemmParams& p, bool pair) {
-    return (size_t)(pair ? 4 : 2) * mid_slab_alloc(32, p.groups) * 16;
+// Dynamic LDS: the scale / bias slabs (32 rows each, the groups of a
+// block's K range)
+size_t mid_lds(const GemmParams& p, bool pair, int splits = 1) {
+    return (size_t)(pair ? 4 : 2) * mid_slab_alloc(32, p.groups / splits) * 16;
 }
 
 size_t mid_static_lds(int ng, int wsl, bool pair) {
@@ -323,15 +353,24 @@ int mid_wsl(const GemmParams& p, bool pair) {
     return 0;
 }
 
-template <bool PAIR, bool KG8, int NG, int WSL>
+template <bool PAIR, bool KG8, int NG, int WSL, bool SPLIT = false>
 hipError_t launch_cfg(const GemmParams& p, const dim3& grid, size_t lds, hipStream_t st) {
-    hipLaunchKernelGGL((q4_mid_kernel<PAIR, KG8, NG, WSL>), grid, dim3(MTHREADS), lds, st, p);
+    hipLaunchKernelGGL((q4_mid_kernel<PAIR, KG8, NG, WSL, SPLIT>), grid, dim3(MTHREADS), lds, st,
+                       p);
     return hipGetLastError();
 }
 
 hipError_t launch_sel(const GemmParams& p, bool pair, int wsl, const dim3& grid, size_t lds,
                       hipStream_t st) {
     const int ng = p.K / 1024;
+    if (grid.y == 2) {   // K in two halves (one set)
+        switch (ng / 2) {
+            case 2: return launch_cfg<false, true, 2, 2, true>(p, grid, lds, st);
+            case 4: return launch_cfg<false, true, 4, 2, true>(p, grid, lds, st);
+            case 5: return launch_cfg<false, true, 5, 2, true>(p, grid, lds, st);
+        }
+        return hipErrorInvalidValue;
+    }
     if (pair) {
         if (ng == 2) return launch_cfg<true, false, 2, 2>(p, grid, lds, st);
         if (ng == 3) return launch_cfg<true, false, 3, 2>(p, grid, lds, st);
@@ -371,10 +410,34 @@ bool mid_plan(const GemmParams& p, bool a_bf16) {
     return (al & 15) == 0;
 }
 
-hipError_t launch_mid(const GemmParams& p, hipStream_t st) {
+// K in two halves across blocks for one weight set whose 32-row blocks would
+// fill at most half of the CUs, where the half-K kernel is built (K = 4096,
+// 8192, 10240).
+int mid_splits(const GemmParams& p) {
+    if (p.w1 != nullptr) return 1;
+    const int nblocks = (p.N + 31) / 32, ng = p.K / 1024;
+    if (2 * nblocks > kCUs || ng % 2 != 0) return 1;
+    const int half = ng / 2;
+    if (half != 2 && half != 4 && half != 5) return 1;
+    // whole 16-byte slab pieces per row; the arrival flag's LDS beside the rest
+    if ((p.groups / 2) % 8 != 0 ||
+        mid_static_lds(ng, 2, false) + 256 + mid_lds(p, false, 2) > kMaxLds)
+        return 1;
+    return 2;
+}
+
+size_t mid_ws_bytes(const GemmParams& p, int splits) {
+    return splits > 1 ? (size_t)splits * p.M * p.N * sizeof(float) : 0;
+}
+
+hipError_t launch_mid(const GemmParams& p, int splits, hipStream_t st) {
     const bool pair = p.w1 != nullptr;
-    const dim3 grid((unsigned)((p.N + 31) / 32));   // 32 output columns per block
-    return launch_sel(p, pair, mid_wsl(p, pair), grid, mid_lds(p, pair), st);
+    const unsigned nblocks = (unsigned)((p.N + 31) / 32);   // 32 output columns per block
+    if (splits != 1 && (splits != 2 || pair || !p.ws || !p.tickets ||
+                        nblocks > (unsigned)kTickets || mid_ws_bytes(p, splits) > 0x7fffffffu))
+        return hipErrorInvalidValue;
+    const dim3 grid(nblocks, (unsigned)splits);
+    return launch_sel(p, pair, mid_wsl(p, pair), grid, mid_lds(p, pair, splits), st);
 }
 
 }  // namespace sltx

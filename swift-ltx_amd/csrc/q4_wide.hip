@@ -41,6 +41,7 @@
 #include "q4_dequant.hpp"
 #include "q4_epilogue.hpp"
 #include "q4_launch.hpp"
+#include "q4_split.hpp"
 
 namespace sltx {
 
@@ -126,70 +127,6 @@ __device__ __forceinline__ int wpos(int row, int w) {
 // both for the fill (consecutive groups of a row) and for the reads (the
 // rows of one group).
 __device__ __forceinline__ int spos(int gi, int row) { return gi * WBN + (row ^ (gi & 63)); }
-
-// Split-K partial sums move through the workspace with accesses that are
-// coherent across the XCDs' L2s: buffer loads and stores with the sc1 cache
-// policy, the one the compiler gives agent-scope atomic loads and stores.
-// The stores have completed (vmcnt) before a block counts its arrival, and
-// the last block loads after reading the count, so no L2-wide write-back or
-// invalidate is needed (agent-scope fences, which do both, made the fix-up
-// slower than the separate reduce pass).
-constexpr int kSc1 = 16;   // cache-policy operand: sc1
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(const float* base) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, 0x7fffffff, 0x00020000);
-}
-
-// NV consecutive partial sums into row[n .. n+NV-1] (element offset `row`
-// in the workspace), columns past N dropped.
-template <int NV>
-__device__ __forceinline__ void store_f32v_sc1(__amdgpu_buffer_rsrc_t rs, size_t row, int n, int N,
-                                               const float* v) {
-    if ((N % NV) == 0 && n + NV <= N) {
-        const int o = (int)((row + n) * sizeof(float));
-        if constexpr (NV == 4) {
-            const u32x4 d = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
-                             __float_as_uint(v[3])};
-            __builtin_amdgcn_raw_buffer_store_b128(d, rs, o, 0, kSc1);
-        } else {
-            typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-            const u32x2 d = {__float_as_uint(v[0]), __float_as_uint(v[1])};
-            __builtin_amdgcn_raw_buffer_store_b64(d, rs, o, 0, kSc1);
-        }
-        return;
-    }
-#pragma unroll
-    for (int e = 0; e < NV; ++e)
-        if (n + e < N)
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[e]), rs,
-                                                  (int)((row + n + e) * sizeof(float)), 0, kSc1);
-}
-
-// NV consecutive partial sums row[n .. n+NV-1], loaded whatever n (columns
-// past N read an earlier column, to be discarded): no load sits behind a
-// branch.  n is a multiple of NV, so with N % NV == 0 a group lies wholly
-// before N or wholly past it, and clamping a group past N moves none of the
-// columns that are kept.
-template <int NV>
-__device__ __forceinline__ void load_f32v_sc1(__amdgpu_buffer_rsrc_t rs, size_t row, int n, int N,
-                                              float* v) {
-    if ((N % NV) == 0) {
-        const int o = (int)((row + min(n, N - NV)) * sizeof(float));
-        if constexpr (NV == 4) {
-            const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, kSc1);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = __uint_as_float(q[e]);
-        } else {
-            const auto q = __builtin_amdgcn_raw_buffer_load_b64(rs, o, 0, kSc1);
-            v[0] = __uint_as_float(q[0]);
-            v[1] = __uint_as_float(q[1]);
-        }
-    } else {
-#pragma unroll
-        for (int e = 0; e < NV; ++e)
-            v[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                rs, (int)((row + min(n + e, N - 1)) * sizeof(float)), 0, kSc1));
-    }
-}
 
 // The last block of an output tile: the S splits' partial sums of the rows
 // and columns this thread summed (32 i + ml, n .. n + NV - 1) -- its own
@@ -562,24 +499,8 @@ __global__ __launch_bounds__(WT, 1) void q4_wide_kernel(GemmParams p, WideArgs w
         }
     }
     if constexpr (SPLIT) {
-        // Arrival on the tile's counter: every thread's sc1 partial stores
-        // have completed (vmcnt) before the barrier, and thread 0 adds 1 after
-        // it (an agent-scope atomic); the block that reads S - 1 loads the
-        // partials (sc1) after its second barrier, and resets the counter
-        // for the next launch.
-        __shared__ int last_block;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (tid == 0) {
-            unsigned* t = p.tickets + blockIdx.y * gridDim.x + blockIdx.x;
-            const unsigned prev = __hip_atomic_fetch_add(t, 1u, __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT);
-            const int last = prev + 1 == gridDim.z;
-            if (last) __hip_atomic_store(t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            last_block = last;
-        }
-        __syncthreads();
-        if (!last_block) return;
+        // the last of the tile's blocks (q4_split.hpp) adds the splits
+        if (!split_arrive_last(p.tickets + blockIdx.y * gridDim.x + blockIdx.x, gridDim.z)) return;
         if (gridDim.z == 2) wide_fixup<2, TM, PAIR, NV>(p, m0, wa.mrows, ml, n, split, own0, own1);
         else if (gridDim.z == 4) wide_fixup<4, TM, PAIR, NV>(p, m0, wa.mrows, ml, n, split, own0, own1);
         else wide_fixup<8, TM, PAIR, NV>(p, m0, wa.mrows, ml, n, split, own0, own1);

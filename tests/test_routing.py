@@ -26,10 +26,11 @@ def test_mid_m_route_above_16_rows(pkg, M):
     11.9 against 15.3 us at M = 32, q|k|v 6.7 against 14.9, o 6.4 against 8.8,
     a single 8192-row set 7.6 against 10.4), and at K = 8192 / 10240, where
     the small-M route does not run (Llama down 15.4 against the GEMM's 23.0,
-    T5 wo 14.9 against 26.9).  At K = 4096 it takes over above 24 rows (T5
-    q/k/v/o 9.9 against 10.9 at M = 32, 9.9 against 9.6 at M = 24; the T5
-    GeGLU pair 31.5 against 36.7 at M = 32); a gated pair at group size 32
-    fits the LDS at K = 2048 only."""
+    T5 wo 14.9 against 26.9; with K in two halves now 11.5 and 11.2).  At
+    K = 4096 a single set of at most 4096 rows, which it splits over K, takes
+    it above 16 rows (T5 q/k/v/o 8.0 against 8.9 at M = 20), any other above
+    24 rows (the T5 GeGLU pair 31.5 against 36.7 at M = 32); a gated pair at
+    group size 32 fits the LDS at K = 2048 only."""
     assert pkg.gemm_route(M, **LLAMA_PAIR) == "mid"
     for N in (5120, 3072, 8192, 64, 33):
         assert pkg.gemm_route(M, N, 3072) == "mid", N
@@ -37,7 +38,8 @@ def test_mid_m_route_above_16_rows(pkg, M):
     assert pkg.gemm_route(M, 3072, 8192) == "mid"
     assert pkg.gemm_route(M, 4096, 10240) == "mid"
     assert pkg.gemm_route(M, **T5_WI_PAIR) == ("mid" if M > 24 else "small_m")
-    assert pkg.gemm_route(M, 4096, 4096) == ("mid" if M > 24 else "small_m")
+    assert pkg.gemm_route(M, 4096, 4096) == "mid"
+    assert pkg.gemm_route(M, 5120, 4096) == ("mid" if M > 24 else "small_m")   # no split
     assert pkg.gemm_route(M, 8192, 3072, group_size=32, gated=True) == "small_m"   # LDS
     assert pkg.gemm_route(M, 8192, 2048, group_size=32, gated=True) == "mid"   # 160 KB
 
@@ -45,12 +47,17 @@ def test_mid_m_route_above_16_rows(pkg, M):
 @pytest.mark.parametrize("M", [9, 12, 16])
 def test_mid_m_route_for_one_set_above_8_rows(pkg, M):
     """9..16 rows: one weight set of 4096..16384 rows at K <= 3072 takes the
-    mid-M route (q|k|v 6.5 against 8.5 us at M = 12); o (3072 rows), the
-    vocabulary head, T5 q/k/v/o (K = 4096) and gated pairs stay on the small-M
-    route."""
+    mid-M route (q|k|v 6.5 against 8.5 us at M = 12), and so does a set of at
+    most 4096 rows that it splits over K, at K = 10240 (T5 wo 10.9-11.1
+    against 12.6 / 14.3 / 16.0 us at M = 9 / 12 / 16) and above 12 rows at
+    K = 8192 (Llama down 11.4 against 12.6 at M = 16, 11.4 against 11.2 at
+    M = 12); o (3072 rows), the vocabulary head, T5 q/k/v/o (K = 4096: 8.0
+    against 7.3 at M = 16) and gated pairs stay on the small-M route."""
     assert pkg.gemm_route(M, 5120, 3072) == "mid"
     assert pkg.gemm_route(M, 8192, 3072) == "mid"
     assert pkg.gemm_route(M, 16384, 2048) == "mid"
+    assert pkg.gemm_route(M, 4096, 10240) == "mid"
+    assert pkg.gemm_route(M, 3072, 8192) == ("mid" if M > 12 else "small_m")
     assert pkg.gemm_route(M, 3072, 3072) == "small_m"
     assert pkg.gemm_route(M, 4096, 4096) == "small_m"
     assert pkg.gemm_route(M, 128256, 3072) == "small_m"
@@ -82,6 +89,8 @@ def test_m_above_4_leaves_the_narrow_route(pkg, N, K):
         if K in (2048, 3072) and (M > 16 or (M > 8 and 4096 <= N <= 16384)):
             want = "mid"
         if M > 24 or (M > 16 and K > 4096):   # K = 4096 / 8192 above the small-M route
+            want = "mid"
+        if N <= 4096 and K in (4096, 8192) and M > (12 if K == 8192 else 16):   # K halves
             want = "mid"
         assert pkg.gemm_route(M, N, K) == want, (M, N, K)
 
