@@ -1025,8 +1025,12 @@ def _trace_rows(folder):
             for r in csv.DictReader(open(f)):
                 wg = int(r.get("Workgroup_Size_X", r.get("Workgroup_Size", 1)) or 1)
                 gr = int(r.get("Grid_Size_X", r.get("Grid_Size", 1)) or 1)
+                blocks = gr // max(1, wg)
+                for d in ("Y", "Z"):   # split launches spread their blocks over y and z
+                    gd = int(r.get(f"Grid_Size_{d}", 1) or 1)
+                    blocks *= gd // max(1, int(r.get(f"Workgroup_Size_{d}", 1) or 1))
                 rows.append((r["Kernel_Name"], int(r["Start_Timestamp"]),
-                             int(r["End_Timestamp"]), gr // max(1, wg), wg,
+                             int(r["End_Timestamp"]), blocks, wg,
                              r.get("Arch_VGPR_Count", ""), r.get("Accum_VGPR_Count", ""),
                              r.get("LDS_Block_Size", r.get("Group_Segment_Size", ""))))
     rows.sort(key=lambda r: r[1])

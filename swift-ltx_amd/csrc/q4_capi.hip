@@ -261,15 +261,17 @@ int gemm_route(const GemmParams& p, bool a_bf16, NarrowPlan* np, SkinnyPlan* sp,
     //   against 7.3 / 7.7; o 6.2 against 5.7 / 6.1, T5 q/k/v/o 9.8 against
     //   6.7 / 7.3, the vocabulary head (M = 8) 87 against 62 us.
     // One weight set that the mid-M route splits over K in two halves
-    // (mid_splits: N <= 4096, K = 4096, 8192 or 10240) takes it above 8 rows
+    // (mid_splits: N <= 4096, K = 4096, 8192 or 10240) takes it above 5 rows
     // at K = 10240, 12 at K = 8192 and 16 at K = 4096.  Measured against the
-    // small-M route at M = 9 / 12 / 16 / 20 / 24: T5 wo 10.9-11.2 against
-    // 12.6 / 14.3 / 16.0 us, Llama down 11.4-11.5 against 9.9 / 11.2 / 12.6,
-    // T5 q/k/v/o 7.9-8.1 against 6.2 / 6.9 / 7.3 / 8.9 / 9.6.
+    // small-M route: T5 wo 11.1 / 11.1 / 11.1 against 11.1 / 11.5 / 12.5 us
+    // at M = 5 / 6 / 8, 10.9-11.2 against 12.6 / 14.3 / 16.0 at M = 9 / 12 /
+    // 16; Llama down 11.4-11.5 against 10.3 / 11.2 / 12.6 at M = 10 / 12 /
+    // 16; T5 q/k/v/o 7.9-8.1 against 6.9 / 7.3 / 8.9 / 9.6 at M = 14 / 16 /
+    // 20 / 24.
     const bool kshort = p.K <= 3072;
     const bool mid_rows = (p.M > 16 && (kshort || !skinny || p.M > 24)) ||
                           (p.M > 8 && kshort && p.w1 == nullptr && p.N >= 4096 && p.N <= 16384) ||
-                          (mid_splits(p) == 2 && p.M > (p.K >= 10240 ? 8 : p.K >= 8192 ? 12 : 16));
+                          (mid_splits(p) == 2 && p.M > (p.K >= 10240 ? 5 : p.K >= 8192 ? 12 : 16));
     if (mid_rows && mid_plan(p, a_bf16)) return SLTX_ROUTE_MID;
     if (skinny) return SLTX_ROUTE_SMALL_M;
     return SLTX_ROUTE_GEMM;

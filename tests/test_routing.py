@@ -49,7 +49,7 @@ def test_mid_m_route_for_one_set_above_8_rows(pkg, M):
     """9..16 rows: one weight set of 4096..16384 rows at K <= 3072 takes the
     mid-M route (q|k|v 6.5 against 8.5 us at M = 12), and so does a set of at
     most 4096 rows that it splits over K, at K = 10240 (T5 wo 10.9-11.1
-    against 12.6 / 14.3 / 16.0 us at M = 9 / 12 / 16) and above 12 rows at
+    against 12.6 / 14.3 / 16.0 us at M = 9 / 12 / 16; from M = 6) and above 12 rows at
     K = 8192 (Llama down 11.4 against 12.6 at M = 16, 11.4 against 11.2 at
     M = 12); o (3072 rows), the vocabulary head, T5 q/k/v/o (K = 4096: 8.0
     against 7.3 at M = 16) and gated pairs stay on the small-M route."""
@@ -72,6 +72,16 @@ def test_one_weight_set_at_m_le_4_is_narrow(pkg, N, K, M):
         assert pkg.gemm_route(M, N, K) == "small_m"
     else:
         assert pkg.gemm_route(M, N, K) == "narrow"
+
+
+def test_t5_wo_takes_the_split_mid_route_from_6_rows(pkg):
+    """T5 wo (4096 x 10240) splits K in halves on the mid-M route from M = 6
+    (11.1 against 11.5 / 12.5 us on the small-M route at M = 6 / 8; even at
+    M = 5)."""
+    assert pkg.gemm_route(5, 4096, 10240) == "small_m"
+    for M in (6, 7, 8, 16, 32):
+        assert pkg.gemm_route(M, 4096, 10240) == "mid", M
+    assert pkg.gemm_route(8, 4200, 10240) == "small_m"   # 132 blocks: no split
 
 
 @pytest.mark.parametrize("M", [1, 2, 4, 8])
