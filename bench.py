@@ -1015,10 +1015,19 @@ def _trace_rows(folder):
     if dbs:
         for db in dbs:
             c = sqlite3.connect(db)
-            for r in c.execute("select name, start, end, grid_x, workgroup_x, vgpr_count, "
-                               "accum_vgpr_count, lds_size from kernels"):
-                rows.append((r[0], int(r[1]), int(r[2]), int(r[3]) // max(1, int(r[4])),
-                             int(r[4]), r[5], r[6], r[7]))
+            try:   # blocks over every grid dimension, where the database has them
+                q = c.execute("select name, start, end, grid_x, workgroup_x, vgpr_count, "
+                              "accum_vgpr_count, lds_size, grid_y, workgroup_y, grid_z, "
+                              "workgroup_z from kernels").fetchall()
+            except sqlite3.Error:
+                q = [r + (1, 1, 1, 1) for r in c.execute(
+                    "select name, start, end, grid_x, workgroup_x, vgpr_count, "
+                    "accum_vgpr_count, lds_size from kernels")]
+            for r in q:
+                blocks = int(r[3]) // max(1, int(r[4]))
+                blocks *= (int(r[8] or 1) // max(1, int(r[9] or 1))) * \
+                    (int(r[10] or 1) // max(1, int(r[11] or 1)))
+                rows.append((r[0], int(r[1]), int(r[2]), blocks, int(r[4]), r[5], r[6], r[7]))
     else:
         for f in sorted(glob.glob(os.path.join(folder, "**", "*kernel_trace.csv"),
                                   recursive=True)):
