@@ -341,8 +341,11 @@ typedef enum {
     SLTX_ROUTE_GEMM = 0,     /* MFMA GEMM, split over K when its tiles would not fill the GPU */
     SLTX_ROUTE_SMALL_M = 1,  /* small-M weight stream (M <= 32, 16x16x32 MFMA) */
     SLTX_ROUTE_NARROW = 2,   /* narrow weight stream (one weight set, M <= 4, 4x4x4 MFMA) */
-    SLTX_ROUTE_MID = 3,      /* pipelined weight stream (8 < M <= 32, X and W through LDS, 32x32x16 MFMA) */
-    SLTX_ROUTE_WIDE = 4      /* 32 < M <= 256: 64 weight rows per block over all K, waves split K */
+    SLTX_ROUTE_MID = 3,      /* pipelined weight stream (8 < M <= 32, from M = 6 for a set of at most
+                                4096 rows at K = 10240; X and W through LDS, 32x32x16 MFMA; such
+                                sets split K in halves across blocks) */
+    SLTX_ROUTE_WIDE = 4      /* 32 < M <= 256: 64 weight rows per block over its K range, waves
+                                split K; K split across blocks where the blocks are few */
 } sltx_route;
 int sltx_gemm_route(int32_t M, int32_t N, int32_t K, int32_t group_size, int32_t gated,
                     int32_t x_dtype);
