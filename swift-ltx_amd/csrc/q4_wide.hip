@@ -502,6 +502,7 @@ __global__ __launch_bounds__(WT, 1) void q4_wide_kernel(GemmParams p, WideArgs w
         // the last of the tile's blocks (q4_split.hpp) adds the splits
         if (!split_arrive_last(p.tickets + blockIdx.y * gridDim.x + blockIdx.x, gridDim.z)) return;
         if (gridDim.z == 2) wide_fixup<2, TM, PAIR, NV>(p, m0, wa.mrows, ml, n, split, own0, own1);
+        else if (gridDim.z == 3) wide_fixup<3, TM, PAIR, NV>(p, m0, wa.mrows, ml, n, split, own0, own1);
         else if (gridDim.z == 4) wide_fixup<4, TM, PAIR, NV>(p, m0, wa.mrows, ml, n, split, own0, own1);
         else wide_fixup<8, TM, PAIR, NV>(p, m0, wa.mrows, ml, n, split, own0, own1);
     }
@@ -542,10 +543,16 @@ bool wide_plan(const GemmParams& p, bool a_bf16, WidePlan* out) {
     const int g = 32 << p.gshift;
     const int rounds = p.K / RK;
     const long blocks = (long)pl.nblocks * pl.mblocks;
-    int s = 1;   // 1, 2, 4 or 8 (the fix-up's instantiations)
+    int s = 1;   // 1, 2, 3, 4 or 8 (the fix-up's instantiations)
     while (s < 8 && rounds % (2 * s) == 0 &&
            ((long)p.K / s / g > SLAB_G || (blocks * s < 160 && rounds / (2 * s) >= 4)))
         s *= 2;
+    // Two splits that leave a quarter of the CUs idle, where three fit one
+    // round: three (Llama q|k|v, 80 blocks: 240 instead of 160; 11.2 / 11.8
+    // / 15.9 against 12.2 / 12.6 / 17.0 us at M = 33 / 64 / 128).
+    if (s < 3 && blocks * s < 192 && blocks * 3 <= kCUs && rounds % 3 == 0 && rounds / 3 >= 4 &&
+        (long)p.K / 3 / g <= SLAB_G)
+        s = 3;
     if ((long)p.K / s / g > SLAB_G) return false;
     // One block per CU: a grid of more than one round of 256 blocks repeats
     // the whole per-block time.  Measured against the GEMM (us, weights

@@ -6,7 +6,7 @@ applies the epilogue; it also resets the counter for the next launch.
 
 Same semantics as every M > 1 route (matmulQ4Fast / matmulQ4FastF32,
 Ops.swift:312-381; the SwiGLU / GeGLU pairs, LlamaModel.swift:275-277,
-T5Encoder.swift:191-199).  Covered: 2, 4 and 8 splits, one and two blocks
+T5Encoder.swift:191-199).  Covered: 2, 3, 4 and 8 splits, one and two blocks
 along M, gated pairs, ragged and odd column counts (element loads and
 stores), fp16 and fp32 outputs (which must agree bit for bit), launches
 back to back on one stream with different tile counts (the counters must
@@ -26,27 +26,35 @@ pytestmark = pytest.mark.gpu
 def wide_splits(M, N, K, g, pair):
     """The K splits the wide route plans for this shape (its rule: split
     while the blocks would not fill the GPU or a split's K range holds more
-    than 64 scale groups, in whole rounds of 128 k, up to 8 splits)."""
+    than 64 scale groups, in whole rounds of 128 k, up to 8 splits; three
+    instead of two where two leave a quarter of the CUs idle and three fit)."""
     mblocks = -(-M // 128)
     nblocks = -(-N // (32 if pair else 64))
     blocks, rounds, s = nblocks * mblocks, K // 128, 1
     while s < 8 and rounds % (2 * s) == 0 and (K // s // g > 64 or
                                                 (blocks * s < 160 and rounds // (2 * s) >= 4)):
         s *= 2
+    if (s < 3 and blocks * s < 192 and blocks * 3 <= 256 and rounds % 3 == 0 and rounds // 3 >= 4
+            and K // 3 // g <= 64):
+        s = 3
     return s
 
 
 # (M, N, K, g, epilogue, splits)
 CASES = [
-    (128, 5120, 3072, 64, None, 2),      # Llama q|k|v at M = 128
+    (128, 5120, 3072, 64, None, 3),      # Llama q|k|v at M = 128
+    (64, 5101, 3072, 32, None, 3),       # three splits, odd N
+    (200, 2600, 3072, 64, None, 3),      # three splits, two blocks along M, ragged N
+    (128, 3072, 3072, 64, None, 4),      # Llama o
     (128, 4096, 10240, 64, None, 4),     # T5 wo at M = 128
     (64, 1024, 8192, 64, None, 8),
     (200, 3072, 8192, 64, None, 2),      # two blocks along M
     (100, 1000, 4096, 32, None, 8),      # ragged last column block
     (64, 1001, 2048, 64, None, 4),       # odd N: element loads and stores
-    (128, 2560, 3072, 64, "gelu", 2),    # gated pairs
+    (128, 2560, 3072, 64, "gelu", 3),    # gated pairs
     (96, 1024, 4096, 64, "silu", 8),
 ]
+T5_WO, GELU_PAIR = CASES[4], CASES[9]
 
 
 def _run(pkg, args, M, N, K, g, epi, out=None, stream=None, f32=False):
@@ -97,7 +105,7 @@ def test_wide_splits_back_to_back(pkg, dev):
     (120 launches): each launch must leave every counter at zero for the
     next, and each must equal the first bit for bit."""
     import torch
-    shapes = [CASES[0], CASES[1], CASES[2]]
+    shapes = [CASES[0], T5_WO, CASES[5]]   # 3, 4 and 8 splits
     inputs = [_inputs(dev, *c[:5], seed=7 + i)[1] for i, c in enumerate(shapes)]
     st = torch.cuda.Stream()
     with torch.cuda.stream(st):
@@ -115,7 +123,7 @@ def test_wide_splits_in_graph(pkg, dev):
     the same stream between the replays: every replay equals the eager
     results bit for bit."""
     import torch
-    shapes = [CASES[1], CASES[6]]
+    shapes = [T5_WO, GELU_PAIR]
     inputs = [_inputs(dev, *c[:5], seed=21 + i)[1] for i, c in enumerate(shapes)]
     st = torch.cuda.Stream()
     with torch.cuda.stream(st):
