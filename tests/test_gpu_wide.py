@@ -28,6 +28,7 @@ SHAPES = [
     (33, 5120, 3072, 64), (64, 3072, 3072, 64), (100, 4096, 4096, 128), (128, 3072, 8192, 64),
     (200, 3072, 8192, 64), (256, 500, 2048, 32), (48, 64, 128, 64), (70, 130, 384, 32),
     (129, 1000, 1024, 64), (96, 8192, 3072, 64), (160, 96, 2048, 128), (41, 4100, 1024, 32),
+    (200, 5120, 3072, 64), (256, 5101, 2048, 32), (129, 5200, 1024, 64),   # three M-blocks
 ]
 
 

@@ -30,6 +30,8 @@ def wide_splits(M, N, K, g, pair):
     instead of two where two leave a quarter of the CUs idle and three fit)."""
     mblocks = -(-M // 128)
     nblocks = -(-N // (32 if pair else 64))
+    if mblocks == 2 and 160 <= nblocks * 2 and nblocks * 3 <= 256:   # three M-blocks
+        mblocks = 3
     blocks, rounds, s = nblocks * mblocks, K // 128, 1
     while s < 8 and rounds % (2 * s) == 0 and (K // s // g > 64 or
                                                 (blocks * s < 160 and rounds // (2 * s) >= 4)):
