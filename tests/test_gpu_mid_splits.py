@@ -75,8 +75,8 @@ def test_mid_split_parity(pkg, dev, M, N, K, g):
 
 @pytest.mark.parametrize("M", [25, 32])
 def test_mid_split_epilogues(pkg, dev, M):
-    """Residual add and bias + GELU-tanh run after the halves are added (on
-    the block that adds them)."""
+    """Residual add (also in place) and bias + GELU-tanh run after the halves
+    are added (on the block that adds them)."""
     import torch
     N, K, g = 4096, 4096, 64
     assert mid_splits(N, K, g) == 2 and pkg.gemm_route(M, N, K, group_size=g) == "mid"
@@ -87,11 +87,14 @@ def test_mid_split_epilogues(pkg, dev, M):
     wt = q4w(pkg, w, s, b, K, g, dev)
     proj = o.matmul_q4_f64(x, w, s, b, g)
     y = pkg.matmul_q4_residual(to_dev(x, dev), wt, to_dev(res, dev), M, N)
+    inplace = to_dev(res, dev)   # out is the residual itself: the adding block reads, then writes
+    pkg.matmul_q4_residual(to_dev(x, dev), wt, inplace, M, N, out=inplace)
     yg = pkg.matmul_q4_ex(to_dev(x, dev), wt, M, N, out_dtype=torch.float32,
                           bias=to_dev(bias, dev), epilogue=pkg.SLTX_EPI_GELU_TANH)
     torch.cuda.synchronize()
     want = res.astype(np.float64) + proj.astype(np.float16).astype(np.float64)
     assert_parity(y.cpu().numpy(), want, TOL_GEMM_F16, f"residual M={M}")
+    assert torch.equal(inplace, y)
     assert_parity(yg.cpu().numpy(), o.gelu_tanh_f64(proj + bias), TOL_GEMM_F16,
                   f"bias+gelu M={M}")
 

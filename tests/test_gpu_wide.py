@@ -97,7 +97,7 @@ def test_wide_gated_pair(pkg, dev, M, N, K, g, gelu):
 @pytest.mark.parametrize("M,N,K", [(40, 200, 2048), (128, 3072, 8192), (250, 136, 1024)])
 def test_wide_residual_and_bias_gelu(pkg, dev, M, N, K):
     """The single-set epilogues on the wide-M route, unsplit and split:
-    residual add (linear + elemAdd, LlamaModel.swift:330-331) and bias +
+    residual add (linear + elemAdd, LlamaModel.swift:330-331; also in place) and bias +
     GELU-tanh with an fp16 activation and fp32 / bf16 outputs (DiTLinear's q4
     branch, DiTModel.swift:102-125)."""
     import torch
@@ -110,6 +110,8 @@ def test_wide_residual_and_bias_gelu(pkg, dev, M, N, K):
     wt = q4w(pkg, w, s, b, K, g, dev)
     proj = o.matmul_q4_f64(x, w, s, b, g)
     y = pkg.matmul_q4_residual(to_dev(x, dev), wt, to_dev(res, dev), M, N)
+    inplace = to_dev(res, dev)   # out is the residual itself
+    pkg.matmul_q4_residual(to_dev(x, dev), wt, inplace, M, N, out=inplace)
     yg = pkg.matmul_q4_ex(to_dev(x, dev), wt, M, N, out_dtype=torch.float32,
                           bias=to_dev(bias, dev), epilogue=pkg.SLTX_EPI_GELU_TANH)
     yb = pkg.matmul_q4_ex(to_dev(x, dev), wt, M, N, out_dtype=torch.bfloat16,
@@ -117,6 +119,7 @@ def test_wide_residual_and_bias_gelu(pkg, dev, M, N, K):
     torch.cuda.synchronize()
     want = (res.astype(np.float64) + proj.astype(np.float16).astype(np.float64))
     assert_parity(y.cpu().numpy(), want, TOL_GEMM_F16, f"residual M={M}")
+    assert torch.equal(inplace, y)
     assert_parity(yg.cpu().numpy(), o.gelu_tanh_f64(proj + bias), TOL_GEMM_F16,
                   f"bias+gelu M={M}")
     assert_parity(yb.float().cpu().numpy(), proj + bias, TOL_GEMM_BF16, f"bias bf16 M={M}")
