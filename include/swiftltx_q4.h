@@ -344,8 +344,10 @@ typedef enum {
     SLTX_ROUTE_MID = 3,      /* pipelined weight stream (8 < M <= 32, from M = 6 for a set of at most
                                 4096 rows at K = 10240; X and W through LDS, 32x32x16 MFMA; such
                                 sets split K in halves across blocks) */
-    SLTX_ROUTE_WIDE = 4      /* 32 < M <= 256: 64 weight rows per block over its K range, waves
+    SLTX_ROUTE_WIDE = 4,     /* 32 < M <= 256: 64 weight rows per block over its K range, waves
                                 split K; K split across blocks where the blocks are few */
+    SLTX_ROUTE_GEMV = 5      /* M = 2, fp16 x, one weight set of at most 5120 x 4096: the GEMV
+                                over both rows (each weight word dequantized once) */
 } sltx_route;
 int sltx_gemm_route(int32_t M, int32_t N, int32_t K, int32_t group_size, int32_t gated,
                     int32_t x_dtype);

@@ -512,12 +512,12 @@ def matmul_q4_residual_rms_norm(x, w: Q4Weight, residual, norm_weight, eps, M, N
     return residual_out, norm_out
 
 
-ROUTES = {0: "gemm", 1: "small_m", 2: "narrow", 3: "mid", 4: "wide"}
+ROUTES = {0: "gemm", 1: "small_m", 2: "narrow", 3: "mid", 4: "wide", 5: "gemv"}
 
 
 def gemm_route(M, N, K, group_size=64, gated=False, x_dtype=None):
     """The kernel family a matmul of this shape runs (sltx_gemm_route):
-    "gemm", "small_m", "narrow", "mid" or "wide".  No device needed."""
+    "gemm", "small_m", "narrow", "mid", "wide" or "gemv" (M = 2).  No device needed."""
     code = SLTX_F16 if x_dtype is None else _dtype_code(x_dtype)
     rc = lib().sltx_gemm_route(M, N, K, group_size, 1 if gated else 0, code)
     if rc < 0:

@@ -147,7 +147,40 @@ int run_gemv(const char* fn, const void* x, const sltx_q4_weight& w0, const sltx
     p.res_out = static_cast<uint16_t*>(fz.res_out);
     p.residual = static_cast<const uint16_t*>(fz.residual);
     p.gelu = fz.gelu ? 1 : 0;
+    p.rows = 1;
+    p.y_dtype = kF16;
+    p.bias = nullptr;
+    p.gelu_tanh = 0;
     return finish(launch_gemv(p, w1 != nullptr, st), fn);
+}
+
+// Two x rows on the GEMV (SLTX_ROUTE_GEMV): the M > 1 operands of p.
+hipError_t launch_gemv2(const GemmParams& g, hipStream_t st) {
+    GemvParams p;
+    p.x = static_cast<const uint16_t*>(g.a);
+    p.w0 = g.w0;
+    p.s0 = g.s0;
+    p.b0 = g.b0;
+    p.w1 = g.w1;
+    p.s1 = g.s1;
+    p.b1 = g.b1;
+    p.y = static_cast<uint16_t*>(g.y);
+    p.N = g.N;
+    p.K = g.K;
+    p.groups = g.groups;
+    p.gshift = g.gshift;
+    p.pro = kProNone;
+    p.xb = nullptr;
+    p.norm_w = nullptr;
+    p.eps = 0.0f;
+    p.res_out = nullptr;
+    p.residual = g.epilogue == kEpiResidual ? g.residual : nullptr;
+    p.gelu = g.epilogue == kEpiGeluMul ? 1 : 0;
+    p.rows = 2;
+    p.y_dtype = g.y_dtype;
+    p.bias = g.w1 ? nullptr : g.bias;
+    p.gelu_tanh = !g.w1 && g.epilogue == kEpiGeluTanh ? 1 : 0;
+    return launch_gemv(p, g.w1 != nullptr, st);
 }
 
 // Per-stream workspace (split-K partial sums, sampling scratch), one per
@@ -241,6 +274,15 @@ int release_workspace(hipStream_t st) {
 // small-M route, up to M = 16.
 int gemm_route(const GemmParams& p, bool a_bf16, NarrowPlan* np, SkinnyPlan* sp, WidePlan* wp) {
     if (p.a_f32) return SLTX_ROUTE_GEMM;   // the only kernel that casts fp32 activations
+    // Two rows of fp16 x through one weight set of at most 5120 x 4096: the
+    // GEMV, each weight word dequantized once for both rows.  Measured (us,
+    // weights rotated over >= 2 GB) against the narrow route: Llama o 3.48 /
+    // 4.11, q|k|v 5.18 / 5.35, T5 q/k/v/o 4.54 / 4.78; slower for Llama down
+    // (K = 8192: 7.20 / 6.73) and, for the gate/up pair, than the small-M
+    // route (8.98 / 8.74).
+    if (p.M == 2 && !a_bf16 && p.w1 == nullptr && p.K <= 4096 && p.N <= 5120 &&
+        gemv2_ok(p.N, p.K))
+        return SLTX_ROUTE_GEMV;
     if (p.M > 32) return wide_plan(p, a_bf16, wp) ? SLTX_ROUTE_WIDE : SLTX_ROUTE_GEMM;
     const bool narrow = narrow_plan(p, a_bf16, np);
     const bool skinny = skinny_plan(p, a_bf16, sp);
@@ -309,6 +351,7 @@ int run_gemm(const char* fn, const void* x, int x_dtype, const sltx_q4_weight& w
     const int route = gemm_route(p, x_dtype == kBF16, &np, &sp, &wp);
     if (route == SLTX_ROUTE_NARROW) return finish(launch_narrow(p, np, st), fn);
     if (route == SLTX_ROUTE_SMALL_M) return finish(launch_skinny(p, sp, st), fn);
+    if (route == SLTX_ROUTE_GEMV) return finish(launch_gemv2(p, st), fn);
     if (route == SLTX_ROUTE_MID) {
         // two K halves where the blocks are few, when the stream's workspace
         // exists (not first allocated under capture); else the whole K

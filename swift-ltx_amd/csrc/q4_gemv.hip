@@ -36,29 +36,30 @@ namespace sltx {
 // (-corr, sum).  Stored planar in LDS: xs[j][chunk] holds pairs 4j..4j+3.
 constexpr int kGemvMaxWaves = 16;   // waves per block: 4 .. 16, chosen per launch
 
-template <int NCH>
+template <int NCH, int MR>
 struct GemvLds {
-    u32x4 xs[4][NCH];
-    float2 xc[NCH];
+    u32x4 xs[MR][4][NCH];       // per x row
+    float2 xc[MR][NCH];
     float red[kGemvMaxWaves];   // per-wave partial sums of squares (RMS-norm prologue)
 };
 
 // One row-iteration's operands for one lane: CPL weight chunks per weight
 // set and their group scale/bias bit patterns (kept as 32-bit registers so
 // the loads are not merged with a wait in between).
-template <int CPL, int NW>
+template <int CPL, int NW, int MR>
 struct GemvStage {
     u32x4 w[NW][CPL];
     uint32_t s[NW][CPL];
     uint32_t b[NW][CPL];
-    uint32_t res;   // residual of the row (residual epilogue only)
+    uint32_t res[MR];   // residual of the row, per x row (residual epilogue only)
+    float bias;         // bias of the row (two x rows only)
 };
 
 // Row index is clamped into [0, N) so every load is unconditional (a
 // predicated load would be compiled into a branch with a wait inside it);
 // clamped rows are computed and discarded.
-template <int L, int CPL, int NW>
-__device__ __forceinline__ void gemv_load(GemvStage<CPL, NW>& st, const GemvParams& p, int r,
+template <int L, int CPL, int NW, int MR>
+__device__ __forceinline__ void gemv_load(GemvStage<CPL, NW, MR>& st, const GemvParams& p, int r,
                                           int kl) {
     constexpr int NCH = L * CPL;
     const int rr = r < p.N ? r : p.N - 1;
@@ -77,29 +78,74 @@ __device__ __forceinline__ void gemv_load(GemvStage<CPL, NW>& st, const GemvPara
         }
     }
     // fetched with the weights so the epilogue does not wait a memory latency
-    if (p.residual) st.res = p.residual[rr];
+    if constexpr (MR == 1) {
+        if (p.residual) st.res[0] = p.residual[rr];
+    } else {
+        if (p.residual) {
+#pragma unroll
+            for (int mr = 0; mr < MR; ++mr) st.res[mr] = p.residual[(size_t)mr * p.N + rr];
+        }
+        if (p.bias) st.bias = p.bias[rr];
+    }
 }
 
-template <int L, int CPL, int NW>
-__device__ __forceinline__ void gemv_compute_store(const GemvStage<CPL, NW>& st,
-                                                   const u32x4 (&xq)[CPL][4],
-                                                   const float2 (&xc)[CPL], const GemvParams& p,
-                                                   int r, int kl) {
-    float acc[NW];
+template <int L, int CPL, int NW, int MR>
+__device__ __forceinline__ void gemv_compute_store(const GemvStage<CPL, NW, MR>& st,
+                                                   const u32x4 (&xq)[MR][CPL][4],
+                                                   const float2 (&xc)[MR][CPL],
+                                                   const GemvParams& p, int r, int kl) {
+    if constexpr (MR == 1) {
+        float acc[NW];
 #pragma unroll
-    for (int m = 0; m < NW; ++m) {
-        float a = 0.0f;
+        for (int m = 0; m < NW; ++m) {
+            float a = 0.0f;
 #pragma unroll
-        for (int i = 0; i < CPL; ++i) {
-            const float d = chunk_dot(st.w[m][i], xq[i], xc[i].x);
-            a = fmaf(h2f((uint16_t)st.s[m][i]), d, a);
-            a = fmaf(h2f((uint16_t)st.b[m][i]), xc[i].y, a);
+            for (int i = 0; i < CPL; ++i) {
+                const float d = chunk_dot(st.w[m][i], xq[0][i], xc[0][i].x);
+                a = fmaf(h2f((uint16_t)st.s[m][i]), d, a);
+                a = fmaf(h2f((uint16_t)st.b[m][i]), xc[0][i].y, a);
+            }
+            acc[m] = row_reduce<L>(a);
         }
-        acc[m] = row_reduce<L>(a);
-    }
-    if (kl == 0 && r < p.N) {
-        const float out = NW == 2 ? glu_f32(p.gelu, acc[0], acc[NW - 1]) : acc[0];
-        p.y[r] = p.residual ? residual_add_f16((uint16_t)st.res, out) : f2h(out);
+        if (kl == 0 && r < p.N) {
+            const float out = NW == 2 ? glu_f32(p.gelu, acc[0], acc[NW - 1]) : acc[0];
+            p.y[r] = p.residual ? residual_add_f16((uint16_t)st.res[0], out) : f2h(out);
+        }
+    } else {
+        // two x rows: each weight word dequantized once for both
+        float acc[NW][2];
+#pragma unroll
+        for (int m = 0; m < NW; ++m) {
+            float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                float d0, d1;
+                chunk_dot_x2(st.w[m][i], xq[0][i], xq[1][i], xc[0][i].x, xc[1][i].x, d0, d1);
+                const float sc = h2f((uint16_t)st.s[m][i]), bc = h2f((uint16_t)st.b[m][i]);
+                a0 = fmaf(sc, d0, a0);
+                a0 = fmaf(bc, xc[0][i].y, a0);
+                a1 = fmaf(sc, d1, a1);
+                a1 = fmaf(bc, xc[1][i].y, a1);
+            }
+            acc[m][0] = row_reduce<L>(a0);
+            acc[m][1] = row_reduce<L>(a1);
+        }
+        if (kl == 0 && r < p.N) {
+#pragma unroll
+            for (int mr = 0; mr < 2; ++mr) {
+                // y [2, N] in y_dtype, + bias and GELU-tanh (one weight set)
+                float out = NW == 2 ? glu_f32(p.gelu, acc[0][mr], acc[NW - 1][mr]) : acc[0][mr];
+                const size_t o = (size_t)mr * p.N + r;
+                if (p.bias) out += st.bias;
+                if (p.gelu_tanh) out = gelu_tanh_f32(out);
+                if (p.residual)
+                    p.y[o] = residual_add_f16((uint16_t)st.res[mr], out);
+                else if (p.y_dtype == kF32)
+                    reinterpret_cast<float*>(p.y)[o] = out;
+                else
+                    p.y[o] = p.y_dtype == kBF16 ? f2bf(out) : f2h(out);
+            }
+        }
     }
 }
 
@@ -115,16 +161,19 @@ __device__ __forceinline__ void gemv_compute_store(const GemvStage<CPL, NW>& st,
 // pipelined (MULTI) kernels hold two to four times the weight registers, and
 // more than 4 chunks per lane doubles them again; each cap keeps its kernel
 // free of spills.
-template <int CPL, bool SWIGLU, bool MULTI>
-constexpr int gemv_max_waves() { return ((SWIGLU || MULTI) ? 8 : 16) / (CPL > 4 ? 2 : 1); }
+template <int CPL, bool SWIGLU, bool MULTI, int MR = 1>
+constexpr int gemv_max_waves() {
+    return ((SWIGLU || MULTI || MR > 1) ? 8 : 16) / (CPL > 4 ? 2 : 1);
+}
 
 // Blocks of 4 to gemv_max_waves() waves (blockDim.x / 64, chosen per launch).
-template <int L, int CPL, bool SWIGLU, bool MULTI, int PRO>
-__global__ __launch_bounds__((64 * gemv_max_waves<CPL, SWIGLU, MULTI>())) void q4_gemv_kernel(GemvParams p, int T) {
+template <int L, int CPL, bool SWIGLU, bool MULTI, int PRO, int MR>
+__global__ __launch_bounds__((64 * gemv_max_waves<CPL, SWIGLU, MULTI, MR>())) void q4_gemv_kernel(GemvParams p, int T) {
     constexpr int RPI = 64 / L;        // rows per wave-wide instruction
     constexpr int NCH = L * CPL;       // chunks per row (K / 32)
     constexpr int NW = SWIGLU ? 2 : 1; // weight sets
-    __shared__ GemvLds<NCH> lds;
+    static_assert(MR == 1 || (PRO == kProNone && !MULTI), "two x rows: no prologue, one iteration");
+    __shared__ GemvLds<NCH, MR> lds;
 
     const int NTH = blockDim.x;        // 256 .. 1024 threads
     const int lane = threadIdx.x & 63;
@@ -156,7 +205,7 @@ __global__ __launch_bounds__((64 * gemv_max_waves<CPL, SWIGLU, MULTI>())) void q
     // loads queued behind them.  Lanes past the vector in a preparing wave
     // (G = 4 only) load the last unit and store nothing.
     auto has_units = [&](int u) { return wave_base + NTH * u < NU; };
-    f16x8 xr[XPU][G];
+    f16x8 xr[MR][XPU][G];
     f16x8 xb[RES ? XPU : 1][G];
     f32x4 nw[NORM ? XPU : 1][2 * G];
 #pragma unroll
@@ -166,7 +215,9 @@ __global__ __launch_bounds__((64 * gemv_max_waves<CPL, SWIGLU, MULTI>())) void q
         const int uc = ui < NU ? ui : NU - 1;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            xr[u][g] = reinterpret_cast<const f16x8*>(p.x)[uc * G + g];
+#pragma unroll
+            for (int mr = 0; mr < MR; ++mr)
+                xr[mr][u][g] = reinterpret_cast<const f16x8*>(p.x)[mr * NWD + uc * G + g];
             if constexpr (RES) xb[u][g] = reinterpret_cast<const f16x8*>(p.xb)[uc * G + g];
         }
         if constexpr (NORM) {
@@ -180,8 +231,8 @@ __global__ __launch_bounds__((64 * gemv_max_waves<CPL, SWIGLU, MULTI>())) void q
     // stay in flight across the barrier below; the second stage follows after
     // it (measured: issuing both at once is slower for the 28 MB gate/up
     // launch, and keeps twice the registers live during the x preparation).
-    GemvStage<CPL, NW> sa, sb;
-    gemv_load<L, CPL, NW>(sa, p, row0, kl);
+    GemvStage<CPL, NW, MR> sa, sb;
+    gemv_load<L, CPL, NW, MR>(sa, p, row0, kl);
     __builtin_amdgcn_sched_barrier(0);
 
     if constexpr (NORM) {
@@ -199,15 +250,15 @@ __global__ __launch_bounds__((64 * gemv_max_waves<CPL, SWIGLU, MULTI>())) void q
             for (int g = 0; g < G; ++g) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    float v = (float)xr[u][g][e];
+                    float v = (float)xr[0][u][g][e];
                     if constexpr (RES) {
                         v += (float)xb[u][g][e];
-                        xr[u][g][e] = (f16)v;
+                        xr[0][u][g][e] = (f16)v;
                     }
                     ss += v * v;
                 }
                 if constexpr (RES) {
-                    if (blockIdx.x == 0) reinterpret_cast<f16x8*>(p.res_out)[ui * G + g] = xr[u][g];
+                    if (blockIdx.x == 0) reinterpret_cast<f16x8*>(p.res_out)[ui * G + g] = xr[0][u][g];
                 }
             }
         }
@@ -229,7 +280,7 @@ __global__ __launch_bounds__((64 * gemv_max_waves<CPL, SWIGLU, MULTI>())) void q
             for (int g = 0; g < G; ++g)
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    xr[u][g][e] = (f16)((float)xr[u][g][e] * rms * nw[u][2 * g + (e >> 2)][e & 3]);
+                    xr[0][u][g][e] = (f16)((float)xr[0][u][g][e] * rms * nw[u][2 * g + (e >> 2)][e & 3]);
         }
     }
 
@@ -240,33 +291,38 @@ __global__ __launch_bounds__((64 * gemv_max_waves<CPL, SWIGLU, MULTI>())) void q
         const int ui = threadIdx.x + NTH * u;
         const bool ok = ui < NU;
         const int c = (ui * G) >> 2, j0 = (ui * G) & 3;
-        float corr = 0.0f, sum = 0.0f;
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            uint32_t pr[4];
-            pair_word(xr[u][g], pr, corr, sum);
-            u32x4 v = {pr[0], pr[1], pr[2], pr[3]};
-            if (ok) lds.xs[j0 + g][c] = v;
+        for (int mr = 0; mr < MR; ++mr) {
+            float corr = 0.0f, sum = 0.0f;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                uint32_t pr[4];
+                pair_word(xr[mr][u][g], pr, corr, sum);
+                u32x4 v = {pr[0], pr[1], pr[2], pr[3]};
+                if (ok) lds.xs[mr][j0 + g][c] = v;
+            }
+            if constexpr (G == 1) {
+                corr = dpp_add<0x4E>(dpp_add<0xB1>(corr));
+                sum = dpp_add<0x4E>(dpp_add<0xB1>(sum));
+            }
+            if (ok && j0 == 0) lds.xc[mr][c] = make_float2(-corr, sum);
         }
-        if constexpr (G == 1) {
-            corr = dpp_add<0x4E>(dpp_add<0xB1>(corr));
-            sum = dpp_add<0x4E>(dpp_add<0xB1>(sum));
-        }
-        if (ok && j0 == 0) lds.xc[c] = make_float2(-corr, sum);
     }
     // LDS-only barrier: __syncthreads() would also wait for every
     // outstanding weight load (its release fence waits on vmcnt(0)).
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-    u32x4 xq[CPL][4];
-    float2 xc[CPL];
+    u32x4 xq[MR][CPL][4];
+    float2 xc[MR][CPL];
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-        const int c = kl + i * L;
+    for (int mr = 0; mr < MR; ++mr)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xq[i][j] = lds.xs[j][c];
-        xc[i] = lds.xc[c];
-    }
+        for (int i = 0; i < CPL; ++i) {
+            const int c = kl + i * L;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xq[mr][i][j] = lds.xs[mr][j][c];
+            xc[mr][i] = lds.xc[mr][c];
+        }
     // Keep these LDS reads here, before the first wait for weights: left to
     // itself the compiler sinks each one to its use (fewer VGPRs, 36 instead of
     // 99 for gate/up), which puts an LDS round trip per chunk after the data
@@ -276,13 +332,14 @@ __global__ __launch_bounds__((64 * gemv_max_waves<CPL, SWIGLU, MULTI>())) void q
 
     if constexpr (MULTI) {
         for (int t = 0; t < T; t += 2) {
-            if (t + 1 < T) gemv_load<L, CPL, NW>(sb, p, row0 + (t + 1) * RPI, kl);
-            gemv_compute_store<L, CPL, NW>(sa, xq, xc, p, row0 + t * RPI, kl);
-            if (t + 2 < T) gemv_load<L, CPL, NW>(sa, p, row0 + (t + 2) * RPI, kl);
-            if (t + 1 < T) gemv_compute_store<L, CPL, NW>(sb, xq, xc, p, row0 + (t + 1) * RPI, kl);
+            if (t + 1 < T) gemv_load<L, CPL, NW, MR>(sb, p, row0 + (t + 1) * RPI, kl);
+            gemv_compute_store<L, CPL, NW, MR>(sa, xq, xc, p, row0 + t * RPI, kl);
+            if (t + 2 < T) gemv_load<L, CPL, NW, MR>(sa, p, row0 + (t + 2) * RPI, kl);
+            if (t + 1 < T)
+                gemv_compute_store<L, CPL, NW, MR>(sb, xq, xc, p, row0 + (t + 1) * RPI, kl);
         }
     } else {
-        gemv_compute_store<L, CPL, NW>(sa, xq, xc, p, row0, kl);
+        gemv_compute_store<L, CPL, NW, MR>(sa, xq, xc, p, row0, kl);
     }
 }
 
@@ -416,14 +473,25 @@ static hipError_t launch_lc(const GemvParams& p, hipStream_t st) {
     const int wpb = gemv_block_waves(waves, T > 1 ? gemv_max_waves<CPL, SWIGLU, true>()
                                                    : gemv_max_waves<CPL, SWIGLU, false>());
     const dim3 grid((unsigned)((waves + wpb - 1) / wpb)), block(64 * wpb);
+    if (p.rows == 2) {   // two x rows: one weight set, one iteration, no prologue (gemv2_ok)
+        if constexpr (CPL <= 4 && !SWIGLU) {
+            if (T > 1 || norm) return hipErrorInvalidValue;
+            const int wpb2 = gemv_block_waves(waves, gemv_max_waves<CPL, SWIGLU, false, 2>());
+            hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, false, kProNone, 2>),
+                               dim3((unsigned)((waves + wpb2 - 1) / wpb2)), dim3(64 * wpb2), 0,
+                               st, p, 1);
+            return hipGetLastError();
+        }
+        return hipErrorInvalidValue;
+    }
     if (T > 1 && norm)
-        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, true, PRO_N>), grid, block, 0, st, p, (int)T);
+        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, true, PRO_N, 1>), grid, block, 0, st, p, (int)T);
     else if (T > 1)
-        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, true, kProNone>), grid, block, 0, st, p, (int)T);
+        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, true, kProNone, 1>), grid, block, 0, st, p, (int)T);
     else if (norm)
-        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, false, PRO_N>), grid, block, 0, st, p, 1);
+        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, false, PRO_N, 1>), grid, block, 0, st, p, 1);
     else
-        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, false, kProNone>), grid, block, 0, st, p, 1);
+        hipLaunchKernelGGL((q4_gemv_kernel<L, CPL, SWIGLU, false, kProNone, 1>), grid, block, 0, st, p, 1);
     return hipGetLastError();
 }
 
@@ -457,8 +525,19 @@ int gemv_pick_lanes(int K, int* cpl_out) {
     return 0;
 }
 
+// Two x rows (p.rows == 2) of one weight set run where a specialised
+// (L, CPL) kernel covers K with at most 4 chunks per lane (both rows' x pairs
+// stay in registers) in one row-iteration per wave, with no prologue.
+bool gemv2_ok(int N, int K) {
+    int cpl = 0;
+    const int L = gemv_pick_lanes(K, &cpl);
+    return L != 0 && cpl <= 4 && (N + 64 / L - 1) / (64 / L) < 8192;
+}
+
 hipError_t launch_gemv(const GemvParams& p, bool swiglu, hipStream_t st) {
     if (p.pro != kProNone && p.pro != (swiglu ? kProResidualRms : kProRms)) return hipErrorInvalidValue;
+    if (p.rows == 2 && (swiglu || p.pro != kProNone || !gemv2_ok(p.N, p.K)))
+        return hipErrorInvalidValue;
     int cpl = 0;
     const int L = gemv_pick_lanes(p.K, &cpl);
     if (L == 64) return swiglu ? launch_l<64, true>(p, cpl, st) : launch_l<64, false>(p, cpl, st);

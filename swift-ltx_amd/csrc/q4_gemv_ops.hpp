@@ -53,6 +53,39 @@ __device__ __forceinline__ float chunk_dot(const u32x4 w, const u32x4 xq[4], flo
     return d0 + d1;
 }
 
+// chunk_dot for two x rows over the same weight chunk: each word is
+// dequantized once and dotted with both rows' pairs (four chains).
+__device__ __forceinline__ void chunk_dot_x2(const u32x4 w, const u32x4 xa[4], const u32x4 xb[4],
+                                             float nca, float ncb, float& ra, float& rb) {
+    float a0, a1, b0, b1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t wj = w[j];
+        const uint32_t w8 = wj >> 8;
+        const uint32_t p0 = and_or(wj, 0x000F000Fu, kMagic1024x2);
+        const uint32_t p1 = and_or(wj, 0x00F000F0u, kMagic1024x2);
+        const uint32_t p2 = and_or(w8, 0x000F000Fu, kMagic1024x2);
+        const uint32_t p3 = and_or(w8, 0x00F000F0u, kMagic1024x2);
+        if (j == 0) {
+            asm("v_dot2_f32_f16 %0, %1, %2, %3" : "=v"(a0) : "v"(p0), "v"(xa[j][0]), "v"(nca));
+            asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(a1) : "v"(p1), "v"(xa[j][1]));
+            asm("v_dot2_f32_f16 %0, %1, %2, %3" : "=v"(b0) : "v"(p0), "v"(xb[j][0]), "v"(ncb));
+            asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(b1) : "v"(p1), "v"(xb[j][1]));
+        } else {
+            a0 = dot2(as_f16x2(p0), as_f16x2(xa[j][0]), a0);
+            a1 = dot2(as_f16x2(p1), as_f16x2(xa[j][1]), a1);
+            b0 = dot2(as_f16x2(p0), as_f16x2(xb[j][0]), b0);
+            b1 = dot2(as_f16x2(p1), as_f16x2(xb[j][1]), b1);
+        }
+        a0 = dot2(as_f16x2(p2), as_f16x2(xa[j][2]), a0);
+        a1 = dot2(as_f16x2(p3), as_f16x2(xa[j][3]), a1);
+        b0 = dot2(as_f16x2(p2), as_f16x2(xb[j][2]), b0);
+        b1 = dot2(as_f16x2(p3), as_f16x2(xb[j][3]), b1);
+    }
+    ra = a0 + a1;
+    rb = b0 + b1;
+}
+
 // v + (v from another lane of the same 16-lane row), by DPP.
 template <int CTRL>
 __device__ __forceinline__ float dpp_add(float v) {

@@ -31,7 +31,16 @@ struct GemvParams {
     // Epilogue: y = half(residual + half(x . W^T)) when non-null.
     const uint16_t* residual;
     int gelu;               // two weight sets: gelu_tanh(g) * u instead of silu(g) * u
+    // Two x rows (rows == 2, no prologue): x, residual and y are [2, N]
+    // (x [2, K]), y in y_dtype (kF16, kF32 or kBF16), and one weight set may
+    // add bias[n] (fp32) and apply GELU-tanh.  rows == 1: fp16 y, neither.
+    int rows;
+    int y_dtype;
+    const float* bias;
+    int gelu_tanh;
 };
+// Whether the two-row GEMV covers N x K (q4_gemv.hip).
+bool gemv2_ok(int N, int K);
 
 enum GemvPro : int { kProNone = 0, kProRms = 1, kProResidualRms = 2 };
 

@@ -25,7 +25,7 @@ pytestmark = pytest.mark.gpu
 # Every run count, N not a multiple of 4, every group size, M = 1..4, and at
 # most 78 KB of X in LDS (M * K * 2 bytes; M = 3 at K = 10240).
 SHAPES = [
-    (1, 50, 2048, 64), (2, 33, 3072, 32), (3, 64, 4096, 128), (4, 97, 5120, 64),
+    (1, 50, 2048, 64), (2, 33, 6144, 32), (3, 64, 4096, 128), (4, 97, 5120, 64),
     (2, 41, 6144, 64), (3, 30, 8192, 32), (3, 21, 10240, 64), (1, 5, 3072, 64),
     (2, 6000, 2048, 64), (4, 4000, 3072, 64), (3, 10001, 4096, 32), (4, 10002, 6144, 128),
     (1, 16400, 4096, 64), (2, 16401, 5120, 128),
@@ -80,7 +80,8 @@ def test_narrow_residual_bias_gelu_dtypes(pkg, dev, M):
     (DiTLinear's q4 branch, DiTModel.swift:102-125), and fp32 / bf16
     outputs (the residual entry sends M = 1 to the GEMV)."""
     import torch
-    N, K, g = 158, 4096, 64
+    N, K, g = 158, 6144, 64   # K > 4096: M = 2 stays off the two-row GEMV
+    assert pkg.gemm_route(M, N, K, group_size=g) == "narrow"
     x, [(w, s, b)] = o.make_inputs(M, N, K, g, seed=700 + M)
     rng = np.random.default_rng(M)
     res = rng.standard_normal((M, N)).astype(np.float16)

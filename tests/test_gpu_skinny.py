@@ -29,7 +29,7 @@ pytestmark = pytest.mark.gpu
 # N not a multiple of 16, every group size.  (At K = 4096 above 16 rows and
 # at K = 10240 above 8, a set of at most 4096 rows takes the mid-M route.)
 SHAPES = [
-    (2, 200, 1024, 64), (5, 64, 2048, 32), (16, 100, 3072, 64), (8, 48, 4096, 128),
+    (3, 200, 1024, 64), (5, 64, 2048, 32), (16, 100, 3072, 64), (8, 48, 4096, 128),
     (5, 80, 5120, 64), (7, 33, 6144, 64), (17, 96, 1024, 32), (32, 112, 1024, 64),
     (24, 4150, 4096, 128), (22, 4160, 4096, 64), (6, 96, 8192, 64), (16, 4200, 10240, 64),
     (9, 24, 14336, 32), (1, 300, 1024, 64), (4, 64, 10240, 64),

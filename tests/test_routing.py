@@ -68,7 +68,12 @@ def test_mid_m_route_for_one_set_above_8_rows(pkg, M):
                                  (4096, 10240)])
 @pytest.mark.parametrize("M", [1, 2, 3, 4])
 def test_one_weight_set_at_m_le_4_is_narrow(pkg, N, K, M):
-    if K == 10240 and M > 3:   # X = M * K * 2 bytes over the route's 78 KB of LDS
+    """M = 2 through a set of at most 5120 x 4096 takes the two-row GEMV
+    (Llama o 3.48 against 4.11 us on the narrow route, q|k|v 5.18 / 5.35,
+    T5 q/k/v/o 4.54 / 4.78); the rest of M <= 4 the narrow route."""
+    if M == 2 and K <= 4096 and N <= 5120:
+        assert pkg.gemm_route(M, N, K) == "gemv"
+    elif K == 10240 and M > 3:   # X = M * K * 2 bytes over the route's 78 KB of LDS
         assert pkg.gemm_route(M, N, K) == "small_m"
     else:
         assert pkg.gemm_route(M, N, K) == "narrow"
