@@ -80,7 +80,7 @@ DECODE = [("qkv_proj", 5120, 3072, 1), ("o_proj", 3072, 3072, 1),
           ("gate_up_proj", 8192, 3072, 2), ("down_proj", 3072, 8192, 1)]
 LAYER_BYTES = sum(gemv_bytes(N, K, n) for _, N, K, n in DECODE)  # 56,696,832
 DOMINANT = "gate_up_proj"
-DOMINANT_KERNEL = "q4_gemv_kernel<32, 3, true, false, 0>"
+DOMINANT_KERNEL = "q4_gemv_kernel<32, 3, true, false, 0, 1>"   # one x row
 DOMINANT_BYTES = gemv_bytes(8192, 3072, 2)  # 28,334,080
 
 
