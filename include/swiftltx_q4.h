@@ -113,14 +113,17 @@ int sltx_release_workspace(void* stream);
 /* matmulQ4(_:weight:scales:biases:M:K:N:groupSize:) -> Tensor  (Ops.swift:285-305)
  * out[M,N] fp16 = x[M,K] fp16 . dequant(W)^T.  M == 1 runs the HBM-streaming
  * GEMV (the reference's matmul_q4, Kernels.swift:444-620); M > 1 runs the
- * MFMA GEMM (the reference re-reads W per row here; results agree within
- * the stated tolerance). */
+ * route sltx_gemm_route names: the same GEMV over two rows at M == 2 on sets
+ * of at most 5120 x 4096, else an MFMA weight stream or the MFMA GEMM (the
+ * reference re-reads W per row here; results agree within the stated
+ * tolerance). */
 int sltx_matmul_q4(const void* x, const uint32_t* weight, const uint16_t* scales,
                    const uint16_t* biases, void* out, int32_t M, int32_t K, int32_t N,
                    int32_t group_size, void* stream);
 
 /* matmulQ4Fast(_:weight:scales:biases:M:K:N:groupSize:) -> Tensor  (Ops.swift:312-345)
- * Same product, fp16 out, through the MFMA GEMM for every M (M == 1 included). */
+ * Same product, fp16 out, through the M > 1 routes for every M (M == 1
+ * included: the MFMA GEMM's numerics). */
 int sltx_matmul_q4_fast(const void* x, const uint32_t* weight, const uint16_t* scales,
                         const uint16_t* biases, void* out, int32_t M, int32_t K, int32_t N,
                         int32_t group_size, void* stream);
